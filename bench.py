@@ -1,0 +1,229 @@
+#!/usr/bin/env python
+"""Benchmark of the quantized-dtype hot path on one MI355X.
+
+One step = BASELINE config [2]: a cast sweep over 2^28 fp32 elements held in
+HBM: fp32 -> fp16 -> fp32, fp32 -> bf16 -> fp32, and for E4M3 and E5M2 the
+per-tensor amax, the scale, the scaled cast and the scaled dequantization
+back to fp32.  `value` is the algorithmic bytes of the step (52 B/element)
+over its wall time, in GB/s.  Each kernel is also bracketed by HIP events on
+the stream it runs on, which gives the per-kernel roofline figures.  A
+secondary leg times the FP8-weight Linear of config [4] (x 2048x4096,
+W 4096x4096 E4M3) in TFLOP/s.  The CPU baseline is the C oracle on a bounded
+sample of the same sweep.
+
+Prints ONE JSON line.  Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+METRIC = "cast GB/s (% HBM peak) at 256M elems; FP8-weight Linear TFLOP/s at 4096^2"
+
+# (op name, algorithmic bytes per element); the sequence of one step
+SWEEP = [
+    ("f32->f16", 6), ("f16->f32", 6), ("f32->bf16", 6), ("bf16->f32", 6),
+    ("amax e4m3", 4), ("scale e4m3", 0), ("f32->e4m3 scaled", 5), ("e4m3->f32 scaled", 5),
+    ("amax e5m2", 4), ("scale e5m2", 0), ("f32->e5m2 scaled", 5), ("e5m2->f32 scaled", 5),
+]
+BYTES_PER_ELEM = sum(b for _, b in SWEEP)
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def make_sweep(n: int, dev):
+    """Device buffers and the list of (name, bytes/elem, launch fn) of a step."""
+    import torch
+
+    from novann_amd import _lib
+    lib = _lib.load()
+    g = torch.Generator(device=dev)
+    g.manual_seed(2)
+    x = torch.empty(n, dtype=torch.float32, device=dev)
+    x.uniform_(-20.0, 20.0, generator=g)
+    x.exp2_()
+    u = torch.empty(n, dtype=torch.float32, device=dev).uniform_(generator=g)
+    x.copysign_(u - 0.5)  # random sign
+    del u
+    y = torch.empty_like(x)
+    h = torch.empty(n, dtype=torch.int16, device=dev)
+    q = torch.empty(n, dtype=torch.uint8, device=dev)
+    amax = torch.zeros(2, dtype=torch.float32, device=dev)
+    scale = torch.ones(2, dtype=torch.float32, device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    P = lambda t: t.data_ptr()  # noqa: E731
+
+    def cast(src, st, dst, dt, sc=None):
+        return lambda: _lib.check(lib.novaq_cast(P(src), st, P(dst), dt, n, sc, stream), "cast")
+
+    ops = [
+        cast(x, 0, h, 1), cast(h, 1, y, 0), cast(x, 0, h, 2), cast(h, 2, y, 0),
+    ]
+    for k, dt in enumerate((3, 4)):
+        a_ptr, s_ptr = P(amax) + 4 * k, P(scale) + 4 * k
+        ops += [
+            lambda a_ptr=a_ptr: _lib.check(lib.novaq_amax(P(x), 0, n, a_ptr, stream), "amax"),
+            lambda a_ptr=a_ptr, s_ptr=s_ptr, dt=dt: _lib.check(
+                lib.novaq_scale_from_amax(a_ptr, dt, s_ptr, stream), "scale"),
+            cast(x, 0, q, dt, s_ptr), cast(q, dt, y, 0, s_ptr),
+        ]
+    return [(name, b, fn) for (name, b), fn in zip(SWEEP, ops)], (x, y, h, q, amax, scale)
+
+
+def bench_sweep(n: int, steps: int, warmup: int, dev):
+    import torch
+    ops, bufs = make_sweep(n, dev)
+    for _ in range(warmup):
+        for _, _, fn in ops:
+            fn()
+    torch.cuda.synchronize(dev)
+    events = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in ops] for _ in range(steps)]
+    torch.cuda.synchronize(dev)
+    t0 = time.perf_counter()
+    for s in range(steps):
+        for (_, _, fn), (e0, e1) in zip(ops, events[s]):
+            e0.record()
+            fn()
+            e1.record()
+    torch.cuda.synchronize(dev)
+    t1 = time.perf_counter()
+    per_op = []
+    for i, (name, b, _) in enumerate(ops):
+        ms = sum(events[s][i][0].elapsed_time(events[s][i][1]) for s in range(steps)) / steps
+        gbs = b * n / (ms * 1e-3) / 1e9 if b else None
+        per_op.append({"op": name, "ms": round(ms, 4),
+                       "GB/s": None if gbs is None else round(gbs, 1),
+                       "frac": None if gbs is None else round(gbs / HBM_PEAK_GBS, 4)})
+    del bufs
+    return (t1 - t0) * 1e3 / steps, per_op
+
+
+def bench_linear(dev, iters: int = 20, warmup: int = 5):
+    """Config [4]: y = x W^T + b, x (2048, 4096) fp32, W (4096, 4096) E4M3."""
+    import torch
+
+    from novann_amd import _lib, quant
+    lib = _lib.load()
+    M, K, N = 2048, 4096, 4096
+    g = torch.Generator(device=dev)
+    g.manual_seed(4)
+    x = torch.randn((M, K), generator=g, device=dev, dtype=torch.float32)
+    w = torch.randn((N, K), generator=g, device=dev, dtype=torch.float32) * (2.0 / K) ** 0.5
+    wq = quant.quantize(w, "e4m3")
+    b = torch.zeros(N, dtype=torch.float32, device=dev)
+    y = torch.empty((M, N), dtype=torch.float32, device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+
+    def run():
+        _lib.check(lib.novaq_linear_forward(x.data_ptr(), M, K, wq.data.data_ptr(), 3,
+                                            wq.scale.data_ptr(), b.data_ptr(), N, y.data_ptr(),
+                                            stream), "linear")
+    try:
+        run()
+    except NotImplementedError:
+        return None
+    for _ in range(warmup):
+        run()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize(dev)
+    e0.record()
+    for _ in range(iters):
+        run()
+    e1.record()
+    torch.cuda.synchronize(dev)
+    ms = e0.elapsed_time(e1) / iters
+    flops = 2.0 * M * N * K
+    tflops = flops / (ms * 1e-3) / 1e12
+    return {"metric": "FP8-weight Linear TFLOP/s at 4096^2", "value": round(tflops, 1),
+            "unit": "TFLOP/s", "ms": round(ms, 4),
+            "config": {"workload": "BASELINE config [4]", "M": M, "K": K, "N": N,
+                       "w_dtype": "e4m3", "mfma": "bf16"},
+            "roofline": {"bound": "mfma", "achieved": round(tflops, 1),
+                         "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "traffic": None}}
+
+
+def cpu_baseline(sample: int):
+    """The C oracle running the same sweep on a bounded sample (all host cores)."""
+    import numpy as np
+
+    import oracle as O
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count() or 1
+    rng = np.random.default_rng(2)
+    x = (np.exp2(rng.uniform(-20, 20, sample)) * np.where(rng.random(sample) < 0.5, -1, 1)
+         ).astype(np.float32)
+    t0 = time.perf_counter()
+    for st in (O.F16, O.BF16):
+        O.cast(O.cast(x, O.F32, st, nthreads=threads), st, O.F32, n=sample, nthreads=threads)
+    for dt in (O.E4M3, O.E5M2):
+        s = O.scale_from_amax(O.amax(x, nthreads=threads), dt)
+        q = O.cast(x, O.F32, dt, scale=s, nthreads=threads)
+        O.cast(q, dt, O.F32, n=sample, scale=s, nthreads=threads)
+    dt_s = time.perf_counter() - t0
+    return {"value": round(BYTES_PER_ELEM * sample / dt_s / 1e9, 3), "unit": "GB/s",
+            "cores": threads, "kind": "port",
+            "sample": f"config [2] sweep on {sample} elements ({sample >> 20}M), C oracle, "
+                      f"{threads} OpenMP threads, {dt_s:.1f} s"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--elems", type=int, default=1 << 28)
+    ap.add_argument("--cpu-sample", type=int, default=1 << 26)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-linear", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(run with --gpus 1)", file=sys.stderr)
+        return 2
+    import torch
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    log(f"sweep: {args.elems} elements, {args.steps} steps, {args.warmup} warmup")
+    ms, per_op = bench_sweep(args.elems, args.steps, args.warmup, dev)
+    value = BYTES_PER_ELEM * args.elems / (ms * 1e-3) / 1e9
+    kernels = [p for p in per_op if p["GB/s"] is not None]
+    dom = max(kernels, key=lambda p: p["ms"])
+    dom_bpe = dict(SWEEP)[dom["op"]]
+    log(f"sweep done: {ms:.3f} ms/step, {value:.1f} GB/s")
+    lin = None if args.no_linear else bench_linear(dev)
+    log(f"linear: {lin}")
+    cpu = None if args.no_cpu else cpu_baseline(args.cpu_sample)
+    log(f"cpu baseline: {cpu}")
+    out = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32<->{f16,bf16,e4m3,e5m2}", "data": "synthetic",
+        "config": {"workload": "BASELINE config [2]: cast sweep, amax-scaled FP8",
+                   "elements": args.elems, "bytes_per_element": BYTES_PER_ELEM},
+        "roofline": {"bound": "hbm", "kernel": dom["op"], "achieved": dom["GB/s"],
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": dom["frac"],
+                     "traffic": None,
+                     "bytes_per_launch": dom_bpe * args.elems},
+        "kernels": per_op,
+        "linear": lin,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,151 @@
+/*
+ * novaq -- MI355X (gfx950) quantized-dtype hot path for NovaNN-style layers.
+ *
+ * C ABI of libnovaq.so.  Plain pointers and sizes only: every tensor argument
+ * is a DEVICE pointer owned by the caller, every entry point takes the HIP
+ * stream to run on as `void *stream` (NULL = the default stream) and returns
+ * an int status (NOVAQ_OK = 0, negative = error).  Nothing is synchronised:
+ * results are ready once the stream has drained.  Calls on different streams
+ * may run concurrently; a call never allocates device memory.
+ *
+ * Dtype codes and element storage:
+ *   NOVAQ_F32   4 B   IEEE binary32
+ *   NOVAQ_F16   2 B   IEEE binary16
+ *   NOVAQ_BF16  2 B   bfloat16
+ *   NOVAQ_E4M3  1 B   OCP FP8 E4M3 (bias 7, max 448, NaN 0x7F/0xFF, no Inf)
+ *   NOVAQ_E5M2  1 B   OCP FP8 E5M2 (bias 15, max 57344, Inf 0x7C, NaN 0x7D-0x7F)
+ *   NOVAQ_E2M1  1/2 B OCP MX FP4 E2M1 {0,.5,1,1.5,2,3,4,6}, two per byte:
+ *                     element 2i in bits 3..0, element 2i+1 in bits 7..4; a
+ *                     buffer of n elements holds ceil(n/2) bytes, an odd tail
+ *                     is padded with +0.
+ *
+ * Rounding and specials (identical on every entry point):
+ *   - narrowing is round-to-nearest-even; widening is exact;
+ *   - fp16: overflow -> +-Inf; NaN -> 0x7C00 + (mantissa >> 13), +1 if that
+ *     reads as Inf (numpy's float32->float16 rule); fp16 -> fp32 keeps the
+ *     NaN payload;
+ *   - bf16: overflow -> +-Inf; NaN -> top 16 bits with bit 6 (quiet) set;
+ *   - E4M3 / E5M2 are saturating: finite overflow and +-Inf go to +-max;
+ *     NaN -> 0x7F | sign; decoded NaN is 0x7FC00000 | sign;
+ *   - E2M1 saturates to +-6 (Inf too); NaN -> +0;
+ *   - -0 and negative values that round to zero keep the sign bit.
+ *
+ * Scaling (per tensor): `scale` points to one fp32 s on the device.  Casting
+ * to E4M3/E5M2/E2M1 encodes x * (1/s); casting from them decodes q * s; each
+ * is one correctly rounded fp32 multiply, and 1/s is a correctly rounded fp32
+ * division.  scale == NULL means unscaled.  Scaling a cast that involves no
+ * quantized type is an error.
+ *
+ * Buffers must be 16-byte aligned (NOVAQ_EALIGN otherwise).
+ */
+#ifndef NOVAQ_H
+#define NOVAQ_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum novaq_dtype {
+  NOVAQ_F32 = 0,
+  NOVAQ_F16 = 1,
+  NOVAQ_BF16 = 2,
+  NOVAQ_E4M3 = 3,
+  NOVAQ_E5M2 = 4,
+  NOVAQ_E2M1 = 5
+};
+
+/* Padding modes of NovaNN's conv2d (novann/functional.py:325-344): numpy.pad's
+ * constant(0) / reflect / edge / wrap. */
+enum novaq_pad_mode {
+  NOVAQ_PAD_ZEROS = 0,
+  NOVAQ_PAD_REFLECT = 1,
+  NOVAQ_PAD_REPLICATE = 2,
+  NOVAQ_PAD_CIRCULAR = 3
+};
+
+enum novaq_status {
+  NOVAQ_OK = 0,
+  NOVAQ_EINVAL = -1,   /* null pointer, negative size, bad geometry */
+  NOVAQ_EDTYPE = -2,   /* dtype code unknown or not allowed here */
+  NOVAQ_ESHAPE = -3,   /* shapes inconsistent (e.g. output size <= 0) */
+  NOVAQ_EPADMODE = -4, /* padding mode unknown (NovaNN raises ValueError) */
+  NOVAQ_EALIGN = -5,   /* a buffer is not 16-byte aligned */
+  NOVAQ_EHIP = -6,     /* the HIP runtime reported an error */
+  NOVAQ_ENOTSUP = -7   /* valid request this build does not implement */
+};
+
+/* Library version as MAJOR*10000 + MINOR*100 + PATCH. */
+int novaq_version(void);
+/* Static text for a status code. */
+const char *novaq_status_string(int status);
+/* HIP error code (hipError_t value) behind the last NOVAQ_EHIP on this thread. */
+int novaq_last_hip_error(void);
+
+/* Element-wise cast of n elements from src (src_dtype) to dst (dst_dtype).
+ * Replaces: NovaNN has no cast entry point; its only dtype conversions are
+ * x.astype(np.float32, copy=False) at layer entry (novann/layers/linear/
+ * linear.py:81, novann/layers/convolutional/conv2d.py:159) and
+ * np.asarray(w, dtype=np.float32) at weight init (linear.py:59,
+ * conv2d.py:65).  This generalises them to every pair of
+ * {F32, F16, BF16} x {F32, F16, BF16, E4M3, E5M2, E2M1} and back; a cast
+ * between two quantized types returns NOVAQ_EDTYPE. */
+int novaq_cast(const void *src, int src_dtype, void *dst, int dst_dtype, int64_t n,
+               const float *scale, void *stream);
+
+/* NaN-ignoring max |x| of n F32/F16/BF16 elements, written to *amax (device).
+ * No reference counterpart (per-tensor scaling is new on this path). */
+int novaq_amax(const void *x, int dtype, int64_t n, float *amax, void *stream);
+
+/* *scale = *amax / fmt_max (448 for E4M3, 57344 for E5M2, 6 for E2M1), or 1
+ * when *amax is 0 or not finite.  Both pointers are device pointers. */
+int novaq_scale_from_amax(const float *amax, int dst_dtype, float *scale, void *stream);
+
+/* Per-tensor scaled quantization in one call: amax, scale, then the scaled
+ * cast.  amax_scale points to two device floats; on completion
+ * amax_scale[0] = amax of src and amax_scale[1] = s.  dst_dtype must be
+ * E4M3, E5M2 or E2M1. */
+int novaq_quantize(const void *src, int src_dtype, void *dst, int dst_dtype, int64_t n,
+                   float *amax_scale, void *stream);
+
+/* FP4 E2M1 pack / unpack of n fp32 elements (equivalent to novaq_cast
+ * F32 <-> E2M1); packed holds ceil(n/2) bytes in the nibble order above. */
+int novaq_pack_fp4(const float *x, int64_t n, const float *scale, uint8_t *packed,
+                   void *stream);
+int novaq_unpack_fp4(const uint8_t *packed, int64_t n, const float *scale, float *y,
+                     void *stream);
+
+/* y[N, D_out] = x[N, D_in] @ (s * dec(w_q))^T + bias.
+ * Replaces: novann.functional.linear(input, weight, bias)
+ * (novann/functional.py:147-163), called by Linear.forward
+ * (novann/layers/linear/linear.py:70-83).  w_q is (D_out, D_in) row-major in
+ * w_dtype (E4M3, E5M2, E2M1 packed along D_in, BF16, F16 or F32); w_scale is
+ * the per-tensor s (NULL = 1); bias is D_out fp32 values or NULL (the
+ * reference's (1, D_out) bias); y is (N, D_out) fp32, freshly written.
+ * Products run on bf16 MFMA with fp32 accumulation; the scale and the bias are
+ * applied in fp32 after accumulation. */
+int novaq_linear_forward(const float *x, int64_t N, int64_t D_in, const void *w_q,
+                         int w_dtype, const float *w_scale, const float *bias,
+                         int64_t D_out, float *y, void *stream);
+
+/* 2-D cross-correlation of x (N, C, H, W) fp32 with s * dec(w_q)
+ * (C_out, C, KH, KW), stride (sh, sw), padding (ph, pw) in pad_mode, plus
+ * bias (C_out values or NULL).  y is contiguous (N, C_out, OH, OW) fp32 with
+ * OH = (H + 2ph - KH)/sh + 1, OW = (W + 2pw - KW)/sw + 1.
+ * Replaces: novann.functional.conv2d(input, weight, kernel_size, stride,
+ * padding, bias=, padding_mode=) (novann/functional.py:275-385), called by
+ * Conv2d.forward (novann/layers/convolutional/conv2d.py:150-177).  The
+ * reference materialises im2col (functional.py:346-368) and returns a
+ * transposed view (:382); this computes the same values with implicit im2col
+ * and writes NCHW directly.  Every padding mode takes any padding width, with
+ * numpy.pad's index rules (reflect repeats with period 2(n-1)). */
+int novaq_conv2d_forward(const float *x, int64_t N, int64_t C, int64_t H, int64_t W,
+                         const void *w_q, int w_dtype, const float *w_scale,
+                         int64_t C_out, int KH, int KW, int sh, int sw, int ph, int pw,
+                         int pad_mode, const float *bias, float *y, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* NOVAQ_H */

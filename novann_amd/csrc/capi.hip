@@ -1,0 +1,139 @@
+// C ABI of libnovaq.so (declared in include/novaq.h): argument validation,
+// status codes and dispatch to the kernel launchers.  No entry point
+// allocates device memory or synchronises the stream.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "novaq_convert.h"
+#include "novaq_internal.h"
+
+namespace novaq {
+
+static thread_local int g_last_hip_error = 0;
+
+int hip_fail(hipError_t e) {
+  g_last_hip_error = (int)e;
+  return NOVAQ_EHIP;
+}
+
+int device_cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 256;
+  if (dev < 64 && cached[dev] > 0) return cached[dev];
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus <= 0)
+    cus = 256;
+  if (dev < 64) cached[dev] = cus;
+  return cus;
+}
+
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+static bool valid_dtype(int dt) { return dt >= F32 && dt <= E2M1; }
+
+}  // namespace novaq
+
+using namespace novaq;
+
+extern "C" {
+
+int novaq_version(void) { return 100; }
+
+const char* novaq_status_string(int status) {
+  switch (status) {
+    case NOVAQ_OK: return "ok";
+    case NOVAQ_EINVAL: return "invalid argument";
+    case NOVAQ_EDTYPE: return "unsupported dtype";
+    case NOVAQ_ESHAPE: return "inconsistent shapes";
+    case NOVAQ_EPADMODE: return "unknown padding mode";
+    case NOVAQ_EALIGN: return "buffer not 16-byte aligned";
+    case NOVAQ_EHIP: return "HIP runtime error";
+    case NOVAQ_ENOTSUP: return "not supported";
+    default: return "unknown status";
+  }
+}
+
+int novaq_last_hip_error(void) { return g_last_hip_error; }
+
+int novaq_cast(const void* src, int src_dtype, void* dst, int dst_dtype, int64_t n,
+               const float* scale, void* stream) {
+  if (!valid_dtype(src_dtype) || !valid_dtype(dst_dtype)) return NOVAQ_EDTYPE;
+  if (is_quant(src_dtype) && is_quant(dst_dtype)) return NOVAQ_EDTYPE;
+  if (n < 0) return NOVAQ_EINVAL;
+  if (scale && !is_quant(src_dtype) && !is_quant(dst_dtype)) return NOVAQ_EINVAL;
+  if (n == 0) return NOVAQ_OK;
+  if (!src || !dst) return NOVAQ_EINVAL;
+  if (!aligned16(src) || !aligned16(dst)) return NOVAQ_EALIGN;
+  return cast_launch(src, src_dtype, dst, dst_dtype, n, scale ? 1 : 0, scale, nullptr,
+                     static_cast<hipStream_t>(stream));
+}
+
+int novaq_amax(const void* x, int dtype, int64_t n, float* amax, void* stream) {
+  if (dtype != F32 && dtype != F16 && dtype != BF16) return NOVAQ_EDTYPE;
+  if (n < 0 || !amax || (n > 0 && !x)) return NOVAQ_EINVAL;
+  if (n > 0 && !aligned16(x)) return NOVAQ_EALIGN;
+  return amax_launch(x, dtype, n, amax, static_cast<hipStream_t>(stream));
+}
+
+int novaq_scale_from_amax(const float* amax, int dst_dtype, float* scale, void* stream) {
+  if (!is_quant(dst_dtype)) return NOVAQ_EDTYPE;
+  if (!amax || !scale) return NOVAQ_EINVAL;
+  return scale_from_amax_launch(amax, dst_dtype, scale, static_cast<hipStream_t>(stream));
+}
+
+int novaq_quantize(const void* src, int src_dtype, void* dst, int dst_dtype, int64_t n,
+                   float* amax_scale, void* stream) {
+  if (src_dtype != F32 && src_dtype != F16 && src_dtype != BF16) return NOVAQ_EDTYPE;
+  if (!is_quant(dst_dtype)) return NOVAQ_EDTYPE;
+  if (n < 0 || !amax_scale || (n > 0 && (!src || !dst))) return NOVAQ_EINVAL;
+  if (n > 0 && (!aligned16(src) || !aligned16(dst))) return NOVAQ_EALIGN;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int rc = amax_launch(src, src_dtype, n, amax_scale, s);
+  if (rc != NOVAQ_OK) return rc;
+  if (n == 0) return scale_from_amax_launch(amax_scale, dst_dtype, amax_scale + 1, s);
+  return cast_launch(src, src_dtype, dst, dst_dtype, n, 2, amax_scale, amax_scale + 1, s);
+}
+
+int novaq_pack_fp4(const float* x, int64_t n, const float* scale, uint8_t* packed,
+                   void* stream) {
+  return novaq_cast(x, F32, packed, E2M1, n, scale, stream);
+}
+
+int novaq_unpack_fp4(const uint8_t* packed, int64_t n, const float* scale, float* y,
+                     void* stream) {
+  return novaq_cast(packed, E2M1, y, F32, n, scale, stream);
+}
+
+int novaq_linear_forward(const float* x, int64_t N, int64_t D_in, const void* w_q,
+                         int w_dtype, const float* w_scale, const float* bias,
+                         int64_t D_out, float* y, void* stream) {
+  if (!valid_dtype(w_dtype)) return NOVAQ_EDTYPE;
+  if (N < 0 || D_in < 0 || D_out < 0) return NOVAQ_EINVAL;
+  if (N == 0 || D_out == 0) return NOVAQ_OK;
+  if (!x || !w_q || !y) return NOVAQ_EINVAL;
+  if (w_dtype == E2M1 && (D_in & 1)) return NOVAQ_ESHAPE;  // rows of whole bytes
+  if (!aligned16(x) || !aligned16(w_q) || !aligned16(y) || (bias && !aligned16(bias)))
+    return NOVAQ_EALIGN;
+  return linear_launch(x, N, D_in, w_q, w_dtype, w_scale, bias, D_out, y,
+                       static_cast<hipStream_t>(stream));
+}
+
+int novaq_conv2d_forward(const float* x, int64_t N, int64_t C, int64_t H, int64_t W,
+                         const void* w_q, int w_dtype, const float* w_scale, int64_t C_out,
+                         int KH, int KW, int sh, int sw, int ph, int pw, int pad_mode,
+                         const float* bias, float* y, void* stream) {
+  if (!valid_dtype(w_dtype)) return NOVAQ_EDTYPE;
+  if (pad_mode < NOVAQ_PAD_ZEROS || pad_mode > NOVAQ_PAD_CIRCULAR) return NOVAQ_EPADMODE;
+  if (N < 0 || C <= 0 || H <= 0 || W <= 0 || C_out <= 0 || KH <= 0 || KW <= 0 || sh <= 0 ||
+      sw <= 0 || ph < 0 || pw < 0)
+    return NOVAQ_EINVAL;
+  if (H + 2 * (int64_t)ph < KH || W + 2 * (int64_t)pw < KW) return NOVAQ_ESHAPE;
+  if (N == 0) return NOVAQ_OK;
+  if (!x || !w_q || !y) return NOVAQ_EINVAL;
+  if (!aligned16(x) || !aligned16(w_q) || !aligned16(y)) return NOVAQ_EALIGN;
+  return conv2d_launch(x, N, C, H, W, w_q, w_dtype, w_scale, C_out, KH, KW, sh, sw, ph, pw,
+                       pad_mode, bias, y, static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

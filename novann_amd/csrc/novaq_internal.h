@@ -1,0 +1,36 @@
+// Internal glue shared by the kernel files and the C ABI (capi.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/novaq.h"
+
+namespace novaq {
+
+// Records a failed HIP call for novaq_last_hip_error() and maps it to a status.
+int hip_fail(hipError_t e);
+
+// Status of the most recent kernel launch on this thread.
+inline int check_launch() {
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? NOVAQ_OK : hip_fail(e);
+}
+
+// Compute units of the current device (cached per device).
+int device_cu_count();
+
+int cast_launch(const void* src, int st, void* dst, int dt, int64_t n, int smode,
+                const float* scale, float* scale_out, hipStream_t stream);
+int amax_launch(const void* x, int dt, int64_t n, float* amax, hipStream_t stream);
+int scale_from_amax_launch(const float* amax, int dt, float* scale, hipStream_t stream);
+
+int linear_launch(const float* x, int64_t N, int64_t D_in, const void* w_q, int w_dtype,
+                  const float* w_scale, const float* bias, int64_t D_out, float* y,
+                  hipStream_t stream);
+int conv2d_launch(const float* x, int64_t N, int64_t C, int64_t H, int64_t W, const void* w_q,
+                  int w_dtype, const float* w_scale, int64_t C_out, int KH, int KW, int sh,
+                  int sw, int ph, int pw, int pad_mode, const float* bias, float* y,
+                  hipStream_t stream);
+
+}  // namespace novaq

@@ -1,0 +1,147 @@
+"""Drop-in ``linear`` / ``conv2d`` with NovaNN's operator signatures.
+
+Mirrors novann/functional.py:147-163 (``linear``) and :275-385 (``conv2d``):
+same argument names, order and meaning, same output shapes, and the same
+``ValueError`` cases.  Arguments may be numpy arrays (copied to the device,
+result copied back as an ndarray, as the reference returns) or device
+tensors (result stays on the device).  The weight is a ``Parameters``
+(fp32 ``.data``) or a ``QuantizedParameters`` (E4M3 / E5M2 / E2M1 codes plus a
+per-tensor scale).  The work runs in libnovaq.so on the GPU; there is no CPU
+path.
+"""
+from __future__ import annotations
+
+from typing import Optional, Tuple, Union
+
+import numpy as np
+import torch
+
+from . import _lib
+from ._lib import DTYPES, PAD_MODES, check
+from .module import Parameters, QuantizedParameters
+
+IntPair = Union[int, Tuple[int, int], str]
+
+
+def _device() -> torch.device:
+    if not torch.cuda.is_available():
+        raise RuntimeError("novann_amd needs a HIP device (no CPU fallback)")
+    return torch.device("cuda", torch.cuda.current_device())
+
+
+def _to_device_f32(a, what: str) -> Tuple[torch.Tensor, bool]:
+    """(contiguous fp32 device tensor, True if the caller passed numpy)."""
+    if isinstance(a, np.ndarray):
+        return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(_device()), True
+    if isinstance(a, torch.Tensor):
+        if not a.is_cuda:
+            a = a.to(_device())
+        return a.to(torch.float32).contiguous(), False
+    raise TypeError(f"{what} must be a numpy array or a torch tensor")
+
+
+def _weight_args(weight, dev: torch.device):
+    """(codes tensor, dtype code, scale tensor or None) for a weight."""
+    if isinstance(weight, QuantizedParameters):
+        return weight.codes.to(dev), DTYPES[weight.dtype], weight.scale.to(dev)
+    data = weight.data if isinstance(weight, Parameters) else weight
+    w, _ = _to_device_f32(data, "weight")
+    return w, DTYPES["f32"], None
+
+
+def _bias_arg(bias, dev: torch.device) -> Optional[torch.Tensor]:
+    if bias is None:
+        return None
+    data = bias.data if isinstance(bias, Parameters) else bias
+    b, _ = _to_device_f32(data, "bias")
+    return b.reshape(-1).contiguous()
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def linear(input, weight, bias: Optional[Parameters] = None):
+    """y = input @ W^T + b  (novann/functional.py:147-163).
+
+    input (N, D_in); weight (D_out, D_in) as Parameters or
+    QuantizedParameters; bias (1, D_out) Parameters or None.  Returns
+    (N, D_out) fp32: an ndarray when input was an ndarray."""
+    x, was_numpy = _to_device_f32(input, "input")
+    if x.dim() != 2:
+        raise ValueError(f"linear expects a 2-D input, got shape {tuple(x.shape)}")
+    wshape = weight.shape if isinstance(weight, QuantizedParameters) else tuple(
+        (weight.data if isinstance(weight, Parameters) else weight).shape)
+    if len(wshape) != 2 or wshape[1] != x.shape[1]:
+        raise ValueError(f"matmul: input {tuple(x.shape)} does not match weight {wshape}")
+    N, D_in = x.shape
+    D_out = wshape[0]
+    w, wdt, ws = _weight_args(weight, x.device)
+    b = _bias_arg(bias, x.device)
+    if b is not None and b.numel() != D_out:
+        raise ValueError(f"bias has {b.numel()} values, expected {D_out}")
+    y = torch.empty((N, D_out), dtype=torch.float32, device=x.device)
+    check(_lib.load().novaq_linear_forward(
+        x.data_ptr(), N, D_in, w.data_ptr(), wdt, None if ws is None else ws.data_ptr(),
+        None if b is None else b.data_ptr(), D_out, y.data_ptr(), _stream(x.device)),
+        "linear")
+    return y.cpu().numpy() if was_numpy else y
+
+
+def _pair(v: IntPair) -> Tuple[int, int]:
+    """int -> (v, v); 'valid' -> (0, 0); 'same' and other strings raise
+    ValueError (novann/functional.py:302-313)."""
+    if isinstance(v, (int, np.integer)):
+        return (int(v), int(v))
+    if isinstance(v, str):
+        if v == "valid":
+            return (0, 0)
+        if v == "same":
+            raise ValueError("The 'same' value is not currently supported")
+        raise ValueError(f"Unsupported value '{v}'")
+    return tuple(int(e) for e in v)
+
+
+def conv2d(input, weight, kernel_size: IntPair, stride: IntPair = 1, padding: IntPair = 0,
+           *, bias: Optional[Parameters] = None, padding_mode: str = "zeros",
+           extras: bool = False):
+    """2-D cross-correlation (novann/functional.py:275-385).
+
+    input (N, C, H, W); weight (C_out, C, KH, KW); returns (N, C_out, OH, OW)
+    fp32 with OH = (H + 2ph - KH)//sh + 1.  The reference materialises the
+    im2col matrix; this computes the same values with implicit im2col, so
+    ``extras=True`` (which asks for that matrix, a training-time cache) is not
+    available."""
+    KH, KW = _pair(kernel_size)
+    ph, pw = _pair(padding)
+    sh, sw = _pair(stride)
+    modes = tuple(PAD_MODES)
+    if padding_mode not in PAD_MODES:
+        raise ValueError(f"padding_mode Only accept {modes} not '{padding_mode}'")
+    if extras:
+        raise NotImplementedError("conv2d(extras=True): the im2col matrix is never "
+                                  "materialised on this path")
+    x, was_numpy = _to_device_f32(input, "input")
+    if x.dim() != 4:
+        raise ValueError(f"conv2d expects (N, C, H, W), got {tuple(x.shape)}")
+    N, C, H, W = x.shape
+    wshape = weight.shape if isinstance(weight, QuantizedParameters) else tuple(
+        (weight.data if isinstance(weight, Parameters) else weight).shape)
+    if len(wshape) != 4 or wshape[1] != C or (wshape[2], wshape[3]) != (KH, KW):
+        raise ValueError(f"weight shape {wshape} does not match input channels {C} and "
+                         f"kernel {(KH, KW)}")
+    C_out = wshape[0]
+    OH = (H + 2 * ph - KH) // sh + 1
+    OW = (W + 2 * pw - KW) // sw + 1
+    if OH <= 0 or OW <= 0:
+        raise ValueError(f"output size {(OH, OW)} is empty")
+    w, wdt, ws = _weight_args(weight, x.device)
+    b = _bias_arg(bias, x.device)
+    if b is not None and b.numel() != C_out:
+        raise ValueError(f"bias has {b.numel()} values, expected {C_out}")
+    y = torch.empty((N, C_out, OH, OW), dtype=torch.float32, device=x.device)
+    check(_lib.load().novaq_conv2d_forward(
+        x.data_ptr(), N, C, H, W, w.data_ptr(), wdt, None if ws is None else ws.data_ptr(),
+        C_out, KH, KW, sh, sw, ph, pw, PAD_MODES[padding_mode],
+        None if b is None else b.data_ptr(), y.data_ptr(), _stream(x.device)), "conv2d")
+    return y.cpu().numpy() if was_numpy else y

@@ -1,0 +1,164 @@
+"""Parameter containers and forward-only layers with NovaNN's interface.
+
+``Parameters`` mirrors novann/module/module.py:6-38 (``.data``, ``.grad``,
+``.name``).  ``QuantizedParameters`` is the packed replacement of ``.data``
+for quantized weights: device codes (E4M3 / E5M2 / E2M1) plus a per-tensor
+scale.  ``Linear`` and ``Conv2d`` mirror the forward halves of
+novann/layers/linear/linear.py:10-83 and
+novann/layers/convolutional/conv2d.py:9-177 (same constructor arguments,
+parameter shapes and defaults) and call the GPU operators in
+``functional``.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import numpy as np
+import torch
+
+
+class Parameters:
+    """Holds a parameter array and its gradient (module.py:6-38)."""
+
+    def __init__(self, data) -> None:
+        self.data = data
+        self.grad = np.zeros_like(data) if isinstance(data, np.ndarray) else None
+        self.name: Optional[str] = None
+
+    @property
+    def shape(self):
+        return tuple(self.data.shape)
+
+    def zero_grad(self, set_to_none: bool = True) -> None:
+        if set_to_none:
+            self.grad = None
+        elif self.grad is None:
+            self.grad = np.zeros_like(self.data)
+        else:
+            self.grad.fill(0.0)
+
+
+class QuantizedParameters:
+    """Per-tensor quantized weight resident on the device.
+
+    codes: flat device tensor of codes (E2M1: two per byte, element 2i in the
+    low nibble, rows of the innermost dimension packed contiguously); shape:
+    logical shape; dtype: 'e4m3' | 'e5m2' | 'e2m1'; scale: one fp32 device
+    value s, the weight being s * decode(codes)."""
+
+    def __init__(self, codes: torch.Tensor, shape, dtype: str, scale: torch.Tensor,
+                 amax: Optional[torch.Tensor] = None, name: Optional[str] = None):
+        self.codes = codes
+        self.shape = tuple(int(d) for d in shape)
+        self.dtype = dtype
+        self.scale = scale
+        self.amax = amax
+        self.name = name
+        self.grad = None
+
+    @classmethod
+    def from_float(cls, w, dtype: str, device=None) -> "QuantizedParameters":
+        """Quantize an fp32 array with per-tensor amax scaling on the GPU."""
+        from . import quant
+        if isinstance(w, Parameters):
+            w = w.data
+        if isinstance(w, np.ndarray):
+            dev = device or torch.device("cuda", torch.cuda.current_device())
+            w = torch.from_numpy(np.ascontiguousarray(w, dtype=np.float32)).to(dev)
+        q = quant.quantize(w.contiguous(), dtype)
+        return cls(q.data, q.shape, dtype, q.scale, q.amax)
+
+    def dequantize(self) -> torch.Tensor:
+        """s * decode(codes) as an fp32 device tensor of the logical shape."""
+        from . import quant
+        return quant.dequantize(quant.Quantized(self.codes, self.shape, self.dtype,
+                                                self.scale), "f32")
+
+
+def kaiming_normal_(shape, gain: float = float(np.sqrt(2.0)),
+                    rng: Optional[np.random.RandomState] = None) -> np.ndarray:
+    """N(0, (gain / sqrt(fan_in))^2) as fp32 (novann/core/init.py:155-179 with
+    the fan rules of :55-90: fan_in = shape[1] * prod(shape[2:]))."""
+    fan_in = int(shape[1]) * int(np.prod(shape[2:])) if len(shape) > 2 else int(shape[1])
+    std = gain / np.sqrt(fan_in)
+    gen = rng if rng is not None else np.random
+    return gen.normal(0.0, std, shape).astype(np.float32)
+
+
+def _pair(v):
+    if isinstance(v, int):
+        return (v, v)
+    if isinstance(v, str):
+        if v == "valid":
+            return (0, 0)
+        if v == "same":
+            raise ValueError("The 'same' value is not currently supported")
+        raise ValueError(f"Unsupported value '{v}'")
+    return tuple(v)
+
+
+class Linear:
+    """Forward-only Linear with an fp32 or quantized weight (linear.py:10-83).
+
+    weight (out_features, in_features); bias (1, out_features) zeros."""
+
+    def __init__(self, in_features: int, out_features: int, bias: bool = True,
+                 weight_dtype: Optional[str] = None, init=None) -> None:
+        self.in_features, self.out_features = in_features, out_features
+        w = (init or kaiming_normal_)((out_features, in_features))
+        self.weight = Parameters(np.asarray(w, dtype=np.float32))
+        self.weight.name = "linear weight"
+        if weight_dtype is not None:
+            self.weight = QuantizedParameters.from_float(self.weight, weight_dtype)
+            self.weight.name = "linear weight"
+        self.bias = None
+        if bias:
+            self.bias = Parameters(np.zeros((1, out_features), dtype=np.float32))
+            self.bias.name = "linear bias"
+
+    def __call__(self, x):
+        return self.forward(x)
+
+    def forward(self, x):
+        from . import functional as F
+        return F.linear(x, self.weight, self.bias)
+
+    def parameters(self):
+        return [self.weight] + ([self.bias] if self.bias is not None else [])
+
+
+class Conv2d:
+    """Forward-only Conv2d with an fp32 or quantized weight (conv2d.py:9-177).
+
+    weight (out_channels, in_channels, KH, KW); bias (out_channels, 1) zeros;
+    stride defaults to 1 (a None stride means kernel_size, conv2d.py:41)."""
+
+    def __init__(self, in_channels: int, out_channels: int, kernel_size, stride=1,
+                 padding=0, bias: bool = True, padding_mode: str = "zeros",
+                 weight_dtype: Optional[str] = None, init=None) -> None:
+        self.in_channels, self.out_channels = in_channels, out_channels
+        self.KH, self.KW = _pair(kernel_size)
+        self.sh, self.sw = _pair(stride if stride is not None else kernel_size)
+        self.ph, self.pw = _pair(padding)
+        self.pm = padding_mode
+        w = (init or kaiming_normal_)((out_channels, in_channels, self.KH, self.KW))
+        self.weight = Parameters(np.asarray(w, dtype=np.float32))
+        self.weight.name = "conv2d weight"
+        if weight_dtype is not None:
+            self.weight = QuantizedParameters.from_float(self.weight, weight_dtype)
+            self.weight.name = "conv2d weight"
+        self.bias = None
+        if bias:
+            self.bias = Parameters(np.zeros((out_channels, 1), dtype=np.float32))
+            self.bias.name = "conv2d bias"
+
+    def __call__(self, x):
+        return self.forward(x)
+
+    def forward(self, x):
+        from . import functional as F
+        return F.conv2d(x, self.weight, (self.KH, self.KW), (self.sh, self.sw),
+                        (self.ph, self.pw), bias=self.bias, padding_mode=self.pm)
+
+    def parameters(self):
+        return [self.weight] + ([self.bias] if self.bias is not None else [])

@@ -1,0 +1,65 @@
+"""numpy restatement of NovaNN's forward operators -- TEST INFRASTRUCTURE ONLY.
+
+Restates, with this build's own code, the arithmetic of
+  - ``novann.functional.linear``  (novann/functional.py:147-163):
+    ``out = input @ weight.T`` then ``out += bias`` (in place, fp32);
+  - ``novann.functional.conv2d``  (novann/functional.py:275-385):
+    pad with numpy.pad (constant / reflect / edge / wrap, :325-344), take
+    (N, C, OH, OW, KH, KW) windows with ``as_strided`` (:358-364), reorder
+    to a (C*KH*KW, N*OH*OW) column matrix (:367), one GEMM with the
+    (C_out, C*KH*KW) weight (:374-377), bias (:378-379), and return the
+    (N, C_out, OH, OW) view (:382).
+The window ordering and the output layout have to match the reference's
+exactly (they decide which products are summed), so they are the same here.
+Used as the fp32 CPU baseline (the reference's own numpy arithmetic) and as a
+second checker next to the C oracle's fp64 loops.
+"""
+from __future__ import annotations
+
+import numpy as np
+from numpy.lib.stride_tricks import as_strided
+
+NP_PAD = {"zeros": "constant", "reflect": "reflect", "replicate": "edge",
+          "circular": "wrap"}
+
+
+def linear(x: np.ndarray, w: np.ndarray, bias: np.ndarray | None = None) -> np.ndarray:
+    out = x @ w.T
+    if bias is not None:
+        out += bias.reshape(1, -1)
+    return out
+
+
+def _pair(v):
+    if isinstance(v, int):
+        return (v, v)
+    return tuple(v)
+
+
+def im2col(x: np.ndarray, KH: int, KW: int, stride=(1, 1), padding=(0, 0),
+           padding_mode: str = "zeros"):
+    """(C*KH*KW, N*OH*OW) column matrix and (OH, OW)."""
+    sh, sw = _pair(stride)
+    ph, pw = _pair(padding)
+    if padding_mode not in NP_PAD:
+        raise ValueError(f"padding_mode Only accept {tuple(NP_PAD)} not '{padding_mode}'")
+    N, C, H, W = x.shape
+    xp = np.pad(x, ((0, 0), (0, 0), (ph, ph), (pw, pw)), mode=NP_PAD[padding_mode])
+    OH = (H + 2 * ph - KH) // sh + 1
+    OW = (W + 2 * pw - KW) // sw + 1
+    s0, s1, s2, s3 = xp.strides
+    win = as_strided(xp, shape=(N, C, OH, OW, KH, KW),
+                     strides=(s0, s1, s2 * sh, s3 * sw, s2, s3))
+    col = win.transpose(1, 4, 5, 0, 2, 3).reshape(C * KH * KW, N * OH * OW)
+    return col, OH, OW
+
+
+def conv2d(x: np.ndarray, w: np.ndarray, stride=(1, 1), padding=(0, 0),
+           padding_mode: str = "zeros", bias: np.ndarray | None = None) -> np.ndarray:
+    C_out, C, KH, KW = w.shape
+    N = x.shape[0]
+    col, OH, OW = im2col(x, KH, KW, stride, padding, padding_mode)
+    out = w.reshape(C_out, -1) @ col
+    if bias is not None:
+        out += bias.reshape(C_out, 1)
+    return out.reshape(C_out, N, OH, OW).transpose(1, 0, 2, 3)

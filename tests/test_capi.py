@@ -1,0 +1,90 @@
+"""C ABI checks that need no GPU: libnovaq.so loads, exports every symbol
+include/novaq.h declares, and rejects bad arguments before touching HIP."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from novann_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "novaq.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"\b(novaq_\w+)\s*\(", text))
+
+
+def test_header_declares_the_entry_points():
+    syms = declared_symbols()
+    for s in ("novaq_cast", "novaq_amax", "novaq_quantize", "novaq_pack_fp4",
+              "novaq_unpack_fp4", "novaq_linear_forward", "novaq_conv2d_forward"):
+        assert s in syms
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    missing = [s for s in declared_symbols() if not hasattr(lib, s)]
+    assert not missing, missing
+    assert set(_lib.SIGNATURES) == declared_symbols()
+
+
+def test_version_and_status_strings():
+    lib = _lib.load()
+    assert lib.novaq_version() == 100
+    assert lib.novaq_status_string(0) == b"ok"
+    assert lib.novaq_status_string(-4) == b"unknown padding mode"
+    assert lib.novaq_status_string(123) == b"unknown status"
+
+
+FAKE = 0x10000  # never dereferenced: every call below fails validation first
+
+
+@pytest.mark.parametrize("args,status", [
+    ((FAKE, 9, FAKE, 0, 16, None, None), _lib.EDTYPE),          # bad src dtype
+    ((FAKE, 0, FAKE, -1, 16, None, None), _lib.EDTYPE),         # bad dst dtype
+    ((FAKE, 3, FAKE, 4, 16, None, None), _lib.EDTYPE),          # quantized -> quantized
+    ((FAKE, 0, FAKE, 3, -1, None, None), _lib.EINVAL),          # negative n
+    ((FAKE, 0, FAKE, 1, 16, FAKE, None), _lib.EINVAL),          # scale on f32->f16
+    ((None, 0, FAKE, 3, 16, None, None), _lib.EINVAL),          # null src
+    ((FAKE + 4, 0, FAKE, 3, 16, None, None), _lib.EALIGN),      # misaligned src
+    ((FAKE, 0, FAKE + 8, 3, 16, None, None), _lib.EALIGN),      # misaligned dst
+    ((None, 0, None, 3, 0, None, None), _lib.OK),               # n == 0 is a no-op
+])
+def test_cast_validation(args, status):
+    assert _lib.load().novaq_cast(*args) == status
+
+
+def test_other_entry_points_validation():
+    lib = _lib.load()
+    assert lib.novaq_amax(FAKE, 3, 16, FAKE, None) == _lib.EDTYPE
+    assert lib.novaq_amax(FAKE + 2, 0, 16, FAKE, None) == _lib.EALIGN
+    assert lib.novaq_scale_from_amax(FAKE, 1, FAKE, None) == _lib.EDTYPE
+    assert lib.novaq_quantize(FAKE, 0, FAKE, 1, 16, FAKE, None) == _lib.EDTYPE
+    assert lib.novaq_quantize(FAKE, 3, FAKE, 4, 16, FAKE, None) == _lib.EDTYPE
+    assert lib.novaq_quantize(FAKE, 0, FAKE, 3, 16, None, None) == _lib.EINVAL
+    # linear: bad dtype, negative size, odd packed rows, misaligned
+    assert lib.novaq_linear_forward(FAKE, 4, 8, FAKE, 7, None, None, 4, FAKE, None) == _lib.EDTYPE
+    assert lib.novaq_linear_forward(FAKE, -1, 8, FAKE, 3, None, None, 4, FAKE, None) == _lib.EINVAL
+    assert lib.novaq_linear_forward(FAKE, 4, 7, FAKE, 5, None, None, 4, FAKE, None) == _lib.ESHAPE
+    assert lib.novaq_linear_forward(FAKE, 4, 8, FAKE + 1, 3, None, None, 4, FAKE, None) == _lib.EALIGN
+    assert lib.novaq_linear_forward(None, 0, 8, None, 3, None, None, 4, None, None) == _lib.OK
+    # conv2d: pad mode, geometry, kernel larger than padded input
+    conv = lib.novaq_conv2d_forward
+    assert conv(FAKE, 1, 1, 8, 8, FAKE, 3, None, 2, 3, 3, 1, 1, 1, 1, 9, None, FAKE, None) == _lib.EPADMODE
+    assert conv(FAKE, 1, 1, 8, 8, FAKE, 3, None, 2, 3, 3, 0, 1, 1, 1, 0, None, FAKE, None) == _lib.EINVAL
+    assert conv(FAKE, 1, 1, 2, 2, FAKE, 3, None, 2, 5, 5, 1, 1, 0, 0, 0, None, FAKE, None) == _lib.ESHAPE
+    assert conv(FAKE, 1, 1, 8, 8, FAKE, 9, None, 2, 3, 3, 1, 1, 1, 1, 0, None, FAKE, None) == _lib.EDTYPE
+
+
+def test_status_maps_to_reference_exceptions():
+    with pytest.raises(ValueError):
+        _lib.check(_lib.EPADMODE, "conv2d")
+    with pytest.raises(TypeError):
+        _lib.check(_lib.EDTYPE, "cast")
+    with pytest.raises(NotImplementedError):
+        _lib.check(_lib.ENOTSUP, "x")
+    _lib.check(_lib.OK, "x")
