@@ -155,6 +155,57 @@ def bench_linear(dev, iters: int = 20, warmup: int = 5):
                          "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "traffic": None}}
 
 
+def bench_conv(dev, iters: int = 20, warmup: int = 5):
+    """Config [5]: MNIST-shaped conv1 (1->32) and conv2 (32->64), 3x3/s1/p1,
+    E2M1 weights; HBM-bound, so reported as GB/s of algorithmic traffic
+    (read x once, write y once)."""
+    import torch
+
+    from novann_amd import _lib, quant
+    lib = _lib.load()
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+    N = 256
+    x = torch.rand((N, 1, 28, 28), generator=g, device=dev, dtype=torch.float32)
+    layers = []
+    for cin, cout in ((1, 32), (32, 64)):
+        w = torch.randn((cout, cin, 3, 3), generator=g, device=dev) * (2.0 / (cin * 9)) ** 0.5
+        layers.append((cin, cout, quant.quantize(w.contiguous(), "e2m1")))
+    y1 = torch.empty((N, 32, 28, 28), device=dev)
+    y2 = torch.empty((N, 64, 28, 28), device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+
+    def conv(src, dst, cin, cout, q):
+        _lib.check(lib.novaq_conv2d_forward(src.data_ptr(), N, cin, 28, 28, q.data.data_ptr(), 5,
+                                            q.scale.data_ptr(), cout, 3, 3, 1, 1, 1, 1, 0, None,
+                                            dst.data_ptr(), stream), "conv2d")
+    runs = [(x, y1) + layers[0], (y1, y2) + layers[1]]
+    # a 512 MiB write between timed launches evicts the 256 MB MALL, so every
+    # launch reads its input from HBM (the working sets would otherwise fit)
+    flush = torch.empty(1 << 27, dtype=torch.float32, device=dev)
+    out = []
+    for src, dst, cin, cout, q in runs:
+        for _ in range(warmup):
+            conv(src, dst, cin, cout, q)
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(iters)]
+        torch.cuda.synchronize(dev)
+        for e0, e1 in ev:
+            flush.zero_()
+            e0.record()
+            conv(src, dst, cin, cout, q)
+            e1.record()
+        torch.cuda.synchronize(dev)
+        ms = sum(e0.elapsed_time(e1) for e0, e1 in ev) / iters
+        nbytes = (src.numel() + dst.numel()) * 4
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        flops = 2.0 * N * 28 * 28 * cout * cin * 9
+        out.append({"layer": f"conv {cin}->{cout}", "ms": round(ms, 4), "GB/s": round(gbs, 1),
+                    "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+                    "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 2), "bytes": nbytes})
+    return {"workload": "BASELINE config [5]", "layers": out}
+
+
 def cpu_baseline(sample: int):
     """The C oracle running the same sweep on a bounded sample (all host cores)."""
     import numpy as np
@@ -187,6 +238,7 @@ def main() -> int:
     ap.add_argument("--cpu-sample", type=int, default=1 << 26)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-linear", action="store_true")
+    ap.add_argument("--no-conv", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -204,6 +256,8 @@ def main() -> int:
     log(f"sweep done: {ms:.3f} ms/step, {value:.1f} GB/s")
     lin = None if args.no_linear else bench_linear(dev)
     log(f"linear: {lin}")
+    conv = None if args.no_conv else bench_conv(dev)
+    log(f"conv2d: {conv}")
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_sample)
     log(f"cpu baseline: {cpu}")
     out = {
@@ -219,6 +273,7 @@ def main() -> int:
                      "bytes_per_launch": dom_bpe * args.elems},
         "kernels": per_op,
         "linear": lin,
+        "conv2d": conv,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

@@ -1,0 +1,50 @@
+"""Host-side argument handling of the NovaNN-compatible operators (no GPU:
+every case here raises before any device work, as the reference raises
+ValueError for the same inputs, novann/functional.py:302-313, :325-344)."""
+import numpy as np
+import pytest
+
+from novann_amd import functional as F
+from novann_amd.module import Parameters, _pair, kaiming_normal_
+
+
+def test_pair_rules():
+    assert F._pair(3) == (3, 3)
+    assert F._pair((3, 5)) == (3, 5)
+    assert F._pair("valid") == (0, 0)
+    with pytest.raises(ValueError, match="'same'"):
+        F._pair("same")
+    with pytest.raises(ValueError, match="Unsupported"):
+        F._pair("full")
+    assert _pair(2) == (2, 2)
+
+
+def test_conv2d_bad_padding_mode_raises_value_error():
+    x = np.ones((1, 1, 8, 8), np.float32)
+    w = Parameters(np.ones((2, 1, 3, 3), np.float32))
+    with pytest.raises(ValueError, match="padding_mode"):
+        F.conv2d(x, w, 3, padding=1, padding_mode="mirror")
+
+
+def test_conv2d_same_padding_raises_value_error():
+    x = np.ones((1, 1, 8, 8), np.float32)
+    w = Parameters(np.ones((2, 1, 3, 3), np.float32))
+    with pytest.raises(ValueError):
+        F.conv2d(x, w, 3, padding="same")
+
+
+def test_conv2d_extras_not_available():
+    x = np.ones((1, 1, 8, 8), np.float32)
+    w = Parameters(np.ones((2, 1, 3, 3), np.float32))
+    with pytest.raises(NotImplementedError):
+        F.conv2d(x, w, 3, extras=True)
+
+
+def test_kaiming_normal_statistics():
+    """std = sqrt(2 / fan_in), fan_in = C*KH*KW (novann/core/init.py:55-90,155-179)."""
+    rng = np.random.RandomState(0)
+    w = kaiming_normal_((64, 32, 3, 3), rng=rng)
+    assert w.dtype == np.float32 and w.shape == (64, 32, 3, 3)
+    assert abs(w.std() - np.sqrt(2.0 / 288)) < 0.01 * np.sqrt(2.0 / 288) * 5
+    w = kaiming_normal_((4096, 4096), rng=rng)
+    assert abs(w.std() - np.sqrt(2.0 / 4096)) < 1e-3

@@ -1,0 +1,145 @@
+"""Quantized Conv2d on the GPU vs the CPU oracle (direct fp64 loops and the
+numpy im2col restatement of novann/functional.py:275-385).
+
+Tolerance: normwise max|y - r| / max|r| <= 1e-2 against fp64 on the same fp32
+input and the dequantized fp32 weights."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from oracle import functional_ref as R
+from novann_amd import _lib
+from novann_amd import functional as F
+from novann_amd.module import Conv2d, Parameters, QuantizedParameters
+from tests.gpu_util import to_dev
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2
+QCODE = {"e4m3": O.E4M3, "e5m2": O.E5M2, "e2m1": O.E2M1, "bf16": O.BF16, "f16": O.F16,
+         "f32": O.F32}
+
+
+def normwise(y, r):
+    return float(np.abs(y.astype(np.float64) - r).max() / max(np.abs(r).max(), 1e-30))
+
+
+def run_conv(x, codes, wdt, wshape, scale, bias, stride, padding, mode):
+    N, C, H, W = x.shape
+    C_out, _, KH, KW = wshape
+    sh, sw = stride
+    ph, pw = padding
+    OH, OW = (H + 2 * ph - KH) // sh + 1, (W + 2 * pw - KW) // sw + 1
+    xd = torch.from_numpy(np.ascontiguousarray(x, np.float32)).cuda()
+    wd = to_dev(codes, QCODE[wdt])
+    sd = None if scale is None else torch.tensor([scale], dtype=torch.float32, device="cuda")
+    bd = None if bias is None else torch.from_numpy(np.ascontiguousarray(bias, np.float32)).cuda()
+    yd = torch.empty((N, C_out, OH, OW), dtype=torch.float32, device="cuda")
+    rc = _lib.load().novaq_conv2d_forward(
+        xd.data_ptr(), N, C, H, W, wd.data_ptr(), _lib.DTYPES[wdt],
+        None if sd is None else sd.data_ptr(), C_out, KH, KW, sh, sw, ph, pw,
+        _lib.PAD_MODES[mode], None if bd is None else bd.data_ptr(), yd.data_ptr(),
+        torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc, "conv2d")
+    torch.cuda.synchronize()
+    return yd.cpu().numpy()
+
+
+def quantize_weights(w, wdt):
+    c = QCODE[wdt]
+    if wdt in ("e4m3", "e5m2", "e2m1"):
+        s = O.scale_from_amax(O.amax(w), c)
+        codes = O.cast(w.reshape(-1), O.F32, c, scale=s)
+        wdeq = O.cast(codes, c, O.F32, n=w.size, scale=s).reshape(w.shape)
+        return codes, s, wdeq
+    if wdt == "f32":
+        return w.reshape(-1).view(np.uint32), None, w
+    codes = O.cast(w.reshape(-1), O.F32, c)
+    return codes, None, O.cast(codes, c, O.F32).reshape(w.shape)
+
+
+def test_golden_fixture_all_padding_modes(golden):
+    g = golden["products"]
+    x = g["conv_x"]
+    for mode in ("zeros", "reflect", "replicate", "circular"):
+        want = g[f"conv_y_{mode}"]
+        y = run_conv(x, g["conv_packed"], "e2m1", (5, 3, 3, 3), float(g["conv_scale"][0]),
+                     g["conv_bias"], (2, 1), (2, 1), mode)
+        assert y.shape == want.shape
+        assert normwise(y, want.astype(np.float64)) <= TOL, mode
+
+
+@pytest.mark.parametrize("wdt", ["e2m1", "e4m3", "e5m2", "bf16", "f16", "f32"])
+@pytest.mark.parametrize("mode", ["zeros", "reflect", "replicate", "circular"])
+@pytest.mark.parametrize("case", [
+    # (N, C, H, W, C_out, KH, KW, sh, sw, ph, pw)
+    (2, 3, 16, 16, 4, 3, 3, 1, 1, 1, 1),
+    (2, 2, 20, 20, 4, 5, 5, 2, 2, 0, 0),
+    (3, 2, 16, 16, 4, 3, 5, 2, 1, 1, 2),
+    (1, 1, 8, 8, 2, 3, 3, 1, 1, 2, 2),
+    (2, 9, 11, 13, 70, 3, 3, 1, 1, 1, 1),
+    (1, 70, 9, 7, 33, 3, 3, 1, 1, 1, 1),
+    (2, 16, 31, 33, 64, 1, 1, 1, 1, 0, 0),
+])
+def test_shapes_and_modes_vs_oracle(wdt, mode, case):
+    N, C, H, W, C_out, KH, KW, sh, sw, ph, pw = case
+    rng = np.random.default_rng(sum(case) + len(mode))
+    x = rng.standard_normal((N, C, H, W)).astype(np.float32)
+    w = (rng.standard_normal((C_out, C, KH, KW)) * np.sqrt(2.0 / (C * KH * KW))).astype(np.float32)
+    b = rng.standard_normal(C_out).astype(np.float32)
+    codes, s, wdeq = quantize_weights(w, wdt)
+    y = run_conv(x, codes, wdt, w.shape, s, b, (sh, sw), (ph, pw), mode)
+    r = O.conv2d_f64(x, wdeq, (sh, sw), (ph, pw), mode, b)
+    assert normwise(y, r.astype(np.float64)) <= TOL
+    # the numpy im2col restatement agrees with the direct loops
+    r2 = R.conv2d(x.astype(np.float64), wdeq.astype(np.float64), (sh, sw), (ph, pw), mode,
+                  b.astype(np.float64))
+    assert np.allclose(r, r2, rtol=1e-5, atol=1e-5)
+
+
+def test_config5_mnist_two_layers():
+    """BASELINE config [5]: x (256, 1, 28, 28) U[0,1]; conv1 1->32 and conv2
+    32->64, 3x3 / stride 1 / pad 1, Kaiming-normal weights in E2M1 with
+    per-tensor scale, bias zero, conv2 applied to conv1's fp32 output."""
+    rng = np.random.default_rng(5)
+    x = rng.uniform(0, 1, (256, 1, 28, 28)).astype(np.float32)
+    w1 = (rng.standard_normal((32, 1, 3, 3)) * np.sqrt(2.0 / 9)).astype(np.float32)
+    w2 = (rng.standard_normal((64, 32, 3, 3)) * np.sqrt(2.0 / 288)).astype(np.float32)
+    q1 = QuantizedParameters.from_float(w1, "e2m1")
+    q2 = QuantizedParameters.from_float(w2, "e2m1")
+    b1 = Parameters(np.zeros((32, 1), np.float32))
+    b2 = Parameters(np.zeros((64, 1), np.float32))
+    xd = torch.from_numpy(x).cuda()
+    y1 = F.conv2d(xd, q1, 3, 1, 1, bias=b1)
+    y2 = F.conv2d(y1, q2, 3, 1, 1, bias=b2)
+    torch.cuda.synchronize()
+    w1d = q1.dequantize().cpu().numpy()
+    w2d = q2.dequantize().cpu().numpy()
+    r1 = O.conv2d_f64(x, w1d, (1, 1), (1, 1))
+    assert normwise(y1.cpu().numpy(), r1.astype(np.float64)) <= TOL
+    # layer 2 checked on the GPU's own layer-1 output (isolates layer 2's error)
+    r2 = O.conv2d_f64(y1.cpu().numpy(), w2d, (1, 1), (1, 1))
+    assert normwise(y2.cpu().numpy(), r2.astype(np.float64)) <= TOL
+    # and end to end against the all-fp64 chain
+    r2_chain = O.conv2d_f64(r1, w2d, (1, 1), (1, 1))
+    assert normwise(y2.cpu().numpy(), r2_chain.astype(np.float64)) <= TOL
+
+
+def test_layer_shape_contracts_like_reference():
+    """novann tests/layers/conv/test_conv2d.py:10-43, :87-132 shape contracts."""
+    rng = np.random.RandomState(0)
+    layer = Conv2d(3, 16, kernel_size=3, stride=1, padding=1, bias=True, weight_dtype="e2m1")
+    out = layer(rng.randn(4, 3, 32, 32).astype(np.float32))
+    assert out.shape == (4, 16, 32, 32) and out.dtype == np.float32
+    layer = Conv2d(2, 4, kernel_size=5, stride=2, padding=0, bias=False, weight_dtype="e4m3")
+    assert layer.bias is None
+    assert layer(rng.randn(2, 2, 20, 20).astype(np.float32)).shape == (2, 4, 8, 8)
+    for k, s, p in [(3, 1, 0), (5, 2, 1), ((3, 5), (2, 1), (1, 2))]:
+        layer = Conv2d(2, 4, kernel_size=k, stride=s, padding=p, bias=False)
+        out = layer(rng.randn(3, 2, 16, 16).astype(np.float32))
+        assert out.shape[:2] == (3, 4) and out.shape[2] > 0 and out.shape[3] > 0
+    for mode in ("zeros", "reflect", "replicate", "circular"):
+        layer = Conv2d(1, 2, kernel_size=3, padding=2, padding_mode=mode, bias=False)
+        out = layer(np.ones((1, 1, 8, 8), dtype=np.float32))
+        assert out.shape[:2] == (1, 2)

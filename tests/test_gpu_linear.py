@@ -1,0 +1,167 @@
+"""Quantized Linear on the GPU vs the CPU oracle (y = x @ (s*dec(Wq))^T + b).
+
+Tolerance: normwise max|y - r| / max|r| <= 1e-2 against
+the fp64 product of the same fp32 inputs and the dequantized fp32 weights.
+The identity-input case is bit-exact: it routes every weight code through the
+in-kernel decode and the MFMA lane layout unchanged."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from novann_amd import _lib, quant
+from novann_amd import functional as F
+from novann_amd.module import Linear, Parameters, QuantizedParameters
+from tests.gpu_util import NAME, to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2
+QCODE = {"e4m3": O.E4M3, "e5m2": O.E5M2, "e2m1": O.E2M1}
+
+
+def run_linear(x, codes, wdt, scale, bias, N, K):
+    """Raw C-ABI call on device buffers; returns y (M, N) as numpy fp32."""
+    M = x.shape[0]
+    xd = torch.from_numpy(np.ascontiguousarray(x, np.float32)).cuda()
+    wd = to_dev(codes, QCODE.get(wdt, {"bf16": O.BF16, "f16": O.F16, "f32": O.F32}.get(wdt)))
+    sd = None if scale is None else torch.tensor([scale], dtype=torch.float32, device="cuda")
+    bd = None if bias is None else torch.from_numpy(np.ascontiguousarray(bias, np.float32)).cuda()
+    yd = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    code = _lib.DTYPES[wdt]
+    rc = _lib.load().novaq_linear_forward(
+        xd.data_ptr(), M, K, wd.data_ptr(), code, None if sd is None else sd.data_ptr(),
+        None if bd is None else bd.data_ptr(), N, yd.data_ptr(),
+        torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc, "linear")
+    torch.cuda.synchronize()
+    return yd.cpu().numpy()
+
+
+def dequant(codes, wdt, n, scale):
+    c = QCODE[wdt]
+    return O.cast(codes, c, O.F32, n=n, scale=scale)
+
+
+def normwise(y, r):
+    return float(np.abs(y.astype(np.float64) - r).max() / max(np.abs(r).max(), 1e-30))
+
+
+def valid_codes(wdt):
+    if wdt == "e4m3":
+        return np.array([c for c in range(256) if (c & 0x7F) != 0x7F], dtype=np.uint8)
+    if wdt == "e5m2":
+        return np.array([c for c in range(256) if (c & 0x7F) < 0x7C], dtype=np.uint8)
+    return np.arange(16, dtype=np.uint8)
+
+
+@pytest.mark.parametrize("wdt", ["e4m3", "e5m2", "e2m1"])
+@pytest.mark.parametrize("scale", [1.0, 0.0123])
+def test_identity_input_reproduces_dequantized_weights_exactly(wdt, scale):
+    """x = I: y[i, j] = s * dec(W[j, i]) exactly, for every finite code."""
+    K, N = 256, 320
+    rng = np.random.default_rng(1)
+    vals = valid_codes(wdt)
+    nib = vals[rng.integers(0, vals.size, size=N * K)]
+    nib[: vals.size] = vals  # every code at least once
+    if wdt == "e2m1":
+        codes = (nib[0::2] | (nib[1::2] << 4)).astype(np.uint8)
+    else:
+        codes = nib.astype(np.uint8)
+    x = np.eye(K, dtype=np.float32)
+    y = run_linear(x, codes, wdt, scale, None, N, K)
+    w = dequant(codes, wdt, N * K, scale).reshape(N, K)
+    # exact values; a -0 weight legitimately sums to +0 (0*w + 1*(-0) = +0)
+    assert np.array_equal(y, np.ascontiguousarray(w.T))
+
+
+def test_golden_fixture(golden):
+    g = golden["products"]
+    codes = g["lin_codes"]
+    N, K = codes.shape
+    y = run_linear(g["lin_x"], codes.reshape(-1), "e4m3", float(g["lin_scale"][0]),
+                   g["lin_bias"], N, K)
+    assert normwise(y, g["lin_y"].astype(np.float64)) <= TOL
+
+
+@pytest.mark.parametrize("wdt", ["e4m3", "e5m2", "e2m1"])
+@pytest.mark.parametrize("M,N,K", [(1, 5, 10), (7, 300, 64), (130, 257, 130), (256, 512, 96),
+                                   (33, 31, 4098), (2, 3, 2)])
+@pytest.mark.parametrize("with_bias", [True, False])
+def test_ragged_shapes_vs_oracle(wdt, M, N, K, with_bias):
+    if wdt == "e2m1" and K % 2:
+        pytest.skip("E2M1 rows are whole bytes")
+    rng = np.random.default_rng(M * 7 + N * 3 + K)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    w = (rng.standard_normal((N, K)) * np.sqrt(2.0 / K)).astype(np.float32)
+    c = QCODE[wdt]
+    s = O.scale_from_amax(O.amax(w), c)
+    codes = O.cast(w.reshape(-1), O.F32, c, scale=s)
+    b = rng.standard_normal(N).astype(np.float32) if with_bias else None
+    y = run_linear(x, codes, wdt, s, b, N, K)
+    r = O.linear_f64(x, dequant(codes, wdt, N * K, s).reshape(N, K), b)
+    assert normwise(y, r.astype(np.float64)) <= TOL
+
+
+@pytest.mark.parametrize("wdt", ["bf16", "f16", "f32"])
+def test_unquantized_weight_dtypes(wdt):
+    rng = np.random.default_rng(3)
+    M, N, K = 96, 200, 300
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    w = (rng.standard_normal((N, K)) * 0.05).astype(np.float32)
+    code = {"bf16": O.BF16, "f16": O.F16, "f32": O.F32}[wdt]
+    stored = O.cast(w.reshape(-1), O.F32, code) if wdt != "f32" else w.reshape(-1)
+    y = run_linear(x, stored, wdt, None, None, N, K)
+    wf = O.cast(stored, code, O.F32).reshape(N, K) if wdt != "f32" else w
+    assert normwise(y, O.linear_f64(x, wf).astype(np.float64)) <= TOL
+
+
+def test_config4_full_size():
+    """BASELINE config [4]: x (2048, 4096) N(0,1), W (4096, 4096) Kaiming-normal
+    -> E4M3 with per-tensor amax scale, b = 0."""
+    rng = np.random.default_rng(4)
+    M, K, N = 2048, 4096, 4096
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    w = (rng.standard_normal((N, K), dtype=np.float32) * np.float32(np.sqrt(2.0 / K)))
+    wq = QuantizedParameters.from_float(w, "e4m3")
+    b = Parameters(np.zeros((1, N), dtype=np.float32))
+    xd = torch.from_numpy(x).cuda()
+    y = F.linear(xd, wq, b)
+    torch.cuda.synchronize()
+    wdeq = wq.dequantize().cpu().numpy().astype(np.float64)
+    r = x.astype(np.float64) @ wdeq.T
+    err = normwise(y.cpu().numpy(), r)
+    assert err <= TOL, err
+    # quantized weights themselves are the oracle's, bit for bit
+    s = O.scale_from_amax(O.amax(w), O.E4M3)
+    assert wq.scale.item() == s
+    assert np.array_equal(to_host(wq.codes), O.cast(w.reshape(-1), O.F32, O.E4M3, scale=s))
+
+
+def test_zero_sizes():
+    lib = _lib.load()
+    stream = torch.cuda.current_stream().cuda_stream
+    y = torch.full((4, 3), 7.0, device="cuda")
+    b = torch.tensor([1.0, 2.0, 3.0], device="cuda")
+    x = torch.empty((4, 0), device="cuda")
+    w = torch.empty(16, dtype=torch.uint8, device="cuda")
+    _lib.check(lib.novaq_linear_forward(x.data_ptr() or y.data_ptr(), 4, 0, w.data_ptr(), 3,
+                                        None, b.data_ptr(), 3, y.data_ptr(), stream), "linear")
+    torch.cuda.synchronize()
+    assert torch.equal(y.cpu(), b.cpu().expand(4, 3))
+
+
+def test_layer_shape_contracts_like_reference():
+    """novann tests/layers/linear/test_linear.py:11-28 shape contracts."""
+    rng = np.random.RandomState(8)
+    layer = Linear(10, 5, bias=True, weight_dtype="e4m3")
+    x = rng.randn(32, 10).astype(np.float32)
+    out = layer(x)
+    assert isinstance(out, np.ndarray) and out.shape == (32, 5) and out.dtype == np.float32
+    layer = Linear(10, 5, bias=False, weight_dtype="e2m1")
+    assert layer.bias is None and layer(x).shape == (32, 5)
+    # fp32 weights, numpy in / numpy out
+    layer = Linear(10, 5, bias=True)
+    out = layer(x)
+    ref = x.astype(np.float64) @ layer.weight.data.T.astype(np.float64)
+    assert normwise(out, ref) <= TOL
