@@ -253,12 +253,225 @@ __global__ __launch_bounds__(THREADS, 1) void linear_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Fast path: whole tiles only (M % 128 == 0, N % 256 == 0, K % 64 == 0), no
+// bounds logic.  W stays in its stored format in LDS (1 byte per E4M3/E5M2
+// element, half a byte per E2M1, 2 bytes for bf16/f16) and each wave decodes
+// its B fragments after the LDS read, so LDS traffic for W is that of the
+// packed codes.  The next K block is fetched into registers while the
+// current one is multiplied; LDS fragments are double-buffered across the
+// four 16-deep MFMA steps of a K block.
+
+template <int WT>
+struct Fast {
+  static constexpr int bits = dtype_bits(WT);
+  static constexpr int row_bytes = BK * bits / 8;        // W bytes per tile row per K block
+  // LDS row pitch: keeps a wave's 32-row fragment reads in distinct banks
+  static constexpr int pitch = bits == 4 ? 36 : bits == 8 ? 72 : 144;
+  static constexpr int chunks = BN * row_bytes / 16 / THREADS;  // 16-byte W chunks per thread
+  static constexpr int cpr = row_bytes / 16;             // chunks per W row
+  static constexpr int frag_bytes = 8 * bits / 8;        // one lane's 8 elements
+};
+
+constexpr int A_PITCH = BK + 8;                      // bf16 per A row in LDS
+constexpr int A_STAGE = BM * A_PITCH * 2;            // bytes
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// 8 stored W elements (one lane's fragment) -> 8 bf16 for the MFMA B operand
+template <int WT>
+__device__ __forceinline__ bf16x8 frag_to_bf16(const uint8_t* p) {
+  uint32_t o[4];
+  if constexpr (WT == E4M3 || WT == E5M2) {
+    u32x2 v = *reinterpret_cast<const u32x2*>(p);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      if constexpr (WT == E4M3) {
+        o[2 * i] = bf16_pair(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v[i], 1.0f, false));
+        o[2 * i + 1] = bf16_pair(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v[i], 1.0f, true));
+      } else {
+        o[2 * i] = bf16_pair(__builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(v[i], 1.0f, false));
+        o[2 * i + 1] = bf16_pair(__builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(v[i], 1.0f, true));
+      }
+    }
+  } else if constexpr (WT == E2M1) {
+    uint32_t v = *reinterpret_cast<const uint32_t*>(p);
+    o[0] = bf16_pair(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, 1.0f, 0));
+    o[1] = bf16_pair(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, 1.0f, 1));
+    o[2] = bf16_pair(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, 1.0f, 2));
+    o[3] = bf16_pair(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, 1.0f, 3));
+  } else if constexpr (WT == BF16) {
+    return *reinterpret_cast<const bf16x8*>(p);
+  } else {  // F16
+    u32x4 v = *reinterpret_cast<const u32x4*>(p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      // the element goes through a scalar first: bit-casting v[i] directly
+      // makes this compiler (ROCm 7.2 clang) reuse element 0 for every i
+      const uint32_t word = v[i];
+      f32x2 f = __builtin_convertvector(__builtin_bit_cast(f16x2, word), f32x2);
+      o[i] = bf16_pair(__builtin_convertvector(f, bf16x2));
+    }
+  }
+  u32x4 r = {o[0], o[1], o[2], o[3]};
+  return __builtin_bit_cast(bf16x8, r);
+}
+
+template <int WT>
+__global__ __launch_bounds__(THREADS, 1) void linear_fast_kernel(
+    const float* __restrict__ x, const uint8_t* __restrict__ w, const float* __restrict__ w_scale,
+    const float* __restrict__ bias, float* __restrict__ y, int M, int N, int K, int tiles_m,
+    int tiles_n) {
+  using F = Fast<WT>;
+  constexpr int B_STAGE = BN * F::pitch;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * (A_STAGE + B_STAGE)];
+
+  const int T = tiles_m * tiles_n;
+  int t = blockIdx.x;
+  if ((T & 7) == 0) t = (t & 7) * (T >> 3) + (t >> 3);
+  constexpr int GM = 4;
+  const int group = t / (GM * tiles_n);
+  const int first_m = group * GM;
+  const int gm = min(tiles_m - first_m, GM);
+  const int rem = t - group * GM * tiles_n;
+  const int m0 = (first_m + rem % gm) * BM;
+  const int n0 = (rem / gm) * BN;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, half = lane >> 5;
+  const int wm = (wave & 1) * WM, wn = (wave >> 1) * WN;
+  const size_t w_row_bytes = (size_t)K * F::bits / 8;
+
+  // per-thread global sources (advanced by one K block per iteration)
+  const float* xsrc[XCH];
+  int xdst[XCH];
+#pragma unroll
+  for (int i = 0; i < XCH; ++i) {
+    const int c = tid + THREADS * i;
+    xsrc[i] = x + (size_t)(m0 + (c >> 4)) * K + (c & 15) * 4;
+    xdst[i] = ((c >> 4) * A_PITCH + (c & 15) * 4) * 2;
+  }
+  const uint8_t* wsrc[F::chunks];
+  int wdst[F::chunks];
+#pragma unroll
+  for (int i = 0; i < F::chunks; ++i) {
+    const int c = tid + THREADS * i;
+    wsrc[i] = w + (size_t)(n0 + c / F::cpr) * w_row_bytes + (c % F::cpr) * 16;
+    wdst[i] = (c / F::cpr) * F::pitch + (c % F::cpr) * 16;
+  }
+
+  u32x4 xr[XCH], wr[F::chunks];
+  auto fetch = [&](int kb) {
+#pragma unroll
+    for (int i = 0; i < XCH; ++i)
+      xr[i] = *reinterpret_cast<const u32x4*>(xsrc[i] + (size_t)kb * BK);
+#pragma unroll
+    for (int i = 0; i < F::chunks; ++i)
+      wr[i] = *reinterpret_cast<const u32x4*>(wsrc[i] + (size_t)kb * F::row_bytes);
+  };
+  auto stage = [&](int buf) {
+    uint8_t* A = lds + buf * (A_STAGE + B_STAGE);
+    uint8_t* B = A + A_STAGE;
+#pragma unroll
+    for (int i = 0; i < XCH; ++i) {
+      uint32_t p0 = f32x2_to_bf16(xr[i][0], xr[i][1]);
+      uint32_t p1 = f32x2_to_bf16(xr[i][2], xr[i][3]);
+      *reinterpret_cast<u32x2*>(A + xdst[i]) = u32x2{p0, p1};
+    }
+#pragma unroll
+    for (int i = 0; i < F::chunks; ++i) {
+      if constexpr (F::pitch % 16 == 0) {
+        *reinterpret_cast<u32x4*>(B + wdst[i]) = wr[i];
+      } else if constexpr (F::pitch % 8 == 0) {
+        *reinterpret_cast<u32x2*>(B + wdst[i]) = u32x2{wr[i][0], wr[i][1]};
+        *reinterpret_cast<u32x2*>(B + wdst[i] + 8) = u32x2{wr[i][2], wr[i][3]};
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) *reinterpret_cast<uint32_t*>(B + wdst[i] + 4 * q) = wr[i][q];
+      }
+    }
+  };
+
+  f32x16 acc[MT][NT];
+#pragma unroll
+  for (int a = 0; a < MT; ++a)
+#pragma unroll
+    for (int b = 0; b < NT; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.0f;
+
+  // fragment addresses (bytes) within a stage
+  int aoff[MT], boff[NT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i) aoff[i] = ((wm + i * 32 + (lane & 31)) * A_PITCH + half * 8) * 2;
+#pragma unroll
+  for (int j = 0; j < NT; ++j)
+    boff[j] = A_STAGE + (wn + j * 32 + (lane & 31)) * F::pitch + half * F::frag_bytes;
+
+  const int kblocks = K / BK;
+  fetch(0);
+  stage(0);
+  __syncthreads();
+  for (int kb = 0; kb < kblocks; ++kb) {
+    const uint8_t* S = lds + (kb & 1) * (A_STAGE + B_STAGE);
+    const bool more = kb + 1 < kblocks;
+    if (more) fetch(kb + 1);
+    bf16x8 a[2][MT], b[2][NT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) a[0][i] = *reinterpret_cast<const bf16x8*>(S + aoff[i]);
+#pragma unroll
+    for (int j = 0; j < NT; ++j) b[0][j] = frag_to_bf16<WT>(S + boff[j]);
+#pragma unroll
+    for (int s = 0; s < BK / 16; ++s) {
+      const int cur = s & 1, nxt = cur ^ 1;
+      if (s + 1 < BK / 16) {
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+          a[nxt][i] = *reinterpret_cast<const bf16x8*>(S + aoff[i] + (s + 1) * 32);
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+          b[nxt][j] = frag_to_bf16<WT>(S + boff[j] + (s + 1) * 2 * F::frag_bytes);
+      }
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[cur][i], b[cur][j], acc[i][j], 0, 0, 0);
+    }
+    if (more) stage((kb + 1) & 1);
+    __syncthreads();
+  }
+
+  const float s = w_scale ? *w_scale : 1.0f;
+#pragma unroll
+  for (int j = 0; j < NT; ++j) {
+    const int col = n0 + wn + j * 32 + (lane & 31);
+    const float bv = bias ? bias[col] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+        __builtin_nontemporal_store(acc[i][j][r] * s + bv, &y[(size_t)row * N + col]);
+      }
+    }
+  }
+}
+
 template <int WT>
 int launch(const float* x, int64_t M, int64_t K, const void* w, const float* w_scale,
            const float* bias, int64_t N, float* y, hipStream_t stream) {
   const int64_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
   const int64_t T = tiles_m * tiles_n;
   if (T > 0x7FFFFFFF || M > 0x7FFFFFFF || N > 0x7FFFFFFF || K > 0x7FFFFFFF) return NOVAQ_EINVAL;
+  if constexpr (WT != F32) {
+    const bool whole = M % BM == 0 && N % BN == 0 && K % BK == 0 && K > 0;
+    if (whole) {
+      hipLaunchKernelGGL((linear_fast_kernel<WT>), dim3((unsigned)T), dim3(THREADS), 0, stream,
+                         x, static_cast<const uint8_t*>(w), w_scale, bias, y, (int)M, (int)N,
+                         (int)K, (int)tiles_m, (int)tiles_n);
+      return check_launch();
+    }
+  }
   const int x_vec = (K % 4) == 0;
   const int w_vec = ((K * W<WT>::bits / 8) % 16) == 0 && (K * W<WT>::bits) % 8 == 0;
   hipLaunchKernelGGL((linear_kernel<WT>), dim3((unsigned)T), dim3(THREADS), 0, stream, x,

@@ -57,9 +57,10 @@ def valid_codes(wdt):
 
 @pytest.mark.parametrize("wdt", ["e4m3", "e5m2", "e2m1"])
 @pytest.mark.parametrize("scale", [1.0, 0.0123])
-def test_identity_input_reproduces_dequantized_weights_exactly(wdt, scale):
-    """x = I: y[i, j] = s * dec(W[j, i]) exactly, for every finite code."""
-    K, N = 256, 320
+@pytest.mark.parametrize("K,N", [(256, 320), (256, 512)], ids=["edge-tiles", "whole-tiles"])
+def test_identity_input_reproduces_dequantized_weights_exactly(wdt, scale, K, N):
+    """x = I: y[i, j] = s * dec(W[j, i]) exactly, for every finite code.  The
+    whole-tiles shape runs the guard-free kernel, the other the edge kernel."""
     rng = np.random.default_rng(1)
     vals = valid_codes(wdt)
     nib = vals[rng.integers(0, vals.size, size=N * K)]
@@ -101,6 +102,27 @@ def test_ragged_shapes_vs_oracle(wdt, M, N, K, with_bias):
     y = run_linear(x, codes, wdt, s, b, N, K)
     r = O.linear_f64(x, dequant(codes, wdt, N * K, s).reshape(N, K), b)
     assert normwise(y, r.astype(np.float64)) <= TOL
+
+
+@pytest.mark.parametrize("wdt", ["e4m3", "e5m2", "e2m1", "bf16", "f16"])
+@pytest.mark.parametrize("M,N,K", [(128, 256, 64), (256, 512, 128), (384, 768, 320)])
+def test_whole_tile_shapes_vs_oracle(wdt, M, N, K):
+    """Shapes that take the guard-free kernel (M % 128, N % 256, K % 64 == 0)."""
+    rng = np.random.default_rng(M + N + K)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    w = (rng.standard_normal((N, K)) * np.sqrt(2.0 / K)).astype(np.float32)
+    b = rng.standard_normal(N).astype(np.float32)
+    code = QCODE.get(wdt, {"bf16": O.BF16, "f16": O.F16}.get(wdt))
+    if wdt in QCODE:
+        s = O.scale_from_amax(O.amax(w), code)
+        codes = O.cast(w.reshape(-1), O.F32, code, scale=s)
+        wf = dequant(codes, wdt, N * K, s).reshape(N, K)
+    else:
+        s = None
+        codes = O.cast(w.reshape(-1), O.F32, code)
+        wf = O.cast(codes, code, O.F32).reshape(N, K)
+    y = run_linear(x, codes, wdt, s, b, N, K)
+    assert normwise(y, O.linear_f64(x, wf, b).astype(np.float64)) <= TOL
 
 
 @pytest.mark.parametrize("wdt", ["bf16", "f16", "f32"])
