@@ -36,6 +36,24 @@ SWEEP = [
     ("amax e5m2", 4), ("scale e5m2", 0), ("f32->e5m2 scaled", 5), ("e5m2->f32 scaled", 5),
 ]
 BYTES_PER_ELEM = sum(b for _, b in SWEEP)
+# kernel behind each single-kernel op (rocprofv3 names), for the measured traffic
+KERNEL_OF = {
+    "f32->f16": "cast_kernel<0, 1, 0>", "f16->f32": "cast_kernel<1, 0, 0>",
+    "f32->bf16": "cast_kernel<0, 2, 0>", "bf16->f32": "cast_kernel<2, 0, 0>",
+    "f32->e4m3 scaled": "cast_kernel<0, 3, 1>", "e4m3->f32 scaled": "cast_kernel<3, 0, 1>",
+    "f32->e5m2 scaled": "cast_kernel<0, 4, 1>", "e5m2->f32 scaled": "cast_kernel<4, 0, 1>",
+}
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+
+
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary (profiles/traffic.json, copy-calibrated), or None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            return json.load(f)["bytes_per_launch"].get(kernel)
+    except (OSError, ValueError, KeyError):
+        return None
 
 
 def log(msg: str) -> None:
@@ -206,7 +224,7 @@ def bench_conv(dev, iters: int = 20, warmup: int = 5):
     return {"workload": "BASELINE config [5]", "layers": out}
 
 
-def cpu_baseline(sample: int):
+def cpu_baseline(sample: int, min_seconds: float = 10.0):
     """The C oracle running the same sweep on a bounded sample (all host cores)."""
     import numpy as np
 
@@ -215,18 +233,24 @@ def cpu_baseline(sample: int):
     rng = np.random.default_rng(2)
     x = (np.exp2(rng.uniform(-20, 20, sample)) * np.where(rng.random(sample) < 0.5, -1, 1)
          ).astype(np.float32)
+    # whole sweeps over the sample until about min_seconds of CPU work are done
+    passes = 0
     t0 = time.perf_counter()
-    for st in (O.F16, O.BF16):
-        O.cast(O.cast(x, O.F32, st, nthreads=threads), st, O.F32, n=sample, nthreads=threads)
-    for dt in (O.E4M3, O.E5M2):
-        s = O.scale_from_amax(O.amax(x, nthreads=threads), dt)
-        q = O.cast(x, O.F32, dt, scale=s, nthreads=threads)
-        O.cast(q, dt, O.F32, n=sample, scale=s, nthreads=threads)
-    dt_s = time.perf_counter() - t0
-    return {"value": round(BYTES_PER_ELEM * sample / dt_s / 1e9, 3), "unit": "GB/s",
+    while True:
+        for st in (O.F16, O.BF16):
+            O.cast(O.cast(x, O.F32, st, nthreads=threads), st, O.F32, n=sample, nthreads=threads)
+        for dt in (O.E4M3, O.E5M2):
+            s = O.scale_from_amax(O.amax(x, nthreads=threads), dt)
+            q = O.cast(x, O.F32, dt, scale=s, nthreads=threads)
+            O.cast(q, dt, O.F32, n=sample, scale=s, nthreads=threads)
+        passes += 1
+        dt_s = time.perf_counter() - t0
+        if dt_s >= min_seconds:
+            break
+    return {"value": round(BYTES_PER_ELEM * sample * passes / dt_s / 1e9, 3), "unit": "GB/s",
             "cores": threads, "kind": "port",
-            "sample": f"config [2] sweep on {sample} elements ({sample >> 20}M), C oracle, "
-                      f"{threads} OpenMP threads, {dt_s:.1f} s"}
+            "sample": f"config [2] sweep (52 B/element) repeated {passes}x on {sample >> 20}M "
+                      f"elements, C oracle, {threads} OpenMP threads, {dt_s:.1f} s"}
 
 
 def main() -> int:
@@ -238,6 +262,9 @@ def main() -> int:
     ap.add_argument("--cpu-sample", type=int, default=1 << 26)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-linear", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="also run one fp32->fp32 copy of the sweep input (known bytes), "
+                         "the reference dispatch for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE")
     ap.add_argument("--no-conv", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -248,9 +275,18 @@ def main() -> int:
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     log(f"sweep: {args.elems} elements, {args.steps} steps, {args.warmup} warmup")
+    if args.copy_probe:
+        from novann_amd import _lib
+        src = torch.empty(args.elems, dtype=torch.float32, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        _lib.check(_lib.load().novaq_cast(src.data_ptr(), 0, dst.data_ptr(), 0, args.elems, None,
+                                          torch.cuda.current_stream(dev).cuda_stream), "copy")
+        torch.cuda.synchronize(dev)
+        del src, dst
     ms, per_op = bench_sweep(args.elems, args.steps, args.warmup, dev)
     value = BYTES_PER_ELEM * args.elems / (ms * 1e-3) / 1e9
-    kernels = [p for p in per_op if p["GB/s"] is not None]
+    # dominant single-kernel op (the amax op also launches a 1-thread fill kernel)
+    kernels = [p for p in per_op if p["op"] in KERNEL_OF]
     dom = max(kernels, key=lambda p: p["ms"])
     dom_bpe = dict(SWEEP)[dom["op"]]
     log(f"sweep done: {ms:.3f} ms/step, {value:.1f} GB/s")
@@ -267,9 +303,11 @@ def main() -> int:
         "dtype": "f32<->{f16,bf16,e4m3,e5m2}", "data": "synthetic",
         "config": {"workload": "BASELINE config [2]: cast sweep, amax-scaled FP8",
                    "elements": args.elems, "bytes_per_element": BYTES_PER_ELEM},
-        "roofline": {"bound": "hbm", "kernel": dom["op"], "achieved": dom["GB/s"],
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": dom["frac"],
-                     "traffic": None,
+        "roofline": {"bound": "hbm", "kernel": f'{dom["op"]} ({KERNEL_OF[dom["op"]]})',
+                     "achieved": dom["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": dom["frac"],
+                     "traffic": (measured_traffic(KERNEL_OF[dom["op"]])
+                                 if args.elems == 1 << 28 else None),
                      "bytes_per_launch": dom_bpe * args.elems},
         "kernels": per_op,
         "linear": lin,

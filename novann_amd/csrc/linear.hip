@@ -262,13 +262,13 @@ __global__ __launch_bounds__(THREADS, 1) void linear_kernel(
 // current one is multiplied; LDS fragments are double-buffered across the
 // four 16-deep MFMA steps of a K block.
 
-template <int WT>
+template <int WT, int FBN>
 struct Fast {
   static constexpr int bits = dtype_bits(WT);
   static constexpr int row_bytes = BK * bits / 8;        // W bytes per tile row per K block
   // LDS row pitch: keeps a wave's 32-row fragment reads in distinct banks
   static constexpr int pitch = bits == 4 ? 36 : bits == 8 ? 72 : 144;
-  static constexpr int chunks = BN * row_bytes / 16 / THREADS;  // 16-byte W chunks per thread
+  static constexpr int chunks = FBN * row_bytes / 16 / THREADS;  // 16-byte W chunks per thread
   static constexpr int cpr = row_bytes / 16;             // chunks per W row
   static constexpr int frag_bytes = 8 * bits / 8;        // one lane's 8 elements
 };
@@ -317,13 +317,21 @@ __device__ __forceinline__ bf16x8 frag_to_bf16(const uint8_t* p) {
   return __builtin_bit_cast(bf16x8, r);
 }
 
-template <int WT>
-__global__ __launch_bounds__(THREADS, 1) void linear_fast_kernel(
+// FBN: tile width in outputs (128 or 256); OCC: workgroups per CU the
+// register budget is sized for; PF: K blocks fetched ahead (1 or 2); WLM:
+// waves along M (2: 2 x 2 waves of 64 x FBN/2; 1: 1 x 4 waves of 128 x
+// FBN/4, where every W element is decoded by exactly one wave).
+template <int WT, int FBN, int OCC, int PF, int WLM>
+__global__ __launch_bounds__(THREADS, OCC) void linear_fast_kernel(
     const float* __restrict__ x, const uint8_t* __restrict__ w, const float* __restrict__ w_scale,
     const float* __restrict__ bias, float* __restrict__ y, int M, int N, int K, int tiles_m,
     int tiles_n) {
-  using F = Fast<WT>;
-  constexpr int B_STAGE = BN * F::pitch;
+  using F = Fast<WT, FBN>;
+  constexpr int WM = BM / WLM;             // per-wave rows
+  constexpr int MT = WM / 32;
+  constexpr int FWN = FBN / (4 / WLM);     // per-wave width
+  constexpr int FNT = FWN / 32;
+  constexpr int B_STAGE = FBN * F::pitch;
   __shared__ __attribute__((aligned(16))) uint8_t lds[2 * (A_STAGE + B_STAGE)];
 
   const int T = tiles_m * tiles_n;
@@ -335,91 +343,87 @@ __global__ __launch_bounds__(THREADS, 1) void linear_fast_kernel(
   const int gm = min(tiles_m - first_m, GM);
   const int rem = t - group * GM * tiles_n;
   const int m0 = (first_m + rem % gm) * BM;
-  const int n0 = (rem / gm) * BN;
+  const int n0 = (rem / gm) * FBN;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, half = lane >> 5;
-  const int wm = (wave & 1) * WM, wn = (wave >> 1) * WN;
+  const int wm = (wave % WLM) * WM, wn = (wave / WLM) * FWN;
   const size_t w_row_bytes = (size_t)K * F::bits / 8;
 
-  // per-thread global sources (advanced by one K block per iteration)
-  const float* xsrc[XCH];
-  int xdst[XCH];
-#pragma unroll
-  for (int i = 0; i < XCH; ++i) {
-    const int c = tid + THREADS * i;
-    xsrc[i] = x + (size_t)(m0 + (c >> 4)) * K + (c & 15) * 4;
-    xdst[i] = ((c >> 4) * A_PITCH + (c & 15) * 4) * 2;
-  }
-  const uint8_t* wsrc[F::chunks];
-  int wdst[F::chunks];
-#pragma unroll
-  for (int i = 0; i < F::chunks; ++i) {
-    const int c = tid + THREADS * i;
-    wsrc[i] = w + (size_t)(n0 + c / F::cpr) * w_row_bytes + (c % F::cpr) * 16;
-    wdst[i] = (c / F::cpr) * F::pitch + (c % F::cpr) * 16;
-  }
+  // Global sources: a uniform tile base, one per-lane offset, and uniform
+  // per-chunk strides (chunk i of a thread is 16*i rows of x / 256*i/cpr rows
+  // of W further down), so addresses cost scalar registers, not vector ones.
+  const float* xtile = x + (size_t)m0 * K;
+  const uint32_t xlane = (uint32_t)((tid >> 4) * K + (tid & 15) * 4);  // floats
+  const size_t xstep = (size_t)16 * K;                                   // floats per chunk
+  const int xdst0 = ((tid >> 4) * A_PITCH + (tid & 15) * 4) * 2;        // LDS bytes
+  constexpr int XDST_STEP = 16 * A_PITCH * 2;
+  const uint8_t* wtile = w + (size_t)n0 * w_row_bytes;
+  const uint32_t wlane = (uint32_t)((tid / F::cpr) * w_row_bytes + (tid % F::cpr) * 16);
+  const size_t wstep = (size_t)(THREADS / F::cpr) * w_row_bytes;
+  const int wdst0 = (tid / F::cpr) * F::pitch + (tid % F::cpr) * 16;
+  constexpr int WDST_STEP = (THREADS / F::cpr) * F::pitch;
 
-  u32x4 xr[XCH], wr[F::chunks];
-  auto fetch = [&](int kb) {
+  struct Regs {
+    u32x4 x[XCH];
+    u32x4 w[F::chunks];
+  };
+  auto fetch = [&](Regs& r, int kb) {
+    const float* xk = xtile + (size_t)kb * BK;
+    const uint8_t* wk = wtile + (size_t)kb * F::row_bytes;
 #pragma unroll
     for (int i = 0; i < XCH; ++i)
-      xr[i] = *reinterpret_cast<const u32x4*>(xsrc[i] + (size_t)kb * BK);
+      r.x[i] = *reinterpret_cast<const u32x4*>(xk + i * xstep + xlane);
 #pragma unroll
     for (int i = 0; i < F::chunks; ++i)
-      wr[i] = *reinterpret_cast<const u32x4*>(wsrc[i] + (size_t)kb * F::row_bytes);
+      r.w[i] = *reinterpret_cast<const u32x4*>(wk + i * wstep + wlane);
   };
-  auto stage = [&](int buf) {
-    uint8_t* A = lds + buf * (A_STAGE + B_STAGE);
-    uint8_t* B = A + A_STAGE;
+  auto stage = [&](const Regs& r, int buf) {
+    uint8_t* A = lds + buf * (A_STAGE + B_STAGE) + xdst0;
+    uint8_t* B = lds + buf * (A_STAGE + B_STAGE) + A_STAGE + wdst0;
 #pragma unroll
     for (int i = 0; i < XCH; ++i) {
-      uint32_t p0 = f32x2_to_bf16(xr[i][0], xr[i][1]);
-      uint32_t p1 = f32x2_to_bf16(xr[i][2], xr[i][3]);
-      *reinterpret_cast<u32x2*>(A + xdst[i]) = u32x2{p0, p1};
+      uint32_t p0 = f32x2_to_bf16(r.x[i][0], r.x[i][1]);
+      uint32_t p1 = f32x2_to_bf16(r.x[i][2], r.x[i][3]);
+      *reinterpret_cast<u32x2*>(A + i * XDST_STEP) = u32x2{p0, p1};
     }
 #pragma unroll
     for (int i = 0; i < F::chunks; ++i) {
+      uint8_t* d = B + i * WDST_STEP;
       if constexpr (F::pitch % 16 == 0) {
-        *reinterpret_cast<u32x4*>(B + wdst[i]) = wr[i];
+        *reinterpret_cast<u32x4*>(d) = r.w[i];
       } else if constexpr (F::pitch % 8 == 0) {
-        *reinterpret_cast<u32x2*>(B + wdst[i]) = u32x2{wr[i][0], wr[i][1]};
-        *reinterpret_cast<u32x2*>(B + wdst[i] + 8) = u32x2{wr[i][2], wr[i][3]};
+        *reinterpret_cast<u32x2*>(d) = u32x2{r.w[i][0], r.w[i][1]};
+        *reinterpret_cast<u32x2*>(d + 8) = u32x2{r.w[i][2], r.w[i][3]};
       } else {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) *reinterpret_cast<uint32_t*>(B + wdst[i] + 4 * q) = wr[i][q];
+        for (int q = 0; q < 4; ++q) *reinterpret_cast<uint32_t*>(d + 4 * q) = r.w[i][q];
       }
     }
   };
 
-  f32x16 acc[MT][NT];
+  f32x16 acc[MT][FNT];
 #pragma unroll
   for (int a = 0; a < MT; ++a)
 #pragma unroll
-    for (int b = 0; b < NT; ++b)
+    for (int b = 0; b < FNT; ++b)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.0f;
 
   // fragment addresses (bytes) within a stage
-  int aoff[MT], boff[NT];
+  int aoff[MT], boff[FNT];
 #pragma unroll
   for (int i = 0; i < MT; ++i) aoff[i] = ((wm + i * 32 + (lane & 31)) * A_PITCH + half * 8) * 2;
 #pragma unroll
-  for (int j = 0; j < NT; ++j)
+  for (int j = 0; j < FNT; ++j)
     boff[j] = A_STAGE + (wn + j * 32 + (lane & 31)) * F::pitch + half * F::frag_bytes;
 
-  const int kblocks = K / BK;
-  fetch(0);
-  stage(0);
-  __syncthreads();
-  for (int kb = 0; kb < kblocks; ++kb) {
-    const uint8_t* S = lds + (kb & 1) * (A_STAGE + B_STAGE);
-    const bool more = kb + 1 < kblocks;
-    if (more) fetch(kb + 1);
-    bf16x8 a[2][MT], b[2][NT];
+  auto compute = [&](int buf) {
+    const uint8_t* S = lds + buf * (A_STAGE + B_STAGE);
+    bf16x8 a[2][MT], b[2][FNT];
 #pragma unroll
     for (int i = 0; i < MT; ++i) a[0][i] = *reinterpret_cast<const bf16x8*>(S + aoff[i]);
 #pragma unroll
-    for (int j = 0; j < NT; ++j) b[0][j] = frag_to_bf16<WT>(S + boff[j]);
+    for (int j = 0; j < FNT; ++j) b[0][j] = frag_to_bf16<WT>(S + boff[j]);
 #pragma unroll
     for (int s = 0; s < BK / 16; ++s) {
       const int cur = s & 1, nxt = cur ^ 1;
@@ -428,22 +432,56 @@ __global__ __launch_bounds__(THREADS, 1) void linear_fast_kernel(
         for (int i = 0; i < MT; ++i)
           a[nxt][i] = *reinterpret_cast<const bf16x8*>(S + aoff[i] + (s + 1) * 32);
 #pragma unroll
-        for (int j = 0; j < NT; ++j)
+        for (int j = 0; j < FNT; ++j)
           b[nxt][j] = frag_to_bf16<WT>(S + boff[j] + (s + 1) * 2 * F::frag_bytes);
       }
 #pragma unroll
       for (int i = 0; i < MT; ++i)
 #pragma unroll
-        for (int j = 0; j < NT; ++j)
+        for (int j = 0; j < FNT; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[cur][i], b[cur][j], acc[i][j], 0, 0, 0);
     }
-    if (more) stage((kb + 1) & 1);
+  };
+
+  // K blocks alternate between LDS buffers 0 and 1; a buffer is rewritten
+  // only after the barrier that ends its last reads.
+  const int kblocks = K / BK;
+  if constexpr (PF == 1) {
+    Regs r;
+    fetch(r, 0);
+    stage(r, 0);
     __syncthreads();
+    for (int kb = 0; kb < kblocks; ++kb) {
+      const bool more = kb + 1 < kblocks;
+      if (more) fetch(r, kb + 1);
+      compute(kb & 1);
+      if (more) stage(r, (kb + 1) & 1);
+      __syncthreads();
+    }
+  } else {
+    // two register sets: K block kb+2 is in flight while kb+1 waits to be staged
+    Regs ra, rb;
+    fetch(ra, 0);
+    if (kblocks > 1) fetch(rb, 1);
+    stage(ra, 0);
+    __syncthreads();
+    for (int kb = 0; kb < kblocks; kb += 2) {
+      if (kb + 2 < kblocks) fetch(ra, kb + 2);
+      compute(0);
+      if (kb + 1 < kblocks) stage(rb, 1);
+      __syncthreads();
+      if (kb + 1 < kblocks) {
+        if (kb + 3 < kblocks) fetch(rb, kb + 3);
+        compute(1);
+        if (kb + 2 < kblocks) stage(ra, 0);
+        __syncthreads();
+      }
+    }
   }
 
   const float s = w_scale ? *w_scale : 1.0f;
 #pragma unroll
-  for (int j = 0; j < NT; ++j) {
+  for (int j = 0; j < FNT; ++j) {
     const int col = n0 + wn + j * 32 + (lane & 31);
     const float bv = bias ? bias[col] : 0.0f;
 #pragma unroll
@@ -457,6 +495,167 @@ __global__ __launch_bounds__(THREADS, 1) void linear_fast_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Staged-decode variant: W is decoded to bf16 once per workgroup while it is
+// written to LDS (instead of once per wave after every LDS read), and the
+// staging of K block kb+1 (x rounding, W decoding, LDS writes) is spread over
+// MFMA steps 1..3 of block kb so the converts issue while the matrix core is
+// busy.  The MFMA loop itself is then only 16-byte LDS reads and MFMAs.
+
+constexpr int B_PITCH = BK + 8;  // bf16 per W row in LDS (144 B, conflict-free fragment reads)
+
+template <int WT, int FBN, int OCC>
+__global__ __launch_bounds__(THREADS, OCC) void linear_sd_kernel(
+    const float* __restrict__ x, const uint8_t* __restrict__ w, const float* __restrict__ w_scale,
+    const float* __restrict__ bias, float* __restrict__ y, int M, int N, int K, int tiles_m,
+    int tiles_n) {
+  using WTr = W<WT>;
+  constexpr int FWN = FBN / 2;
+  constexpr int FNT = FWN / 32;
+  constexpr int B_STAGE = FBN * B_PITCH * 2;
+  constexpr int STAGE = A_STAGE + B_STAGE;
+  constexpr int WCH = FBN * BK / WTr::epc / THREADS;  // W chunks per thread
+  constexpr int WCPR = BK / WTr::epc;                  // W chunks per row
+  constexpr int UNITS = XCH + WCH;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * STAGE];
+
+  const int T = tiles_m * tiles_n;
+  int t = blockIdx.x;
+  if ((T & 7) == 0) t = (t & 7) * (T >> 3) + (t >> 3);
+  constexpr int GM = 4;
+  const int group = t / (GM * tiles_n);
+  const int first_m = group * GM;
+  const int gm = min(tiles_m - first_m, GM);
+  const int rem = t - group * GM * tiles_n;
+  const int m0 = (first_m + rem % gm) * BM;
+  const int n0 = (rem / gm) * FBN;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, half = lane >> 5;
+  const int wm = (wave & 1) * WM, wn = (wave >> 1) * FWN;
+  const size_t w_row_bytes = (size_t)K * WTr::bits / 8;
+
+  const float* xtile = x + (size_t)m0 * K;
+  const uint32_t xlane = (uint32_t)((tid >> 4) * K + (tid & 15) * 4);
+  const size_t xstep = (size_t)16 * K;
+  const int xdst0 = ((tid >> 4) * A_PITCH + (tid & 15) * 4) * 2;
+  constexpr int XDST_STEP = 16 * A_PITCH * 2;
+  const uint8_t* wtile = w + (size_t)n0 * w_row_bytes;
+  const uint32_t wlane = (uint32_t)((tid / WCPR) * w_row_bytes + (tid % WCPR) * 16);
+  const size_t wstep = (size_t)(THREADS / WCPR) * w_row_bytes;
+  const int wdst0 = A_STAGE + ((tid / WCPR) * B_PITCH + (tid % WCPR) * WTr::epc) * 2;
+  constexpr int WDST_STEP = (THREADS / WCPR) * B_PITCH * 2;
+
+  u32x4 xr[XCH], wr[WCH];
+  auto fetch = [&](int kb) {
+    const float* xk = xtile + (size_t)kb * BK;
+    const uint8_t* wk = wtile + (size_t)kb * (BK * WTr::bits / 8);
+#pragma unroll
+    for (int i = 0; i < XCH; ++i) xr[i] = *reinterpret_cast<const u32x4*>(xk + i * xstep + xlane);
+#pragma unroll
+    for (int i = 0; i < WCH; ++i) wr[i] = *reinterpret_cast<const u32x4*>(wk + i * wstep + wlane);
+  };
+  // staging units u in [u0, u1): x chunks first, then W chunks
+  auto stage_units = [&](uint8_t* S, int u0, int u1) {
+#pragma unroll
+    for (int u = 0; u < UNITS; ++u) {
+      if (u < u0 || u >= u1) continue;
+      if (u < XCH) {
+        uint32_t p0 = f32x2_to_bf16(xr[u][0], xr[u][1]);
+        uint32_t p1 = f32x2_to_bf16(xr[u][2], xr[u][3]);
+        *reinterpret_cast<u32x2*>(S + xdst0 + u * XDST_STEP) = u32x2{p0, p1};
+      } else {
+        const int i = u - XCH;
+        uint32_t words[WTr::words];
+        decode_chunk<WT>(wr[i], words);
+        uint8_t* d = S + wdst0 + i * WDST_STEP;
+#pragma unroll
+        for (int q = 0; q < WTr::words; q += 4)
+          *reinterpret_cast<u32x4*>(d + 4 * q) = u32x4{words[q], words[q + 1], words[q + 2], words[q + 3]};
+      }
+    }
+  };
+
+  f32x16 acc[MT][FNT];
+#pragma unroll
+  for (int a = 0; a < MT; ++a)
+#pragma unroll
+    for (int b = 0; b < FNT; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.0f;
+
+  int aoff[MT], boff[FNT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i) aoff[i] = ((wm + i * 32 + (lane & 31)) * A_PITCH + half * 8) * 2;
+#pragma unroll
+  for (int j = 0; j < FNT; ++j) boff[j] = A_STAGE + ((wn + j * 32 + (lane & 31)) * B_PITCH + half * 8) * 2;
+
+  const int kblocks = K / BK;
+  fetch(0);
+  stage_units(lds, 0, UNITS);
+  __syncthreads();
+  for (int kb = 0; kb < kblocks; ++kb) {
+    const uint8_t* S = lds + (kb & 1) * STAGE;
+    uint8_t* Snext = lds + ((kb + 1) & 1) * STAGE;
+    // The last block fetches and stages itself once more into the idle
+    // buffer, so the loop body has no branch and schedules as one region.
+    fetch(min(kb + 1, kblocks - 1));
+    bf16x8 a[2][MT], b[2][FNT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) a[0][i] = *reinterpret_cast<const bf16x8*>(S + aoff[i]);
+#pragma unroll
+    for (int j = 0; j < FNT; ++j) b[0][j] = *reinterpret_cast<const bf16x8*>(S + boff[j]);
+#pragma unroll
+    for (int s = 0; s < BK / 16; ++s) {
+      const int cur = s & 1, nxt = cur ^ 1;
+      if (s + 1 < BK / 16) {
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+          a[nxt][i] = *reinterpret_cast<const bf16x8*>(S + aoff[i] + (s + 1) * 32);
+#pragma unroll
+        for (int j = 0; j < FNT; ++j)
+          b[nxt][j] = *reinterpret_cast<const bf16x8*>(S + boff[j] + (s + 1) * 32);
+      }
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < FNT; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[cur][i], b[cur][j], acc[i][j], 0, 0, 0);
+      // a third of the next block's staging after each of MFMA steps 1..3
+      if (s >= 1) stage_units(Snext, (s - 1) * UNITS / 3, s * UNITS / 3);
+    }
+    __syncthreads();
+  }
+
+  const float s = w_scale ? *w_scale : 1.0f;
+#pragma unroll
+  for (int j = 0; j < FNT; ++j) {
+    const int col = n0 + wn + j * 32 + (lane & 31);
+    const float bv = bias ? bias[col] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+        __builtin_nontemporal_store(acc[i][j][r] * s + bv, &y[(size_t)row * N + col]);
+      }
+    }
+  }
+}
+
+// Whole-tile configuration: tile width, workgroups per CU, prefetch depth.
+#ifndef NOVAQ_LINEAR_CFG
+#define NOVAQ_LINEAR_CFG 5
+#endif
+constexpr int kCfg = NOVAQ_LINEAR_CFG;
+constexpr bool kSD = kCfg >= 4;  // staged-decode kernel
+constexpr int kFBN = (kCfg == 2 || kCfg == 3 || kCfg == 5) ? 128 : 256;
+constexpr int kOCC = (kCfg == 2 || kCfg == 3 || kCfg == 5) ? 2 : 1;
+constexpr int kPF = (kCfg == 1 || kCfg == 3) ? 2 : 1;
+#ifndef NOVAQ_LINEAR_WLM
+#define NOVAQ_LINEAR_WLM 2
+#endif
+constexpr int kWLM = NOVAQ_LINEAR_WLM;
+
 template <int WT>
 int launch(const float* x, int64_t M, int64_t K, const void* w, const float* w_scale,
            const float* bias, int64_t N, float* y, hipStream_t stream) {
@@ -464,11 +663,19 @@ int launch(const float* x, int64_t M, int64_t K, const void* w, const float* w_s
   const int64_t T = tiles_m * tiles_n;
   if (T > 0x7FFFFFFF || M > 0x7FFFFFFF || N > 0x7FFFFFFF || K > 0x7FFFFFFF) return NOVAQ_EINVAL;
   if constexpr (WT != F32) {
-    const bool whole = M % BM == 0 && N % BN == 0 && K % BK == 0 && K > 0;
+    const bool whole = M % BM == 0 && N % kFBN == 0 && K % BK == 0 && K > 0;
     if (whole) {
-      hipLaunchKernelGGL((linear_fast_kernel<WT>), dim3((unsigned)T), dim3(THREADS), 0, stream,
-                         x, static_cast<const uint8_t*>(w), w_scale, bias, y, (int)M, (int)N,
-                         (int)K, (int)tiles_m, (int)tiles_n);
+      const int64_t ftn = N / kFBN;
+      if constexpr (kSD) {
+        hipLaunchKernelGGL((linear_sd_kernel<WT, kFBN, kOCC>), dim3((unsigned)(tiles_m * ftn)),
+                           dim3(THREADS), 0, stream, x, static_cast<const uint8_t*>(w), w_scale,
+                           bias, y, (int)M, (int)N, (int)K, (int)tiles_m, (int)ftn);
+      } else {
+        hipLaunchKernelGGL((linear_fast_kernel<WT, kFBN, kOCC, kPF, kWLM>),
+                           dim3((unsigned)(tiles_m * ftn)), dim3(THREADS), 0, stream, x,
+                           static_cast<const uint8_t*>(w), w_scale, bias, y, (int)M, (int)N,
+                           (int)K, (int)tiles_m, (int)ftn);
+      }
       return check_launch();
     }
   }
