@@ -33,6 +33,8 @@ namespace novaq {
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int THREADS = 256;
@@ -53,6 +55,7 @@ struct ConvGeom {
   int rows;      // staged input rows per tile
   int wp;        // staged input columns
   int tiles_per_image;
+  int raw_in_lds;  // weights staged through a raw LDS copy (one channel block, fits)
   int64_t tiles;
 };
 
@@ -105,26 +108,67 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_kernel(
   const bool two_m = co0 + 32 < g.C_out;
   const float s = w_scale ? *w_scale : 1.0f;
 
-  auto stage_weights = [&](int cb) {
-    const int kcols = 16 * g.ksteps;
-    for (int idx = tid; idx < CO_TILE * kcols; idx += THREADS) {
-      const int co = idx / kcols, k = idx - co * kcols;
-      const int grp = k >> 3;
-      uint16_t v = 0;
+  // Weights: one item = (output channel, group of 8 consecutive K values), i.e.
+  // 8 channels of one (kh, kw) tap: 8 decoded weights packed into one 16-byte
+  // LDS write.  Channels past C (and K groups past the window) are zeros.
+  // `src` holds the (co0.., c, kh, kw) weights in storage order starting at
+  // output channel `cofs` (the global tensor, or its raw copy in LDS).
+  auto stage_weights = [&](int cb, const uint8_t* src, int cofs) {
+    const int gpr = 2 * g.ksteps;  // 8-wide K groups per LDS row
+    const int cstep = g.KH * g.KW;
+    for (int it = tid; it < CO_TILE * gpr; it += THREADS) {
+      const int co = it / gpr, grp = it - co * gpr;
+      uint32_t p[4] = {0u, 0u, 0u, 0u};
       if (grp < g.groups && co0 + co < g.C_out) {
         const int khkw = grp / c8;
-        const int c = cb * g.CB + (grp - khkw * c8) * 8 + (k & 7);
-        if (c < g.C) {
-          const int kh = khkw / g.KW, kw = khkw - kh * g.KW;
-          const int64_t e = (((int64_t)(co0 + co) * g.C + c) * g.KH + kh) * g.KW + kw;
-          v = weight_bf16<WT>(w, e);
+        const int cbase = cb * g.CB + (grp - khkw * c8) * 8;
+        const int64_t e0 = ((int64_t)(co0 + co - cofs) * g.C + cbase) * cstep + khkw;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const uint32_t v = cbase + j < g.C ? weight_bf16<WT>(src, e0 + j * cstep) : 0u;
+          p[j >> 1] |= v << ((j & 1) * 16);
         }
       }
-      wl[co * g.wrow + k] = v;
+      *reinterpret_cast<uint4*>(&wl[co * g.wrow + grp * 8]) = make_uint4(p[0], p[1], p[2], p[3]);
     }
   };
+  // Raw copy of this workgroup's weight rows into the (not yet used) input
+  // tile region with coalesced dword loads, all in flight at once; the
+  // decode above then reads LDS instead of issuing dependent global loads.
+  // Used when all channels fit one block and the raw rows fit the region.
+  auto stage_weights_via_lds = [&]() {
+    const int rows = min(CO_TILE, g.C_out - co0);
+    const int64_t row_elems = (int64_t)g.C * g.KH * g.KW;
+    const int64_t first = (int64_t)co0 * row_elems;  // first element (even: co0 % 64 == 0)
+    const int nbytes = (int)(rows * row_elems * dtype_bits(WT) / 8 + (dtype_bits(WT) == 4 ? (rows * row_elems) & 1 : 0));
+    const uint8_t* gsrc = w + first * dtype_bits(WT) / 8;  // 4-byte aligned (row_elems * 64 elems)
+    uint8_t* raw = reinterpret_cast<uint8_t*>(xl);
+    const int nwords = nbytes >> 2;
+#pragma unroll 8
+    for (int i = tid; i < nwords; i += THREADS)
+      reinterpret_cast<uint32_t*>(raw)[i] = reinterpret_cast<const uint32_t*>(gsrc)[i];
+    for (int i = (nwords << 2) + tid; i < nbytes; i += THREADS) raw[i] = gsrc[i];
+    __syncthreads();
+    stage_weights(0, raw, co0);
+  };
 
-  if (cblocks == 1) stage_weights(0);
+  // window offset (in staged-input elements) of each 8-wide K group, -1 for
+  // the padding group past the window
+  int* ktab = reinterpret_cast<int*>(xl + g.rows * g.wp * g.cstride);
+  for (int i = tid; i < 2 * g.ksteps; i += THREADS) {
+    int koff = -1;
+    if (i < g.groups) {
+      const int khkw = i / c8;
+      const int kh = khkw / g.KW, kw = khkw - kh * g.KW;
+      koff = (kh * g.wp + kw) * g.cstride + (i - khkw * c8) * 8;
+    }
+    ktab[i] = koff;
+  }
+
+  if (cblocks == 1) {
+    if (g.raw_in_lds) stage_weights_via_lds();
+    else stage_weights(0, w, 0);
+  }
 
   for (int64_t tile = blockIdx.x; tile < g.tiles; tile += gridDim.x) {
     const int n = (int)(tile / g.tiles_per_image);
@@ -152,51 +196,91 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_kernel(
 
     for (int cb = 0; cb < cblocks; ++cb) {
       __syncthreads();  // previous readers of the LDS tile are done
-      if (cblocks > 1) stage_weights(cb);
-      // stage input rows [ih0, ih0 + rows) x cols [-pw, -pw + wp), channels of block cb
-      const int per_c = g.rows * g.wp;
-      for (int idx = tid; idx < g.CB * per_c; idx += THREADS) {
-        const int c = idx / per_c;
-        const int rc = idx - c * per_c;
-        const int r = rc / g.wp, col = rc - r * g.wp;
-        const int cg = cb * g.CB + c;
-        float v = 0.0f;
-        if (cg < g.C) {
-          const int hi = pad_index(ih0 + r, g.H, g.pad_mode);
-          const int wi = pad_index(col - g.pw, g.W, g.pad_mode);
-          if (hi >= 0 && wi >= 0) v = x[(((int64_t)n * g.C + cg) * g.H + hi) * g.W + wi];
-        }
-        xl[(r * g.wp + col) * g.cstride + c] = f32_to_bf16_rne(v);
-      }
-      __syncthreads();
-
-      for (int st = 0; st < g.ksteps; ++st) {
-        const int grp = 2 * st + half;
-        const bool live = grp < g.groups;
-        int koff = 0;
-        if (live) {
-          const int khkw = grp / c8;
-          const int kh = khkw / g.KW, kw = khkw - kh * g.KW;
-          koff = (kh * g.wp + kw) * g.cstride + (grp - khkw * c8) * 8;
-        }
-        const int kcol = st * 16 + half * 8;
-        bf16x8 a0 = *reinterpret_cast<const bf16x8*>(&wl[(lane & 31) * g.wrow + kcol]);
-        bf16x8 a1 = *reinterpret_cast<const bf16x8*>(&wl[(32 + (lane & 31)) * g.wrow + kcol]);
-        bf16x8 b[2];
+      if (cblocks > 1) stage_weights(cb, w, 0);
+      // Stage input rows [ih0, ih0 + rows) x cols [-pw, -pw + wp) of channel
+      // block cb.  One item = one staged pixel x 8 channels: 8 independent
+      // loads (consecutive lanes take consecutive pixels, so each load
+      // instruction reads a contiguous row segment), 4 packed bf16 converts
+      // (RNE) and one 16-byte LDS write.
+      const int pix = g.rows * g.wp;
+      const int total = pix * c8;
+      const int64_t hw = (int64_t)g.H * g.W;
+      // batches of IB items per thread: all 8*IB loads are issued before the
+      // first conversion
+      constexpr int IB = 4;
+      for (int base = 0; base < total; base += IB * THREADS) {
+        float v[IB][8];
+        int dst[IB];
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
-          if (live) {
-            b[nt] = *reinterpret_cast<const bf16x8*>(&xl[pbase[nt] + koff]);
-          } else {
+        for (int b = 0; b < IB; ++b) {
+          const int it = base + b * THREADS + tid;
+          dst[b] = -1;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) b[nt][j] = (__bf16)0.0f;
+          for (int j = 0; j < 8; ++j) v[b][j] = 0.0f;
+          if (it < total) {
+            const int cgi = it / pix, p = it - cgi * pix;
+            const int r = p / g.wp, col = p - r * g.wp;
+            const int hi = pad_index(ih0 + r, g.H, g.pad_mode);
+            const int wi = pad_index(col - g.pw, g.W, g.pad_mode);
+            const int cbase = cb * g.CB + cgi * 8;
+            dst[b] = (r * g.wp + col) * g.cstride + cgi * 8;
+            if (hi >= 0 && wi >= 0) {
+              const float* src = x + ((int64_t)n * g.C + cbase) * hw + (int64_t)hi * g.W + wi;
+#pragma unroll
+              for (int j = 0; j < 8; ++j)
+                if (cbase + j < g.C) v[b][j] = src[j * hw];
+            }
           }
         }
 #pragma unroll
+        for (int b = 0; b < IB; ++b) {
+          if (dst[b] < 0) continue;
+          uint32_t q[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            f32x2 f = {v[b][2 * j], v[b][2 * j + 1]};
+            q[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));
+          }
+          *reinterpret_cast<uint4*>(&xl[dst[b]]) = make_uint4(q[0], q[1], q[2], q[3]);
+        }
+      }
+      __syncthreads();
+
+      // fragments of K step st into register set `buf`; the window offset
+      // of each 8-wide K group comes from the per-workgroup table (-1: the
+      // zero padding group past the window)
+      bf16x8 fa0[2], fa1[2], fb[2][2];
+      auto load = [&](int st, int buf) {
+        const int koff = ktab[2 * st + half];
+        const int kcol = st * 16 + half * 8;
+        fa0[buf] = *reinterpret_cast<const bf16x8*>(&wl[(lane & 31) * g.wrow + kcol]);
+        fa1[buf] = *reinterpret_cast<const bf16x8*>(&wl[(32 + (lane & 31)) * g.wrow + kcol]);
+#pragma unroll
         for (int nt = 0; nt < 2; ++nt) {
-          acc[0][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b[nt], acc[0][nt], 0, 0, 0);
+          if (koff >= 0) {
+            fb[buf][nt] = *reinterpret_cast<const bf16x8*>(&xl[pbase[nt] + koff]);
+          } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) fb[buf][nt][j] = (__bf16)0.0f;
+          }
+        }
+      };
+      auto mfma = [&](int buf) {
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+          acc[0][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa0[buf], fb[buf][nt], acc[0][nt], 0, 0, 0);
           if (two_m)
-            acc[1][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b[nt], acc[1][nt], 0, 0, 0);
+            acc[1][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa1[buf], fb[buf][nt], acc[1][nt], 0, 0, 0);
+        }
+      };
+      // the next step's fragments are read while the current step multiplies
+      load(0, 0);
+      for (int st = 0; st < g.ksteps; st += 2) {
+        if (st + 1 < g.ksteps) load(st + 1, 1);
+        mfma(0);
+        if (st + 1 < g.ksteps) {
+          if (st + 2 < g.ksteps) load(st + 2, 0);
+          mfma(1);
         }
       }
     }
@@ -231,7 +315,11 @@ int launch(const float* x, const void* w, const float* w_scale, const float* bia
   const int out_rows = (PIX_TILE - 1) / g.OW + 2;
   g.rows = (out_rows - 1) * g.sh + g.KH;
   g.wp = (g.OW - 1) * g.sw + g.KW;
-  const size_t lds = (size_t)CO_TILE * g.wrow * 2 + (size_t)g.rows * g.wp * g.cstride * 2;
+  const size_t xl_bytes = (size_t)g.rows * g.wp * g.cstride * 2;
+  // weights, staged input, then the K-group offset table (2*ksteps ints)
+  const size_t lds = (size_t)CO_TILE * g.wrow * 2 + xl_bytes + (size_t)8 * g.ksteps;
+  const size_t raw_bytes = ((size_t)CO_TILE * g.C * g.KH * g.KW * dtype_bits(WT) + 7) / 8;
+  g.raw_in_lds = g.C <= g.CB && raw_bytes <= xl_bytes;
   if (lds > LDS_LIMIT) return NOVAQ_ENOTSUP;  // rows too wide for one LDS tile
   auto kern = conv2d_kernel<WT>;
   if (lds > 64 * 1024) {
