@@ -42,6 +42,14 @@ constexpr int CO_TILE = 64;
 constexpr int PIX_WAVE = 64;
 constexpr int PIX_TILE = PIX_WAVE * (THREADS / 64);
 constexpr int MAX_CB = 64;
+// workgroups per CU the registers are sized for (the grid is CUs x this), and
+// input-staging items per thread whose loads are issued together
+#ifndef CONV_OCC
+#define CONV_OCC 2
+#endif
+#ifndef CONV_IB
+#define CONV_IB 4
+#endif
 constexpr size_t LDS_LIMIT = 160 * 1024;
 
 struct ConvGeom {
@@ -51,7 +59,7 @@ struct ConvGeom {
   int cstride;   // bf16 per staged input pixel (CB, +8 if CB/8 is even)
   int groups;    // K groups of 8 per channel block = KH*KW*CB/8
   int ksteps;    // ceil(groups / 2)
-  int wrow;      // bf16 per weight LDS row = 16*ksteps + 8
+  int wrow;      // bytes per weight LDS row (2*ksteps K groups, padded for banks)
   int rows;      // staged input rows per tile
   int wp;        // staged input columns
   int tiles_per_image;
@@ -78,6 +86,55 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
   return (uint16_t)enc_bf16(__float_as_uint(f));
 }
 
+// Bytes of one 8-wide K group of a weight row in LDS: the packed codes for
+// E2M1 (4 B) and E4M3 / E5M2 (8 B), decoded bf16 otherwise (16 B).
+template <int WT>
+__host__ __device__ constexpr int group_bytes() {
+  return WT == E2M1 ? 4 : (WT == E4M3 || WT == E5M2) ? 8 : 16;
+}
+
+// Stored code of weight element e (E2M1 nibble or FP8 byte).
+template <int WT>
+__device__ __forceinline__ uint32_t weight_code(const uint8_t* __restrict__ w, int64_t e) {
+  if constexpr (WT == E2M1) return (w[e >> 1] >> ((e & 1) * 4)) & 0xFu;
+  else return w[e];
+}
+
+typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+
+// One lane's A fragment (8 weights of one K group) from LDS as 8 bf16; FP8
+// and FP4 codes are decoded exactly with gfx950's packed converts.
+template <int WT>
+__device__ __forceinline__ bf16x8 weight_frag(const uint8_t* p) {
+  if constexpr (WT == E2M1) {
+    const uint32_t v = *reinterpret_cast<const uint32_t*>(p);
+    uint32_t o[4];
+    o[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, 1.0f, 0));
+    o[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, 1.0f, 1));
+    o[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, 1.0f, 2));
+    o[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, 1.0f, 3));
+    return __builtin_bit_cast(bf16x8, make_uint4(o[0], o[1], o[2], o[3]));
+  } else if constexpr (WT == E4M3 || WT == E5M2) {
+    const u32x2v v = *reinterpret_cast<const u32x2v*>(p);
+    const uint32_t lo = v[0], hi = v[1];
+    uint32_t o[4];
+    if constexpr (WT == E4M3) {
+      o[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, false));
+      o[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, true));
+      o[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, false));
+      o[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, true));
+    } else {
+      o[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(lo, 1.0f, false));
+      o[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(lo, 1.0f, true));
+      o[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(hi, 1.0f, false));
+      o[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(hi, 1.0f, true));
+    }
+    return __builtin_bit_cast(bf16x8, make_uint4(o[0], o[1], o[2], o[3]));
+  } else {
+    return *reinterpret_cast<const bf16x8*>(p);
+  }
+}
+
 // Decoded weight element e (flat (co, c, kh, kw) index) as bf16 bits.
 template <int WT>
 __device__ __forceinline__ uint16_t weight_bf16(const uint8_t* __restrict__ w, int64_t e) {
@@ -93,12 +150,13 @@ __device__ __forceinline__ uint16_t weight_bf16(const uint8_t* __restrict__ w, i
 }
 
 template <int WT>
-__global__ __launch_bounds__(THREADS, 2) void conv2d_kernel(
+__global__ __launch_bounds__(THREADS, CONV_OCC) void conv2d_kernel(
     const float* __restrict__ x, const uint8_t* __restrict__ w, const float* __restrict__ w_scale,
     const float* __restrict__ bias, float* __restrict__ y, ConvGeom g) {
-  extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
-  uint16_t* wl = lds;                                  // [CO_TILE][g.wrow]
-  uint16_t* xl = lds + CO_TILE * g.wrow;               // [rows][wp][cstride]
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  constexpr int GB = group_bytes<WT>();
+  uint8_t* wl = lds;                                                     // [CO_TILE][g.wrow B]
+  uint16_t* xl = reinterpret_cast<uint16_t*>(lds + CO_TILE * g.wrow);    // [rows][wp][cstride]
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, half = lane >> 5;
   const int co0 = blockIdx.y * CO_TILE;
@@ -109,10 +167,11 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_kernel(
   const float s = w_scale ? *w_scale : 1.0f;
 
   // Weights: one item = (output channel, group of 8 consecutive K values), i.e.
-  // 8 channels of one (kh, kw) tap: 8 decoded weights packed into one 16-byte
-  // LDS write.  Channels past C (and K groups past the window) are zeros.
-  // `src` holds the (co0.., c, kh, kw) weights in storage order starting at
-  // output channel `cofs` (the global tensor, or its raw copy in LDS).
+  // 8 channels of one (kh, kw) tap, written as one LDS group: 8 packed E2M1
+  // nibbles (4 B), 8 FP8 bytes (8 B) or 8 decoded bf16 (16 B).  Channels
+  // past C and K groups past the window are zeros (code 0 is +0 in every
+  // format).  `src` holds the (co, c, kh, kw) weights in storage order
+  // starting at output channel `cofs` (the global tensor, or its raw copy).
   auto stage_weights = [&](int cb, const uint8_t* src, int cofs) {
     const int gpr = 2 * g.ksteps;  // 8-wide K groups per LDS row
     const int cstep = g.KH * g.KW;
@@ -125,11 +184,20 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_kernel(
         const int64_t e0 = ((int64_t)(co0 + co - cofs) * g.C + cbase) * cstep + khkw;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          const uint32_t v = cbase + j < g.C ? weight_bf16<WT>(src, e0 + j * cstep) : 0u;
-          p[j >> 1] |= v << ((j & 1) * 16);
+          if (cbase + j >= g.C) continue;
+          if constexpr (GB == 4) {
+            p[0] |= weight_code<WT>(src, e0 + j * cstep) << (4 * j);
+          } else if constexpr (GB == 8) {
+            p[j >> 2] |= weight_code<WT>(src, e0 + j * cstep) << (8 * (j & 3));
+          } else {
+            p[j >> 1] |= (uint32_t)weight_bf16<WT>(src, e0 + j * cstep) << ((j & 1) * 16);
+          }
         }
       }
-      *reinterpret_cast<uint4*>(&wl[co * g.wrow + grp * 8]) = make_uint4(p[0], p[1], p[2], p[3]);
+      uint8_t* d = wl + co * g.wrow + grp * GB;
+      if constexpr (GB == 4) *reinterpret_cast<uint32_t*>(d) = p[0];
+      else if constexpr (GB == 8) *reinterpret_cast<u32x2v*>(d) = u32x2v{p[0], p[1]};
+      else *reinterpret_cast<uint4*>(d) = make_uint4(p[0], p[1], p[2], p[3]);
     }
   };
   // Raw copy of this workgroup's weight rows into the (not yet used) input
@@ -207,7 +275,7 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_kernel(
       const int64_t hw = (int64_t)g.H * g.W;
       // batches of IB items per thread: all 8*IB loads are issued before the
       // first conversion
-      constexpr int IB = 4;
+      constexpr int IB = CONV_IB;
       for (int base = 0; base < total; base += IB * THREADS) {
         float v[IB][8];
         int dst[IB];
@@ -252,9 +320,9 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_kernel(
       bf16x8 fa0[2], fa1[2], fb[2][2];
       auto load = [&](int st, int buf) {
         const int koff = ktab[2 * st + half];
-        const int kcol = st * 16 + half * 8;
-        fa0[buf] = *reinterpret_cast<const bf16x8*>(&wl[(lane & 31) * g.wrow + kcol]);
-        fa1[buf] = *reinterpret_cast<const bf16x8*>(&wl[(32 + (lane & 31)) * g.wrow + kcol]);
+        const int kbyte = (2 * st + half) * GB;
+        fa0[buf] = weight_frag<WT>(wl + (lane & 31) * g.wrow + kbyte);
+        fa1[buf] = weight_frag<WT>(wl + (32 + (lane & 31)) * g.wrow + kbyte);
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) {
           if (koff >= 0) {
@@ -315,20 +383,31 @@ int launch(const float* x, const void* w, const float* w_scale, const float* bia
   const int out_rows = (PIX_TILE - 1) / g.OW + 2;
   g.rows = (out_rows - 1) * g.sh + g.KH;
   g.wp = (g.OW - 1) * g.sw + g.KW;
+  // weight row: 2*ksteps groups of GB bytes, padded so the 32 rows one
+  // fragment read touches fall in distinct LDS banks (row stride in dwords
+  // odd for 4-byte reads, 2 mod 4 for 8-byte reads, 4 mod 8 for 16-byte reads)
+  constexpr int GB = group_bytes<WT>();
+  int stride_dw = 2 * g.ksteps * GB / 4;
+  while ((GB == 4 && stride_dw % 2 != 1) || (GB == 8 && stride_dw % 4 != 2) ||
+         (GB == 16 && stride_dw % 8 != 4))
+    stride_dw += GB / 4;
+  g.wrow = stride_dw * 4;
   const size_t xl_bytes = (size_t)g.rows * g.wp * g.cstride * 2;
   // weights, staged input, then the K-group offset table (2*ksteps ints)
-  const size_t lds = (size_t)CO_TILE * g.wrow * 2 + xl_bytes + (size_t)8 * g.ksteps;
+  const size_t lds = (size_t)CO_TILE * g.wrow + xl_bytes + (size_t)8 * g.ksteps;
   const size_t raw_bytes = ((size_t)CO_TILE * g.C * g.KH * g.KW * dtype_bits(WT) + 7) / 8;
   g.raw_in_lds = g.C <= g.CB && raw_bytes <= xl_bytes;
   if (lds > LDS_LIMIT) return NOVAQ_ENOTSUP;  // rows too wide for one LDS tile
   auto kern = conv2d_kernel<WT>;
-  if (lds > 64 * 1024) {
+  static size_t lds_enabled = 64 * 1024;  // per instantiation: raise the limit once
+  if (lds > lds_enabled) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_LIMIT);
     if (e != hipSuccess) return hip_fail(e);
+    lds_enabled = LDS_LIMIT;
   }
   const int64_t co_blocks = (g.C_out + CO_TILE - 1) / CO_TILE;
-  int64_t grid = (int64_t)device_cu_count() * 2;
+  int64_t grid = (int64_t)device_cu_count() * CONV_OCC;
   if (grid > g.tiles) grid = g.tiles;
   if (grid < 1) grid = 1;
   hipLaunchKernelGGL(kern, dim3((unsigned)grid, (unsigned)co_blocks), dim3(THREADS), lds, stream, x,
@@ -357,7 +436,6 @@ int conv2d_launch(const float* x, int64_t N, int64_t C, int64_t H, int64_t W, co
   g.cstride = ((g.CB / 8) % 2 == 0) ? g.CB + 8 : g.CB;
   g.groups = KH * KW * g.CB / 8;
   g.ksteps = (g.groups + 1) / 2;
-  g.wrow = 16 * g.ksteps + 8;
   g.tiles_per_image = (int)((OH * OW + PIX_TILE - 1) / PIX_TILE);
   g.tiles = (int64_t)N * g.tiles_per_image;
   switch (w_dtype) {
