@@ -2,22 +2,22 @@
 //
 //   y[M, N] = x[M, K] . (s * dec(W[N, K]))^T + bias[N]
 //
-// Both operands are K-contiguous ("NT" GEMM).  One workgroup owns a
-// BM x BN = 128 x 256 tile of y and walks K in BK = 64 steps:
-//   - x (fp32) is read with 16-byte loads, rounded to bf16 (RNE,
-//     v_cvt_pk_bf16_f32) and written to LDS;
-//   - W is read in its stored format (E4M3 / E5M2 / E2M1 / bf16 / f16 / f32)
-//     and decoded to bf16 on the way into LDS; the FP8 / FP4 decodes are exact
-//     (every E4M3, E5M2 and E2M1 value is a bf16 value) and use gfx950's
-//     packed converts (v_cvt_scalef32_pk_bf16_{fp8,bf8,fp4}, scale 1.0);
-//   - four waves (2 x 2) each compute a 64 x 128 sub-tile with
-//     v_mfma_f32_32x32x16_bf16 (fp32 accumulation), reading 16-byte fragments
-//     from LDS rows padded to 72 bf16 (144 B) so a wave's 32 rows fall in
-//     distinct banks;
-//   - LDS is double-buffered: the next K block is fetched into registers
-//     while the current one is multiplied, then converted and stored into the
-//     other buffer (one barrier per K block).
-// The per-tensor scale s and the bias are applied in fp32 after accumulation.
+// Both operands are K-contiguous ("NT" GEMM).  x (fp32) is rounded to bf16
+// (RNE, v_cvt_pk_bf16_f32) on its way into LDS; W is read in its stored
+// format (E4M3 / E5M2 / E2M1 / bf16 / f16 / f32) and decoded to bf16 with
+// gfx950's packed converts (v_cvt_scalef32_pk_bf16_{fp8,bf8,fp4}, scale 1.0),
+// which are exact: every E4M3, E5M2 and E2M1 value is a bf16 value.  Products
+// run on v_mfma_f32_32x32x16_bf16 with fp32 accumulation; the per-tensor scale
+// s and the bias are applied in fp32 after accumulation.
+//
+// Three kernels, chosen by shape and weight format:
+//   - linear_wide_kernel (FP8 / FP4 weights, M % 128, N % 256, K % 128): one
+//     128 x 256 tile per workgroup of 8 waves, K blocks of 128 (one 128-byte
+//     line of an FP8 W row), W raw in LDS and decoded per MFMA fragment,
+//     buffer loads with SGPR offsets;
+//   - linear_pipe_kernel (whole 128-row tiles, K % 64): W decoded once per
+//     workgroup into bf16 LDS tiles, loads kept up to 3 K blocks ahead;
+//   - linear_kernel: any shape (guarded edge tiles) and fp32 weights.
 // Tiles are numbered so that the workgroups the hardware sends to one XCD
 // (block id mod 8) cover a compact 4-row group of tiles, so their x rows and W
 // rows are shared through that XCD's L2.
@@ -253,26 +253,6 @@ __global__ __launch_bounds__(THREADS, 1) void linear_kernel(
   }
 }
 
-// ---------------------------------------------------------------------------
-// Fast path: whole tiles only (M % 128 == 0, N % 256 == 0, K % 64 == 0), no
-// bounds logic.  W stays in its stored format in LDS (1 byte per E4M3/E5M2
-// element, half a byte per E2M1, 2 bytes for bf16/f16) and each wave decodes
-// its B fragments after the LDS read, so LDS traffic for W is that of the
-// packed codes.  The next K block is fetched into registers while the
-// current one is multiplied; LDS fragments are double-buffered across the
-// four 16-deep MFMA steps of a K block.
-
-template <int WT, int FBN>
-struct Fast {
-  static constexpr int bits = dtype_bits(WT);
-  static constexpr int row_bytes = BK * bits / 8;        // W bytes per tile row per K block
-  // LDS row pitch: keeps a wave's 32-row fragment reads in distinct banks
-  static constexpr int pitch = bits == 4 ? 36 : bits == 8 ? 72 : 144;
-  static constexpr int chunks = FBN * row_bytes / 16 / THREADS;  // 16-byte W chunks per thread
-  static constexpr int cpr = row_bytes / 16;             // chunks per W row
-  static constexpr int frag_bytes = 8 * bits / 8;        // one lane's 8 elements
-};
-
 constexpr int A_PITCH = BK + 8;                      // bf16 per A row in LDS
 constexpr int A_STAGE = BM * A_PITCH * 2;            // bytes
 
@@ -317,206 +297,33 @@ __device__ __forceinline__ bf16x8 frag_to_bf16(const uint8_t* p) {
   return __builtin_bit_cast(bf16x8, r);
 }
 
-// FBN: tile width in outputs (128 or 256); OCC: workgroups per CU the
-// register budget is sized for; PF: K blocks fetched ahead (1 or 2); WLM:
-// waves along M (2: 2 x 2 waves of 64 x FBN/2; 1: 1 x 4 waves of 128 x
-// FBN/4, where every W element is decoded by exactly one wave).
-template <int WT, int FBN, int OCC, int PF, int WLM>
-__global__ __launch_bounds__(THREADS, OCC) void linear_fast_kernel(
-    const float* __restrict__ x, const uint8_t* __restrict__ w, const float* __restrict__ w_scale,
-    const float* __restrict__ bias, float* __restrict__ y, int M, int N, int K, int tiles_m,
-    int tiles_n) {
-  using F = Fast<WT, FBN>;
-  constexpr int WM = BM / WLM;             // per-wave rows
-  constexpr int MT = WM / 32;
-  constexpr int FWN = FBN / (4 / WLM);     // per-wave width
-  constexpr int FNT = FWN / 32;
-  constexpr int B_STAGE = FBN * F::pitch;
-  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * (A_STAGE + B_STAGE)];
-
-  const int T = tiles_m * tiles_n;
-  int t = blockIdx.x;
-  if ((T & 7) == 0) t = (t & 7) * (T >> 3) + (t >> 3);
-  constexpr int GM = 4;
-  const int group = t / (GM * tiles_n);
-  const int first_m = group * GM;
-  const int gm = min(tiles_m - first_m, GM);
-  const int rem = t - group * GM * tiles_n;
-  const int m0 = (first_m + rem % gm) * BM;
-  const int n0 = (rem / gm) * FBN;
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, half = lane >> 5;
-  const int wm = (wave % WLM) * WM, wn = (wave / WLM) * FWN;
-  const size_t w_row_bytes = (size_t)K * F::bits / 8;
-
-  // Global sources: a uniform tile base, one per-lane offset, and uniform
-  // per-chunk strides (chunk i of a thread is 16*i rows of x / 256*i/cpr rows
-  // of W further down), so addresses cost scalar registers, not vector ones.
-  const float* xtile = x + (size_t)m0 * K;
-  const uint32_t xlane = (uint32_t)((tid >> 4) * K + (tid & 15) * 4);  // floats
-  const size_t xstep = (size_t)16 * K;                                   // floats per chunk
-  const int xdst0 = ((tid >> 4) * A_PITCH + (tid & 15) * 4) * 2;        // LDS bytes
-  constexpr int XDST_STEP = 16 * A_PITCH * 2;
-  const uint8_t* wtile = w + (size_t)n0 * w_row_bytes;
-  const uint32_t wlane = (uint32_t)((tid / F::cpr) * w_row_bytes + (tid % F::cpr) * 16);
-  const size_t wstep = (size_t)(THREADS / F::cpr) * w_row_bytes;
-  const int wdst0 = (tid / F::cpr) * F::pitch + (tid % F::cpr) * 16;
-  constexpr int WDST_STEP = (THREADS / F::cpr) * F::pitch;
-
-  struct Regs {
-    u32x4 x[XCH];
-    u32x4 w[F::chunks];
-  };
-  auto fetch = [&](Regs& r, int kb) {
-    const float* xk = xtile + (size_t)kb * BK;
-    const uint8_t* wk = wtile + (size_t)kb * F::row_bytes;
-#pragma unroll
-    for (int i = 0; i < XCH; ++i)
-      r.x[i] = *reinterpret_cast<const u32x4*>(xk + i * xstep + xlane);
-#pragma unroll
-    for (int i = 0; i < F::chunks; ++i)
-      r.w[i] = *reinterpret_cast<const u32x4*>(wk + i * wstep + wlane);
-  };
-  auto stage = [&](const Regs& r, int buf) {
-    uint8_t* A = lds + buf * (A_STAGE + B_STAGE) + xdst0;
-    uint8_t* B = lds + buf * (A_STAGE + B_STAGE) + A_STAGE + wdst0;
-#pragma unroll
-    for (int i = 0; i < XCH; ++i) {
-      uint32_t p0 = f32x2_to_bf16(r.x[i][0], r.x[i][1]);
-      uint32_t p1 = f32x2_to_bf16(r.x[i][2], r.x[i][3]);
-      *reinterpret_cast<u32x2*>(A + i * XDST_STEP) = u32x2{p0, p1};
-    }
-#pragma unroll
-    for (int i = 0; i < F::chunks; ++i) {
-      uint8_t* d = B + i * WDST_STEP;
-      if constexpr (F::pitch % 16 == 0) {
-        *reinterpret_cast<u32x4*>(d) = r.w[i];
-      } else if constexpr (F::pitch % 8 == 0) {
-        *reinterpret_cast<u32x2*>(d) = u32x2{r.w[i][0], r.w[i][1]};
-        *reinterpret_cast<u32x2*>(d + 8) = u32x2{r.w[i][2], r.w[i][3]};
-      } else {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) *reinterpret_cast<uint32_t*>(d + 4 * q) = r.w[i][q];
-      }
-    }
-  };
-
-  f32x16 acc[MT][FNT];
-#pragma unroll
-  for (int a = 0; a < MT; ++a)
-#pragma unroll
-    for (int b = 0; b < FNT; ++b)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.0f;
-
-  // fragment addresses (bytes) within a stage
-  int aoff[MT], boff[FNT];
-#pragma unroll
-  for (int i = 0; i < MT; ++i) aoff[i] = ((wm + i * 32 + (lane & 31)) * A_PITCH + half * 8) * 2;
-#pragma unroll
-  for (int j = 0; j < FNT; ++j)
-    boff[j] = A_STAGE + (wn + j * 32 + (lane & 31)) * F::pitch + half * F::frag_bytes;
-
-  auto compute = [&](int buf) {
-    const uint8_t* S = lds + buf * (A_STAGE + B_STAGE);
-    bf16x8 a[2][MT], b[2][FNT];
-#pragma unroll
-    for (int i = 0; i < MT; ++i) a[0][i] = *reinterpret_cast<const bf16x8*>(S + aoff[i]);
-#pragma unroll
-    for (int j = 0; j < FNT; ++j) b[0][j] = frag_to_bf16<WT>(S + boff[j]);
-#pragma unroll
-    for (int s = 0; s < BK / 16; ++s) {
-      const int cur = s & 1, nxt = cur ^ 1;
-      if (s + 1 < BK / 16) {
-#pragma unroll
-        for (int i = 0; i < MT; ++i)
-          a[nxt][i] = *reinterpret_cast<const bf16x8*>(S + aoff[i] + (s + 1) * 32);
-#pragma unroll
-        for (int j = 0; j < FNT; ++j)
-          b[nxt][j] = frag_to_bf16<WT>(S + boff[j] + (s + 1) * 2 * F::frag_bytes);
-      }
-#pragma unroll
-      for (int i = 0; i < MT; ++i)
-#pragma unroll
-        for (int j = 0; j < FNT; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[cur][i], b[cur][j], acc[i][j], 0, 0, 0);
-    }
-  };
-
-  // K blocks alternate between LDS buffers 0 and 1; a buffer is rewritten
-  // only after the barrier that ends its last reads.
-  const int kblocks = K / BK;
-  if constexpr (PF == 1) {
-    Regs r;
-    fetch(r, 0);
-    stage(r, 0);
-    __syncthreads();
-    for (int kb = 0; kb < kblocks; ++kb) {
-      const bool more = kb + 1 < kblocks;
-      if (more) fetch(r, kb + 1);
-      compute(kb & 1);
-      if (more) stage(r, (kb + 1) & 1);
-      __syncthreads();
-    }
-  } else {
-    // two register sets: K block kb+2 is in flight while kb+1 waits to be staged
-    Regs ra, rb;
-    fetch(ra, 0);
-    if (kblocks > 1) fetch(rb, 1);
-    stage(ra, 0);
-    __syncthreads();
-    for (int kb = 0; kb < kblocks; kb += 2) {
-      if (kb + 2 < kblocks) fetch(ra, kb + 2);
-      compute(0);
-      if (kb + 1 < kblocks) stage(rb, 1);
-      __syncthreads();
-      if (kb + 1 < kblocks) {
-        if (kb + 3 < kblocks) fetch(rb, kb + 3);
-        compute(1);
-        if (kb + 2 < kblocks) stage(ra, 0);
-        __syncthreads();
-      }
-    }
-  }
-
-  const float s = w_scale ? *w_scale : 1.0f;
-#pragma unroll
-  for (int j = 0; j < FNT; ++j) {
-    const int col = n0 + wn + j * 32 + (lane & 31);
-    const float bv = bias ? bias[col] : 0.0f;
-#pragma unroll
-    for (int i = 0; i < MT; ++i) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-        __builtin_nontemporal_store(acc[i][j][r] * s + bv, &y[(size_t)row * N + col]);
-      }
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Staged-decode variant: W is decoded to bf16 once per workgroup while it is
-// written to LDS (instead of once per wave after every LDS read), and the
-// staging of K block kb+1 (x rounding, W decoding, LDS writes) is spread over
-// MFMA steps 1..3 of block kb so the converts issue while the matrix core is
-// busy.  The MFMA loop itself is then only 16-byte LDS reads and MFMAs.
-
 constexpr int B_PITCH = BK + 8;  // bf16 per W row in LDS (144 B, conflict-free fragment reads)
 
-template <int WT, int FBN, int OCC>
-__global__ __launch_bounds__(THREADS, OCC) void linear_sd_kernel(
+// ---------------------------------------------------------------------------
+// Pipelined staged-decode kernel (whole tiles, any weight format but fp32):
+// W is decoded to bf16 once per workgroup while it is written to LDS, so the
+// MFMA loop is only 16-byte LDS reads and MFMAs.  NW waves (2 along M x NW/2
+// along N, each 64 x FBN*2/NW); PF register sets keep global loads PF K
+// blocks ahead: block kb+PF is loaded while block kb+1 (loaded PF-1 blocks
+// earlier) is converted into the idle LDS buffer after MFMA steps 1..3.
+
+template <int WT, int FBN, int NW, int OCC, int PF>
+__global__ __launch_bounds__(NW * 64, OCC) void linear_pipe_kernel(
     const float* __restrict__ x, const uint8_t* __restrict__ w, const float* __restrict__ w_scale,
     const float* __restrict__ bias, float* __restrict__ y, int M, int N, int K, int tiles_m,
     int tiles_n) {
   using WTr = W<WT>;
-  constexpr int FWN = FBN / 2;
+  constexpr int NTH = NW * 64;
+  constexpr int FWN = FBN * 2 / NW;
   constexpr int FNT = FWN / 32;
   constexpr int B_STAGE = FBN * B_PITCH * 2;
   constexpr int STAGE = A_STAGE + B_STAGE;
-  constexpr int WCH = FBN * BK / WTr::epc / THREADS;  // W chunks per thread
-  constexpr int WCPR = BK / WTr::epc;                  // W chunks per row
-  constexpr int UNITS = XCH + WCH;
+  constexpr int XC = BM * BK / 4 / NTH;               // x chunks per thread
+  constexpr int WCPR = BK / WTr::epc;                 // W chunks per row
+  constexpr int WC = FBN * BK / WTr::epc / NTH;       // W chunks per thread
+  constexpr int UNITS = XC + WC;
+  static_assert(FNT >= 1 && XC >= 1 && WC >= 1 && NTH % WCPR == 0, "tile shape");
+  static_assert(PF >= 1 && PF <= 3, "prefetch distance");
   __shared__ __attribute__((aligned(16))) uint8_t lds[2 * STAGE];
 
   const int T = tiles_m * tiles_n;
@@ -536,37 +343,40 @@ __global__ __launch_bounds__(THREADS, OCC) void linear_sd_kernel(
 
   const float* xtile = x + (size_t)m0 * K;
   const uint32_t xlane = (uint32_t)((tid >> 4) * K + (tid & 15) * 4);
-  const size_t xstep = (size_t)16 * K;
+  const size_t xstep = (size_t)(NTH / 16) * K;
   const int xdst0 = ((tid >> 4) * A_PITCH + (tid & 15) * 4) * 2;
-  constexpr int XDST_STEP = 16 * A_PITCH * 2;
+  constexpr int XDST_STEP = (NTH / 16) * A_PITCH * 2;
   const uint8_t* wtile = w + (size_t)n0 * w_row_bytes;
   const uint32_t wlane = (uint32_t)((tid / WCPR) * w_row_bytes + (tid % WCPR) * 16);
-  const size_t wstep = (size_t)(THREADS / WCPR) * w_row_bytes;
+  const size_t wstep = (size_t)(NTH / WCPR) * w_row_bytes;
   const int wdst0 = A_STAGE + ((tid / WCPR) * B_PITCH + (tid % WCPR) * WTr::epc) * 2;
-  constexpr int WDST_STEP = (THREADS / WCPR) * B_PITCH * 2;
+  constexpr int WDST_STEP = (NTH / WCPR) * B_PITCH * 2;
 
-  u32x4 xr[XCH], wr[WCH];
-  auto fetch = [&](int kb) {
+  struct Regs {
+    u32x4 x[XC];
+    u32x4 w[WC];
+  };
+  auto fetch = [&](Regs& r, int kb) {
     const float* xk = xtile + (size_t)kb * BK;
     const uint8_t* wk = wtile + (size_t)kb * (BK * WTr::bits / 8);
 #pragma unroll
-    for (int i = 0; i < XCH; ++i) xr[i] = *reinterpret_cast<const u32x4*>(xk + i * xstep + xlane);
+    for (int i = 0; i < XC; ++i) r.x[i] = *reinterpret_cast<const u32x4*>(xk + i * xstep + xlane);
 #pragma unroll
-    for (int i = 0; i < WCH; ++i) wr[i] = *reinterpret_cast<const u32x4*>(wk + i * wstep + wlane);
+    for (int i = 0; i < WC; ++i) r.w[i] = *reinterpret_cast<const u32x4*>(wk + i * wstep + wlane);
   };
   // staging units u in [u0, u1): x chunks first, then W chunks
-  auto stage_units = [&](uint8_t* S, int u0, int u1) {
+  auto stage_units = [&](const Regs& r, uint8_t* S, int u0, int u1) {
 #pragma unroll
     for (int u = 0; u < UNITS; ++u) {
       if (u < u0 || u >= u1) continue;
-      if (u < XCH) {
-        uint32_t p0 = f32x2_to_bf16(xr[u][0], xr[u][1]);
-        uint32_t p1 = f32x2_to_bf16(xr[u][2], xr[u][3]);
+      if (u < XC) {
+        uint32_t p0 = f32x2_to_bf16(r.x[u][0], r.x[u][1]);
+        uint32_t p1 = f32x2_to_bf16(r.x[u][2], r.x[u][3]);
         *reinterpret_cast<u32x2*>(S + xdst0 + u * XDST_STEP) = u32x2{p0, p1};
       } else {
-        const int i = u - XCH;
+        const int i = u - XC;
         uint32_t words[WTr::words];
-        decode_chunk<WT>(wr[i], words);
+        decode_chunk<WT>(r.w[i], words);
         uint8_t* d = S + wdst0 + i * WDST_STEP;
 #pragma unroll
         for (int q = 0; q < WTr::words; q += 4)
@@ -590,15 +400,15 @@ __global__ __launch_bounds__(THREADS, OCC) void linear_sd_kernel(
   for (int j = 0; j < FNT; ++j) boff[j] = A_STAGE + ((wn + j * 32 + (lane & 31)) * B_PITCH + half * 8) * 2;
 
   const int kblocks = K / BK;
-  fetch(0);
-  stage_units(lds, 0, UNITS);
-  __syncthreads();
-  for (int kb = 0; kb < kblocks; ++kb) {
+  // One K block: fetch block kb+PF into `rf` (free: its previous block is
+  // already in LDS), multiply the LDS buffer of block kb, and convert block
+  // kb+1 from `rs` into the other buffer after MFMA steps 1..3.  Past the end
+  // the last block is fetched and staged again into the idle buffer, so the
+  // body has no branch.
+  auto body = [&](int kb, Regs& rf, const Regs& rs) {
     const uint8_t* S = lds + (kb & 1) * STAGE;
     uint8_t* Snext = lds + ((kb + 1) & 1) * STAGE;
-    // The last block fetches and stages itself once more into the idle
-    // buffer, so the loop body has no branch and schedules as one region.
-    fetch(min(kb + 1, kblocks - 1));
+    fetch(rf, min(kb + PF, kblocks - 1));
     bf16x8 a[2][MT], b[2][FNT];
 #pragma unroll
     for (int i = 0; i < MT; ++i) a[0][i] = *reinterpret_cast<const bf16x8*>(S + aoff[i]);
@@ -620,10 +430,30 @@ __global__ __launch_bounds__(THREADS, OCC) void linear_sd_kernel(
 #pragma unroll
         for (int j = 0; j < FNT; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[cur][i], b[cur][j], acc[i][j], 0, 0, 0);
-      // a third of the next block's staging after each of MFMA steps 1..3
-      if (s >= 1) stage_units(Snext, (s - 1) * UNITS / 3, s * UNITS / 3);
+      if (s >= 1) stage_units(rs, Snext, (s - 1) * UNITS / 3, s * UNITS / 3);
     }
     __syncthreads();
+  };
+
+  Regs r0, r1, r2;
+  fetch(r0, 0);
+  if constexpr (PF >= 2) fetch(r1, min(1, kblocks - 1));
+  if constexpr (PF >= 3) fetch(r2, min(2, kblocks - 1));
+  stage_units(r0, lds, 0, UNITS);
+  __syncthreads();
+  if constexpr (PF == 1) {
+    for (int kb = 0; kb < kblocks; ++kb) body(kb, r0, r0);
+  } else if constexpr (PF == 2) {
+    for (int kb = 0; kb < kblocks; kb += 2) {
+      body(kb, r0, r1);
+      if (kb + 1 < kblocks) body(kb + 1, r1, r0);
+    }
+  } else {
+    for (int kb = 0; kb < kblocks; kb += 3) {
+      body(kb, r0, r1);
+      if (kb + 1 < kblocks) body(kb + 1, r1, r2);
+      if (kb + 2 < kblocks) body(kb + 2, r2, r0);
+    }
   }
 
   const float s = w_scale ? *w_scale : 1.0f;
@@ -642,19 +472,185 @@ __global__ __launch_bounds__(THREADS, OCC) void linear_sd_kernel(
   }
 }
 
-// Whole-tile configuration: tile width, workgroups per CU, prefetch depth.
-#ifndef NOVAQ_LINEAR_CFG
-#define NOVAQ_LINEAR_CFG 5
-#endif
-constexpr int kCfg = NOVAQ_LINEAR_CFG;
-constexpr bool kSD = kCfg >= 4;  // staged-decode kernel
-constexpr int kFBN = (kCfg == 2 || kCfg == 3 || kCfg == 5) ? 128 : 256;
-constexpr int kOCC = (kCfg == 2 || kCfg == 3 || kCfg == 5) ? 2 : 1;
-constexpr int kPF = (kCfg == 1 || kCfg == 3) ? 2 : 1;
-#ifndef NOVAQ_LINEAR_WLM
-#define NOVAQ_LINEAR_WLM 2
-#endif
-constexpr int kWLM = NOVAQ_LINEAR_WLM;
+// ---------------------------------------------------------------------------
+// Wide-K kernel (E4M3 / E5M2 / E2M1 weights, K % 128 == 0): K blocks of 128,
+// so one K block of a W row is a whole 128-byte line for FP8 (64 bytes for
+// E2M1) and each W load fetches no line it uses only half of; barriers are
+// half as many.  W stays in its stored format in LDS (decoded per fragment),
+// x is rounded to bf16 on the way in; two LDS stages, two register sets
+// (block kb+2 is loaded while block kb+1 is staged).
+
+template <int WT>
+struct Wide {
+  static constexpr int KB = 128;                        // K per block
+  static constexpr int bits = dtype_bits(WT);
+  static constexpr int row_bytes = KB * bits / 8;       // W bytes per row per block
+  static constexpr int pitch = bits == 8 ? 136 : 68;    // W LDS row pitch (bytes)
+  static constexpr int a_pitch = KB + 8;                // bf16 per x row in LDS
+  static constexpr int frag_bytes = 8 * bits / 8;
+  static constexpr int cpr = row_bytes / 16;            // W 16-byte chunks per row
+};
+
+template <int WT>
+__global__ __launch_bounds__(512, 1) void linear_wide_kernel(
+    const float* __restrict__ x, const uint8_t* __restrict__ w, const float* __restrict__ w_scale,
+    const float* __restrict__ bias, float* __restrict__ y, int M, int N, int K, int tiles_m,
+    int tiles_n) {
+  using F = Wide<WT>;
+  constexpr int KB = F::KB;
+  constexpr int FBN = 256, NTH = 512;
+  constexpr int FWN = 64, FNT = 2;
+  constexpr int A_ST = BM * F::a_pitch * 2;
+  constexpr int STAGE = A_ST + FBN * F::pitch;
+  constexpr int XC = BM * KB / 4 / NTH;                 // 8 x chunks per thread
+  constexpr int WC = FBN * F::row_bytes / 16 / NTH;     // 4 (FP8) or 2 (E2M1) W chunks
+  constexpr int UNITS = XC + WC;
+  constexpr int STEPS = KB / 16;
+  static_assert(F::bits <= 8 && NTH % F::cpr == 0, "tile shape");
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * STAGE];
+
+  const int T = tiles_m * tiles_n;
+  int t = blockIdx.x;
+  if ((T & 7) == 0) t = (t & 7) * (T >> 3) + (t >> 3);
+  constexpr int GM = 4;
+  const int group = t / (GM * tiles_n);
+  const int first_m = group * GM;
+  const int gm = min(tiles_m - first_m, GM);
+  const int rem = t - group * GM * tiles_n;
+  const int m0 = (first_m + rem % gm) * BM;
+  const int n0 = (rem / gm) * FBN;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, half = lane >> 5;
+  const int wm = (wave & 1) * WM, wn = (wave >> 1) * FWN;
+
+  // Global loads are buffer loads through per-tile descriptors: a 32-bit
+  // per-lane byte offset in one VGPR, block and chunk offsets in SGPRs.
+  // x: 32 chunks (512 B) per row, 16 rows per pass of the workgroup;
+  // W: cpr chunks per row, NTH / cpr rows per pass.
+  const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(x + (size_t)m0 * K), (short)0, BM * K * 4, 0x00020000);
+  const uint32_t xlane = (uint32_t)((tid >> 5) * K + (tid & 31) * 4) * 4u;
+  const uint32_t xstep = 16u * (uint32_t)K * 4u;
+  const uint32_t w_row_bytes = (uint32_t)K * F::bits / 8;
+  const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(w + (size_t)n0 * w_row_bytes), (short)0, (int)(FBN * w_row_bytes),
+      0x00020000);
+  const uint32_t wlane = (uint32_t)(tid / F::cpr) * w_row_bytes + (uint32_t)(tid % F::cpr) * 16u;
+  const uint32_t wstep = (uint32_t)(NTH / F::cpr) * w_row_bytes;
+
+  // LDS: [A0 | A1 | B0 | B1].  Per-lane bases below; every other offset is a
+  // compile-time constant that fits a ds instruction's 16-bit offset field.
+  constexpr int B_ST = FBN * F::pitch;
+  constexpr int XDST_STEP = 16 * F::a_pitch * 2;
+  constexpr int WDST_STEP = (NTH / F::cpr) * F::pitch;
+  constexpr int A_ROWS32 = 32 * F::a_pitch * 2;
+  constexpr int B_ROWS32 = 32 * F::pitch;
+  const int xw = ((tid >> 5) * F::a_pitch + (tid & 31) * 4) * 2;
+  const int ww0 = 2 * A_ST + (tid / F::cpr) * F::pitch + (tid % F::cpr) * 16, ww1 = ww0 + B_ST;
+  const int ar = ((wm + (lane & 31)) * F::a_pitch + half * 8) * 2;
+  const int br0 = 2 * A_ST + (wn + (lane & 31)) * F::pitch + half * F::frag_bytes, br1 = br0 + B_ST;
+
+  struct Regs {
+    u32x4 x[XC];
+    u32x4 w[WC];
+  };
+  auto fetch = [&](Regs& r, int kb) {
+    const uint32_t xk = (uint32_t)kb * (KB * 4), wk = (uint32_t)kb * F::row_bytes;
+#pragma unroll
+    for (int i = 0; i < XC; ++i) r.x[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xlane, xk + i * xstep, 0);
+#pragma unroll
+    for (int i = 0; i < WC; ++i) r.w[i] = __builtin_amdgcn_raw_buffer_load_b128(wrs, wlane, wk + i * wstep, 0);
+  };
+  auto stage_units = [&](const Regs& r, const int BUF, int u0, int u1) {
+#pragma unroll
+    for (int u = 0; u < UNITS; ++u) {
+      if (u < u0 || u >= u1) continue;
+      if (u < XC) {
+        uint32_t p0 = f32x2_to_bf16(r.x[u][0], r.x[u][1]);
+        uint32_t p1 = f32x2_to_bf16(r.x[u][2], r.x[u][3]);
+        *reinterpret_cast<u32x2*>(lds + xw + BUF * A_ST + u * XDST_STEP) = u32x2{p0, p1};
+      } else {
+        const int i = u - XC;
+        uint8_t* d = lds + (BUF ? ww1 : ww0) + i * WDST_STEP;
+        if constexpr (F::pitch % 8 == 0) {
+          *reinterpret_cast<u32x2*>(d) = u32x2{r.w[i][0], r.w[i][1]};
+          *reinterpret_cast<u32x2*>(d + 8) = u32x2{r.w[i][2], r.w[i][3]};
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) *reinterpret_cast<uint32_t*>(d + 4 * q) = r.w[i][q];
+        }
+      }
+    }
+  };
+
+  f32x16 acc[MT][FNT];
+#pragma unroll
+  for (int a = 0; a < MT; ++a)
+#pragma unroll
+    for (int b = 0; b < FNT; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.0f;
+
+  const int kblocks = K / KB;
+  // Block kb in buffer BUF: fetch block kb+2 into `rf` (its block kb is in
+  // LDS already), multiply, and stage block kb+1 from `rs` into buffer BUF^1
+  // after MFMA steps 1..6.  Past the end the last block is fetched and staged
+  // again into the idle buffer, so the body has no branch.
+  auto body = [&](int kb, const int BUF, Regs& rf, const Regs& rs) {
+    const uint8_t* SA = lds + ar + BUF * A_ST;
+    const uint8_t* SB = lds + (BUF ? br1 : br0);
+    fetch(rf, min(kb + 2, kblocks - 1));
+    bf16x8 a[2][MT], b[2][FNT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) a[0][i] = *reinterpret_cast<const bf16x8*>(SA + i * A_ROWS32);
+#pragma unroll
+    for (int j = 0; j < FNT; ++j) b[0][j] = frag_to_bf16<WT>(SB + j * B_ROWS32);
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s) {
+      const int cur = s & 1, nxt = cur ^ 1;
+      if (s + 1 < STEPS) {
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+          a[nxt][i] = *reinterpret_cast<const bf16x8*>(SA + i * A_ROWS32 + (s + 1) * 32);
+#pragma unroll
+        for (int j = 0; j < FNT; ++j)
+          b[nxt][j] = frag_to_bf16<WT>(SB + j * B_ROWS32 + (s + 1) * 2 * F::frag_bytes);
+      }
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < FNT; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[cur][i], b[cur][j], acc[i][j], 0, 0, 0);
+      if (s >= 1 && s <= 6) stage_units(rs, BUF ^ 1, (s - 1) * UNITS / 6, s * UNITS / 6);
+    }
+    __syncthreads();
+  };
+
+  Regs r0, r1;
+  fetch(r0, 0);
+  fetch(r1, min(1, kblocks - 1));
+  stage_units(r0, 0, 0, UNITS);
+  __syncthreads();
+  for (int kb = 0; kb < kblocks; kb += 2) {
+    body(kb, 0, r0, r1);
+    if (kb + 1 < kblocks) body(kb + 1, 1, r1, r0);
+  }
+
+  const float s = w_scale ? *w_scale : 1.0f;
+#pragma unroll
+  for (int j = 0; j < FNT; ++j) {
+    const int col = n0 + wn + j * 32 + (lane & 31);
+    const float bv = bias ? bias[col] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+        __builtin_nontemporal_store(acc[i][j][r] * s + bv, &y[(size_t)row * N + col]);
+      }
+    }
+  }
+}
 
 template <int WT>
 int launch(const float* x, int64_t M, int64_t K, const void* w, const float* w_scale,
@@ -662,28 +658,36 @@ int launch(const float* x, int64_t M, int64_t K, const void* w, const float* w_s
   const int64_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
   const int64_t T = tiles_m * tiles_n;
   if (T > 0x7FFFFFFF || M > 0x7FFFFFFF || N > 0x7FFFFFFF || K > 0x7FFFFFFF) return NOVAQ_EINVAL;
+  const auto* wq = static_cast<const uint8_t*>(w);
+  const bool rows_whole = M % BM == 0 && K > 0;
+  if constexpr (dtype_bits(WT) <= 8) {
+    // tile byte sizes (BM * K * 4 for x) must fit the 31-bit buffer range
+    if (rows_whole && N % 256 == 0 && K % 128 == 0 && K <= (1 << 21)) {
+      hipLaunchKernelGGL((linear_wide_kernel<WT>), dim3((unsigned)(tiles_m * (N / 256))),
+                         dim3(512), 0, stream, x, wq, w_scale, bias, y, (int)M, (int)N, (int)K,
+                         (int)tiles_m, (int)(N / 256));
+      return check_launch();
+    }
+  }
   if constexpr (WT != F32) {
-    const bool whole = M % BM == 0 && N % kFBN == 0 && K % BK == 0 && K > 0;
-    if (whole) {
-      const int64_t ftn = N / kFBN;
-      if constexpr (kSD) {
-        hipLaunchKernelGGL((linear_sd_kernel<WT, kFBN, kOCC>), dim3((unsigned)(tiles_m * ftn)),
-                           dim3(THREADS), 0, stream, x, static_cast<const uint8_t*>(w), w_scale,
-                           bias, y, (int)M, (int)N, (int)K, (int)tiles_m, (int)ftn);
-      } else {
-        hipLaunchKernelGGL((linear_fast_kernel<WT, kFBN, kOCC, kPF, kWLM>),
-                           dim3((unsigned)(tiles_m * ftn)), dim3(THREADS), 0, stream, x,
-                           static_cast<const uint8_t*>(w), w_scale, bias, y, (int)M, (int)N,
-                           (int)K, (int)tiles_m, (int)ftn);
-      }
+    if (rows_whole && N % 256 == 0 && K % BK == 0) {
+      hipLaunchKernelGGL((linear_pipe_kernel<WT, 256, 8, 1, 3>),
+                         dim3((unsigned)(tiles_m * (N / 256))), dim3(512), 0, stream, x, wq,
+                         w_scale, bias, y, (int)M, (int)N, (int)K, (int)tiles_m, (int)(N / 256));
+      return check_launch();
+    }
+    if (rows_whole && N % 128 == 0 && K % BK == 0) {
+      hipLaunchKernelGGL((linear_pipe_kernel<WT, 128, 4, 2, 2>),
+                         dim3((unsigned)(tiles_m * (N / 128))), dim3(256), 0, stream, x, wq,
+                         w_scale, bias, y, (int)M, (int)N, (int)K, (int)tiles_m, (int)(N / 128));
       return check_launch();
     }
   }
   const int x_vec = (K % 4) == 0;
   const int w_vec = ((K * W<WT>::bits / 8) % 16) == 0 && (K * W<WT>::bits) % 8 == 0;
-  hipLaunchKernelGGL((linear_kernel<WT>), dim3((unsigned)T), dim3(THREADS), 0, stream, x,
-                     static_cast<const uint8_t*>(w), w_scale, bias, y, (int)M, (int)N, (int)K,
-                     (int)tiles_m, (int)tiles_n, x_vec, w_vec);
+  hipLaunchKernelGGL((linear_kernel<WT>), dim3((unsigned)T), dim3(THREADS), 0, stream, x, wq,
+                     w_scale, bias, y, (int)M, (int)N, (int)K, (int)tiles_m, (int)tiles_n, x_vec,
+                     w_vec);
   return check_launch();
 }
 

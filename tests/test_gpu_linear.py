@@ -57,10 +57,13 @@ def valid_codes(wdt):
 
 @pytest.mark.parametrize("wdt", ["e4m3", "e5m2", "e2m1"])
 @pytest.mark.parametrize("scale", [1.0, 0.0123])
-@pytest.mark.parametrize("K,N", [(256, 320), (256, 512)], ids=["edge-tiles", "whole-tiles"])
+@pytest.mark.parametrize("K,N", [(256, 320), (256, 512), (192, 512), (256, 384)],
+                         ids=["edge-tiles", "wide-k", "staged-256", "staged-128"])
 def test_identity_input_reproduces_dequantized_weights_exactly(wdt, scale, K, N):
     """x = I: y[i, j] = s * dec(W[j, i]) exactly, for every finite code.  The
-    whole-tiles shape runs the guard-free kernel, the other the edge kernel."""
+    shapes reach each kernel: guarded edge tiles (N % 128 != 0), the wide-K
+    kernel (N % 256 == 0, K % 128 == 0) and the staged-decode kernel at both
+    tile widths (K % 128 != 0; N % 256 != 0)."""
     rng = np.random.default_rng(1)
     vals = valid_codes(wdt)
     nib = vals[rng.integers(0, vals.size, size=N * K)]
@@ -69,11 +72,14 @@ def test_identity_input_reproduces_dequantized_weights_exactly(wdt, scale, K, N)
         codes = (nib[0::2] | (nib[1::2] << 4)).astype(np.uint8)
     else:
         codes = nib.astype(np.uint8)
-    x = np.eye(K, dtype=np.float32)
+    M = -(-K // 128) * 128  # whole 128-row tiles; rows past K are zero
+    x = np.zeros((M, K), dtype=np.float32)
+    x[:K] = np.eye(K, dtype=np.float32)
     y = run_linear(x, codes, wdt, scale, None, N, K)
     w = dequant(codes, wdt, N * K, scale).reshape(N, K)
     # exact values; a -0 weight legitimately sums to +0 (0*w + 1*(-0) = +0)
-    assert np.array_equal(y, np.ascontiguousarray(w.T))
+    assert np.array_equal(y[:K], np.ascontiguousarray(w.T))
+    assert not np.any(y[K:])
 
 
 def test_golden_fixture(golden):
@@ -105,9 +111,12 @@ def test_ragged_shapes_vs_oracle(wdt, M, N, K, with_bias):
 
 
 @pytest.mark.parametrize("wdt", ["e4m3", "e5m2", "e2m1", "bf16", "f16"])
-@pytest.mark.parametrize("M,N,K", [(128, 256, 64), (256, 512, 128), (384, 768, 320)])
+@pytest.mark.parametrize("M,N,K", [(128, 256, 64), (256, 512, 128), (384, 768, 320),
+                                   (256, 384, 192), (128, 256, 1024)])
 def test_whole_tile_shapes_vs_oracle(wdt, M, N, K):
-    """Shapes that take the guard-free kernel (M % 128, N % 256, K % 64 == 0)."""
+    """Shapes that take the guard-free kernels (M % 128, N % 128, K % 64 == 0):
+    wide-K for FP8/FP4 when N % 256 and K % 128 are 0, staged-decode at tile
+    width 256 or 128 otherwise and for 16-bit weights."""
     rng = np.random.default_rng(M + N + K)
     x = rng.standard_normal((M, K)).astype(np.float32)
     w = (rng.standard_normal((N, K)) * np.sqrt(2.0 / K)).astype(np.float32)
