@@ -164,13 +164,75 @@ def bench_linear(dev, iters: int = 20, warmup: int = 5):
     ms = e0.elapsed_time(e1) / iters
     flops = 2.0 * M * N * K
     tflops = flops / (ms * 1e-3) / 1e12
+    # context: the vendor bf16 GEMM (torch -> hipBLASLt) on the same shape with
+    # bf16 operands already in HBM (no fp32 x conversion, no W decode)
+    xb, wb = x.to(torch.bfloat16), w.to(torch.bfloat16).contiguous()
+    for _ in range(warmup):
+        torch.nn.functional.linear(xb, wb)
+    torch.cuda.synchronize(dev)
+    e0.record()
+    for _ in range(iters):
+        torch.nn.functional.linear(xb, wb)
+    e1.record()
+    torch.cuda.synchronize(dev)
+    vms = e0.elapsed_time(e1) / iters
     return {"metric": "FP8-weight Linear TFLOP/s at 4096^2", "value": round(tflops, 1),
             "unit": "TFLOP/s", "ms": round(ms, 4),
+            "vendor_bf16_gemm": {"what": "torch.nn.functional.linear, bf16 x and W in HBM",
+                                 "ms": round(vms, 4),
+                                 "TFLOP/s": round(flops / (vms * 1e-3) / 1e12, 1)},
             "config": {"workload": "BASELINE config [4]", "M": M, "K": K, "N": N,
                        "w_dtype": "e4m3", "mfma": "bf16"},
             "roofline": {"bound": "mfma", "achieved": round(tflops, 1),
                          "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "traffic": None}}
+
+
+def bench_fp4(dev, n: int = 1 << 26, iters: int = 20, warmup: int = 3):
+    """Config [3]: fp32 -> E2M1 pack and E2M1 -> fp32 unpack of 2^26 N(0,1)
+    elements with the per-tensor scale s = amax / 6 (4.5 algorithmic bytes per
+    element each way).  The 256 MiB input is at the MALL's size, so a 512 MiB
+    write evicts it before every timed launch."""
+    import torch
+
+    from novann_amd import _lib
+    lib = _lib.load()
+    g = torch.Generator(device=dev)
+    g.manual_seed(3)
+    x = torch.randn(n, generator=g, device=dev, dtype=torch.float32)
+    packed = torch.empty((n + 1) // 2, dtype=torch.uint8, device=dev)
+    y = torch.empty_like(x)
+    amax_scale = torch.empty(2, dtype=torch.float32, device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    _lib.check(lib.novaq_amax(x.data_ptr(), 0, n, amax_scale.data_ptr(), stream), "amax")
+    s_ptr = amax_scale.data_ptr() + 4
+    _lib.check(lib.novaq_scale_from_amax(amax_scale.data_ptr(), 5, s_ptr, stream), "scale")
+    ops = {
+        "pack f32->e2m1": lambda: _lib.check(
+            lib.novaq_pack_fp4(x.data_ptr(), n, s_ptr, packed.data_ptr(), stream), "pack"),
+        "unpack e2m1->f32": lambda: _lib.check(
+            lib.novaq_unpack_fp4(packed.data_ptr(), n, s_ptr, y.data_ptr(), stream), "unpack"),
+    }
+    flush = torch.empty(1 << 27, dtype=torch.float32, device=dev)
+    out = []
+    for name, fn in ops.items():
+        for _ in range(warmup):
+            fn()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(iters)]
+        torch.cuda.synchronize(dev)
+        for e0, e1 in ev:
+            flush.zero_()
+            e0.record()
+            fn()
+            e1.record()
+        torch.cuda.synchronize(dev)
+        ms = sum(e0.elapsed_time(e1) for e0, e1 in ev) / iters
+        gbs = 4.5 * n / (ms * 1e-3) / 1e9
+        out.append({"op": name, "ms": round(ms, 4), "GB/s": round(gbs, 1),
+                    "frac": round(gbs / HBM_PEAK_GBS, 4)})
+    return {"workload": "BASELINE config [3]", "elements": n, "bytes_per_element": 4.5,
+            "kernels": out}
 
 
 def bench_conv(dev, iters: int = 20, warmup: int = 5):
@@ -266,6 +328,7 @@ def main() -> int:
                     help="also run one fp32->fp32 copy of the sweep input (known bytes), "
                          "the reference dispatch for scaling rocprofv3 FETCH_SIZE/WRITE_SIZE")
     ap.add_argument("--no-conv", action="store_true")
+    ap.add_argument("--no-fp4", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -294,6 +357,8 @@ def main() -> int:
     log(f"linear: {lin}")
     conv = None if args.no_conv else bench_conv(dev)
     log(f"conv2d: {conv}")
+    fp4 = None if args.no_fp4 else bench_fp4(dev)
+    log(f"fp4: {fp4}")
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_sample)
     log(f"cpu baseline: {cpu}")
     out = {
@@ -312,6 +377,7 @@ def main() -> int:
         "kernels": per_op,
         "linear": lin,
         "conv2d": conv,
+        "fp4": fp4,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

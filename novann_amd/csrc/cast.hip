@@ -2,8 +2,8 @@
 //
 // Layout: each thread moves UNITS_PER_THREAD "units"; a unit is EPL
 // consecutive elements, sized so that the wider side of the cast is one
-// 16-byte access per lane (two for fp32 <-> fp4) and the narrower side at
-// least 4 bytes.  Unit u of a block sits at (block * UNITS_PER_THREAD + j) *
+// 16-byte access per lane (the narrower side is 2 to 8 bytes: fp32 <-> fp4
+// moves 16 bytes against 2).  Unit u of a block sits at (block * UNITS_PER_THREAD + j) *
 // blockDim + tid, so every load and store instruction of a wave covers one
 // contiguous span (fully coalesced).  All loads of a thread are issued before
 // any conversion, to keep several 16-byte requests in flight per lane.  The
@@ -22,11 +22,11 @@ constexpr int kUnitsPerThread = 4;
 template <int ST, int DT>
 struct CastShape {
   static constexpr int bmax = dtype_bits(ST) > dtype_bits(DT) ? dtype_bits(ST) : dtype_bits(DT);
-  static constexpr int bmin = dtype_bits(ST) < dtype_bits(DT) ? dtype_bits(ST) : dtype_bits(DT);
-  static constexpr int a = 128 / bmax, b = 32 / bmin;
-  static constexpr int epl = a > b ? a : b;           // elements per unit
-  static constexpr int src_words = epl * dtype_bits(ST) / 32;  // 32-bit words per unit
-  static constexpr int dst_words = epl * dtype_bits(DT) / 32;
+  static constexpr int epl = 128 / bmax;               // elements per unit
+  static constexpr int src_bits = epl * dtype_bits(ST);  // bits per unit, 16 .. 128
+  static constexpr int dst_bits = epl * dtype_bits(DT);
+  static constexpr int src_words = (src_bits + 31) / 32;  // 32-bit words holding a unit
+  static constexpr int dst_words = (dst_bits + 31) / 32;
 };
 
 template <int N>
@@ -53,10 +53,14 @@ __device__ __forceinline__ void put_elem(Words<N>& v, int i, uint32_t c) {
   else v.w[i / per] |= (c & mask) << ((i % per) * BITS);
 }
 
-template <int N>
-__device__ __forceinline__ Words<N> load_words(const uint32_t* __restrict__ p) {
+// One unit of BITS bits (16 .. 128) at byte address p.
+template <int BITS, int N = (BITS + 31) / 32>
+__device__ __forceinline__ Words<N> load_words(const uint8_t* __restrict__ bp) {
   Words<N> v;
-  if constexpr (N % 4 == 0) {
+  const uint32_t* p = reinterpret_cast<const uint32_t*>(bp);
+  if constexpr (BITS == 16) {
+    v.w[0] = __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(bp));
+  } else if constexpr (N % 4 == 0) {
 #pragma unroll
     for (int k = 0; k < N / 4; ++k) {
       u32x4 q = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p) + k);
@@ -72,9 +76,12 @@ __device__ __forceinline__ Words<N> load_words(const uint32_t* __restrict__ p) {
   return v;
 }
 
-template <int N>
-__device__ __forceinline__ void store_words(uint32_t* __restrict__ p, const Words<N>& v) {
-  if constexpr (N % 4 == 0) {
+template <int BITS, int N = (BITS + 31) / 32>
+__device__ __forceinline__ void store_words(uint8_t* __restrict__ bp, const Words<N>& v) {
+  uint32_t* p = reinterpret_cast<uint32_t*>(bp);
+  if constexpr (BITS == 16) {
+    __builtin_nontemporal_store((uint16_t)v.w[0], reinterpret_cast<uint16_t*>(bp));
+  } else if constexpr (N % 4 == 0) {
 #pragma unroll
     for (int k = 0; k < N / 4; ++k) {
       u32x4 q = {v.w[4 * k], v.w[4 * k + 1], v.w[4 * k + 2], v.w[4 * k + 3]};
@@ -123,14 +130,12 @@ __global__ __launch_bounds__(kCastThreads) void cast_kernel(
   }
   const int64_t units = n / EPL;
   const int64_t base = (int64_t)blockIdx.x * kUnitsPerThread * kCastThreads + threadIdx.x;
-  const uint32_t* s32 = reinterpret_cast<const uint32_t*>(src);
-  uint32_t* d32 = reinterpret_cast<uint32_t*>(dst);
 
   Words<Sh::src_words> in[kUnitsPerThread];
 #pragma unroll
   for (int j = 0; j < kUnitsPerThread; ++j) {
     int64_t u = base + (int64_t)j * kCastThreads;
-    if (u < units) in[j] = load_words<Sh::src_words>(s32 + u * Sh::src_words);
+    if (u < units) in[j] = load_words<Sh::src_bits>(src + u * (Sh::src_bits / 8));
   }
 #pragma unroll
   for (int j = 0; j < kUnitsPerThread; ++j) {
@@ -142,7 +147,7 @@ __global__ __launch_bounds__(kCastThreads) void cast_kernel(
         uint32_t c = get_elem<dtype_bits(ST)>(in[j], i);
         put_elem<dtype_bits(DT)>(out, i, convert<ST, DT, SCALED>(c, s, inv_s));
       }
-      store_words<Sh::dst_words>(d32 + u * Sh::dst_words, out);
+      store_words<Sh::dst_bits>(dst + u * (Sh::dst_bits / 8), out);
     }
   }
 

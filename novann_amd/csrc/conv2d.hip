@@ -375,9 +375,322 @@ __global__ __launch_bounds__(THREADS, CONV_OCC) void conv2d_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Band kernel (C <= 64 input channels, at most 256 output pixels per band).
+//
+// A workgroup owns one band of R whole output rows of one image and up to 64
+// output channels, so its output is R*OW consecutive floats of each channel
+// plane.  GEMM orientation: M = the band's pixels in 16-pixel tiles, N = output
+// channels in 16-channel tiles, K = (kh, kw, c) in 8-channel groups, on
+// v_mfma_f32_16x16x32_bf16.  With pixels as rows, a lane's four accumulators
+// are four consecutive pixels of one channel: one 16-byte store each.
+//   - input rows of the band are staged in LDS channel-last in bf16 (RNE);
+//     whole 4-column groups of the interior come in as 16-byte loads of 8
+//     channels and are transposed in registers, the padding columns are
+//     resolved element-wise with numpy.pad's index rules;
+//   - the weights of the workgroup's output channels are regrouped from
+//     (co, c, kh, kw) order into (co, [kh, kw, 8 channels]) groups in LDS,
+//     FP8 / FP4 codes kept packed and decoded per MFMA fragment (exact);
+//   - one barrier before staging the input, one before the MFMA loop.
+
+struct BandGeom {
+  int N, C, H, W, C_out, KH, KW, sh, sw, ph, pw, pad_mode, OH, OW;
+  int c8;        // 8-channel groups (C padded to a multiple of 8)
+  int cstride;   // bf16 per staged pixel
+  int taps;      // KH * KW
+  int groups;    // taps * c8 K groups of 8
+  int gpr;       // groups rounded up to whole MFMA K steps (4 groups)
+  int wrow;      // bytes per weight row in LDS
+  int R;         // output rows per band
+  int bands;     // bands per image
+  int rows_in;   // staged input rows per band
+  int wp;        // staged input columns
+  int nborder;   // staged columns outside [0, W) (element-wise path)
+  int vec;       // interior columns staged with 16-byte loads (W % 4 == 0)
+  int raw_ok;    // packed weights copied to LDS before regrouping
+  int x_off;     // LDS byte offset of the staged input
+};
+
+template <int WT>
+__global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
+    const float* __restrict__ x, const uint8_t* __restrict__ w, const float* __restrict__ w_scale,
+    const float* __restrict__ bias, float* __restrict__ y, BandGeom g) {
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  constexpr int GB = group_bytes<WT>();
+  uint8_t* wl = lds;                                           // [64][g.wrow]
+  int* ktab = reinterpret_cast<int*>(lds + CO_TILE * g.wrow);  // [g.gpr]
+  uint16_t* xl = reinterpret_cast<uint16_t*>(lds + g.x_off);   // [rows_in][wp][cstride]
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lr = lane & 15, lg = lane >> 4;
+  const int band = blockIdx.x % g.bands, n = blockIdx.x / g.bands;
+  const int oh0 = band * g.R;
+  const int P = min(g.R, g.OH - oh0) * g.OW;  // output pixels of this band
+  const int co0 = blockIdx.y * CO_TILE;
+  const int ih0 = oh0 * g.sh - g.ph;
+
+  // --- weights: (co, c, kh, kw) -> [co][K group] ---------------------------
+  const int row_elems = g.C * g.taps;
+  const uint8_t* src = w;
+  int cofs = 0;
+  if (g.raw_ok) {
+    // packed codes of rows co0 .. co0+63 (the first element is even, so the
+    // E2M1 byte boundary matches), coalesced dwords then bytes
+    const int rows = min(CO_TILE, g.C_out - co0);
+    const int64_t first = (int64_t)co0 * row_elems;
+    const int nbytes = (int)(((int64_t)rows * row_elems * dtype_bits(WT) + 7) / 8);
+    const uint8_t* gsrc = w + first * dtype_bits(WT) / 8;
+    uint8_t* raw = reinterpret_cast<uint8_t*>(xl);
+    const int nwords = (reinterpret_cast<uintptr_t>(gsrc) & 3) ? 0 : nbytes >> 2;
+    for (int i = tid; i < nwords; i += THREADS)
+      reinterpret_cast<uint32_t*>(raw)[i] = reinterpret_cast<const uint32_t*>(gsrc)[i];
+    for (int i = (nwords << 2) + tid; i < nbytes; i += THREADS) raw[i] = gsrc[i];
+    __syncthreads();
+    src = raw;
+    cofs = co0;
+  }
+  {
+    // four threads per output channel row, each taking every fourth group
+    const int co = tid >> 2;
+    const bool live = co0 + co < g.C_out;
+    int tap = 0, q = tid & 3;
+    while (q >= g.c8) { q -= g.c8; ++tap; }
+    for (int gi = tid & 3; gi < g.gpr; gi += 4) {
+      uint32_t p[4] = {0u, 0u, 0u, 0u};
+      if (live && gi < g.groups) {
+        const int cbase = q * 8;
+        const int64_t e0 = ((int64_t)(co0 + co - cofs) * g.C + cbase) * g.taps + tap;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          if (cbase + j >= g.C) break;
+          if constexpr (GB == 4) {
+            p[0] |= weight_code<WT>(src, e0 + j * g.taps) << (4 * j);
+          } else if constexpr (GB == 8) {
+            p[j >> 2] |= weight_code<WT>(src, e0 + j * g.taps) << (8 * (j & 3));
+          } else {
+            p[j >> 1] |= (uint32_t)weight_bf16<WT>(src, e0 + j * g.taps) << ((j & 1) * 16);
+          }
+        }
+      }
+      uint8_t* d = wl + co * g.wrow + gi * GB;
+      if constexpr (GB == 4) *reinterpret_cast<uint32_t*>(d) = p[0];
+      else if constexpr (GB == 8) *reinterpret_cast<u32x2v*>(d) = u32x2v{p[0], p[1]};
+      else *reinterpret_cast<uint4*>(d) = make_uint4(p[0], p[1], p[2], p[3]);
+      // advance (tap, q) by four groups
+      q += 4;
+      while (q >= g.c8) { q -= g.c8; ++tap; }
+    }
+  }
+  // window offset (staged elements) of each K group; -1 past the window
+  for (int gi = tid; gi < g.gpr; gi += THREADS) {
+    int koff = -1;
+    if (gi < g.groups) {
+      const int tap = gi / g.c8, q = gi - tap * g.c8;
+      const int kh = tap / g.KW, kw = tap - kh * g.KW;
+      koff = (kh * g.wp + kw) * g.cstride + q * 8;
+    }
+    ktab[gi] = koff;
+  }
+  __syncthreads();  // weights regrouped; the raw copy region is free
+
+  // --- input band: rows [ih0, ih0 + rows_in), staged columns [0, wp) --------
+  const int64_t HW = (int64_t)g.H * g.W;
+  const float* xn = x + (int64_t)n * g.C * HW;
+  if (g.vec) {
+    const int W4 = g.W >> 2;
+    const int items = g.rows_in * W4 * g.c8;
+    for (int it = tid; it < items; it += THREADS) {
+      const int q = it % g.c8, rest = it / g.c8;
+      const int cg = rest % W4, r = rest / W4;
+      const int col0 = cg * 4 + g.pw;  // staged column of input column 4*cg
+      if (col0 >= g.wp) continue;
+      const int hi = pad_index(ih0 + r, g.H, g.pad_mode);
+      f32x4 v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int c = q * 8 + j;
+        v[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        if (hi >= 0 && c < g.C)
+          v[j] = *reinterpret_cast<const f32x4*>(xn + c * HW + (int64_t)hi * g.W + cg * 4);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int col = col0 + i;
+        if (col >= g.wp) break;
+        uint32_t pk[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          f32x2 f = {v[2 * j][i], v[2 * j + 1][i]};
+          pk[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));
+        }
+        *reinterpret_cast<uint4*>(&xl[(r * g.wp + col) * g.cstride + q * 8]) =
+            make_uint4(pk[0], pk[1], pk[2], pk[3]);
+      }
+    }
+  }
+  {
+    // element-wise columns: the padding columns, or every column when the
+    // rows are not 16-byte aligned
+    const int ncols = g.vec ? g.nborder : g.wp;
+    const int left = min(g.pw, g.wp);
+    const int items = g.rows_in * ncols * g.c8;
+    for (int it = tid; it < items; it += THREADS) {
+      const int q = it % g.c8, rest = it / g.c8;
+      const int bi = rest % ncols, r = rest / ncols;
+      const int col = !g.vec ? bi : (bi < left ? bi : g.pw + g.W + (bi - left));
+      const int hi = pad_index(ih0 + r, g.H, g.pad_mode);
+      const int wi = pad_index(col - g.pw, g.W, g.pad_mode);
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int c = q * 8 + j;
+        v[j] = (hi >= 0 && wi >= 0 && c < g.C) ? xn[c * HW + (int64_t)hi * g.W + wi] : 0.0f;
+      }
+      uint32_t pk[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        f32x2 f = {v[2 * j], v[2 * j + 1]};
+        pk[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));
+      }
+      *reinterpret_cast<uint4*>(&xl[(r * g.wp + col) * g.cstride + q * 8]) =
+          make_uint4(pk[0], pk[1], pk[2], pk[3]);
+    }
+  }
+  __syncthreads();
+
+  // --- MFMA: wave w takes M tiles w, w+4, w+8, w+12 -----------------------
+  const int mtiles = (P + 15) >> 4;
+  const int my_mt = wave < mtiles ? (mtiles - wave + 3) >> 2 : 0;
+  const int nt_live = min(4, (min(CO_TILE, g.C_out - co0) + 15) >> 4);
+  int pb[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    int p = (wave + 4 * m) * 16 + lr;
+    if (p >= P) p = 0;  // a valid address; the product is never stored
+    const int ohr = p / g.OW, ow = p - ohr * g.OW;
+    pb[m] = ((ohr * g.sh) * g.wp + ow * g.sw) * g.cstride;
+  }
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc[m][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  const uint8_t* wfrag = wl + lr * g.wrow + lg * GB;
+  const int steps = g.gpr >> 2;
+  const bf16x8 zero8 = __builtin_bit_cast(bf16x8, make_uint4(0u, 0u, 0u, 0u));
+  for (int st = 0; st < steps; ++st) {
+    const int koff = ktab[st * 4 + lg];
+    bf16x8 bf[4], af[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      if (t < nt_live) bf[t] = weight_frag<WT>(wfrag + t * 16 * g.wrow + st * 4 * GB);
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+      if (m < my_mt) af[m] = koff >= 0 ? *reinterpret_cast<const bf16x8*>(&xl[pb[m] + koff]) : zero8;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      if (m >= my_mt) break;
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        if (t < nt_live) acc[m][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[m], bf[t], acc[m][t], 0, 0, 0);
+    }
+  }
+
+  // --- epilogue: lane holds pixels 4*lg .. 4*lg+3 of channel lr per tile ---
+  const float s = w_scale ? *w_scale : 1.0f;
+  const int64_t npix = (int64_t)g.OH * g.OW;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    if (m >= my_mt) break;
+    const int p = (wave + 4 * m) * 16 + 4 * lg;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int co = co0 + t * 16 + lr;
+      if (t >= nt_live || co >= g.C_out) continue;
+      const float bv = bias ? bias[co] : 0.0f;
+      float* dst = y + ((int64_t)n * g.C_out + co) * npix + (int64_t)oh0 * g.OW + p;
+      const f32x4 v = acc[m][t] * s + bv;
+      // plain stores: the 64-byte pieces of a line written by neighbouring
+      // lanes and waves merge in L2 before they reach HBM
+      if (p + 3 < P && (reinterpret_cast<uintptr_t>(dst) & 15) == 0) {
+        *reinterpret_cast<f32x4*>(dst) = v;
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (p + i < P) dst[i] = v[i];
+      }
+    }
+  }
+}
+
+// Band geometry for this convolution, or false when the band kernel does not
+// apply (too many channels, rows too wide, or LDS too small).
+template <int WT>
+bool band_geometry(const ConvGeom& cg, BandGeom& b, size_t& lds) {
+  if (cg.C > MAX_CB || cg.OW > 256) return false;
+  b = BandGeom{};
+  b.N = cg.N; b.C = cg.C; b.H = cg.H; b.W = cg.W; b.C_out = cg.C_out; b.KH = cg.KH;
+  b.KW = cg.KW; b.sh = cg.sh; b.sw = cg.sw; b.ph = cg.ph; b.pw = cg.pw; b.pad_mode = cg.pad_mode;
+  b.OH = cg.OH; b.OW = cg.OW;
+  b.c8 = (cg.C + 7) / 8;
+  // pixel stride in LDS of 8 mod 16 bf16 (4 mod 8 banks): the 16 pixels of a
+  // fragment read fall in distinct banks
+  b.cstride = (b.c8 % 2 == 0) ? b.c8 * 8 + 8 : b.c8 * 8;
+  b.taps = cg.KH * cg.KW;
+  b.groups = b.taps * b.c8;
+  b.gpr = (b.groups + 3) / 4 * 4;
+  // bands of whole output rows, at most 256 pixels, balanced across the image
+  const int64_t npix = (int64_t)cg.OH * cg.OW;
+  const int nb = (int)((npix + 255) / 256);
+  b.R = (cg.OH + nb - 1) / nb;
+  while ((int64_t)b.R * cg.OW > 256) --b.R;
+  if (b.R < 1) return false;
+  b.bands = (cg.OH + b.R - 1) / b.R;
+  b.rows_in = (b.R - 1) * cg.sh + cg.KH;
+  b.wp = (cg.OW - 1) * cg.sw + cg.KW;
+  b.vec = (cg.W % 4) == 0;
+  b.nborder = min(cg.pw, b.wp) + max(0, b.wp - cg.pw - cg.W);
+  // weight row: gpr groups of GB bytes, stride padded so the 16 rows a
+  // fragment read touches fall in distinct banks
+  constexpr int GB = group_bytes<WT>();
+  int stride_dw = b.gpr * GB / 4;
+  while ((GB == 4 && stride_dw % 2 != 1) || (GB == 8 && stride_dw % 4 != 2) ||
+         (GB == 16 && stride_dw % 8 != 4))
+    stride_dw += GB / 4;
+  b.wrow = stride_dw * 4;
+  b.x_off = (CO_TILE * b.wrow + 4 * b.gpr + 15) / 16 * 16;
+  const size_t xl_bytes = (size_t)b.rows_in * b.wp * b.cstride * 2;
+  const size_t raw_bytes = ((size_t)CO_TILE * cg.C * b.taps * dtype_bits(WT) + 7) / 8;
+  b.raw_ok = dtype_bits(WT) <= 8 && raw_bytes <= xl_bytes;
+  lds = b.x_off + xl_bytes;
+  return lds <= 80 * 1024;
+}
+
 template <int WT>
 int launch(const float* x, const void* w, const float* w_scale, const float* bias, float* y,
            ConvGeom g, hipStream_t stream) {
+  {
+    BandGeom b;
+    size_t lds = 0;
+    if (band_geometry<WT>(g, b, lds)) {
+      auto kern = conv2d_band_kernel<WT>;
+      static size_t lds_enabled = 64 * 1024;
+      if (lds > lds_enabled) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           (int)LDS_LIMIT);
+        if (e != hipSuccess) return hip_fail(e);
+        lds_enabled = LDS_LIMIT;
+      }
+      const int64_t blocks = (int64_t)g.N * b.bands;
+      const int64_t co_blocks = (g.C_out + CO_TILE - 1) / CO_TILE;
+      if (blocks > 0x7FFFFFFF) return NOVAQ_EINVAL;
+      hipLaunchKernelGGL(kern, dim3((unsigned)blocks, (unsigned)co_blocks), dim3(THREADS), lds,
+                         stream, x, static_cast<const uint8_t*>(w), w_scale, bias, y, b);
+      return check_launch();
+    }
+  }
   // staged rows for a run of PIX_TILE pixels: it spans at most
   // ceil((PIX_TILE - 1) / OW) + 1 output rows
   const int out_rows = (PIX_TILE - 1) / g.OW + 2;
