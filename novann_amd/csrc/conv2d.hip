@@ -26,6 +26,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
+
 #include "novaq_convert.h"
 #include "novaq_internal.h"
 
@@ -378,20 +380,24 @@ __global__ __launch_bounds__(THREADS, CONV_OCC) void conv2d_kernel(
 // ---------------------------------------------------------------------------
 // Band kernel (C <= 64 input channels, at most 256 output pixels per band).
 //
-// A workgroup owns one band of R whole output rows of one image and up to 64
-// output channels, so its output is R*OW consecutive floats of each channel
-// plane.  GEMM orientation: M = the band's pixels in 16-pixel tiles, N = output
-// channels in 16-channel tiles, K = (kh, kw, c) in 8-channel groups, on
-// v_mfma_f32_16x16x32_bf16.  With pixels as rows, a lane's four accumulators
-// are four consecutive pixels of one channel: one 16-byte store each.
-//   - input rows of the band are staged in LDS channel-last in bf16 (RNE);
-//     whole 4-column groups of the interior come in as 16-byte loads of 8
-//     channels and are transposed in registers, the padding columns are
-//     resolved element-wise with numpy.pad's index rules;
-//   - the weights of the workgroup's output channels are regrouped from
+// A workgroup owns up to 64 output channels of one band of R whole output
+// rows of one image; the band's output is R*OW consecutive floats of each
+// channel plane.  GEMM orientation per band: M = the band's pixels in
+// 16-pixel tiles, N = output channels in 16-channel tiles, K = (kh, kw, c) in
+// 8-channel groups, on v_mfma_f32_16x16x32_bf16.  With pixels as rows, a
+// lane's four accumulators are four consecutive pixels of one channel: one
+// 16-byte store.
+//   - the weights of the workgroup's output channels are regrouped once from
 //     (co, c, kh, kw) order into (co, [kh, kw, 8 channels]) groups in LDS,
 //     FP8 / FP4 codes kept packed and decoded per MFMA fragment (exact);
-//   - one barrier before staging the input, one before the MFMA loop.
+//   - the band's input rows are staged in LDS channel-last in bf16 (RNE);
+//     whole 4-column groups of the interior come in as 16-byte loads of 8
+//     channels, issued into registers before the weights are regrouped (when
+//     there is at most one such item per thread) so their latency overlaps
+//     that work, and are transposed in registers; padding columns are
+//     resolved element-wise with numpy.pad's index rules;
+//   - many small workgroups per CU: one's loads overlap another's MFMAs and
+//     stores.
 
 struct BandGeom {
   int N, C, H, W, C_out, KH, KW, sh, sw, ph, pw, pad_mode, OH, OW;
@@ -407,28 +413,60 @@ struct BandGeom {
   int wp;        // staged input columns
   int nborder;   // staged columns outside [0, W) (element-wise path)
   int vec;       // interior columns staged with 16-byte loads (W % 4 == 0)
+  int vitems;    // 16-byte-load items per band (rows_in * W/4 * c8)
   int raw_ok;    // packed weights copied to LDS before regrouping
   int x_off;     // LDS byte offset of the staged input
+  int x_bytes;   // bytes of the staged input
 };
 
-template <int WT>
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// 16-byte-load items of one band held in registers: IPT items per thread,
+// each 8 channels x 4 columns.
+template <int IPT>
+struct BandRegs {
+  f32x4 v[IPT > 0 ? IPT : 1][8];
+};
+
+// K9: 3x3 window, C a multiple of 8 and packed FP8 / FP4 codes copied to LDS:
+// the 8 channels x 9 taps of one (co, channel group) are 72 consecutive codes
+// (aligned 32-bit words), regrouped with constant shifts.
+template <int WT, int IPT, bool K9>
 __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
     const float* __restrict__ x, const uint8_t* __restrict__ w, const float* __restrict__ w_scale,
     const float* __restrict__ bias, float* __restrict__ y, BandGeom g) {
-  typedef float f32x4 __attribute__((ext_vector_type(4)));
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   constexpr int GB = group_bytes<WT>();
   uint8_t* wl = lds;                                           // [64][g.wrow]
   int* ktab = reinterpret_cast<int*>(lds + CO_TILE * g.wrow);  // [g.gpr]
-  uint16_t* xl = reinterpret_cast<uint16_t*>(lds + g.x_off);   // [rows_in][wp][cstride]
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int lr = lane & 15, lg = lane >> 4;
   const int band = blockIdx.x % g.bands, n = blockIdx.x / g.bands;
-  const int oh0 = band * g.R;
-  const int P = min(g.R, g.OH - oh0) * g.OW;  // output pixels of this band
   const int co0 = blockIdx.y * CO_TILE;
-  const int ih0 = oh0 * g.sh - g.ph;
+  const int64_t HW = (int64_t)g.H * g.W;
+  const float* xn = x + (int64_t)n * g.C * HW;
+  const int W4 = g.W >> 2;
+
+  // 16-byte-load item `it` of band b: (row r, column group cg, channel group q)
+  auto vload = [&](int b, int it, f32x4* v) {
+    const int q = it % g.c8, rest = it / g.c8;
+    const int cg = rest % W4, r = rest / W4;
+    const int hi = pad_index(b * g.R * g.sh - g.ph + r, g.H, g.pad_mode);
+    const bool used = cg * 4 + g.pw < g.wp;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int c = q * 8 + j;
+      v[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      if (used && hi >= 0 && c < g.C)
+        v[j] = *reinterpret_cast<const f32x4*>(xn + c * HW + (int64_t)hi * g.W + cg * 4);
+    }
+  };
+  // the band's 16-byte loads go out first
+  BandRegs<IPT> r0;
+  if constexpr (IPT > 0) {
+    if (tid < g.vitems) vload(band, tid, r0.v[0]);
+  }
 
   // --- weights: (co, c, kh, kw) -> [co][K group] ---------------------------
   const int row_elems = g.C * g.taps;
@@ -436,12 +474,13 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
   int cofs = 0;
   if (g.raw_ok) {
     // packed codes of rows co0 .. co0+63 (the first element is even, so the
-    // E2M1 byte boundary matches), coalesced dwords then bytes
+    // E2M1 byte boundary matches), coalesced dwords then bytes, into the
+    // staged-input region
     const int rows = min(CO_TILE, g.C_out - co0);
     const int64_t first = (int64_t)co0 * row_elems;
     const int nbytes = (int)(((int64_t)rows * row_elems * dtype_bits(WT) + 7) / 8);
     const uint8_t* gsrc = w + first * dtype_bits(WT) / 8;
-    uint8_t* raw = reinterpret_cast<uint8_t*>(xl);
+    uint8_t* raw = lds + g.x_off;
     const int nwords = (reinterpret_cast<uintptr_t>(gsrc) & 3) ? 0 : nbytes >> 2;
     for (int i = tid; i < nwords; i += THREADS)
       reinterpret_cast<uint32_t*>(raw)[i] = reinterpret_cast<const uint32_t*>(gsrc)[i];
@@ -450,7 +489,52 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
     src = raw;
     cofs = co0;
   }
-  {
+  if constexpr (K9 && GB < 16) {
+    constexpr int BITS = dtype_bits(WT);
+    constexpr int NW = 72 * BITS / 32;  // words of one (co, q) run
+    for (int item = tid; item < CO_TILE * g.c8; item += THREADS) {
+      const int co = item / g.c8, q = item - co * g.c8;
+      uint32_t o[9][GB / 4];
+      if (co0 + co < g.C_out) {
+        const uint32_t* run = reinterpret_cast<const uint32_t*>(
+            src + (size_t)(co * g.C + q * 8) * 9 * BITS / 8);
+        uint32_t wv[NW];
+#pragma unroll
+        for (int i = 0; i < NW; ++i) wv[i] = run[i];
+#pragma unroll
+        for (int t = 0; t < 9; ++t) {
+#pragma unroll
+          for (int k = 0; k < GB / 4; ++k) o[t][k] = 0u;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            constexpr uint32_t mask = (1u << BITS) - 1u;
+            const int e = 9 * j + t;
+            const uint32_t code = (wv[e * BITS / 32] >> ((e * BITS) % 32)) & mask;
+            o[t][(j * BITS) / 32] |= code << ((j * BITS) % 32);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int t = 0; t < 9; ++t)
+#pragma unroll
+          for (int k = 0; k < GB / 4; ++k) o[t][k] = 0u;
+      }
+#pragma unroll
+      for (int t = 0; t < 9; ++t) {
+        uint8_t* d = wl + co * g.wrow + (t * g.c8 + q) * GB;
+        if constexpr (GB == 4) *reinterpret_cast<uint32_t*>(d) = o[t][0];
+        else *reinterpret_cast<u32x2v*>(d) = u32x2v{o[t][0], o[t][1]};
+      }
+    }
+    // zero groups past the window (K padding to whole MFMA steps)
+    const int pad = g.gpr - g.groups;
+    for (int item = tid; item < CO_TILE * pad; item += THREADS) {
+      const int co = item / pad, gi = g.groups + (item - co * pad);
+      uint8_t* d = wl + co * g.wrow + gi * GB;
+      if constexpr (GB == 4) *reinterpret_cast<uint32_t*>(d) = 0u;
+      else *reinterpret_cast<u32x2v*>(d) = u32x2v{0u, 0u};
+    }
+  } else {
     // four threads per output channel row, each taking every fourth group
     const int co = tid >> 2;
     const bool live = co0 + co < g.C_out;
@@ -494,47 +578,47 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
   }
   __syncthreads();  // weights regrouped; the raw copy region is free
 
-  // --- input band: rows [ih0, ih0 + rows_in), staged columns [0, wp) --------
-  const int64_t HW = (int64_t)g.H * g.W;
-  const float* xn = x + (int64_t)n * g.C * HW;
-  if (g.vec) {
-    const int W4 = g.W >> 2;
-    const int items = g.rows_in * W4 * g.c8;
-    for (int it = tid; it < items; it += THREADS) {
-      const int q = it % g.c8, rest = it / g.c8;
-      const int cg = rest % W4, r = rest / W4;
-      const int col0 = cg * 4 + g.pw;  // staged column of input column 4*cg
-      if (col0 >= g.wp) continue;
-      const int hi = pad_index(ih0 + r, g.H, g.pad_mode);
-      f32x4 v[8];
+  auto vstore = [&](uint16_t* xl, int it, const f32x4* v) {
+    const int q = it % g.c8, rest = it / g.c8;
+    const int cg = rest % W4, r = rest / W4;
+    const int col0 = cg * 4 + g.pw;  // staged column of input column 4*cg
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int c = q * 8 + j;
-        v[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        if (hi >= 0 && c < g.C)
-          v[j] = *reinterpret_cast<const f32x4*>(xn + c * HW + (int64_t)hi * g.W + cg * 4);
+    for (int i = 0; i < 4; ++i) {
+      const int col = col0 + i;
+      if (col >= g.wp) break;
+      uint32_t pk[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        f32x2 f = {v[2 * j][i], v[2 * j + 1][i]};
+        pk[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));
       }
+      *reinterpret_cast<uint4*>(&xl[(r * g.wp + col) * g.cstride + q * 8]) =
+          make_uint4(pk[0], pk[1], pk[2], pk[3]);
+    }
+  };
+  // stage band b into buffer xl (from the registers when IPT > 0)
+  auto stage = [&](const BandRegs<IPT>& rg, int b, uint16_t* xl) {
+    if (g.vec) {
+      if constexpr (IPT > 0) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int col = col0 + i;
-        if (col >= g.wp) break;
-        uint32_t pk[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          f32x2 f = {v[2 * j][i], v[2 * j + 1][i]};
-          pk[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));
+        for (int k = 0; k < IPT; ++k) {
+          const int it = tid + k * THREADS;
+          if (it < g.vitems) vstore(xl, it, rg.v[k]);
         }
-        *reinterpret_cast<uint4*>(&xl[(r * g.wp + col) * g.cstride + q * 8]) =
-            make_uint4(pk[0], pk[1], pk[2], pk[3]);
+      } else {
+        for (int it = tid; it < g.vitems; it += THREADS) {
+          f32x4 v[8];
+          vload(b, it, v);
+          vstore(xl, it, v);
+        }
       }
     }
-  }
-  {
     // element-wise columns: the padding columns, or every column when the
     // rows are not 16-byte aligned
     const int ncols = g.vec ? g.nborder : g.wp;
     const int left = min(g.pw, g.wp);
     const int items = g.rows_in * ncols * g.c8;
+    const int ih0 = b * g.R * g.sh - g.ph;
     for (int it = tid; it < items; it += THREADS) {
       const int q = it % g.c8, rest = it / g.c8;
       const int bi = rest % ncols, r = rest / ncols;
@@ -556,78 +640,97 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
       *reinterpret_cast<uint4*>(&xl[(r * g.wp + col) * g.cstride + q * 8]) =
           make_uint4(pk[0], pk[1], pk[2], pk[3]);
     }
-  }
-  __syncthreads();
+  };
 
-  // --- MFMA: wave w takes M tiles w, w+4, w+8, w+12 -----------------------
-  const int mtiles = (P + 15) >> 4;
-  const int my_mt = wave < mtiles ? (mtiles - wave + 3) >> 2 : 0;
+  const float s = w_scale ? *w_scale : 1.0f;
+  const int64_t npix = (int64_t)g.OH * g.OW;
   const int nt_live = min(4, (min(CO_TILE, g.C_out - co0) + 15) >> 4);
-  int pb[4];
-#pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    int p = (wave + 4 * m) * 16 + lr;
-    if (p >= P) p = 0;  // a valid address; the product is never stored
-    const int ohr = p / g.OW, ow = p - ohr * g.OW;
-    pb[m] = ((ohr * g.sh) * g.wp + ow * g.sw) * g.cstride;
-  }
-  f32x4 acc[4][4];
-#pragma unroll
-  for (int m = 0; m < 4; ++m)
-#pragma unroll
-    for (int t = 0; t < 4; ++t) acc[m][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   const uint8_t* wfrag = wl + lr * g.wrow + lg * GB;
   const int steps = g.gpr >> 2;
   const bf16x8 zero8 = __builtin_bit_cast(bf16x8, make_uint4(0u, 0u, 0u, 0u));
-  for (int st = 0; st < steps; ++st) {
-    const int koff = ktab[st * 4 + lg];
-    bf16x8 bf[4], af[4];
+
+  // MFMA and store of band b from buffer xl; wave w takes M tiles w, w+4, ...
+  auto compute = [&](int b, const uint16_t* xl) {
+    const int oh0 = b * g.R;
+    const int P = min(g.R, g.OH - oh0) * g.OW;
+    const int mtiles = (P + 15) >> 4;
+    const int my_mt = wave < mtiles ? (mtiles - wave + 3) >> 2 : 0;
+    int pb[4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
-      if (t < nt_live) bf[t] = weight_frag<WT>(wfrag + t * 16 * g.wrow + st * 4 * GB);
+    for (int m = 0; m < 4; ++m) {
+      int p = (wave + 4 * m) * 16 + lr;
+      if (p >= P) p = 0;  // a valid address; the product is never stored
+      const int ohr = p / g.OW, ow = p - ohr * g.OW;
+      pb[m] = ((ohr * g.sh) * g.wp + ow * g.sw) * g.cstride;
+    }
+    f32x4 acc[4][4];
 #pragma unroll
     for (int m = 0; m < 4; ++m)
-      if (m < my_mt) af[m] = koff >= 0 ? *reinterpret_cast<const bf16x8*>(&xl[pb[m] + koff]) : zero8;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) acc[m][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    // (the fragments are not double-buffered: the extra registers would cost
+    // a workgroup per CU, and other workgroups hide the LDS latency)
+    auto frags = [&](int st, bf16x8* af, bf16x8* bf) {
+      const int koff = ktab[st * 4 + lg];
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        if (t < nt_live) bf[t] = weight_frag<WT>(wfrag + t * 16 * g.wrow + st * 4 * GB);
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+        if (m < my_mt) af[m] = koff >= 0 ? *reinterpret_cast<const bf16x8*>(&xl[pb[m] + koff]) : zero8;
+    };
+    auto mma = [&](const bf16x8* af, const bf16x8* bf) {
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        if (m >= my_mt) break;
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          if (t < nt_live)
+            acc[m][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[m], bf[t], acc[m][t], 0, 0, 0);
+      }
+    };
+    for (int st = 0; st < steps; ++st) {
+      bf16x8 af[4], bf[4];
+      frags(st, af, bf);
+      mma(af, bf);
+    }
+    // lane holds pixels 4*lg .. 4*lg+3 of channel lr of each tile
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
       if (m >= my_mt) break;
+      const int p = (wave + 4 * m) * 16 + 4 * lg;
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
-        if (t < nt_live) acc[m][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[m], bf[t], acc[m][t], 0, 0, 0);
-    }
-  }
-
-  // --- epilogue: lane holds pixels 4*lg .. 4*lg+3 of channel lr per tile ---
-  const float s = w_scale ? *w_scale : 1.0f;
-  const int64_t npix = (int64_t)g.OH * g.OW;
+      for (int t = 0; t < 4; ++t) {
+        const int co = co0 + t * 16 + lr;
+        if (t >= nt_live || co >= g.C_out) continue;
+        const float bv = bias ? bias[co] : 0.0f;
+        float* dst = y + ((int64_t)n * g.C_out + co) * npix + (int64_t)oh0 * g.OW + p;
+        const f32x4 v = acc[m][t] * s + bv;
+        // plain stores: the 64-byte pieces of a line written by neighbouring
+        // lanes and waves merge in L2 before they reach HBM
+        if (p + 3 < P && (reinterpret_cast<uintptr_t>(dst) & 15) == 0) {
+          *reinterpret_cast<f32x4*>(dst) = v;
+        } else {
 #pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    if (m >= my_mt) break;
-    const int p = (wave + 4 * m) * 16 + 4 * lg;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int co = co0 + t * 16 + lr;
-      if (t >= nt_live || co >= g.C_out) continue;
-      const float bv = bias ? bias[co] : 0.0f;
-      float* dst = y + ((int64_t)n * g.C_out + co) * npix + (int64_t)oh0 * g.OW + p;
-      const f32x4 v = acc[m][t] * s + bv;
-      // plain stores: the 64-byte pieces of a line written by neighbouring
-      // lanes and waves merge in L2 before they reach HBM
-      if (p + 3 < P && (reinterpret_cast<uintptr_t>(dst) & 15) == 0) {
-        *reinterpret_cast<f32x4*>(dst) = v;
-      } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (p + i < P) dst[i] = v[i];
+          for (int i = 0; i < 4; ++i)
+            if (p + i < P) dst[i] = v[i];
+        }
       }
     }
-  }
+  };
+
+  uint16_t* xl = reinterpret_cast<uint16_t*>(lds + g.x_off);
+  stage(r0, band, xl);
+  __syncthreads();
+  compute(band, xl);
 }
 
 // Band geometry for this convolution, or false when the band kernel does not
-// apply (too many channels, rows too wide, or LDS too small).
+// apply (too many channels, rows too wide, or LDS too small).  *ipt is the
+// number of 16-byte-load items per thread held in registers (0: loaded while
+// staging).
 template <int WT>
-bool band_geometry(const ConvGeom& cg, BandGeom& b, size_t& lds) {
+bool band_geometry(const ConvGeom& cg, BandGeom& b, size_t& lds, int* ipt) {
   if (cg.C > MAX_CB || cg.OW > 256) return false;
   b = BandGeom{};
   b.N = cg.N; b.C = cg.C; b.H = cg.H; b.W = cg.W; b.C_out = cg.C_out; b.KH = cg.KH;
@@ -650,7 +753,9 @@ bool band_geometry(const ConvGeom& cg, BandGeom& b, size_t& lds) {
   b.rows_in = (b.R - 1) * cg.sh + cg.KH;
   b.wp = (cg.OW - 1) * cg.sw + cg.KW;
   b.vec = (cg.W % 4) == 0;
-  b.nborder = min(cg.pw, b.wp) + max(0, b.wp - cg.pw - cg.W);
+  b.nborder = std::min(cg.pw, b.wp) + std::max(0, b.wp - cg.pw - cg.W);
+  b.vitems = b.vec ? b.rows_in * (cg.W / 4) * b.c8 : 0;
+  *ipt = (b.vec && b.vitems <= THREADS) ? 1 : 0;
   // weight row: gpr groups of GB bytes, stride padded so the 16 rows a
   // fragment read touches fall in distinct banks
   constexpr int GB = group_bytes<WT>();
@@ -660,11 +765,29 @@ bool band_geometry(const ConvGeom& cg, BandGeom& b, size_t& lds) {
     stride_dw += GB / 4;
   b.wrow = stride_dw * 4;
   b.x_off = (CO_TILE * b.wrow + 4 * b.gpr + 15) / 16 * 16;
-  const size_t xl_bytes = (size_t)b.rows_in * b.wp * b.cstride * 2;
+  b.x_bytes = (int)(((size_t)b.rows_in * b.wp * b.cstride * 2 + 15) / 16 * 16);
   const size_t raw_bytes = ((size_t)CO_TILE * cg.C * b.taps * dtype_bits(WT) + 7) / 8;
-  b.raw_ok = dtype_bits(WT) <= 8 && raw_bytes <= xl_bytes;
-  lds = b.x_off + xl_bytes;
+  b.raw_ok = dtype_bits(WT) <= 8 && raw_bytes <= (size_t)b.x_bytes;
+  lds = b.x_off + (size_t)b.x_bytes;
   return lds <= 80 * 1024;
+}
+
+template <int WT, int IPT, bool K9>
+int launch_band(const float* x, const void* w, const float* w_scale, const float* bias, float* y,
+                const BandGeom& b, size_t lds, int64_t co_blocks, hipStream_t stream) {
+  auto kern = conv2d_band_kernel<WT, IPT, K9>;
+  static size_t lds_enabled = 64 * 1024;  // per instantiation: raise the limit once
+  if (lds > lds_enabled) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_LIMIT);
+    if (e != hipSuccess) return hip_fail(e);
+    lds_enabled = LDS_LIMIT;
+  }
+  const int64_t blocks = (int64_t)b.N * b.bands;
+  if (blocks > 0x7FFFFFFF) return NOVAQ_EINVAL;
+  hipLaunchKernelGGL(kern, dim3((unsigned)blocks, (unsigned)co_blocks), dim3(THREADS), lds, stream,
+                     x, static_cast<const uint8_t*>(w), w_scale, bias, y, b);
+  return check_launch();
 }
 
 template <int WT>
@@ -673,22 +796,17 @@ int launch(const float* x, const void* w, const float* w_scale, const float* bia
   {
     BandGeom b;
     size_t lds = 0;
-    if (band_geometry<WT>(g, b, lds)) {
-      auto kern = conv2d_band_kernel<WT>;
-      static size_t lds_enabled = 64 * 1024;
-      if (lds > lds_enabled) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           (int)LDS_LIMIT);
-        if (e != hipSuccess) return hip_fail(e);
-        lds_enabled = LDS_LIMIT;
-      }
-      const int64_t blocks = (int64_t)g.N * b.bands;
+    int ipt = 0;
+    if (band_geometry<WT>(g, b, lds, &ipt)) {
       const int64_t co_blocks = (g.C_out + CO_TILE - 1) / CO_TILE;
-      if (blocks > 0x7FFFFFFF) return NOVAQ_EINVAL;
-      hipLaunchKernelGGL(kern, dim3((unsigned)blocks, (unsigned)co_blocks), dim3(THREADS), lds,
-                         stream, x, static_cast<const uint8_t*>(w), w_scale, bias, y, b);
-      return check_launch();
+      if constexpr (group_bytes<WT>() < 16) {
+        if (b.taps == 9 && g.C % 8 == 0 && b.raw_ok) {
+          if (ipt == 1) return launch_band<WT, 1, true>(x, w, w_scale, bias, y, b, lds, co_blocks, stream);
+          return launch_band<WT, 0, true>(x, w, w_scale, bias, y, b, lds, co_blocks, stream);
+        }
+      }
+      if (ipt == 1) return launch_band<WT, 1, false>(x, w, w_scale, bias, y, b, lds, co_blocks, stream);
+      return launch_band<WT, 0, false>(x, w, w_scale, bias, y, b, lds, co_blocks, stream);
     }
   }
   // staged rows for a run of PIX_TILE pixels: it spans at most

@@ -81,6 +81,10 @@ def test_golden_fixture_all_padding_modes(golden):
     (2, 9, 11, 13, 70, 3, 3, 1, 1, 1, 1),
     (1, 70, 9, 7, 33, 3, 3, 1, 1, 1, 1),
     (2, 16, 31, 33, 64, 1, 1, 1, 1, 0, 0),
+    # 3x3 with C a multiple of 8 (the constant-shift weight regrouping) and a
+    # partial output-channel block
+    (2, 16, 12, 12, 40, 3, 3, 1, 1, 1, 1),
+    (1, 8, 9, 16, 70, 3, 3, 2, 2, 1, 1),
 ])
 def test_shapes_and_modes_vs_oracle(wdt, mode, case):
     N, C, H, W, C_out, KH, KW, sh, sw, ph, pw = case
