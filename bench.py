@@ -6,10 +6,11 @@ HBM: fp32 -> fp16 -> fp32, fp32 -> bf16 -> fp32, and for E4M3 and E5M2 the
 per-tensor amax, the scale, the scaled cast and the scaled dequantization
 back to fp32.  `value` is the algorithmic bytes of the step (52 B/element)
 over its wall time, in GB/s.  Each kernel is also bracketed by HIP events on
-the stream it runs on, which gives the per-kernel roofline figures.  A
-secondary leg times the FP8-weight Linear of config [4] (x 2048x4096,
-W 4096x4096 E4M3) in TFLOP/s.  The CPU baseline is the C oracle on a bounded
-sample of the same sweep.
+the stream it runs on, which gives the per-kernel roofline figures.  Further
+legs, each with its own roofline: the FP8-weight Linear of config [4]
+(x 2048x4096, W 4096x4096 E4M3) in TFLOP/s, the FP4 pack / unpack of config
+[3] and the two FP4-weight convolutions of config [5] in GB/s.  The CPU
+baseline is the C oracle on a bounded sample of the same sweep.
 
 Prints ONE JSON line.  Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -43,6 +44,8 @@ KERNEL_OF = {
     "f32->e4m3 scaled": "cast_kernel<0, 3, 1>", "e4m3->f32 scaled": "cast_kernel<3, 0, 1>",
     "f32->e5m2 scaled": "cast_kernel<0, 4, 1>", "e5m2->f32 scaled": "cast_kernel<4, 0, 1>",
 }
+FP4_KERNEL = {"pack f32->e2m1": "cast_kernel<0, 5, 1>", "unpack e2m1->f32": "cast_kernel<5, 0, 1>"}
+CONV_KERNEL = {1: "conv2d_band_kernel<5, 1, false>", 32: "conv2d_band_kernel<5, 1, true>"}
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 
 
@@ -185,7 +188,8 @@ def bench_linear(dev, iters: int = 20, warmup: int = 5):
                        "w_dtype": "e4m3", "mfma": "bf16"},
             "roofline": {"bound": "mfma", "achieved": round(tflops, 1),
                          "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                         "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "traffic": None}}
+                         "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+                         "traffic": measured_traffic("linear_wide_kernel<3>")}}
 
 
 def bench_fp4(dev, n: int = 1 << 26, iters: int = 20, warmup: int = 3):
@@ -230,7 +234,8 @@ def bench_fp4(dev, n: int = 1 << 26, iters: int = 20, warmup: int = 3):
         ms = sum(e0.elapsed_time(e1) for e0, e1 in ev) / iters
         gbs = 4.5 * n / (ms * 1e-3) / 1e9
         out.append({"op": name, "ms": round(ms, 4), "GB/s": round(gbs, 1),
-                    "frac": round(gbs / HBM_PEAK_GBS, 4)})
+                    "frac": round(gbs / HBM_PEAK_GBS, 4),
+                    "traffic": measured_traffic(FP4_KERNEL[name]) if n == 1 << 26 else None})
     return {"workload": "BASELINE config [3]", "elements": n, "bytes_per_element": 4.5,
             "kernels": out}
 
@@ -282,7 +287,8 @@ def bench_conv(dev, iters: int = 20, warmup: int = 5):
         flops = 2.0 * N * 28 * 28 * cout * cin * 9
         out.append({"layer": f"conv {cin}->{cout}", "ms": round(ms, 4), "GB/s": round(gbs, 1),
                     "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
-                    "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 2), "bytes": nbytes})
+                    "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 2), "bytes": nbytes,
+                    "traffic": measured_traffic(CONV_KERNEL[cin])})
     return {"workload": "BASELINE config [5]", "layers": out}
 
 
