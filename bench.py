@@ -8,7 +8,7 @@ back to fp32.  `value` is the algorithmic bytes of the step (52 B/element)
 over its wall time, in GB/s.  Each kernel is also bracketed by HIP events on
 the stream it runs on, which gives the per-kernel roofline figures.  Further
 legs, each with its own roofline: the FP8-weight Linear of config [4]
-(x 2048x4096, W 4096x4096 E4M3) in TFLOP/s, the FP4 pack / unpack of config
+(x 2048x4096, W 4096x4096 E4M3) and its backward in TFLOP/s, the FP4 pack / unpack of config
 [3] and the two FP4-weight convolutions of config [5] in GB/s.  The CPU
 baseline is the C oracle on a bounded sample of the same sweep.
 
@@ -192,6 +192,53 @@ def bench_linear(dev, iters: int = 20, warmup: int = 5):
                          "traffic": measured_traffic("linear_wide_kernel<3>")}}
 
 
+def bench_linear_backward(dev, iters: int = 10, warmup: int = 3):
+    """Linear.backward at config [4]'s shape (linear.py:85-108): grad_input
+    = grad @ (s * dec(W)), grad_weight = grad^T @ x, grad_bias = column sums,
+    E4M3 W; 2 x 68.72 GFLOP per call, all kernels (transposes included) timed."""
+    import torch
+
+    from novann_amd import _lib, quant
+    lib = _lib.load()
+    M, K, N = 2048, 4096, 4096  # batch, D_in, D_out
+    g = torch.Generator(device=dev)
+    g.manual_seed(6)
+    x = torch.randn((M, K), generator=g, device=dev, dtype=torch.float32)
+    w = torch.randn((N, K), generator=g, device=dev, dtype=torch.float32) * (2.0 / K) ** 0.5
+    wq = quant.quantize(w, "e4m3")
+    grad = torch.randn((M, N), generator=g, device=dev, dtype=torch.float32)
+    gi = torch.empty((M, K), device=dev)
+    gw = torch.empty((N, K), device=dev)
+    gb = torch.empty(N, device=dev)
+    nbytes = lib.novaq_linear_backward_workspace(M, K, N, 3)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+
+    def run():
+        _lib.check(lib.novaq_linear_backward(
+            grad.data_ptr(), x.data_ptr(), M, K, wq.data.data_ptr(), 3, wq.scale.data_ptr(), N,
+            gi.data_ptr(), gw.data_ptr(), gb.data_ptr(), ws.data_ptr(), nbytes, stream),
+            "linear backward")
+    for _ in range(warmup):
+        run()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize(dev)
+    e0.record()
+    for _ in range(iters):
+        run()
+    e1.record()
+    torch.cuda.synchronize(dev)
+    ms = e0.elapsed_time(e1) / iters
+    flops = 2 * 2.0 * M * N * K
+    tflops = flops / (ms * 1e-3) / 1e12
+    return {"metric": "Linear backward TFLOP/s (grad_input + grad_weight) at config [4]",
+            "value": round(tflops, 1), "unit": "TFLOP/s", "ms": round(ms, 4),
+            "workspace_bytes": nbytes,
+            "roofline": {"bound": "mfma", "achieved": round(tflops, 1),
+                         "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(tflops / BF16_PEAK_TFLOPS, 4)}}
+
+
 def bench_fp4(dev, n: int = 1 << 26, iters: int = 20, warmup: int = 3):
     """Config [3]: fp32 -> E2M1 pack and E2M1 -> fp32 unpack of 2^26 N(0,1)
     elements with the per-tensor scale s = amax / 6 (4.5 algorithmic bytes per
@@ -361,6 +408,8 @@ def main() -> int:
     log(f"sweep done: {ms:.3f} ms/step, {value:.1f} GB/s")
     lin = None if args.no_linear else bench_linear(dev)
     log(f"linear: {lin}")
+    lin_bwd = None if args.no_linear else bench_linear_backward(dev)
+    log(f"linear backward: {lin_bwd}")
     conv = None if args.no_conv else bench_conv(dev)
     log(f"conv2d: {conv}")
     fp4 = None if args.no_fp4 else bench_fp4(dev)
@@ -382,6 +431,7 @@ def main() -> int:
                      "bytes_per_launch": dom_bpe * args.elems},
         "kernels": per_op,
         "linear": lin,
+        "linear_backward": lin_bwd,
         "conv2d": conv,
         "fp4": fp4,
         "cpu_baseline": cpu,

@@ -41,6 +41,7 @@
 #ifndef NOVAQ_H
 #define NOVAQ_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -144,6 +145,41 @@ int novaq_conv2d_forward(const float *x, int64_t N, int64_t C, int64_t H, int64_
                          const void *w_q, int w_dtype, const float *w_scale,
                          int64_t C_out, int KH, int KW, int sh, int sw, int ph, int pw,
                          int pad_mode, const float *bias, float *y, void *stream);
+
+/* dst (cols x rows, dst_dtype) = src (rows x cols, src_dtype) transposed, both
+ * row-major.  src_dtype == dst_dtype permutes the stored values (quantized
+ * codes are never re-encoded; E2M1 needs even rows and cols, both sides
+ * nibble-packed along their rows); F32 -> BF16 / F16 rounds to nearest even.
+ * No reference counterpart: it stands in for the strided `.T` views NovaNN's
+ * backward passes multiply with (novann/layers/linear/linear.py:101,107). */
+int novaq_transpose(const void *src, int src_dtype, int64_t rows, int64_t cols, void *dst,
+                    int dst_dtype, void *stream);
+
+/* out[c] = sum over r of x[r][c] (rows x cols fp32, fp32 sums in a fixed
+ * order).  Replaces: np.sum(grad, axis=0, keepdims=True), the bias gradient of
+ * Linear.backward (novann/layers/linear/linear.py:103-104). */
+int novaq_colsum(const float *x, int64_t rows, int64_t cols, float *out, void *stream);
+
+/* Bytes of device workspace novaq_linear_backward needs for these shapes. */
+size_t novaq_linear_backward_workspace(int64_t N, int64_t D_in, int64_t D_out, int w_dtype);
+
+/* Gradients of y = x @ (s * dec(w_q))^T + bias with respect to x, the
+ * dequantized weight and the bias, given grad = dL/dy (N, D_out) fp32 and the
+ * forward input x (N, D_in) fp32:
+ *   grad_input  (N, D_in)     = grad @ (s * dec(w_q))
+ *   grad_weight (D_out, D_in) = grad^T @ x
+ *   grad_bias   (D_out)       = grad summed over the N rows
+ * Replaces: Linear.backward (novann/layers/linear/linear.py:85-108).  Any of
+ * the three outputs may be NULL (not computed).  The products run on the
+ * Linear forward kernels (bf16 MFMA, fp32 accumulation): grad_input on w_q's
+ * codes transposed (exact), grad_weight on grad^T in fp32 and x^T rounded to
+ * bf16.  workspace: device memory of novaq_linear_backward_workspace() bytes
+ * (16-byte aligned) the call may overwrite; it is not used after the call's
+ * kernels complete. */
+int novaq_linear_backward(const float *grad, const float *x, int64_t N, int64_t D_in,
+                          const void *w_q, int w_dtype, const float *w_scale, int64_t D_out,
+                          float *grad_input, float *grad_weight, float *grad_bias,
+                          void *workspace, size_t workspace_bytes, void *stream);
 
 #ifdef __cplusplus
 }

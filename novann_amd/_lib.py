@@ -35,6 +35,11 @@ SIGNATURES = {
     "novaq_conv2d_forward": (_i32, [_f32p, _i64, _i64, _i64, _i64, _vp, _i32, _f32p, _i64,
                                     _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32p, _f32p,
                                     _vp]),
+    "novaq_transpose": (_i32, [_vp, _i32, _i64, _i64, _vp, _i32, _vp]),
+    "novaq_colsum": (_i32, [_f32p, _i64, _i64, _f32p, _vp]),
+    "novaq_linear_backward_workspace": (ctypes.c_size_t, [_i64, _i64, _i64, _i32]),
+    "novaq_linear_backward": (_i32, [_f32p, _f32p, _i64, _i64, _vp, _i32, _f32p, _i64, _f32p,
+                                     _f32p, _f32p, _vp, ctypes.c_size_t, _vp]),
 }
 
 _lib = None

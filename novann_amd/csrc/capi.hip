@@ -30,6 +30,21 @@ int device_cu_count() {
 }
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+// Workspace of novaq_linear_backward: W^T in W's format, grad^T (fp32) and
+// x^T (bf16), each 256-byte aligned.
+struct LinearBwdWs {
+  size_t wt, gyt, xt, total;
+};
+static LinearBwdWs linear_bwd_ws(int64_t N, int64_t D_in, int64_t D_out, int w_dtype) {
+  LinearBwdWs w;
+  w.wt = 0;
+  w.gyt = align256(((size_t)D_in * (size_t)D_out * dtype_bits(w_dtype) + 7) / 8);
+  w.xt = w.gyt + align256((size_t)D_out * (size_t)N * 4);
+  w.total = w.xt + align256((size_t)D_in * (size_t)N * 2);
+  return w;
+}
 static bool valid_dtype(int dt) { return dt >= F32 && dt <= E2M1; }
 
 }  // namespace novaq
@@ -134,6 +149,73 @@ int novaq_conv2d_forward(const float* x, int64_t N, int64_t C, int64_t H, int64_
   if (!aligned16(x) || !aligned16(w_q) || !aligned16(y)) return NOVAQ_EALIGN;
   return conv2d_launch(x, N, C, H, W, w_q, w_dtype, w_scale, C_out, KH, KW, sh, sw, ph, pw,
                        pad_mode, bias, y, static_cast<hipStream_t>(stream));
+}
+
+int novaq_transpose(const void* src, int src_dtype, int64_t rows, int64_t cols, void* dst,
+                    int dst_dtype, void* stream) {
+  if (!valid_dtype(src_dtype) || !valid_dtype(dst_dtype)) return NOVAQ_EDTYPE;
+  if (rows < 0 || cols < 0) return NOVAQ_EINVAL;
+  if (rows == 0 || cols == 0) return NOVAQ_OK;
+  if (!src || !dst) return NOVAQ_EINVAL;
+  if (!aligned16(src) || !aligned16(dst)) return NOVAQ_EALIGN;
+  return transpose_launch(src, src_dtype, rows, cols, dst, dst_dtype,
+                          static_cast<hipStream_t>(stream));
+}
+
+int novaq_colsum(const float* x, int64_t rows, int64_t cols, float* out, void* stream) {
+  if (rows < 0 || cols < 0) return NOVAQ_EINVAL;
+  if (cols == 0) return NOVAQ_OK;
+  if (!out || (rows > 0 && !x)) return NOVAQ_EINVAL;
+  if ((rows > 0 && !aligned16(x)) || !aligned16(out)) return NOVAQ_EALIGN;
+  return colsum_launch(x, rows, cols, out, static_cast<hipStream_t>(stream));
+}
+
+size_t novaq_linear_backward_workspace(int64_t N, int64_t D_in, int64_t D_out, int w_dtype) {
+  if (!valid_dtype(w_dtype) || N < 0 || D_in < 0 || D_out < 0) return 0;
+  return linear_bwd_ws(N, D_in, D_out, w_dtype).total;
+}
+
+int novaq_linear_backward(const float* grad, const float* x, int64_t N, int64_t D_in,
+                          const void* w_q, int w_dtype, const float* w_scale, int64_t D_out,
+                          float* grad_input, float* grad_weight, float* grad_bias,
+                          void* workspace, size_t workspace_bytes, void* stream) {
+  if (!valid_dtype(w_dtype)) return NOVAQ_EDTYPE;
+  if (N < 0 || D_in < 0 || D_out < 0) return NOVAQ_EINVAL;
+  if (w_dtype == E2M1 && ((D_in | D_out) & 1)) return NOVAQ_ESHAPE;  // whole bytes both ways
+  const LinearBwdWs ws = linear_bwd_ws(N, D_in, D_out, w_dtype);
+  if ((grad_input || grad_weight) && (!workspace || workspace_bytes < ws.total))
+    return NOVAQ_EINVAL;
+  if (N > 0 && D_out > 0 && !grad) return NOVAQ_EINVAL;
+  if (grad_input && N > 0 && D_in > 0 && D_out > 0 && !w_q) return NOVAQ_EINVAL;
+  if (grad_weight && N > 0 && D_in > 0 && !x) return NOVAQ_EINVAL;
+  for (const void* p : {(const void*)grad, (const void*)x, w_q, (const void*)grad_input,
+                        (const void*)grad_weight, (const void*)grad_bias, (const void*)workspace})
+    if (p && !aligned16(p)) return NOVAQ_EALIGN;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  uint8_t* base = static_cast<uint8_t*>(workspace);
+  int rc = NOVAQ_OK;
+  // grad_input = grad @ (s * dec(W)): the forward product on W^T (codes permuted)
+  if (grad_input && N > 0 && D_in > 0) {
+    void* wt = base + ws.wt;
+    rc = transpose_launch(w_q, w_dtype, D_out, D_in, wt, w_dtype, s);
+    if (rc != NOVAQ_OK) return rc;
+    rc = linear_launch(grad, N, D_out, wt, w_dtype, w_scale, nullptr, D_in, grad_input, s);
+    if (rc != NOVAQ_OK) return rc;
+  }
+  // grad_weight = grad^T @ x: the forward product of grad^T (fp32) and x^T (bf16)
+  if (grad_weight && D_out > 0 && D_in > 0) {
+    float* gyt = reinterpret_cast<float*>(base + ws.gyt);
+    void* xt = base + ws.xt;
+    rc = transpose_launch(grad, F32, N, D_out, gyt, F32, s);
+    if (rc != NOVAQ_OK) return rc;
+    rc = transpose_launch(x, F32, N, D_in, xt, BF16, s);
+    if (rc != NOVAQ_OK) return rc;
+    rc = linear_launch(gyt, D_out, N, xt, BF16, nullptr, nullptr, D_in, grad_weight, s);
+    if (rc != NOVAQ_OK) return rc;
+  }
+  // grad_bias = grad summed over the batch
+  if (grad_bias && D_out > 0) rc = colsum_launch(grad, N, D_out, grad_bias, s);
+  return rc;
 }
 
 }  // extern "C"

@@ -1,0 +1,162 @@
+// Layout kernels for the backward products: 2-D transpose (with an optional
+// fp32 -> bf16 / fp16 rounding on the way) and a column sum.
+//
+// Transpose: dst (cols x rows) = src (rows x cols)^T, both row-major.  A
+// workgroup moves one 64 x 64 tile through LDS: every global load and store
+// instruction of a wave covers 64 consecutive elements of one row.  Quantized
+// codes are permuted, never re-encoded (E2M1: both sides nibble-packed along
+// their rows, element 2i in the low nibble; a lane writes one byte, i.e. two
+// consecutive elements of a destination row).  fp32 -> bf16 / fp16 rounds to
+// nearest even with the same rules as the cast kernels.
+//
+// Column sum: out[c] = sum over rows of x[r][c] in fp32, in a fixed order
+// (each of 16 row slices summed in four interleaved row chains, the chains
+// added in order, then the slices added in slice order), so repeated calls
+// agree bit for bit.  A workgroup owns 64 columns (each wave load instruction
+// reads 256 contiguous bytes of one row) and 16 waves split the rows.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "novaq_convert.h"
+#include "novaq_internal.h"
+
+namespace novaq {
+namespace {
+
+constexpr int TILE = 64;
+constexpr int TT = 256;  // threads per transpose workgroup
+
+template <int DT>
+__device__ __forceinline__ uint32_t load_code(const uint8_t* __restrict__ p, int64_t e) {
+  if constexpr (dtype_bits(DT) == 32) return reinterpret_cast<const uint32_t*>(p)[e];
+  else if constexpr (dtype_bits(DT) == 16) return reinterpret_cast<const uint16_t*>(p)[e];
+  else if constexpr (dtype_bits(DT) == 8) return p[e];
+  else return (p[e >> 1] >> ((e & 1) * 4)) & 0xFu;
+}
+
+template <int ST, int DT>
+__device__ __forceinline__ uint32_t convert_code(uint32_t c) {
+  if constexpr (ST == DT) return c;
+  else if constexpr (DT == BF16) return enc_bf16(c);  // ST == F32
+  else return enc_f16(c);                             // ST == F32, DT == F16
+}
+
+template <int ST, int DT>
+__global__ __launch_bounds__(TT) void transpose_kernel(const uint8_t* __restrict__ src,
+                                                       uint8_t* __restrict__ dst, int64_t rows,
+                                                       int64_t cols) {
+  __shared__ uint32_t tile[TILE][TILE + 1];
+  const int64_t r0 = (int64_t)blockIdx.y * TILE, c0 = (int64_t)blockIdx.x * TILE;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+#pragma unroll
+  for (int k = 0; k < TILE / 4; ++k) {
+    const int i = ty + 4 * k;
+    const int64_t r = r0 + i, c = c0 + tx;
+    tile[i][tx] = (r < rows && c < cols) ? load_code<ST>(src, r * cols + c) : 0u;
+  }
+  __syncthreads();
+  if constexpr (DT == E2M1) {
+    // lane tx < 32 writes destination elements (2tx, 2tx+1) of its row
+#pragma unroll
+    for (int k = 0; k < TILE / 4; ++k) {
+      const int i = ty + 4 * k;  // destination row offset (source column)
+      const int64_t c = c0 + i;
+      if (tx >= TILE / 2 || c >= cols) continue;
+      const int64_t r = r0 + 2 * tx;  // even; rows is even
+      if (r >= rows) continue;
+      const uint32_t lo = tile[2 * tx][i], hi = tile[2 * tx + 1][i];
+      dst[(c * rows + r) >> 1] = (uint8_t)(lo | (hi << 4));
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < TILE / 4; ++k) {
+      const int i = ty + 4 * k;
+      const int64_t c = c0 + i, r = r0 + tx;
+      if (c >= cols || r >= rows) continue;
+      const uint32_t v = convert_code<ST, DT>(tile[tx][i]);
+      const int64_t e = c * rows + r;
+      if constexpr (dtype_bits(DT) == 32) reinterpret_cast<uint32_t*>(dst)[e] = v;
+      else if constexpr (dtype_bits(DT) == 16) reinterpret_cast<uint16_t*>(dst)[e] = (uint16_t)v;
+      else dst[e] = (uint8_t)v;
+    }
+  }
+}
+
+constexpr int CS_COLS = 64;    // columns per workgroup
+constexpr int CS_SLICES = 16;  // row slices per workgroup (one wave each)
+
+__global__ __launch_bounds__(CS_COLS * CS_SLICES) void colsum_kernel(const float* __restrict__ x,
+                                                                    int64_t rows, int64_t cols,
+                                                                    float* __restrict__ out) {
+  __shared__ float part[CS_SLICES][CS_COLS];
+  const int tx = threadIdx.x % CS_COLS, ty = threadIdx.x / CS_COLS;
+  const int64_t c = (int64_t)blockIdx.x * CS_COLS + tx;
+  const int64_t per = (rows + CS_SLICES - 1) / CS_SLICES;
+  const int64_t rb = ty * per, re = min(rows, rb + per);
+  float s = 0.0f;
+  if (c < cols) {
+    // four independent chains keep four loads in flight per lane
+    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+    int64_t r = rb;
+    for (; r + 3 < re; r += 4) {
+      a0 += x[r * cols + c];
+      a1 += x[(r + 1) * cols + c];
+      a2 += x[(r + 2) * cols + c];
+      a3 += x[(r + 3) * cols + c];
+    }
+    for (; r < re; ++r) a0 += x[r * cols + c];
+    s = (a0 + a1) + (a2 + a3);
+  }
+  part[ty][tx] = s;
+  __syncthreads();
+  if (ty == 0 && c < cols) {
+    float t = part[0][tx];
+#pragma unroll
+    for (int k = 1; k < CS_SLICES; ++k) t += part[k][tx];
+    out[c] = t;
+  }
+}
+
+template <int ST, int DT>
+int launch_transpose(const void* src, void* dst, int64_t rows, int64_t cols, hipStream_t stream) {
+  const int64_t gx = (cols + TILE - 1) / TILE, gy = (rows + TILE - 1) / TILE;
+  if (gx > 0x7FFFFFFF || gy > 65535) return NOVAQ_EINVAL;
+  hipLaunchKernelGGL((transpose_kernel<ST, DT>), dim3((unsigned)gx, (unsigned)gy), dim3(TT), 0,
+                     stream, static_cast<const uint8_t*>(src), static_cast<uint8_t*>(dst), rows,
+                     cols);
+  return check_launch();
+}
+
+}  // namespace
+
+int transpose_launch(const void* src, int st, int64_t rows, int64_t cols, void* dst, int dt,
+                     hipStream_t stream) {
+  if (rows == 0 || cols == 0) return NOVAQ_OK;
+  if (st == dt) {
+    switch (st) {
+      case F32: return launch_transpose<F32, F32>(src, dst, rows, cols, stream);
+      case F16: return launch_transpose<F16, F16>(src, dst, rows, cols, stream);
+      case BF16: return launch_transpose<BF16, BF16>(src, dst, rows, cols, stream);
+      case E4M3: return launch_transpose<E4M3, E4M3>(src, dst, rows, cols, stream);
+      case E5M2: return launch_transpose<E5M2, E5M2>(src, dst, rows, cols, stream);
+      case E2M1:
+        if (rows % 2 || cols % 2) return NOVAQ_ESHAPE;
+        return launch_transpose<E2M1, E2M1>(src, dst, rows, cols, stream);
+      default: return NOVAQ_EDTYPE;
+    }
+  }
+  if (st == F32 && dt == BF16) return launch_transpose<F32, BF16>(src, dst, rows, cols, stream);
+  if (st == F32 && dt == F16) return launch_transpose<F32, F16>(src, dst, rows, cols, stream);
+  return NOVAQ_EDTYPE;
+}
+
+int colsum_launch(const float* x, int64_t rows, int64_t cols, float* out, hipStream_t stream) {
+  if (cols == 0) return NOVAQ_OK;
+  const int64_t blocks = (cols + CS_COLS - 1) / CS_COLS;
+  if (blocks > 0x7FFFFFFF) return NOVAQ_EINVAL;
+  hipLaunchKernelGGL(colsum_kernel, dim3((unsigned)blocks), dim3(CS_COLS * CS_SLICES), 0, stream,
+                     x, rows, cols, out);
+  return check_launch();
+}
+
+}  // namespace novaq

@@ -33,4 +33,8 @@ int conv2d_launch(const float* x, int64_t N, int64_t C, int64_t H, int64_t W, co
                   int sw, int ph, int pw, int pad_mode, const float* bias, float* y,
                   hipStream_t stream);
 
+int transpose_launch(const void* src, int st, int64_t rows, int64_t cols, void* dst, int dt,
+                     hipStream_t stream);
+int colsum_launch(const float* x, int64_t rows, int64_t cols, float* out, hipStream_t stream);
+
 }  // namespace novaq

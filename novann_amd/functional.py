@@ -88,6 +88,44 @@ def linear(input, weight, bias: Optional[Parameters] = None):
     return y.cpu().numpy() if was_numpy else y
 
 
+def linear_backward(grad, input, weight, bias: bool = True):
+    """Gradients of ``linear(input, weight, bias)`` for ``grad`` = dL/dy.
+
+    Restates Linear.backward (novann/layers/linear/linear.py:85-108) on the
+    GPU: returns ``(grad_input, grad_weight, grad_bias)`` with
+    grad_input = grad @ W (N, D_in), grad_weight = grad.T @ input
+    (D_out, D_in) and grad_bias = grad summed over the batch (1, D_out), or
+    None when ``bias`` is false.  A quantized weight enters as s * decode(codes)
+    (its gradient is the gradient of that dequantized matrix).  ndarrays in ->
+    ndarrays out."""
+    g, was_numpy = _to_device_f32(grad, "grad")
+    x, _ = _to_device_f32(input, "input")
+    if g.dim() != 2 or x.dim() != 2 or g.shape[0] != x.shape[0]:
+        raise ValueError(f"grad {tuple(g.shape)} does not match input {tuple(x.shape)}")
+    N, D_out = g.shape
+    D_in = x.shape[1]
+    wshape = weight.shape if isinstance(weight, QuantizedParameters) else tuple(
+        (weight.data if isinstance(weight, Parameters) else weight).shape)
+    if tuple(wshape) != (D_out, D_in):
+        raise ValueError(f"weight {tuple(wshape)} does not match grad {tuple(g.shape)} and "
+                         f"input {tuple(x.shape)}")
+    w, wdt, ws = _weight_args(weight, x.device)
+    lib = _lib.load()
+    gi = torch.empty((N, D_in), dtype=torch.float32, device=x.device)
+    gw = torch.empty((D_out, D_in), dtype=torch.float32, device=x.device)
+    gb = torch.empty((1, D_out), dtype=torch.float32, device=x.device) if bias else None
+    nbytes = lib.novaq_linear_backward_workspace(N, D_in, D_out, wdt)
+    work = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=x.device)
+    check(lib.novaq_linear_backward(
+        g.data_ptr(), x.data_ptr(), N, D_in, w.data_ptr(), wdt,
+        None if ws is None else ws.data_ptr(), D_out, gi.data_ptr(), gw.data_ptr(),
+        None if gb is None else gb.data_ptr(), work.data_ptr(), nbytes,
+        _stream(x.device)), "linear backward")
+    if was_numpy:
+        return (gi.cpu().numpy(), gw.cpu().numpy(), None if gb is None else gb.cpu().numpy())
+    return gi, gw, gb
+
+
 def _pair(v: IntPair) -> Tuple[int, int]:
     """int -> (v, v); 'valid' -> (0, 0); 'same' and other strings raise
     ValueError (novann/functional.py:302-313)."""

@@ -1,12 +1,12 @@
-"""Parameter containers and forward-only layers with NovaNN's interface.
+"""Parameter containers and layers with NovaNN's interface.
 
 ``Parameters`` mirrors novann/module/module.py:6-38 (``.data``, ``.grad``,
 ``.name``).  ``QuantizedParameters`` is the packed replacement of ``.data``
 for quantized weights: device codes (E4M3 / E5M2 / E2M1) plus a per-tensor
-scale.  ``Linear`` and ``Conv2d`` mirror the forward halves of
-novann/layers/linear/linear.py:10-83 and
+scale.  ``Linear`` mirrors novann/layers/linear/linear.py:10-108 (forward and
+backward) and ``Conv2d`` the forward half of
 novann/layers/convolutional/conv2d.py:9-177 (same constructor arguments,
-parameter shapes and defaults) and call the GPU operators in
+parameter shapes and defaults); both call the GPU operators in
 ``functional``.
 """
 from __future__ import annotations
@@ -98,9 +98,10 @@ def _pair(v):
 
 
 class Linear:
-    """Forward-only Linear with an fp32 or quantized weight (linear.py:10-83).
+    """Linear with an fp32 or quantized weight (linear.py:10-108).
 
-    weight (out_features, in_features); bias (1, out_features) zeros."""
+    weight (out_features, in_features); bias (1, out_features) zeros.  The
+    forward input is cached for ``backward`` (linear.py:81-82)."""
 
     def __init__(self, in_features: int, out_features: int, bias: bool = True,
                  weight_dtype: Optional[str] = None, init=None) -> None:
@@ -115,13 +116,26 @@ class Linear:
         if bias:
             self.bias = Parameters(np.zeros((1, out_features), dtype=np.float32))
             self.bias.name = "linear bias"
+        self._cache_input = None
 
     def __call__(self, x):
         return self.forward(x)
 
     def forward(self, x):
         from . import functional as F
+        self._cache_input = x
         return F.linear(x, self.weight, self.bias)
+
+    def backward(self, grad):
+        """Sets weight.grad = grad.T @ x and bias.grad = grad summed over the
+        batch, returns grad @ W (linear.py:85-108)."""
+        from . import functional as F
+        gi, gw, gb = F.linear_backward(grad, self._cache_input, self.weight,
+                                       self.bias is not None)
+        self.weight.grad = gw
+        if self.bias is not None:
+            self.bias.grad = gb
+        return gi
 
     def parameters(self):
         return [self.weight] + ([self.bias] if self.bias is not None else [])

@@ -3,6 +3,9 @@
 Restates, with this build's own code, the arithmetic of
   - ``novann.functional.linear``  (novann/functional.py:147-163):
     ``out = input @ weight.T`` then ``out += bias`` (in place, fp32);
+  - ``Linear.backward`` (novann/layers/linear/linear.py:85-108):
+    grad_weight = grad.T @ x, grad_bias = grad summed over the batch
+    (keepdims), grad_input = grad @ weight;
   - ``novann.functional.conv2d``  (novann/functional.py:275-385):
     pad with numpy.pad (constant / reflect / edge / wrap, :325-344), take
     (N, C, OH, OW, KH, KW) windows with ``as_strided`` (:358-364), reorder
@@ -28,6 +31,15 @@ def linear(x: np.ndarray, w: np.ndarray, bias: np.ndarray | None = None) -> np.n
     if bias is not None:
         out += bias.reshape(1, -1)
     return out
+
+
+def linear_backward(grad: np.ndarray, x: np.ndarray, w: np.ndarray, bias: bool = True):
+    """(grad_input, grad_weight, grad_bias) of ``linear`` for grad = dL/dy,
+    in the order Linear.backward forms them (linear.py:100-107)."""
+    grad_weight = grad.T @ x
+    grad_bias = np.sum(grad, axis=0, keepdims=True) if bias else None
+    grad_input = grad @ w
+    return grad_input, grad_weight, grad_bias
 
 
 def _pair(v):

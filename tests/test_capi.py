@@ -80,6 +80,31 @@ def test_other_entry_points_validation():
     assert conv(FAKE, 1, 1, 8, 8, FAKE, 9, None, 2, 3, 3, 1, 1, 1, 1, 0, None, FAKE, None) == _lib.EDTYPE
 
 
+def test_backward_entry_points_validation():
+    lib = _lib.load()
+    # transpose: quantized -> other format, fp8 -> fp32, odd E2M1 sides, alignment, empty
+    assert lib.novaq_transpose(FAKE, 3, 4, 4, FAKE, 0, None) == _lib.EDTYPE
+    assert lib.novaq_transpose(FAKE, 2, 4, 4, FAKE, 0, None) == _lib.EDTYPE
+    assert lib.novaq_transpose(FAKE, 5, 3, 4, FAKE, 5, None) == _lib.ESHAPE
+    assert lib.novaq_transpose(FAKE + 4, 0, 4, 4, FAKE, 2, None) == _lib.EALIGN
+    assert lib.novaq_transpose(None, 0, 0, 4, None, 0, None) == _lib.OK
+    assert lib.novaq_colsum(FAKE, 4, -1, FAKE, None) == _lib.EINVAL
+    assert lib.novaq_colsum(FAKE, 4, 0, None, None) == _lib.OK
+    # workspace: W^T, grad^T (fp32) and x^T (bf16), each 256-byte aligned
+    ws = lib.novaq_linear_backward_workspace(8, 64, 32, 3)
+    assert ws == 2048 + 1024 + 1024
+    assert lib.novaq_linear_backward_workspace(8, 64, 32, 9) == 0
+    bwd = lib.novaq_linear_backward
+    assert bwd(FAKE, FAKE, 8, 64, FAKE, 9, None, 32, FAKE, FAKE, None, FAKE, ws, None) == _lib.EDTYPE
+    assert bwd(FAKE, FAKE, 8, 63, FAKE, 5, None, 32, FAKE, FAKE, None, FAKE, ws, None) == _lib.ESHAPE
+    # too small a workspace, or none
+    assert bwd(FAKE, FAKE, 8, 64, FAKE, 3, None, 32, FAKE, FAKE, None, FAKE, ws - 1, None) == _lib.EINVAL
+    assert bwd(FAKE, FAKE, 8, 64, FAKE, 3, None, 32, FAKE, None, None, None, 0, None) == _lib.EINVAL
+    assert bwd(FAKE, FAKE, 8, 64, FAKE + 8, 3, None, 32, FAKE, None, None, FAKE, ws, None) == _lib.EALIGN
+    # nothing requested: no work, no workspace needed
+    assert bwd(FAKE, FAKE, 8, 64, FAKE, 3, None, 32, None, None, None, None, 0, None) == _lib.OK
+
+
 def test_status_maps_to_reference_exceptions():
     with pytest.raises(ValueError):
         _lib.check(_lib.EPADMODE, "conv2d")
