@@ -181,6 +181,32 @@ int novaq_linear_backward(const float *grad, const float *x, int64_t N, int64_t 
                           float *grad_input, float *grad_weight, float *grad_bias,
                           void *workspace, size_t workspace_bytes, void *stream);
 
+/* Bytes of device workspace novaq_conv2d_backward needs for these shapes. */
+size_t novaq_conv2d_backward_workspace(int64_t N, int64_t C, int64_t C_out, int KH, int KW,
+                                       int w_dtype);
+
+/* Gradients of the convolution novaq_conv2d_forward computes, given grad =
+ * dL/dy (N, C_out, OH, OW) fp32 and the forward input x (N, C, H, W) fp32:
+ *   grad_weight (C_out, C, KH, KW) = sum over (n, oh, ow) of grad times the
+ *       input window padded in pad_mode (the reference's column matrix);
+ *   grad_bias   (C_out)            = grad summed over (n, oh, ow);
+ *   grad_input  (N, C, H, W)       = the transposed convolution of grad with
+ *       s * dec(w_q), accumulated into a zero-padded image whose border is
+ *       then cropped -- for every pad_mode, as the reference's col2im does.
+ * Replaces: Conv2d.backward and Conv2d._col2im
+ * (novann/layers/convolutional/conv2d.py:117-148, 179-207).  Any output may
+ * be NULL.  grad_weight runs on bf16 MFMA (grad and the input rounded to
+ * bf16, fp32 accumulation) with per-chunk partial sums added in a fixed
+ * order; grad_input runs the forward kernels on the flipped weight codes when
+ * the stride is 1 and the padding is below the kernel size, fp32 element
+ * sums otherwise.  workspace: novaq_conv2d_backward_workspace() bytes. */
+int novaq_conv2d_backward(const float *grad, const float *x, int64_t N, int64_t C, int64_t H,
+                          int64_t W, const void *w_q, int w_dtype, const float *w_scale,
+                          int64_t C_out, int KH, int KW, int sh, int sw, int ph, int pw,
+                          int pad_mode, float *grad_input, float *grad_weight,
+                          float *grad_bias, void *workspace, size_t workspace_bytes,
+                          void *stream);
+
 #ifdef __cplusplus
 }
 #endif

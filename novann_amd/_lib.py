@@ -40,6 +40,10 @@ SIGNATURES = {
     "novaq_linear_backward_workspace": (ctypes.c_size_t, [_i64, _i64, _i64, _i32]),
     "novaq_linear_backward": (_i32, [_f32p, _f32p, _i64, _i64, _vp, _i32, _f32p, _i64, _f32p,
                                      _f32p, _f32p, _vp, ctypes.c_size_t, _vp]),
+    "novaq_conv2d_backward_workspace": (ctypes.c_size_t, [_i64, _i64, _i64, _i32, _i32, _i32]),
+    "novaq_conv2d_backward": (_i32, [_f32p, _f32p, _i64, _i64, _i64, _i64, _vp, _i32, _f32p,
+                                     _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32p,
+                                     _f32p, _f32p, _vp, ctypes.c_size_t, _vp]),
 }
 
 _lib = None

@@ -218,4 +218,39 @@ int novaq_linear_backward(const float* grad, const float* x, int64_t N, int64_t 
   return rc;
 }
 
+size_t novaq_conv2d_backward_workspace(int64_t N, int64_t C, int64_t C_out, int KH, int KW,
+                                       int w_dtype) {
+  if (!valid_dtype(w_dtype) || N < 0 || C <= 0 || C_out <= 0 || KH <= 0 || KW <= 0) return 0;
+  return conv2d_bwd_workspace(N, C, C_out, KH, KW, w_dtype, device_cu_count()).total;
+}
+
+int novaq_conv2d_backward(const float* grad, const float* x, int64_t N, int64_t C, int64_t H,
+                          int64_t W, const void* w_q, int w_dtype, const float* w_scale,
+                          int64_t C_out, int KH, int KW, int sh, int sw, int ph, int pw,
+                          int pad_mode, float* grad_input, float* grad_weight,
+                          float* grad_bias, void* workspace, size_t workspace_bytes,
+                          void* stream) {
+  if (!valid_dtype(w_dtype)) return NOVAQ_EDTYPE;
+  if (pad_mode < NOVAQ_PAD_ZEROS || pad_mode > NOVAQ_PAD_CIRCULAR) return NOVAQ_EPADMODE;
+  if (N < 0 || C <= 0 || H <= 0 || W <= 0 || C_out <= 0 || KH <= 0 || KW <= 0 || sh <= 0 ||
+      sw <= 0 || ph < 0 || pw < 0)
+    return NOVAQ_EINVAL;
+  if (H + 2 * (int64_t)ph < KH || W + 2 * (int64_t)pw < KW) return NOVAQ_ESHAPE;
+  if (N > 0x7FFFFFFF || C * H * W > 0x7FFFFFFF || C_out * C * KH * KW > 0x7FFFFFFF ||
+      C_out > 0x7FFFFFFF)
+    return NOVAQ_EINVAL;
+  if (!grad_input && !grad_weight && !grad_bias) return NOVAQ_OK;
+  const size_t need = conv2d_bwd_workspace(N, C, C_out, KH, KW, w_dtype, device_cu_count()).total;
+  if (!workspace || workspace_bytes < need) return NOVAQ_EINVAL;
+  if (N > 0 && !grad) return NOVAQ_EINVAL;
+  if (grad_input && N > 0 && !w_q) return NOVAQ_EINVAL;
+  if (grad_weight && N > 0 && !x) return NOVAQ_EINVAL;
+  for (const void* p : {(const void*)grad, (const void*)x, w_q, (const void*)grad_input,
+                        (const void*)grad_weight, (const void*)grad_bias, (const void*)workspace})
+    if (p && !aligned16(p)) return NOVAQ_EALIGN;
+  return conv2d_backward_launch(grad, x, N, C, H, W, w_q, w_dtype, w_scale, C_out, KH, KW, sh,
+                                sw, ph, pw, pad_mode, grad_input, grad_weight, grad_bias,
+                                workspace, static_cast<hipStream_t>(stream));
+}
+
 }  // extern "C"

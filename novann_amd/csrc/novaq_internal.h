@@ -35,6 +35,21 @@ int conv2d_launch(const float* x, int64_t N, int64_t C, int64_t H, int64_t W, co
 
 int transpose_launch(const void* src, int st, int64_t rows, int64_t cols, void* dst, int dt,
                      hipStream_t stream);
+
+// Workspace parts of conv2d_backward_launch (byte offsets, 256-byte aligned):
+// the flipped weights, the grad_weight partials (chunks x C_out x C*KH*KW
+// fp32) and the grad_bias partials (slices x C_out fp32).
+struct ConvBwdWs {
+  size_t wf, part, bpart, total;
+  int chunks, slices;
+};
+ConvBwdWs conv2d_bwd_workspace(int64_t N, int64_t C, int64_t C_out, int KH, int KW, int w_dtype,
+                               int cus);
+int conv2d_backward_launch(const float* grad, const float* x, int64_t N, int64_t C, int64_t H,
+                           int64_t W, const void* w_q, int w_dtype, const float* w_scale,
+                           int64_t C_out, int KH, int KW, int sh, int sw, int ph, int pw,
+                           int pad_mode, float* grad_input, float* grad_weight,
+                           float* grad_bias, void* workspace, hipStream_t stream);
 int colsum_launch(const float* x, int64_t rows, int64_t cols, float* out, hipStream_t stream);
 
 }  // namespace novaq

@@ -183,3 +183,50 @@ def conv2d(input, weight, kernel_size: IntPair, stride: IntPair = 1, padding: In
         C_out, KH, KW, sh, sw, ph, pw, PAD_MODES[padding_mode],
         None if b is None else b.data_ptr(), y.data_ptr(), _stream(x.device)), "conv2d")
     return y.cpu().numpy() if was_numpy else y
+
+
+def conv2d_backward(grad, input, weight, kernel_size: IntPair, stride: IntPair = 1,
+                    padding: IntPair = 0, *, bias: bool = True, padding_mode: str = "zeros"):
+    """Gradients of ``conv2d(input, weight, ...)`` for ``grad`` = dL/dy.
+
+    Restates Conv2d.backward with its _col2im
+    (novann/layers/convolutional/conv2d.py:117-148, 179-207) on the GPU:
+    returns ``(grad_input, grad_weight, grad_bias)``; grad_weight has the
+    weight's shape, grad_bias the reference's (C_out, 1) (None when ``bias``
+    is false), grad_input the input's shape (accumulated into a zero-padded
+    image whose border is cropped, as the reference does, in every padding
+    mode).  ndarrays in -> ndarrays out."""
+    KH, KW = _pair(kernel_size)
+    ph, pw = _pair(padding)
+    sh, sw = _pair(stride)
+    if padding_mode not in PAD_MODES:
+        raise ValueError(f"padding_mode Only accept {tuple(PAD_MODES)} not '{padding_mode}'")
+    g, was_numpy = _to_device_f32(grad, "grad")
+    x, _ = _to_device_f32(input, "input")
+    if x.dim() != 4 or g.dim() != 4:
+        raise ValueError(f"conv2d_backward expects 4-D grad and input, got {tuple(g.shape)} "
+                         f"and {tuple(x.shape)}")
+    N, C, H, W = x.shape
+    wshape = weight.shape if isinstance(weight, QuantizedParameters) else tuple(
+        (weight.data if isinstance(weight, Parameters) else weight).shape)
+    C_out = wshape[0]
+    OH, OW = (H + 2 * ph - KH) // sh + 1, (W + 2 * pw - KW) // sw + 1
+    if tuple(wshape) != (C_out, C, KH, KW) or tuple(g.shape) != (N, C_out, OH, OW):
+        raise ValueError(f"grad {tuple(g.shape)}, input {tuple(x.shape)} and weight "
+                         f"{tuple(wshape)} do not match")
+    w, wdt, ws = _weight_args(weight, x.device)
+    lib = _lib.load()
+    gi = torch.empty((N, C, H, W), dtype=torch.float32, device=x.device)
+    gw = torch.empty((C_out, C, KH, KW), dtype=torch.float32, device=x.device)
+    gb = torch.empty((C_out, 1), dtype=torch.float32, device=x.device) if bias else None
+    nbytes = lib.novaq_conv2d_backward_workspace(N, C, C_out, KH, KW, wdt)
+    work = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=x.device)
+    check(lib.novaq_conv2d_backward(
+        g.data_ptr(), x.data_ptr(), N, C, H, W, w.data_ptr(), wdt,
+        None if ws is None else ws.data_ptr(), C_out, KH, KW, sh, sw, ph, pw,
+        PAD_MODES[padding_mode], gi.data_ptr(), gw.data_ptr(),
+        None if gb is None else gb.data_ptr(), work.data_ptr(), nbytes, _stream(x.device)),
+        "conv2d backward")
+    if was_numpy:
+        return (gi.cpu().numpy(), gw.cpu().numpy(), None if gb is None else gb.cpu().numpy())
+    return gi, gw, gb

@@ -3,11 +3,10 @@
 ``Parameters`` mirrors novann/module/module.py:6-38 (``.data``, ``.grad``,
 ``.name``).  ``QuantizedParameters`` is the packed replacement of ``.data``
 for quantized weights: device codes (E4M3 / E5M2 / E2M1) plus a per-tensor
-scale.  ``Linear`` mirrors novann/layers/linear/linear.py:10-108 (forward and
-backward) and ``Conv2d`` the forward half of
-novann/layers/convolutional/conv2d.py:9-177 (same constructor arguments,
-parameter shapes and defaults); both call the GPU operators in
-``functional``.
+scale.  ``Linear`` mirrors novann/layers/linear/linear.py:10-108 and
+``Conv2d`` novann/layers/convolutional/conv2d.py:9-207 (same constructor
+arguments, parameter shapes and defaults, forward and backward); both call the
+GPU operators in ``functional``.
 """
 from __future__ import annotations
 
@@ -142,7 +141,9 @@ class Linear:
 
 
 class Conv2d:
-    """Forward-only Conv2d with an fp32 or quantized weight (conv2d.py:9-177).
+    """Conv2d with an fp32 or quantized weight (conv2d.py:9-207); the forward
+    input is cached for ``backward`` (the reference caches its im2col matrix,
+    conv2d.py:173-175; here the input itself, the matrix is never built).
 
     weight (out_channels, in_channels, KH, KW); bias (out_channels, 1) zeros;
     stride defaults to 1 (a None stride means kernel_size, conv2d.py:41)."""
@@ -165,14 +166,29 @@ class Conv2d:
         if bias:
             self.bias = Parameters(np.zeros((out_channels, 1), dtype=np.float32))
             self.bias.name = "conv2d bias"
+        self._cache_input = None
 
     def __call__(self, x):
         return self.forward(x)
 
     def forward(self, x):
         from . import functional as F
+        self._cache_input = x
         return F.conv2d(x, self.weight, (self.KH, self.KW), (self.sh, self.sw),
                         (self.ph, self.pw), bias=self.bias, padding_mode=self.pm)
+
+    def backward(self, grad):
+        """Sets weight.grad and bias.grad, returns the input gradient
+        (conv2d.py:179-207)."""
+        from . import functional as F
+        gi, gw, gb = F.conv2d_backward(grad, self._cache_input, self.weight,
+                                       (self.KH, self.KW), (self.sh, self.sw),
+                                       (self.ph, self.pw), bias=self.bias is not None,
+                                       padding_mode=self.pm)
+        self.weight.grad = gw
+        if self.bias is not None:
+            self.bias.grad = gb
+        return gi
 
     def parameters(self):
         return [self.weight] + ([self.bias] if self.bias is not None else [])

@@ -6,6 +6,11 @@ Restates, with this build's own code, the arithmetic of
   - ``Linear.backward`` (novann/layers/linear/linear.py:85-108):
     grad_weight = grad.T @ x, grad_bias = grad summed over the batch
     (keepdims), grad_input = grad @ weight;
+  - ``Conv2d.backward`` and ``Conv2d._col2im``
+    (novann/layers/convolutional/conv2d.py:117-148, 179-207): grad_weight =
+    grad (C_out, N*OH*OW) @ col.T, grad_bias = row sums, grad_col = w_col.T @
+    grad scattered with np.add.at into a zero-padded (N, C, H_p, W_p) buffer
+    whose border is then cropped;
   - ``novann.functional.conv2d``  (novann/functional.py:275-385):
     pad with numpy.pad (constant / reflect / edge / wrap, :325-344), take
     (N, C, OH, OW, KH, KW) windows with ``as_strided`` (:358-364), reorder
@@ -75,3 +80,38 @@ def conv2d(x: np.ndarray, w: np.ndarray, stride=(1, 1), padding=(0, 0),
     if bias is not None:
         out += bias.reshape(C_out, 1)
     return out.reshape(C_out, N, OH, OW).transpose(1, 0, 2, 3)
+
+
+def col2im(col: np.ndarray, x_shape, KH: int, KW: int, stride=(1, 1), padding=(0, 0)):
+    """Scatter-add a (C*KH*KW, N*OH*OW) column gradient into a zero-padded
+    (N, C, H+2ph, W+2pw) image and crop the border (conv2d.py:117-148).  Rows
+    are (c, kh, kw), columns (n, oh, ow), as ``im2col`` lays them out."""
+    sh, sw = _pair(stride)
+    ph, pw = _pair(padding)
+    N, C, H, W = x_shape
+    OH = (H + 2 * ph - KH) // sh + 1
+    OW = (W + 2 * pw - KW) // sw + 1
+    cols = col.reshape(C, KH, KW, N, OH, OW)
+    out = np.zeros((N, C, H + 2 * ph, W + 2 * pw), dtype=col.dtype)
+    for kh in range(KH):
+        for kw in range(KW):
+            # window position (kh, kw) of output pixel (oh, ow) lands on padded
+            # row oh*sh + kh, column ow*sw + kw; within one (kh, kw) the targets
+            # are distinct, so a sliced += accumulates exactly as np.add.at
+            out[:, :, kh:kh + sh * (OH - 1) + 1:sh, kw:kw + sw * (OW - 1) + 1:sw] += \
+                cols[:, kh, kw].transpose(1, 0, 2, 3)
+    return out[:, :, ph:ph + H, pw:pw + W]
+
+
+def conv2d_backward(grad: np.ndarray, x: np.ndarray, w: np.ndarray, stride=(1, 1),
+                    padding=(0, 0), padding_mode: str = "zeros", bias: bool = True):
+    """(grad_input, grad_weight, grad_bias) in the order Conv2d.backward forms
+    them (conv2d.py:194-207); grad_bias has the reference's (C_out, 1) shape."""
+    C_out, C, KH, KW = w.shape
+    col, OH, OW = im2col(x, KH, KW, stride, padding, padding_mode)
+    g = grad.transpose(1, 0, 2, 3).reshape(C_out, -1)
+    grad_weight = (g @ col.T).reshape(w.shape)
+    grad_bias = np.sum(g, axis=1).reshape(-1, 1) if bias else None
+    grad_col = w.reshape(C_out, -1).T @ g
+    grad_input = col2im(grad_col, x.shape, KH, KW, stride, padding)
+    return grad_input, grad_weight, grad_bias

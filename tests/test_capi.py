@@ -105,6 +105,28 @@ def test_backward_entry_points_validation():
     assert bwd(FAKE, FAKE, 8, 64, FAKE, 3, None, 32, None, None, None, None, 0, None) == _lib.OK
 
 
+def test_conv2d_backward_validation():
+    lib = _lib.load()
+    nb = lib.novaq_conv2d_backward_workspace(2, 3, 4, 3, 3, 5)
+    assert nb > 0 and lib.novaq_conv2d_backward_workspace(2, 3, 4, 3, 3, 9) == 0
+    bwd = lib.novaq_conv2d_backward
+    args = [FAKE, FAKE, 2, 3, 8, 8, FAKE, 5, None, 4, 3, 3, 1, 1, 1, 1, 0, FAKE, FAKE, FAKE,
+            FAKE, nb, None]
+
+    def call(**kw):
+        a = list(args)
+        for i, v in kw.items():
+            a[int(i[1:])] = v
+        return bwd(*a)
+    assert call(a7=9) == _lib.EDTYPE                       # weight dtype
+    assert call(a16=7) == _lib.EPADMODE                    # padding mode
+    assert call(a12=0) == _lib.EINVAL                      # stride
+    assert call(a10=11) == _lib.ESHAPE                     # kernel past the padded input
+    assert call(a21=nb - 1) == _lib.EINVAL                 # workspace too small
+    assert call(a17=FAKE + 4) == _lib.EALIGN               # misaligned output
+    assert call(a17=None, a18=None, a19=None, a20=None, a21=0) == _lib.OK  # nothing asked
+
+
 def test_status_maps_to_reference_exceptions():
     with pytest.raises(ValueError):
         _lib.check(_lib.EPADMODE, "conv2d")

@@ -1,0 +1,155 @@
+"""Backward products of the quantized Conv2d on the GPU (through the C ABI) vs
+the CPU restatement of Conv2d.backward and _col2im
+(novann/layers/convolutional/conv2d.py:117-148, 179-207).
+
+Tolerance: normwise max|g - r| / max|r| <= 1e-2 against fp64 on the same fp32
+grad and input and the dequantized weight (the BASELINE tolerance of the
+forward products).  grad_bias is an fp32 sum, so it is held to 1e-5."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import functional_ref as R
+from novann_amd import _lib
+from novann_amd import functional as F
+from novann_amd.module import Conv2d, Parameters, QuantizedParameters
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2
+
+
+def normwise(g, r):
+    return float(np.abs(g.astype(np.float64) - r).max() / max(np.abs(r).max(), 1e-30))
+
+
+def weight_of(w, wdt):
+    if wdt in ("e4m3", "e5m2", "e2m1"):
+        q = QuantizedParameters.from_float(w, wdt)
+        return q, q.dequantize().cpu().numpy().astype(np.float64).reshape(w.shape)
+    return Parameters(w), w.astype(np.float64)
+
+
+def check_case(N, C, H, W, C_out, KH, KW, stride, pad, wdt, mode="zeros", seed=0):
+    print(f"conv2d_backward N={N} C={C} H={H} W={W} C_out={C_out} k={KH}x{KW} s={stride} "
+          f"p={pad} {wdt} {mode}", flush=True)
+    rng = np.random.default_rng(seed + N * 7 + C * 11 + C_out * 13 + KH)
+    x = rng.standard_normal((N, C, H, W)).astype(np.float32)
+    w = (rng.standard_normal((C_out, C, KH, KW)) * np.sqrt(2.0 / (C * KH * KW))).astype(np.float32)
+    OH = (H + 2 * pad[0] - KH) // stride[0] + 1
+    OW = (W + 2 * pad[1] - KW) // stride[1] + 1
+    g = rng.standard_normal((N, C_out, OH, OW)).astype(np.float32)
+    weight, wdeq = weight_of(w, wdt)
+    gi, gw, gb = F.conv2d_backward(torch.from_numpy(g).cuda(), torch.from_numpy(x).cuda(),
+                                   weight, (KH, KW), stride, pad, bias=True, padding_mode=mode)
+    torch.cuda.synchronize()
+    ri, rw, rb = R.conv2d_backward(g.astype(np.float64), x.astype(np.float64), wdeq, stride,
+                                   pad, mode)
+    assert gi.shape == (N, C, H, W) and gw.shape == (C_out, C, KH, KW) and gb.shape == (C_out, 1)
+    ei, ew = normwise(gi.cpu().numpy(), ri), normwise(gw.cpu().numpy(), rw)
+    assert ei <= TOL, f"grad_input {ei}"
+    assert ew <= TOL, f"grad_weight {ew}"
+    np.testing.assert_allclose(gb.cpu().numpy(), rb, rtol=1e-5,
+                               atol=1e-5 * np.sqrt(N * OH * OW))
+
+
+GEOMETRIES = [
+    # N, C, H, W, C_out, KH, KW, stride, pad
+    (2, 2, 6, 6, 3, 3, 3, (1, 1), (1, 1)),       # reference test_conv2d.py:44-86 shape
+    (4, 8, 12, 12, 16, 3, 3, (1, 1), (1, 1)),    # grad_input on the forward band kernel
+    (3, 5, 9, 11, 70, 3, 3, (2, 2), (1, 1)),     # stride 2: direct grad_input; C_out > 64
+    (2, 3, 10, 10, 7, 5, 5, (1, 1), (2, 2)),     # 5x5; E2M1 weight count odd (525)
+    (2, 4, 7, 9, 6, 3, 2, (1, 1), (3, 2)),       # padding >= kernel: direct grad_input
+    (1, 16, 16, 16, 8, 1, 1, (1, 1), (0, 0)),    # 1x1
+    (5, 64, 9, 9, 24, 3, 3, (1, 2), (0, 1)),     # mixed strides, C = 64
+    (2, 3, 33, 70, 65, 3, 3, (1, 1), (1, 1)),    # long rows (OW > 64), many pixels per image
+]
+
+
+@pytest.mark.parametrize("wdt", ["e4m3", "e5m2", "e2m1", "f32"])
+@pytest.mark.parametrize("geom", GEOMETRIES, ids=lambda g: "x".join(map(str, g[:7])))
+def test_conv2d_backward_vs_oracle(geom, wdt):
+    check_case(*geom, wdt)
+
+
+@pytest.mark.parametrize("mode", ["zeros", "reflect", "replicate", "circular"])
+@pytest.mark.parametrize("geom", [(2, 3, 8, 9, 5, 3, 3, (1, 1), (1, 2)),
+                                  (2, 4, 11, 10, 6, 3, 3, (2, 1), (2, 1))],
+                         ids=["s1", "s2"])
+def test_conv2d_backward_padding_modes(geom, mode):
+    """grad_weight reads the input padded in the forward's mode; grad_input is
+    the cropped col2im, the same in every mode (conv2d.py:141-148)."""
+    check_case(*geom, "e4m3", mode=mode)
+
+
+@pytest.mark.parametrize("layer,cin,cout", [("conv1", 1, 32), ("conv2", 32, 64)])
+def test_conv2d_backward_mnist_shapes(layer, cin, cout):
+    """Config [5]'s two convolutions (batch 256, 28x28, 3x3/s1/p1, FP4 E2M1)."""
+    check_case(256, cin, 28, 28, cout, 3, 3, (1, 1), (1, 1), "e2m1")
+
+
+def test_conv2d_backward_deterministic_and_partial_outputs():
+    rng = np.random.default_rng(5)
+    N, C, H, W, C_out = 8, 16, 14, 14, 32
+    x = torch.from_numpy(rng.standard_normal((N, C, H, W)).astype(np.float32)).cuda()
+    g = torch.from_numpy(rng.standard_normal((N, C_out, H, W)).astype(np.float32)).cuda()
+    w = QuantizedParameters.from_float(
+        (rng.standard_normal((C_out, C, 3, 3)) * 0.1).astype(np.float32), "e4m3")
+    a = F.conv2d_backward(g, x, w, 3, 1, 1)
+    b = F.conv2d_backward(g, x, w, 3, 1, 1)
+    torch.cuda.synchronize()
+    for u, v in zip(a, b):
+        assert torch.equal(u, v)
+    # one output at a time through the C ABI gives the same bits
+    lib = _lib.load()
+    st = torch.cuda.current_stream().cuda_stream
+    nbytes = lib.novaq_conv2d_backward_workspace(N, C, C_out, 3, 3, _lib.DTYPES["e4m3"])
+    ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    outs = [torch.full_like(t, 7.0) for t in a]
+    for k in range(3):
+        ptrs = [None, None, None]
+        ptrs[k] = outs[k].data_ptr()
+        _lib.check(lib.novaq_conv2d_backward(
+            g.data_ptr(), x.data_ptr(), N, C, H, W, w.codes.data_ptr(), _lib.DTYPES["e4m3"],
+            w.scale.data_ptr(), C_out, 3, 3, 1, 1, 1, 1, _lib.PAD_MODES["zeros"], *ptrs,
+            ws.data_ptr(), nbytes, st), "conv2d backward")
+    torch.cuda.synchronize()
+    for u, v in zip(a, outs):
+        assert torch.equal(u, v)
+
+
+def test_conv2d_backward_empty_batch():
+    lib = _lib.load()
+    st = torch.cuda.current_stream().cuda_stream
+    C, C_out = 4, 6
+    w = QuantizedParameters.from_float(np.ones((C_out, C, 3, 3), np.float32), "e2m1")
+    nbytes = lib.novaq_conv2d_backward_workspace(0, C, C_out, 3, 3, _lib.DTYPES["e2m1"])
+    ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    gw = torch.full((C_out, C, 3, 3), 7.0, device="cuda")
+    gb = torch.full((C_out, 1), 7.0, device="cuda")
+    _lib.check(lib.novaq_conv2d_backward(None, None, 0, C, 5, 5, w.codes.data_ptr(),
+                                         _lib.DTYPES["e2m1"], w.scale.data_ptr(), C_out, 3, 3,
+                                         1, 1, 1, 1, 0, None, gw.data_ptr(), gb.data_ptr(),
+                                         ws.data_ptr(), nbytes, st), "conv2d backward")
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(gw).item() == 0 and torch.count_nonzero(gb).item() == 0
+
+
+def test_layer_backward_like_reference():
+    """novann tests/layers/conv/test_conv2d.py:44-86 on the quantized layer:
+    gradients against the oracle (whose finite-difference agreement is pinned
+    on the CPU) and the grad_input shape."""
+    rng = np.random.RandomState(0)
+    layer = Conv2d(in_channels=2, out_channels=3, kernel_size=3, stride=1, padding=1,
+                   bias=True, weight_dtype="e4m3")
+    x = rng.randn(2, 2, 6, 6).astype(np.float32) * 0.1
+    out = layer(x)
+    G = rng.randn(*out.shape).astype(np.float32) * 0.1
+    grad_input = layer.backward(G)
+    wdeq = layer.weight.dequantize().cpu().numpy().astype(np.float64).reshape(3, 2, 3, 3)
+    ri, rw, rb = R.conv2d_backward(G.astype(np.float64), x.astype(np.float64), wdeq, 1, 1)
+    assert isinstance(grad_input, np.ndarray) and grad_input.shape == x.shape
+    assert layer.weight.grad.shape == (3, 2, 3, 3) and layer.bias.grad.shape == (3, 1)
+    assert normwise(layer.weight.grad, rw) <= TOL
+    assert np.abs(layer.bias.grad - rb).max() < 5e-3
+    assert normwise(grad_input, ri) <= TOL
