@@ -339,6 +339,60 @@ def bench_conv(dev, iters: int = 20, warmup: int = 5):
     return {"workload": "BASELINE config [5]", "layers": out}
 
 
+def bench_conv_backward(dev, iters: int = 20, warmup: int = 5):
+    """Conv2d.backward (conv2d.py:179-207) for config [5]'s two layers, E2M1
+    weights, all three gradients per call.  Algorithmic traffic: read grad
+    twice (grad_input and grad_weight each need all of it) and x once, write
+    grad_input once; the weight-sized arrays are negligible."""
+    import torch
+
+    from novann_amd import _lib, quant
+    lib = _lib.load()
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    N = 256
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    flush = torch.empty(1 << 27, dtype=torch.float32, device=dev)
+    out = []
+    for cin, cout in ((1, 32), (32, 64)):
+        x = torch.rand((N, cin, 28, 28), generator=g, device=dev, dtype=torch.float32)
+        w = torch.randn((cout, cin, 3, 3), generator=g, device=dev) * (2.0 / (cin * 9)) ** 0.5
+        q = quant.quantize(w.contiguous(), "e2m1")
+        grad = torch.randn((N, cout, 28, 28), generator=g, device=dev, dtype=torch.float32)
+        gi = torch.empty_like(x)
+        gw = torch.empty((cout, cin, 3, 3), device=dev)
+        gb = torch.empty((cout, 1), device=dev)
+        nbytes = lib.novaq_conv2d_backward_workspace(N, cin, cout, 3, 3, 5)
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+
+        def run():
+            _lib.check(lib.novaq_conv2d_backward(
+                grad.data_ptr(), x.data_ptr(), N, cin, 28, 28, q.data.data_ptr(), 5,
+                q.scale.data_ptr(), cout, 3, 3, 1, 1, 1, 1, 0, gi.data_ptr(), gw.data_ptr(),
+                gb.data_ptr(), ws.data_ptr(), nbytes, stream), "conv2d backward")
+        for _ in range(warmup):
+            run()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(iters)]
+        torch.cuda.synchronize(dev)
+        for e0, e1 in ev:
+            flush.zero_()
+            e0.record()
+            run()
+            e1.record()
+        torch.cuda.synchronize(dev)
+        ms = sum(e0.elapsed_time(e1) for e0, e1 in ev) / iters
+        nb = (2 * grad.numel() + 2 * x.numel()) * 4
+        gbs = nb / (ms * 1e-3) / 1e9
+        flops = 2 * 2.0 * N * 28 * 28 * cout * cin * 9
+        out.append({"layer": f"conv {cin}->{cout} backward", "ms": round(ms, 4),
+                    "GB/s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+                    "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 2), "bytes": nb,
+                    "workspace_bytes": nbytes})
+        del x, grad, gi, ws
+    return {"workload": "BASELINE config [5] shapes, backward", "layers": out}
+
+
 def cpu_baseline(sample: int, min_seconds: float = 10.0):
     """The C oracle running the same sweep on a bounded sample (all host cores)."""
     import numpy as np
@@ -412,6 +466,8 @@ def main() -> int:
     log(f"linear backward: {lin_bwd}")
     conv = None if args.no_conv else bench_conv(dev)
     log(f"conv2d: {conv}")
+    conv_bwd = None if args.no_conv else bench_conv_backward(dev)
+    log(f"conv2d backward: {conv_bwd}")
     fp4 = None if args.no_fp4 else bench_fp4(dev)
     log(f"fp4: {fp4}")
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_sample)
@@ -433,6 +489,7 @@ def main() -> int:
         "linear": lin,
         "linear_backward": lin_bwd,
         "conv2d": conv,
+        "conv2d_backward": conv_bwd,
         "fp4": fp4,
         "cpu_baseline": cpu,
     }

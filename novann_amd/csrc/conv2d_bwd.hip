@@ -21,14 +21,13 @@
 //     other strides and paddings;
 //   - dweight_kernel: implicit GEMM on bf16 MFMA (v_mfma_f32_32x32x16_bf16):
 //     M = output channels (64 per workgroup), N = (c, kh, kw) (64 per
-//     workgroup), K = the output pixels of a run of images, 64 per LDS stage
-//     (grad rows staged with consecutive loads, the padded-input operand
-//     gathered element-wise with the padding mode resolved); each workgroup
-//     writes one partial to the workspace;
-//   - chansum_partial_kernel: per-channel partial sums of grad over a slice
-//     of (n, pixel);
-//   - reduce_partials_kernel: adds the partials in slice order, so results do
-//     not depend on scheduling.
+//     workgroup), K = the output pixels of a run of images (a chunk), 64 per
+//     LDS stage (grad rows staged with 16-byte loads, the padded-input
+//     operand gathered element-wise with the padding mode resolved); each
+//     workgroup writes one partial grad_weight tile to the workspace, and the
+//     first j block also the per-channel grad sums of its chunk (grad_bias);
+//   - layout.hip's column sum then adds the chunk partials in a fixed order,
+//     so results do not depend on scheduling.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -140,6 +139,8 @@ __global__ __launch_bounds__(256) void dinput_direct_kernel(const float* __restr
 constexpr int DW_THREADS = 256;
 constexpr int DW_M = 64, DW_N = 64, DW_K = 64;  // workgroup tile and K stage
 constexpr int DW_PITCH = DW_K + 8;              // bf16 per LDS row (144 B: conflict-free reads)
+constexpr int DW_PER_CU = 8;        // target workgroups per CU
+constexpr int DW_MAX_CHUNKS = 512;  // a multiple of 8
 
 __device__ __forceinline__ uint32_t bf16_pair(float a, float b) {
   f32x2 f = {a, b};
@@ -148,122 +149,185 @@ __device__ __forceinline__ uint32_t bf16_pair(float a, float b) {
 
 // Partial grad_weight of one (image chunk, co block, j block):
 // part[chunk][co][j] fp32, j = (c, kh, kw) flattened (the weight's layout).
+// The workgroups of j block 0 also write the partial grad_bias of their
+// (chunk, co block) to bpart[chunk][co] when bpart is given: the fp32 sum of
+// the grad values they stage (per lane in stage order, then a fixed butterfly
+// over the 32 lanes that share a row).
+//
+// BIAS_ONLY: the same grid and grad reads, bias partials only (so a call
+// that asks for grad_bias alone gets the same bits as one that also asks for
+// grad_weight).
+//
+// Staging: lane l of wave w holds the two consecutive pixels 2*(l%32), +1 of
+// the stage for the tile rows 2w + l/32 + 8i (i < 8): grad rows are read as
+// 8-byte pairs, 256 contiguous bytes per half-wave.  The (c, kh, kw) of the
+// B rows come from a 64-entry table built once per workgroup.
+template <bool ZEROPAD, bool BIAS_ONLY>
 __global__ __launch_bounds__(DW_THREADS, 2) void dweight_kernel(
     const float* __restrict__ grad, const float* __restrict__ x, float* __restrict__ part,
-    BwdGeom g, int ckk, int chunks) {
+    float* __restrict__ bpart, BwdGeom g, int ckk, int chunks, int co_blocks, int j_blocks) {
   __shared__ __attribute__((aligned(16))) __bf16 As[DW_M * DW_PITCH];  // [co][k]
   __shared__ __attribute__((aligned(16))) __bf16 Bs[DW_N * DW_PITCH];  // [j][k]
+  // per B row: c*H*W + (kh - ph)*W + (kw - pw), kh - ph, kw - pw, j < ckk
+  __shared__ int4 jtab[DW_N];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, half = lane >> 5;
-  const int chunk = blockIdx.x, co0 = blockIdx.y * DW_M, j0 = blockIdx.z * DW_N;
-  const int n_begin = (int)((int64_t)g.N * chunk / chunks);
-  const int n_end = (int)((int64_t)g.N * (chunk + 1) / chunks);
+  // 1-D grid; the workgroups of one chunk (all its co and j blocks) share an
+  // XCD (workgroup i runs on XCD i % 8) so its grad rows are fetched into
+  // that XCD's L2 once: on XCD x, the k-th run of `per` workgroups is chunk
+  // 8k + x (chunks is a multiple of 8 when it is at least 8)
+  const int per = co_blocks * j_blocks;
+  int chunk, member;
+  if (chunks >= 8) {
+    const int x8 = blockIdx.x & 7, i = blockIdx.x >> 3;
+    chunk = (i / per) * 8 + x8;
+    member = i % per;
+  } else {
+    chunk = blockIdx.x / per;
+    member = blockIdx.x % per;
+  }
+  const int jb = member % j_blocks, cb = member / j_blocks;
+  const int co0 = cb * DW_M, j0 = jb * DW_N;
   const int P = g.OH * g.OW;
-  const int64_t HW = (int64_t)g.H * g.W;
+  const int SP = (P + DW_K - 1) / DW_K;  // stages per image
+  // this chunk's run of (image, stage) pairs
+  const int64_t T = (int64_t)g.N * SP;
+  const int64_t t_begin = T * chunk / chunks, t_end = T * (chunk + 1) / chunks;
+  const int HW = g.H * g.W;  // C*H*W < 2^31 (checked by the entry point)
   const int wm = (wave & 1) * 32, wn = (wave >> 1) * 32;
+  const bool want_bias = bpart != nullptr && jb == 0;
+
+  if (!BIAS_ONLY && tid < DW_N) {
+    const int j = j0 + tid;
+    const int kw = j % g.KW, ckh = j / g.KW;
+    const int kh = ckh % g.KH, c = ckh / g.KH;
+    const int dh = kh - g.ph, dw = kw - g.pw;
+    jtab[tid] = make_int4(c * HW + dh * g.W + dw, dh, dw, j < ckk ? 1 : 0);
+  }
+  float bsum[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) bsum[i] = 0.0f;
 
   f32x16 acc;
 #pragma unroll
   for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+  if (!BIAS_ONLY) __syncthreads();  // jtab
 
-  for (int n = n_begin; n < n_end; ++n) {
+  // one stage = 64 pixels of one image; stage s + 1 is loaded into registers
+  // while stage s is multiplied
+  const int k = 2 * (lane & 31), rbase = 2 * wave + half;
+  const bool pvec = (P & 1) == 0;
+  float a[8][2], bv[8][2];
+  auto load_stage = [&](int n, int p0) {
     const float* gn = grad + (int64_t)n * g.C_out * P;
     const float* xn = x + (int64_t)n * g.C * HW;
-    for (int p0 = 0; p0 < P; p0 += DW_K) {
-      // A: grad[n, co0 + i, p0 .. p0+63] -> As[i][k], four pixels per item
+    const int p = p0 + k;
+    const bool v0 = p < P, v1 = p + 1 < P;
+    // A: grad rows co0 + rbase + 8i at pixels p, p+1
 #pragma unroll
-      for (int it = 0; it < DW_M * DW_K / 4 / DW_THREADS; ++it) {
-        const int item = tid + it * DW_THREADS;
-        const int i = item / (DW_K / 4), k4 = (item % (DW_K / 4)) * 4;
-        const int co = co0 + i;
-        float v[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int p = p0 + k4 + q;
-          v[q] = (co < g.C_out && p < P) ? gn[(int64_t)co * P + p] : 0.0f;
+    for (int i = 0; i < 8; ++i) {
+      const int co = co0 + rbase + 8 * i;
+      a[i][0] = a[i][1] = 0.0f;
+      if (co < g.C_out) {
+        const float* row = gn + (int64_t)co * P + p;
+        if (pvec && v1) {
+          const float2 f = *reinterpret_cast<const float2*>(row);
+          a[i][0] = f.x; a[i][1] = f.y;
+        } else {
+          if (v0) a[i][0] = row[0];
+          if (v1) a[i][1] = row[1];
         }
-        *reinterpret_cast<uint2*>(&As[i * DW_PITCH + k4]) =
-            make_uint2(bf16_pair(v[0], v[1]), bf16_pair(v[2], v[3]));
       }
-      // B: xpad[n, c, oh*sh + kh - ph, ow*sw + kw - pw] for j = (c, kh, kw)
+    }
+    if constexpr (!BIAS_ONLY) {
+      // B: xpad[n, c, oh*sh + kh - ph, ow*sw + kw - pw] for the rows' (c, kh, kw)
+      int hb[2], wb[2];
+      const int oh = p / g.OW, ow = p - oh * g.OW;
+      hb[0] = oh * g.sh;
+      wb[0] = ow * g.sw;
+      const bool wrap = ow + 1 == g.OW;
+      hb[1] = wrap ? hb[0] + g.sh : hb[0];
+      wb[1] = wrap ? 0 : wb[0] + g.sw;
 #pragma unroll
-      for (int it = 0; it < DW_N * DW_K / 4 / DW_THREADS; ++it) {
-        const int item = tid + it * DW_THREADS;
-        const int jj = item / (DW_K / 4), k4 = (item % (DW_K / 4)) * 4;
-        const int j = j0 + jj;
-        float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        if (j < ckk) {
-          const int kw = j % g.KW, ckh = j / g.KW;
-          const int kh = ckh % g.KH, c = ckh / g.KH;
-          const float* xc = xn + (int64_t)c * HW;
+      for (int i = 0; i < 8; ++i) {
+        const int4 t = jtab[rbase + 8 * i];
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const int p = p0 + k4 + q;
-            if (p < P) {
-              const int oh = p / g.OW, ow = p - oh * g.OW;
-              const int hi = pad_idx(oh * g.sh + kh - g.ph, g.H, g.pad_mode);
-              const int wi = pad_idx(ow * g.sw + kw - g.pw, g.W, g.pad_mode);
-              if (hi >= 0 && wi >= 0) v[q] = xc[(int64_t)hi * g.W + wi];
-            }
+        for (int q = 0; q < 2; ++q) {
+          bv[i][q] = 0.0f;
+          if (!(t.w && (q ? v1 : v0))) continue;
+          int hi = hb[q] + t.y, wi = wb[q] + t.z;
+          if constexpr (ZEROPAD) {
+            if ((unsigned)hi < (unsigned)g.H && (unsigned)wi < (unsigned)g.W)
+              bv[i][q] = xn[t.x + hb[q] * g.W + wb[q]];
+          } else {
+            hi = pad_idx(hi, g.H, g.pad_mode);
+            wi = pad_idx(wi, g.W, g.pad_mode);
+            if (hi >= 0 && wi >= 0) bv[i][q] = xn[t.x - t.y * g.W - t.z + hi * g.W + wi];
           }
         }
-        *reinterpret_cast<uint2*>(&Bs[jj * DW_PITCH + k4]) =
-            make_uint2(bf16_pair(v[0], v[1]), bf16_pair(v[2], v[3]));
       }
-      __syncthreads();
+    }
+  };
+  int64_t t = t_begin;
+  int n = (int)(t / SP), p0 = (int)(t - (int64_t)n * SP) * DW_K;
+  if (t < t_end) load_stage(n, p0);
+  while (t < t_end) {
+    if (want_bias) {
 #pragma unroll
-      for (int st = 0; st < DW_K / 16; ++st) {
-        const int kk = st * 16 + half * 8;
-        const bf16x8 a = *reinterpret_cast<const bf16x8*>(&As[(wm + (lane & 31)) * DW_PITCH + kk]);
-        const bf16x8 b = *reinterpret_cast<const bf16x8*>(&Bs[(wn + (lane & 31)) * DW_PITCH + kk]);
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc, 0, 0, 0);
+      for (int i = 0; i < 8; ++i) bsum[i] += a[i][0] + a[i][1];
+    }
+    if constexpr (!BIAS_ONLY) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int r = rbase + 8 * i;
+        *reinterpret_cast<uint32_t*>(&As[r * DW_PITCH + k]) = bf16_pair(a[i][0], a[i][1]);
+        *reinterpret_cast<uint32_t*>(&Bs[r * DW_PITCH + k]) = bf16_pair(bv[i][0], bv[i][1]);
       }
-      __syncthreads();
+    }
+    // next stage
+    ++t;
+    p0 += DW_K;
+    if (p0 >= P) { p0 = 0; ++n; }
+    if constexpr (BIAS_ONLY) {
+      if (t < t_end) load_stage(n, p0);
+      continue;
+    }
+    // barriers order only LDS traffic: wait for this wave's LDS operations,
+    // not for the prefetch loads in flight
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (t < t_end) load_stage(n, p0);
+#pragma unroll
+    for (int st = 0; st < DW_K / 16; ++st) {
+      const int kk = st * 16 + half * 8;
+      const bf16x8 av = *reinterpret_cast<const bf16x8*>(&As[(wm + (lane & 31)) * DW_PITCH + kk]);
+      const bf16x8 bw = *reinterpret_cast<const bf16x8*>(&Bs[(wn + (lane & 31)) * DW_PITCH + kk]);
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bw, acc, 0, 0, 0);
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  }
+  if constexpr (!BIAS_ONLY) {
+    // lane holds column wn + (lane & 31) and rows wm + 8*(r/4) + 4*half + r%4
+    float* pc = part + (int64_t)chunk * g.C_out * ckk;
+    const int j = j0 + wn + (lane & 31);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int co = co0 + wm + 8 * (r >> 2) + 4 * half + (r & 3);
+      if (co < g.C_out && j < ckk) pc[(int64_t)co * ckk + j] = acc[r];
     }
   }
-  // lane holds column wn + (lane & 31) and rows wm + 8*(r/4) + 4*half + r%4
-  float* pc = part + (int64_t)chunk * g.C_out * ckk;
-  const int j = j0 + wn + (lane & 31);
+  if (want_bias) {
+    // the 32 lanes of a half share rows rbase + 8i
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int co = co0 + wm + 8 * (r >> 2) + 4 * half + (r & 3);
-    if (co < g.C_out && j < ckk) pc[(int64_t)co * ckk + j] = acc[r];
+    for (int i = 0; i < 8; ++i) {
+      float s = bsum[i];
+      s += __shfl_xor(s, 16, 32);
+      s += __shfl_xor(s, 8, 32);
+      s += __shfl_xor(s, 4, 32);
+      s += __shfl_xor(s, 2, 32);
+      s += __shfl_xor(s, 1, 32);
+      const int co = co0 + rbase + 8 * i;
+      if ((lane & 31) == 0 && co < g.C_out) bpart[(int64_t)chunk * g.C_out + co] = s;
+    }
   }
-}
-
-constexpr int CH_THREADS = 256;
-
-// bpart[slice][co] = sum of grad[n, co, p] over this slice's (n, p) range, in
-// a fixed order (thread-strided, then a fixed tree through LDS).
-__global__ __launch_bounds__(CH_THREADS) void chansum_partial_kernel(const float* __restrict__ grad,
-                                                                    int N, int C_out, int P,
-                                                                    int slices,
-                                                                    float* __restrict__ bpart) {
-  __shared__ float red[CH_THREADS];
-  const int co = blockIdx.x, slice = blockIdx.y;
-  const int64_t total = (int64_t)N * P;
-  const int64_t b = total * slice / slices, e = total * (slice + 1) / slices;
-  float s = 0.0f;
-  for (int64_t i = b + threadIdx.x; i < e; i += CH_THREADS) {
-    const int64_t n = i / P, p = i - n * P;
-    s += grad[(n * C_out + co) * P + p];
-  }
-  red[threadIdx.x] = s;
-  __syncthreads();
-  for (int w = CH_THREADS / 2; w > 0; w >>= 1) {
-    if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
-    __syncthreads();
-  }
-  if (threadIdx.x == 0) bpart[(int64_t)slice * C_out + co] = red[0];
-}
-
-// out[i] = sum over k < parts of part[k][i], in k order.
-__global__ void reduce_partials_kernel(const float* __restrict__ part, int parts, int64_t len,
-                                       float* __restrict__ out) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= len) return;
-  float s = 0.0f;
-  for (int k = 0; k < parts; ++k) s += part[(int64_t)k * len + i];
-  out[i] = s;
 }
 
 template <int WT>
@@ -300,22 +364,29 @@ int launch_dinput(const float* grad, const void* w, const void* wf, const float*
 
 }  // namespace
 
-// Workspace layout of conv2d_backward (each part 256-byte aligned).
+// Workspace layout of conv2d_backward (each part 256-byte aligned), sized
+// for the largest chunk count a launch uses.
 ConvBwdWs conv2d_bwd_workspace(int64_t N, int64_t C, int64_t C_out, int KH, int KW, int w_dtype,
                                int cus) {
   ConvBwdWs ws{};
   auto a256 = [](size_t b) { return (b + 255) & ~(size_t)255; };
   const int64_t ckk = C * KH * KW;
   const int64_t co_blocks = (C_out + DW_M - 1) / DW_M, j_blocks = (ckk + DW_N - 1) / DW_N;
-  // enough image chunks for about two workgroups per CU
-  const int64_t want = std::max<int64_t>(1, (2LL * cus + co_blocks * j_blocks - 1) /
-                                                (co_blocks * j_blocks));
-  ws.chunks = (int)std::max<int64_t>(1, std::min<int64_t>(N, want));
-  ws.slices = (int)std::max<int64_t>(1, std::min<int64_t>(N, 64));
+  // enough chunks of (image, 64-pixel stage) pairs for about DW_PER_CU
+  // workgroups per CU (resident waves hide the gathers' latency), a multiple
+  // of 8 for the XCD mapping; a launch uses fewer when there are fewer stages
+  // (at most DW_MAX_CHUNKS: the partials are summed by a column sum whose
+  // cost grows with their number)
+  int64_t want = std::max<int64_t>(1, ((int64_t)DW_PER_CU * cus + co_blocks * j_blocks - 1) /
+                                          (co_blocks * j_blocks));
+  want = std::min<int64_t>(want, DW_MAX_CHUNKS);
+  if (want >= 8) want = (want + 7) / 8 * 8;
+  (void)N;
+  ws.chunks = (int)want;
   ws.wf = 0;
   ws.part = a256(((size_t)C_out * ckk * dtype_bits(w_dtype) + 7) / 8);
   ws.bpart = ws.part + a256((size_t)ws.chunks * C_out * ckk * 4);
-  ws.total = ws.bpart + a256((size_t)ws.slices * C_out * 4);
+  ws.total = ws.bpart + a256((size_t)ws.chunks * C_out * 4);
   return ws;
 }
 
@@ -330,6 +401,12 @@ int conv2d_backward_launch(const float* grad, const float* x, int64_t N, int64_t
   g.OH = (int)((H + 2 * (int64_t)ph - KH) / sh + 1);
   g.OW = (int)((W + 2 * (int64_t)pw - KW) / sw + 1);
   const ConvBwdWs ws = conv2d_bwd_workspace(N, C, C_out, KH, KW, w_dtype, device_cu_count());
+  // chunks for this launch: at most one per (image, stage) pair, rounded up to
+  // a multiple of 8 when at least 8 (never above ws.chunks, itself such a
+  // multiple); chunks past the last stage add zeros
+  const int64_t T = N * (((int64_t)g.OH * g.OW + DW_K - 1) / DW_K);
+  int64_t chunks = std::min<int64_t>(ws.chunks, std::max<int64_t>(T, 1));
+  if (chunks >= 8) chunks = (chunks + 7) / 8 * 8;
   uint8_t* base = static_cast<uint8_t*>(workspace);
   int rc = NOVAQ_OK;
   if (grad_input && N > 0) {
@@ -346,33 +423,28 @@ int conv2d_backward_launch(const float* grad, const float* x, int64_t N, int64_t
     if (rc != NOVAQ_OK) return rc;
   }
   const int64_t ckk = C * KH * KW;
+  if (!grad_weight && !grad_bias) return rc;
+  float* part = reinterpret_cast<float*>(base + ws.part);
+  float* bpart = grad_bias ? reinterpret_cast<float*>(base + ws.bpart) : nullptr;
+  const int64_t co_blocks = (C_out + DW_M - 1) / DW_M;
+  const int64_t j_blocks = grad_weight ? (ckk + DW_N - 1) / DW_N : 1;
+  if (co_blocks > 65535 || j_blocks > 65535) return NOVAQ_EINVAL;
+  const int64_t blocks = chunks * co_blocks * j_blocks;
+  if (blocks > 0x7FFFFFFF) return NOVAQ_EINVAL;
+  const dim3 grid((unsigned)blocks);
+  const bool zp = pad_mode == NOVAQ_PAD_ZEROS;
+  auto kern = grad_weight ? (zp ? dweight_kernel<true, false> : dweight_kernel<false, false>)
+                          : dweight_kernel<true, true>;
+  hipLaunchKernelGGL(kern, grid, dim3(DW_THREADS), 0, stream, grad, x, part, bpart, g, (int)ckk,
+                     (int)chunks, (int)co_blocks, (int)j_blocks);
+  rc = check_launch();
+  if (rc != NOVAQ_OK) return rc;
+  // partials added over the chunks in a fixed order
   if (grad_weight) {
-    float* part = reinterpret_cast<float*>(base + ws.part);
-    const int64_t co_blocks = (C_out + DW_M - 1) / DW_M, j_blocks = (ckk + DW_N - 1) / DW_N;
-    if (co_blocks > 65535 || j_blocks > 65535) return NOVAQ_EINVAL;
-    hipLaunchKernelGGL(dweight_kernel, dim3((unsigned)ws.chunks, (unsigned)co_blocks,
-                                            (unsigned)j_blocks),
-                       dim3(DW_THREADS), 0, stream, grad, x, part, g, (int)ckk, ws.chunks);
-    rc = check_launch();
-    if (rc != NOVAQ_OK) return rc;
-    const int64_t len = C_out * ckk;
-    hipLaunchKernelGGL(reduce_partials_kernel, dim3((unsigned)((len + 255) / 256)), dim3(256), 0,
-                       stream, part, ws.chunks, len, grad_weight);
-    rc = check_launch();
+    rc = colsum_launch(part, chunks, C_out * ckk, grad_weight, stream);
     if (rc != NOVAQ_OK) return rc;
   }
-  if (grad_bias) {
-    float* bpart = reinterpret_cast<float*>(base + ws.bpart);
-    if (C_out > 0x7FFFFFFF) return NOVAQ_EINVAL;
-    hipLaunchKernelGGL(chansum_partial_kernel, dim3((unsigned)C_out, (unsigned)ws.slices),
-                       dim3(CH_THREADS), 0, stream, grad, g.N, g.C_out, g.OH * g.OW, ws.slices,
-                       bpart);
-    rc = check_launch();
-    if (rc != NOVAQ_OK) return rc;
-    hipLaunchKernelGGL(reduce_partials_kernel, dim3((unsigned)((C_out + 255) / 256)), dim3(256),
-                       0, stream, bpart, ws.slices, C_out, grad_bias);
-    rc = check_launch();
-  }
+  if (grad_bias) rc = colsum_launch(bpart, chunks, C_out, grad_bias, stream);
   return rc;
 }
 

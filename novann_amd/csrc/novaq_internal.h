@@ -38,10 +38,10 @@ int transpose_launch(const void* src, int st, int64_t rows, int64_t cols, void* 
 
 // Workspace parts of conv2d_backward_launch (byte offsets, 256-byte aligned):
 // the flipped weights, the grad_weight partials (chunks x C_out x C*KH*KW
-// fp32) and the grad_bias partials (slices x C_out fp32).
+// fp32) and the grad_bias partials (chunks x C_out fp32).
 struct ConvBwdWs {
   size_t wf, part, bpart, total;
-  int chunks, slices;
+  int chunks;
 };
 ConvBwdWs conv2d_bwd_workspace(int64_t N, int64_t C, int64_t C_out, int KH, int KW, int w_dtype,
                                int cus);
