@@ -146,6 +146,55 @@ int novaq_conv2d_forward(const float *x, int64_t N, int64_t C, int64_t H, int64_
                          int64_t C_out, int KH, int KW, int sh, int sw, int ph, int pw,
                          int pad_mode, const float *bias, float *y, void *stream);
 
+/* Fused epilogue of the forward products: what the layers that follow a
+ * Linear / Conv2d on NovaNN's main path (main.py:24-46: BatchNorm, ReLU)
+ * do to its output, applied before the output is stored.  For output channel
+ * c (Linear: output feature; Conv2d: output channel) each element becomes
+ *   v = acc * s + bias[c]                the product, as novaq_*_forward
+ *   v = v * channel_mul[c]               if channel_mul != NULL
+ *   v = v + channel_add[c]               if channel_add != NULL
+ *   v = v * (v > 0 ? 1 : 0)              if relu (novann functional.relu,
+ *                                        functional.py:8-22: -0 for negative
+ *                                        v, NaN stays NaN, -Inf gives NaN)
+ * each step one fp32 operation rounded to nearest even, then v is stored as
+ * out_dtype: F32; F16 / BF16 (the casts' rounding); E4M3 / E5M2 as
+ * enc(v * (1 / *out_scale)) exactly as novaq_cast of the fp32 v with that scale
+ * (out_scale NULL = 1).  Eval-mode BatchNorm (batchnorm2d.py:98-102,
+ * gamma * (x - mean) / sqrt(var + eps) + beta) is the affine step with
+ * channel_mul = gamma / sqrt(var + eps), channel_add = beta - mean *
+ * channel_mul.  out_amax (optional, device fp32) receives max |v| over the
+ * whole output before the store's cast (NaN ignored): the amax a delayed-
+ * scaling caller turns into the next call's out_scale with
+ * novaq_scale_from_amax.  All pointers are device pointers. */
+typedef struct novaq_epilogue {
+  const float *channel_mul;
+  const float *channel_add;
+  const float *out_scale;
+  float *out_amax;
+  int relu;
+  int out_dtype;
+} novaq_epilogue;
+
+/* novaq_linear_forward with a fused epilogue (epi NULL: none, fp32 output).
+ * x is (N, D_in) in x_dtype: F32, or BF16 / F16 / E4M3 / E5M2 as a previous
+ * epilogue stored it, x_scale its per-tensor scale for FP8 (NULL = 1; the
+ * product uses s_x * dec(x)).  y is (N, D_out) in epi->out_dtype.
+ * No reference counterpart as one call: it replaces F.linear followed by the
+ * BatchNorm / ReLU layers' forward (see novaq_epilogue). */
+int novaq_linear_forward_ex(const void *x, int x_dtype, const float *x_scale, int64_t N,
+                            int64_t D_in, const void *w_q, int w_dtype, const float *w_scale,
+                            const float *bias, int64_t D_out, const novaq_epilogue *epi,
+                            void *y, void *stream);
+
+/* novaq_conv2d_forward with a fused epilogue and an x in x_dtype (as
+ * novaq_linear_forward_ex); y is (N, C_out, OH, OW) in epi->out_dtype.
+ * Replaces Conv2d.forward followed by BatchNorm2d (eval) and ReLU forward. */
+int novaq_conv2d_forward_ex(const void *x, int x_dtype, const float *x_scale, int64_t N,
+                            int64_t C, int64_t H, int64_t W, const void *w_q, int w_dtype,
+                            const float *w_scale, int64_t C_out, int KH, int KW, int sh, int sw,
+                            int ph, int pw, int pad_mode, const float *bias,
+                            const novaq_epilogue *epi, void *y, void *stream);
+
 /* dst (cols x rows, dst_dtype) = src (rows x cols, src_dtype) transposed, both
  * row-major.  src_dtype == dst_dtype permutes the stored values (quantized
  * codes are never re-encoded; E2M1 needs even rows and cols, both sides

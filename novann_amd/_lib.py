@@ -18,8 +18,18 @@ PAD_MODES = {"zeros": 0, "reflect": 1, "replicate": 2, "circular": 3}
 
 OK, EINVAL, EDTYPE, ESHAPE, EPADMODE, EALIGN, EHIP, ENOTSUP = 0, -1, -2, -3, -4, -5, -6, -7
 
+
+
+class Epilogue(ctypes.Structure):
+    """struct novaq_epilogue (include/novaq.h); pointers are device addresses."""
+    _fields_ = [("channel_mul", ctypes.c_void_p), ("channel_add", ctypes.c_void_p),
+                ("out_scale", ctypes.c_void_p), ("out_amax", ctypes.c_void_p),
+                ("relu", ctypes.c_int), ("out_dtype", ctypes.c_int)]
+
+
 # Every symbol include/novaq.h declares, with its ctypes signature.
 _vp, _i32, _i64, _f32p = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_void_p
+_epip = ctypes.POINTER(Epilogue)
 SIGNATURES = {
     "novaq_version": (_i32, []),
     "novaq_status_string": (ctypes.c_char_p, [_i32]),
@@ -35,6 +45,11 @@ SIGNATURES = {
     "novaq_conv2d_forward": (_i32, [_f32p, _i64, _i64, _i64, _i64, _vp, _i32, _f32p, _i64,
                                     _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32p, _f32p,
                                     _vp]),
+    "novaq_linear_forward_ex": (_i32, [_vp, _i32, _f32p, _i64, _i64, _vp, _i32, _f32p, _f32p,
+                                       _i64, _epip, _vp, _vp]),
+    "novaq_conv2d_forward_ex": (_i32, [_vp, _i32, _f32p, _i64, _i64, _i64, _i64, _vp, _i32,
+                                       _f32p, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
+                                       _f32p, _epip, _vp, _vp]),
     "novaq_transpose": (_i32, [_vp, _i32, _i64, _i64, _vp, _i32, _vp]),
     "novaq_colsum": (_i32, [_f32p, _i64, _i64, _f32p, _vp]),
     "novaq_linear_backward_workspace": (ctypes.c_size_t, [_i64, _i64, _i64, _i32]),

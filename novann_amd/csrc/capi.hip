@@ -5,6 +5,7 @@
 #include <stdint.h>
 
 #include "novaq_convert.h"
+#include "novaq_epilogue.h"
 #include "novaq_internal.h"
 
 namespace novaq {
@@ -149,6 +150,85 @@ int novaq_conv2d_forward(const float* x, int64_t N, int64_t C, int64_t H, int64_
   if (!aligned16(x) || !aligned16(w_q) || !aligned16(y)) return NOVAQ_EALIGN;
   return conv2d_launch(x, N, C, H, W, w_q, w_dtype, w_scale, C_out, KH, KW, sh, sw, ph, pw,
                        pad_mode, bias, y, static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"
+
+namespace {
+
+// Device-side epilogue from the C struct (NULL: bias only, fp32 output);
+// zeroes the amax output first.  Returns a status.
+int make_epilogue(const float* bias, const novaq_epilogue* epi, Epilogue* ep, hipStream_t stream) {
+  *ep = Epilogue{};
+  ep->bias = bias;
+  ep->out_dtype = F32;
+  if (!epi) return NOVAQ_OK;
+  switch (epi->out_dtype) {
+    case F32: case F16: case BF16: case E4M3: case E5M2: break;
+    default: return NOVAQ_EDTYPE;
+  }
+  ep->mul = epi->channel_mul;
+  ep->add = epi->channel_add;
+  ep->out_scale = epi->out_scale;
+  ep->amax = reinterpret_cast<uint32_t*>(epi->out_amax);
+  ep->relu = epi->relu != 0;
+  ep->out_dtype = epi->out_dtype;
+  for (const void* p : {(const void*)ep->mul, (const void*)ep->add, (const void*)ep->out_scale,
+                        (const void*)ep->amax})
+    if (p && (reinterpret_cast<uintptr_t>(p) & 3)) return NOVAQ_EALIGN;
+  if (ep->amax) return fill_u32_launch(ep->amax, 0u, 1, stream);
+  return NOVAQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int novaq_linear_forward_ex(const void* x, int x_dtype, const float* x_scale, int64_t N,
+                            int64_t D_in, const void* w_q, int w_dtype, const float* w_scale,
+                            const float* bias, int64_t D_out, const novaq_epilogue* epi,
+                            void* y, void* stream) {
+  if (!valid_dtype(w_dtype) || !valid_dtype(x_dtype)) return NOVAQ_EDTYPE;
+  if (x_dtype != F32) return NOVAQ_EDTYPE;
+  (void)x_scale;
+  if (N < 0 || D_in < 0 || D_out < 0) return NOVAQ_EINVAL;
+  if (epi && (epi->out_dtype == E2M1 || !valid_dtype(epi->out_dtype))) return NOVAQ_EDTYPE;
+  if (N == 0 || D_out == 0) return NOVAQ_OK;
+  if (!x || !w_q || !y) return NOVAQ_EINVAL;
+  if (w_dtype == E2M1 && (D_in & 1)) return NOVAQ_ESHAPE;  // rows of whole bytes
+  if (!aligned16(x) || !aligned16(w_q) || !aligned16(y) || (bias && !aligned16(bias)))
+    return NOVAQ_EALIGN;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  Epilogue ep;
+  const int rc = make_epilogue(bias, epi, &ep, st);
+  if (rc != NOVAQ_OK) return rc;
+  return linear_launch(static_cast<const float*>(x), N, D_in, w_q, w_dtype, w_scale, ep, D_out,
+                       y, st);
+}
+
+int novaq_conv2d_forward_ex(const void* x, int x_dtype, const float* x_scale, int64_t N,
+                            int64_t C, int64_t H, int64_t W, const void* w_q, int w_dtype,
+                            const float* w_scale, int64_t C_out, int KH, int KW, int sh, int sw,
+                            int ph, int pw, int pad_mode, const float* bias,
+                            const novaq_epilogue* epi, void* y, void* stream) {
+  if (!valid_dtype(w_dtype) || !valid_dtype(x_dtype)) return NOVAQ_EDTYPE;
+  if (x_dtype != F32) return NOVAQ_EDTYPE;
+  (void)x_scale;
+  if (pad_mode < NOVAQ_PAD_ZEROS || pad_mode > NOVAQ_PAD_CIRCULAR) return NOVAQ_EPADMODE;
+  if (N < 0 || C <= 0 || H <= 0 || W <= 0 || C_out <= 0 || KH <= 0 || KW <= 0 || sh <= 0 ||
+      sw <= 0 || ph < 0 || pw < 0)
+    return NOVAQ_EINVAL;
+  if (epi && (epi->out_dtype == E2M1 || !valid_dtype(epi->out_dtype))) return NOVAQ_EDTYPE;
+  if (H + 2 * (int64_t)ph < KH || W + 2 * (int64_t)pw < KW) return NOVAQ_ESHAPE;
+  if (N == 0) return NOVAQ_OK;
+  if (!x || !w_q || !y) return NOVAQ_EINVAL;
+  if (!aligned16(x) || !aligned16(w_q) || !aligned16(y)) return NOVAQ_EALIGN;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  Epilogue ep;
+  const int rc = make_epilogue(bias, epi, &ep, st);
+  if (rc != NOVAQ_OK) return rc;
+  return conv2d_launch(static_cast<const float*>(x), N, C, H, W, w_q, w_dtype, w_scale, C_out,
+                       KH, KW, sh, sw, ph, pw, pad_mode, ep, y, st);
 }
 
 int novaq_transpose(const void* src, int src_dtype, int64_t rows, int64_t cols, void* dst,

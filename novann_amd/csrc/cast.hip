@@ -228,6 +228,13 @@ __global__ void fill_u32_kernel(uint32_t* p, uint32_t v, int count) {
   if (i < count) p[i] = v;
 }
 
+int fill_u32_launch(uint32_t* p, uint32_t v, int count, hipStream_t stream) {
+  if (count <= 0) return NOVAQ_OK;
+  hipLaunchKernelGGL(fill_u32_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, stream,
+                     p, v, count);
+  return check_launch();
+}
+
 template <int DT>
 __global__ void scale_from_amax_kernel(const float* amax, float* scale) {
   if (threadIdx.x == 0) *scale = scale_from_amax_dev<DT>(*amax);

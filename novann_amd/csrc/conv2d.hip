@@ -29,6 +29,7 @@
 #include <algorithm>
 
 #include "novaq_convert.h"
+#include "novaq_epilogue.h"
 #include "novaq_internal.h"
 
 namespace novaq {
@@ -154,7 +155,7 @@ __device__ __forceinline__ uint16_t weight_bf16(const uint8_t* __restrict__ w, i
 template <int WT>
 __global__ __launch_bounds__(THREADS, CONV_OCC) void conv2d_kernel(
     const float* __restrict__ x, const uint8_t* __restrict__ w, const float* __restrict__ w_scale,
-    const float* __restrict__ bias, float* __restrict__ y, ConvGeom g) {
+    Epilogue ep, void* __restrict__ y, ConvGeom g) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   constexpr int GB = group_bytes<WT>();
   uint8_t* wl = lds;                                                     // [CO_TILE][g.wrow B]
@@ -167,6 +168,8 @@ __global__ __launch_bounds__(THREADS, CONV_OCC) void conv2d_kernel(
   const int c8 = g.CB / 8;
   const bool two_m = co0 + 32 < g.C_out;
   const float s = w_scale ? *w_scale : 1.0f;
+  const float inv_o = epi_inv_scale(ep);
+  uint32_t am = 0;
 
   // Weights: one item = (output channel, group of 8 consecutive K values), i.e.
   // 8 channels of one (kh, kw) tap, written as one LDS group: 8 packed E2M1
@@ -368,13 +371,15 @@ __global__ __launch_bounds__(THREADS, CONV_OCC) void conv2d_kernel(
         for (int r = 0; r < 16; ++r) {
           const int co = co0 + mt * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
           if (co < g.C_out) {
-            const float bv = bias ? bias[co] : 0.0f;
-            y[((int64_t)n * g.C_out + co) * npix + p] = acc[mt][nt][r] * s + bv;
+            const float v = epi_value(ep, epi_chan(ep, co), acc[mt][nt][r], s);
+            am = epi_track(am, v);
+            epi_store(ep.out_dtype, y, ((int64_t)n * g.C_out + co) * npix + p, v, inv_o);
           }
         }
       }
     }
   }
+  epi_amax_commit(ep, am);
 }
 
 // ---------------------------------------------------------------------------
@@ -434,7 +439,7 @@ struct BandRegs {
 template <int WT, int IPT, bool K9>
 __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
     const float* __restrict__ x, const uint8_t* __restrict__ w, const float* __restrict__ w_scale,
-    const float* __restrict__ bias, float* __restrict__ y, BandGeom g) {
+    Epilogue ep, void* __restrict__ y, BandGeom g) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   constexpr int GB = group_bytes<WT>();
   uint8_t* wl = lds;                                           // [64][g.wrow]
@@ -643,6 +648,8 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
   };
 
   const float s = w_scale ? *w_scale : 1.0f;
+  const float inv_o = epi_inv_scale(ep);
+  uint32_t am = 0;
   const int64_t npix = (int64_t)g.OH * g.OW;
   const int nt_live = min(4, (min(CO_TILE, g.C_out - co0) + 15) >> 4);
   const uint8_t* wfrag = wl + lr * g.wrow + lg * GB;
@@ -703,17 +710,22 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
       for (int t = 0; t < 4; ++t) {
         const int co = co0 + t * 16 + lr;
         if (t >= nt_live || co >= g.C_out) continue;
-        const float bv = bias ? bias[co] : 0.0f;
-        float* dst = y + ((int64_t)n * g.C_out + co) * npix + (int64_t)oh0 * g.OW + p;
-        const f32x4 v = acc[m][t] * s + bv;
+        const EpiChan k = epi_chan(ep, co);
+        const int64_t di = ((int64_t)n * g.C_out + co) * npix + (int64_t)oh0 * g.OW + p;
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          v[i] = epi_value(ep, k, acc[m][t][i], s);
+          if (p + i < P) am = epi_track(am, v[i]);
+        }
         // plain stores: the 64-byte pieces of a line written by neighbouring
         // lanes and waves merge in L2 before they reach HBM
-        if (p + 3 < P && (reinterpret_cast<uintptr_t>(dst) & 15) == 0) {
-          *reinterpret_cast<f32x4*>(dst) = v;
+        if (p + 3 < P && (di & 3) == 0) {
+          epi_store4(ep.out_dtype, y, di, v, inv_o);
         } else {
 #pragma unroll
           for (int i = 0; i < 4; ++i)
-            if (p + i < P) dst[i] = v[i];
+            if (p + i < P) epi_store(ep.out_dtype, y, di + i, v[i], inv_o);
         }
       }
     }
@@ -723,6 +735,7 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
   stage(r0, band, xl);
   __syncthreads();
   compute(band, xl);
+  epi_amax_commit(ep, am);
 }
 
 // Band geometry for this convolution, or false when the band kernel does not
@@ -773,7 +786,7 @@ bool band_geometry(const ConvGeom& cg, BandGeom& b, size_t& lds, int* ipt) {
 }
 
 template <int WT, int IPT, bool K9>
-int launch_band(const float* x, const void* w, const float* w_scale, const float* bias, float* y,
+int launch_band(const float* x, const void* w, const float* w_scale, const Epilogue& ep, void* y,
                 const BandGeom& b, size_t lds, int64_t co_blocks, hipStream_t stream) {
   auto kern = conv2d_band_kernel<WT, IPT, K9>;
   static size_t lds_enabled = 64 * 1024;  // per instantiation: raise the limit once
@@ -786,12 +799,12 @@ int launch_band(const float* x, const void* w, const float* w_scale, const float
   const int64_t blocks = (int64_t)b.N * b.bands;
   if (blocks > 0x7FFFFFFF) return NOVAQ_EINVAL;
   hipLaunchKernelGGL(kern, dim3((unsigned)blocks, (unsigned)co_blocks), dim3(THREADS), lds, stream,
-                     x, static_cast<const uint8_t*>(w), w_scale, bias, y, b);
+                     x, static_cast<const uint8_t*>(w), w_scale, ep, y, b);
   return check_launch();
 }
 
 template <int WT>
-int launch(const float* x, const void* w, const float* w_scale, const float* bias, float* y,
+int launch(const float* x, const void* w, const float* w_scale, const Epilogue& ep, void* y,
            ConvGeom g, hipStream_t stream) {
   {
     BandGeom b;
@@ -801,12 +814,12 @@ int launch(const float* x, const void* w, const float* w_scale, const float* bia
       const int64_t co_blocks = (g.C_out + CO_TILE - 1) / CO_TILE;
       if constexpr (group_bytes<WT>() < 16) {
         if (b.taps == 9 && g.C % 8 == 0 && b.raw_ok) {
-          if (ipt == 1) return launch_band<WT, 1, true>(x, w, w_scale, bias, y, b, lds, co_blocks, stream);
-          return launch_band<WT, 0, true>(x, w, w_scale, bias, y, b, lds, co_blocks, stream);
+          if (ipt == 1) return launch_band<WT, 1, true>(x, w, w_scale, ep, y, b, lds, co_blocks, stream);
+          return launch_band<WT, 0, true>(x, w, w_scale, ep, y, b, lds, co_blocks, stream);
         }
       }
-      if (ipt == 1) return launch_band<WT, 1, false>(x, w, w_scale, bias, y, b, lds, co_blocks, stream);
-      return launch_band<WT, 0, false>(x, w, w_scale, bias, y, b, lds, co_blocks, stream);
+      if (ipt == 1) return launch_band<WT, 1, false>(x, w, w_scale, ep, y, b, lds, co_blocks, stream);
+      return launch_band<WT, 0, false>(x, w, w_scale, ep, y, b, lds, co_blocks, stream);
     }
   }
   // staged rows for a run of PIX_TILE pixels: it spans at most
@@ -842,7 +855,7 @@ int launch(const float* x, const void* w, const float* w_scale, const float* bia
   if (grid > g.tiles) grid = g.tiles;
   if (grid < 1) grid = 1;
   hipLaunchKernelGGL(kern, dim3((unsigned)grid, (unsigned)co_blocks), dim3(THREADS), lds, stream, x,
-                     static_cast<const uint8_t*>(w), w_scale, bias, y, g);
+                     static_cast<const uint8_t*>(w), w_scale, ep, y, g);
   return check_launch();
 }
 
@@ -850,7 +863,7 @@ int launch(const float* x, const void* w, const float* w_scale, const float* bia
 
 int conv2d_launch(const float* x, int64_t N, int64_t C, int64_t H, int64_t W, const void* w_q,
                   int w_dtype, const float* w_scale, int64_t C_out, int KH, int KW, int sh,
-                  int sw, int ph, int pw, int pad_mode, const float* bias, float* y,
+                  int sw, int ph, int pw, int pad_mode, const Epilogue& ep, void* y,
                   hipStream_t stream) {
   const int64_t OH = (H + 2 * (int64_t)ph - KH) / sh + 1;
   const int64_t OW = (W + 2 * (int64_t)pw - KW) / sw + 1;
@@ -870,14 +883,25 @@ int conv2d_launch(const float* x, int64_t N, int64_t C, int64_t H, int64_t W, co
   g.tiles_per_image = (int)((OH * OW + PIX_TILE - 1) / PIX_TILE);
   g.tiles = (int64_t)N * g.tiles_per_image;
   switch (w_dtype) {
-    case E4M3: return launch<E4M3>(x, w_q, w_scale, bias, y, g, stream);
-    case E5M2: return launch<E5M2>(x, w_q, w_scale, bias, y, g, stream);
-    case E2M1: return launch<E2M1>(x, w_q, w_scale, bias, y, g, stream);
-    case BF16: return launch<BF16>(x, w_q, w_scale, bias, y, g, stream);
-    case F16: return launch<F16>(x, w_q, w_scale, bias, y, g, stream);
-    case F32: return launch<F32>(x, w_q, w_scale, bias, y, g, stream);
+    case E4M3: return launch<E4M3>(x, w_q, w_scale, ep, y, g, stream);
+    case E5M2: return launch<E5M2>(x, w_q, w_scale, ep, y, g, stream);
+    case E2M1: return launch<E2M1>(x, w_q, w_scale, ep, y, g, stream);
+    case BF16: return launch<BF16>(x, w_q, w_scale, ep, y, g, stream);
+    case F16: return launch<F16>(x, w_q, w_scale, ep, y, g, stream);
+    case F32: return launch<F32>(x, w_q, w_scale, ep, y, g, stream);
     default: return NOVAQ_EDTYPE;
   }
+}
+
+int conv2d_launch(const float* x, int64_t N, int64_t C, int64_t H, int64_t W, const void* w_q,
+                  int w_dtype, const float* w_scale, int64_t C_out, int KH, int KW, int sh,
+                  int sw, int ph, int pw, int pad_mode, const float* bias, float* y,
+                  hipStream_t stream) {
+  Epilogue ep{};
+  ep.bias = bias;
+  ep.out_dtype = F32;
+  return conv2d_launch(x, N, C, H, W, w_q, w_dtype, w_scale, C_out, KH, KW, sh, sw, ph, pw,
+                       pad_mode, ep, y, stream);
 }
 
 }  // namespace novaq

@@ -25,6 +25,7 @@
 #include <stdint.h>
 
 #include "novaq_convert.h"
+#include "novaq_epilogue.h"
 #include "novaq_internal.h"
 
 namespace novaq {
@@ -134,7 +135,7 @@ __device__ __forceinline__ u32x4 load_x_chunk(const float* __restrict__ x, int r
 template <int WT>
 __global__ __launch_bounds__(THREADS, 1) void linear_kernel(
     const float* __restrict__ x, const uint8_t* __restrict__ w, const float* __restrict__ w_scale,
-    const float* __restrict__ bias, float* __restrict__ y, int M, int N, int K, int tiles_m,
+    Epilogue ep, void* __restrict__ y, int M, int N, int K, int tiles_m,
     int tiles_n, int x_vec, int w_vec) {
   __shared__ __attribute__((aligned(16))) __bf16 As[2][BM * LDS_ROW];
   __shared__ __attribute__((aligned(16))) __bf16 Bs[2][BN * LDS_ROW];
@@ -237,20 +238,27 @@ __global__ __launch_bounds__(THREADS, 1) void linear_kernel(
 
   // epilogue: lane holds column (lane & 31) and rows 8*(r/4) + 4*(lane/32) + r%4
   const float s = w_scale ? *w_scale : 1.0f;
+  const float inv_o = epi_inv_scale(ep);
+  uint32_t am = 0;
 #pragma unroll
   for (int j = 0; j < NT; ++j) {
     const int col = n0 + wn + j * 32 + (lane & 31);
     if (col >= N) continue;
-    const float bv = bias ? bias[col] : 0.0f;
+    const EpiChan k = epi_chan(ep, col);
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (row < M) y[(size_t)row * N + col] = acc[i][j][r] * s + bv;
+        if (row < M) {
+          const float v = epi_value(ep, k, acc[i][j][r], s);
+          am = epi_track(am, v);
+          epi_store(ep.out_dtype, y, (size_t)row * N + col, v, inv_o);
+        }
       }
     }
   }
+  epi_amax_commit(ep, am);
 }
 
 constexpr int A_PITCH = BK + 8;                      // bf16 per A row in LDS
@@ -310,7 +318,7 @@ constexpr int B_PITCH = BK + 8;  // bf16 per W row in LDS (144 B, conflict-free 
 template <int WT, int FBN, int NW, int OCC, int PF>
 __global__ __launch_bounds__(NW * 64, OCC) void linear_pipe_kernel(
     const float* __restrict__ x, const uint8_t* __restrict__ w, const float* __restrict__ w_scale,
-    const float* __restrict__ bias, float* __restrict__ y, int M, int N, int K, int tiles_m,
+    Epilogue ep, void* __restrict__ y, int M, int N, int K, int tiles_m,
     int tiles_n) {
   using WTr = W<WT>;
   constexpr int NTH = NW * 64;
@@ -457,19 +465,27 @@ __global__ __launch_bounds__(NW * 64, OCC) void linear_pipe_kernel(
   }
 
   const float s = w_scale ? *w_scale : 1.0f;
+  const float inv_o = epi_inv_scale(ep);
+  uint32_t am = 0;
 #pragma unroll
   for (int j = 0; j < FNT; ++j) {
     const int col = n0 + wn + j * 32 + (lane & 31);
-    const float bv = bias ? bias[col] : 0.0f;
+    const EpiChan k = epi_chan(ep, col);
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-        __builtin_nontemporal_store(acc[i][j][r] * s + bv, &y[(size_t)row * N + col]);
+        const float v = epi_value(ep, k, acc[i][j][r], s);
+        am = epi_track(am, v);
+        if (ep.out_dtype == F32)
+          __builtin_nontemporal_store(v, reinterpret_cast<float*>(y) + (size_t)row * N + col);
+        else
+          epi_store(ep.out_dtype, y, (size_t)row * N + col, v, inv_o);
       }
     }
   }
+  epi_amax_commit(ep, am);
 }
 
 // ---------------------------------------------------------------------------
@@ -494,7 +510,7 @@ struct Wide {
 template <int WT>
 __global__ __launch_bounds__(512, 1) void linear_wide_kernel(
     const float* __restrict__ x, const uint8_t* __restrict__ w, const float* __restrict__ w_scale,
-    const float* __restrict__ bias, float* __restrict__ y, int M, int N, int K, int tiles_m,
+    Epilogue ep, void* __restrict__ y, int M, int N, int K, int tiles_m,
     int tiles_n) {
   using F = Wide<WT>;
   constexpr int KB = F::KB;
@@ -637,24 +653,32 @@ __global__ __launch_bounds__(512, 1) void linear_wide_kernel(
   }
 
   const float s = w_scale ? *w_scale : 1.0f;
+  const float inv_o = epi_inv_scale(ep);
+  uint32_t am = 0;
 #pragma unroll
   for (int j = 0; j < FNT; ++j) {
     const int col = n0 + wn + j * 32 + (lane & 31);
-    const float bv = bias ? bias[col] : 0.0f;
+    const EpiChan k = epi_chan(ep, col);
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-        __builtin_nontemporal_store(acc[i][j][r] * s + bv, &y[(size_t)row * N + col]);
+        const float v = epi_value(ep, k, acc[i][j][r], s);
+        am = epi_track(am, v);
+        if (ep.out_dtype == F32)
+          __builtin_nontemporal_store(v, reinterpret_cast<float*>(y) + (size_t)row * N + col);
+        else
+          epi_store(ep.out_dtype, y, (size_t)row * N + col, v, inv_o);
       }
     }
   }
+  epi_amax_commit(ep, am);
 }
 
 template <int WT>
 int launch(const float* x, int64_t M, int64_t K, const void* w, const float* w_scale,
-           const float* bias, int64_t N, float* y, hipStream_t stream) {
+           const Epilogue& ep, int64_t N, void* y, hipStream_t stream) {
   const int64_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
   const int64_t T = tiles_m * tiles_n;
   if (T > 0x7FFFFFFF || M > 0x7FFFFFFF || N > 0x7FFFFFFF || K > 0x7FFFFFFF) return NOVAQ_EINVAL;
@@ -664,7 +688,7 @@ int launch(const float* x, int64_t M, int64_t K, const void* w, const float* w_s
     // tile byte sizes (BM * K * 4 for x) must fit the 31-bit buffer range
     if (rows_whole && N % 256 == 0 && K % 128 == 0 && K <= (1 << 21)) {
       hipLaunchKernelGGL((linear_wide_kernel<WT>), dim3((unsigned)(tiles_m * (N / 256))),
-                         dim3(512), 0, stream, x, wq, w_scale, bias, y, (int)M, (int)N, (int)K,
+                         dim3(512), 0, stream, x, wq, w_scale, ep, y, (int)M, (int)N, (int)K,
                          (int)tiles_m, (int)(N / 256));
       return check_launch();
     }
@@ -673,20 +697,20 @@ int launch(const float* x, int64_t M, int64_t K, const void* w, const float* w_s
     if (rows_whole && N % 256 == 0 && K % BK == 0) {
       hipLaunchKernelGGL((linear_pipe_kernel<WT, 256, 8, 1, 3>),
                          dim3((unsigned)(tiles_m * (N / 256))), dim3(512), 0, stream, x, wq,
-                         w_scale, bias, y, (int)M, (int)N, (int)K, (int)tiles_m, (int)(N / 256));
+                         w_scale, ep, y, (int)M, (int)N, (int)K, (int)tiles_m, (int)(N / 256));
       return check_launch();
     }
     if (rows_whole && N % 128 == 0 && K % BK == 0) {
       hipLaunchKernelGGL((linear_pipe_kernel<WT, 128, 4, 2, 2>),
                          dim3((unsigned)(tiles_m * (N / 128))), dim3(256), 0, stream, x, wq,
-                         w_scale, bias, y, (int)M, (int)N, (int)K, (int)tiles_m, (int)(N / 128));
+                         w_scale, ep, y, (int)M, (int)N, (int)K, (int)tiles_m, (int)(N / 128));
       return check_launch();
     }
   }
   const int x_vec = (K % 4) == 0;
   const int w_vec = ((K * W<WT>::bits / 8) % 16) == 0 && (K * W<WT>::bits) % 8 == 0;
   hipLaunchKernelGGL((linear_kernel<WT>), dim3((unsigned)T), dim3(THREADS), 0, stream, x, wq,
-                     w_scale, bias, y, (int)M, (int)N, (int)K, (int)tiles_m, (int)tiles_n, x_vec,
+                     w_scale, ep, y, (int)M, (int)N, (int)K, (int)tiles_m, (int)tiles_n, x_vec,
                      w_vec);
   return check_launch();
 }
@@ -694,17 +718,26 @@ int launch(const float* x, int64_t M, int64_t K, const void* w, const float* w_s
 }  // namespace
 
 int linear_launch(const float* x, int64_t N, int64_t D_in, const void* w_q, int w_dtype,
-                  const float* w_scale, const float* bias, int64_t D_out, float* y,
+                  const float* w_scale, const Epilogue& ep, int64_t D_out, void* y,
                   hipStream_t stream) {
   switch (w_dtype) {
-    case E4M3: return launch<E4M3>(x, N, D_in, w_q, w_scale, bias, D_out, y, stream);
-    case E5M2: return launch<E5M2>(x, N, D_in, w_q, w_scale, bias, D_out, y, stream);
-    case E2M1: return launch<E2M1>(x, N, D_in, w_q, w_scale, bias, D_out, y, stream);
-    case BF16: return launch<BF16>(x, N, D_in, w_q, w_scale, bias, D_out, y, stream);
-    case F16: return launch<F16>(x, N, D_in, w_q, w_scale, bias, D_out, y, stream);
-    case F32: return launch<F32>(x, N, D_in, w_q, w_scale, bias, D_out, y, stream);
+    case E4M3: return launch<E4M3>(x, N, D_in, w_q, w_scale, ep, D_out, y, stream);
+    case E5M2: return launch<E5M2>(x, N, D_in, w_q, w_scale, ep, D_out, y, stream);
+    case E2M1: return launch<E2M1>(x, N, D_in, w_q, w_scale, ep, D_out, y, stream);
+    case BF16: return launch<BF16>(x, N, D_in, w_q, w_scale, ep, D_out, y, stream);
+    case F16: return launch<F16>(x, N, D_in, w_q, w_scale, ep, D_out, y, stream);
+    case F32: return launch<F32>(x, N, D_in, w_q, w_scale, ep, D_out, y, stream);
     default: return NOVAQ_EDTYPE;
   }
+}
+
+int linear_launch(const float* x, int64_t N, int64_t D_in, const void* w_q, int w_dtype,
+                  const float* w_scale, const float* bias, int64_t D_out, float* y,
+                  hipStream_t stream) {
+  Epilogue ep{};
+  ep.bias = bias;
+  ep.out_dtype = F32;
+  return linear_launch(x, N, D_in, w_q, w_dtype, w_scale, ep, D_out, y, stream);
 }
 
 }  // namespace novaq

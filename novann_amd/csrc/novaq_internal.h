@@ -25,13 +25,25 @@ int cast_launch(const void* src, int st, void* dst, int dt, int64_t n, int smode
 int amax_launch(const void* x, int dt, int64_t n, float* amax, hipStream_t stream);
 int scale_from_amax_launch(const float* amax, int dt, float* scale, hipStream_t stream);
 
+struct Epilogue;  // novaq_epilogue.h
+
 int linear_launch(const float* x, int64_t N, int64_t D_in, const void* w_q, int w_dtype,
                   const float* w_scale, const float* bias, int64_t D_out, float* y,
+                  hipStream_t stream);
+int linear_launch(const float* x, int64_t N, int64_t D_in, const void* w_q, int w_dtype,
+                  const float* w_scale, const Epilogue& ep, int64_t D_out, void* y,
                   hipStream_t stream);
 int conv2d_launch(const float* x, int64_t N, int64_t C, int64_t H, int64_t W, const void* w_q,
                   int w_dtype, const float* w_scale, int64_t C_out, int KH, int KW, int sh,
                   int sw, int ph, int pw, int pad_mode, const float* bias, float* y,
                   hipStream_t stream);
+int conv2d_launch(const float* x, int64_t N, int64_t C, int64_t H, int64_t W, const void* w_q,
+                  int w_dtype, const float* w_scale, int64_t C_out, int KH, int KW, int sh,
+                  int sw, int ph, int pw, int pad_mode, const Epilogue& ep, void* y,
+                  hipStream_t stream);
+
+// Sets count 32-bit words at p to v (a kernel, so it may be captured in graphs).
+int fill_u32_launch(uint32_t* p, uint32_t v, int count, hipStream_t stream);
 
 int transpose_launch(const void* src, int st, int64_t rows, int64_t cols, void* dst, int dt,
                      hipStream_t stream);

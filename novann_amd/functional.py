@@ -11,7 +11,9 @@ path.
 """
 from __future__ import annotations
 
-from typing import Optional, Tuple, Union
+import ctypes
+from dataclasses import dataclass
+from typing import Any, Optional, Tuple, Union
 
 import numpy as np
 import torch
@@ -61,12 +63,101 @@ def _stream(dev: torch.device) -> int:
     return torch.cuda.current_stream(dev).cuda_stream
 
 
-def linear(input, weight, bias: Optional[Parameters] = None):
+OUT_STORAGE = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16,
+               "e4m3": torch.float8_e4m3fn, "e5m2": torch.float8_e5m2}
+
+
+@dataclass
+class Epilogue:
+    """Fused epilogue of ``linear`` / ``conv2d`` (struct novaq_epilogue).
+
+    Per output channel c: v = v * channel_mul[c] + channel_add[c] (each step
+    only when given), then ReLU as novann's ``v * (v > 0)``
+    (novann/functional.py:8-22) when ``relu``, then the store in
+    ``out_dtype``: 'f32', 'f16' / 'bf16' (round to nearest even) or
+    'e4m3' / 'e5m2' as encode(v / s) with ``out_scale`` s (a one-element fp32
+    device tensor, default 1).  ``out_amax`` (a one-element fp32 device
+    tensor) receives max |v| before the cast.  channel_mul / channel_add are
+    arrays or tensors of C_out values."""
+    channel_mul: Any = None
+    channel_add: Any = None
+    relu: bool = False
+    out_dtype: str = "f32"
+    out_scale: Optional[torch.Tensor] = None
+    out_amax: Optional[torch.Tensor] = None
+
+    @classmethod
+    def batchnorm(cls, gamma, beta, running_mean, running_var, eps: float = 1e-5,
+                  **kw) -> "Epilogue":
+        """Eval-mode BatchNorm (batchnorm2d.py:98-102, batchnorm1d.py:138-149)
+        gamma * (v - mean) / sqrt(var + eps) + beta, folded in fp64 into
+        channel_mul = gamma / sqrt(var + eps), channel_add = beta - mean *
+        channel_mul, rounded to fp32."""
+        def flat(a):
+            a = a.data if isinstance(a, Parameters) else a
+            if isinstance(a, torch.Tensor):
+                a = a.detach().cpu().numpy()
+            return np.asarray(a, dtype=np.float64).reshape(-1)
+        g, b, m, v = flat(gamma), flat(beta), flat(running_mean), flat(running_var)
+        mul = g / np.sqrt(v + eps)
+        return cls(channel_mul=mul.astype(np.float32), channel_add=(b - m * mul).astype(np.float32),
+                   **kw)
+
+
+def _epilogue_args(ep: Optional[Epilogue], channels: int, dev: torch.device):
+    """(ctypes struct or None, output storage dtype, tensors to keep alive)."""
+    if ep is None:
+        return None, torch.float32, []
+    if ep.out_dtype not in OUT_STORAGE:
+        raise TypeError(f"epilogue out_dtype must be one of {tuple(OUT_STORAGE)}")
+    keep = []
+
+    def chan(a, what):
+        if a is None:
+            return None
+        t, _ = _to_device_f32(a, what)
+        t = t.reshape(-1).contiguous()
+        if t.numel() != channels:
+            raise ValueError(f"epilogue {what} has {t.numel()} values, expected {channels}")
+        keep.append(t)
+        return t.data_ptr()
+
+    def scalar(t, what):
+        if t is None:
+            return None
+        if not isinstance(t, torch.Tensor) or not t.is_cuda or t.dtype != torch.float32:
+            raise TypeError(f"epilogue {what} must be a float32 device tensor")
+        return t.data_ptr()
+
+    st = _lib.Epilogue(chan(ep.channel_mul, "channel_mul"), chan(ep.channel_add, "channel_add"),
+                       scalar(ep.out_scale, "out_scale"), scalar(ep.out_amax, "out_amax"),
+                       1 if ep.relu else 0, DTYPES[ep.out_dtype])
+    return st, OUT_STORAGE[ep.out_dtype], keep
+
+
+def _finish(y: torch.Tensor, ep: Optional[Epilogue], was_numpy: bool):
+    """The caller-facing output: ndarray for numpy callers with f32 / f16
+    output; FP8 outputs as quant.Quantized (codes + the scale they carry)."""
+    from . import quant
+    if ep is not None and ep.out_dtype in ("e4m3", "e5m2"):
+        scale = ep.out_scale if ep.out_scale is not None else torch.ones(
+            1, dtype=torch.float32, device=y.device)
+        return quant.Quantized(data=y.reshape(-1), shape=tuple(y.shape), dtype=ep.out_dtype,
+                               scale=scale, amax=ep.out_amax)
+    if was_numpy and y.dtype in (torch.float32, torch.float16):
+        return y.cpu().numpy()
+    return y
+
+
+def linear(input, weight, bias: Optional[Parameters] = None, *,
+           epilogue: Optional[Epilogue] = None):
     """y = input @ W^T + b  (novann/functional.py:147-163).
 
     input (N, D_in); weight (D_out, D_in) as Parameters or
     QuantizedParameters; bias (1, D_out) Parameters or None.  Returns
-    (N, D_out) fp32: an ndarray when input was an ndarray."""
+    (N, D_out) fp32: an ndarray when input was an ndarray.  ``epilogue``
+    (keyword only, not in the reference) fuses what follows the layer (eval
+    BatchNorm1d, ReLU, a cast of y) into the product; see Epilogue."""
     x, was_numpy = _to_device_f32(input, "input")
     if x.dim() != 2:
         raise ValueError(f"linear expects a 2-D input, got shape {tuple(x.shape)}")
@@ -80,6 +171,14 @@ def linear(input, weight, bias: Optional[Parameters] = None):
     b = _bias_arg(bias, x.device)
     if b is not None and b.numel() != D_out:
         raise ValueError(f"bias has {b.numel()} values, expected {D_out}")
+    if epilogue is not None:
+        st, ydt, keep = _epilogue_args(epilogue, D_out, x.device)
+        y = torch.empty((N, D_out), dtype=ydt, device=x.device)
+        check(_lib.load().novaq_linear_forward_ex(
+            x.data_ptr(), DTYPES["f32"], None, N, D_in, w.data_ptr(), wdt,
+            None if ws is None else ws.data_ptr(), None if b is None else b.data_ptr(), D_out,
+            ctypes.byref(st), y.data_ptr(), _stream(x.device)), "linear")
+        return _finish(y, epilogue, was_numpy)
     y = torch.empty((N, D_out), dtype=torch.float32, device=x.device)
     check(_lib.load().novaq_linear_forward(
         x.data_ptr(), N, D_in, w.data_ptr(), wdt, None if ws is None else ws.data_ptr(),
@@ -142,14 +241,15 @@ def _pair(v: IntPair) -> Tuple[int, int]:
 
 def conv2d(input, weight, kernel_size: IntPair, stride: IntPair = 1, padding: IntPair = 0,
            *, bias: Optional[Parameters] = None, padding_mode: str = "zeros",
-           extras: bool = False):
+           extras: bool = False, epilogue: Optional[Epilogue] = None):
     """2-D cross-correlation (novann/functional.py:275-385).
 
     input (N, C, H, W); weight (C_out, C, KH, KW); returns (N, C_out, OH, OW)
     fp32 with OH = (H + 2ph - KH)//sh + 1.  The reference materialises the
     im2col matrix; this computes the same values with implicit im2col, so
     ``extras=True`` (which asks for that matrix, a training-time cache) is not
-    available."""
+    available.  ``epilogue`` (not in the reference) fuses eval BatchNorm2d,
+    ReLU and a cast of y into the convolution; see Epilogue."""
     KH, KW = _pair(kernel_size)
     ph, pw = _pair(padding)
     sh, sw = _pair(stride)
@@ -177,6 +277,15 @@ def conv2d(input, weight, kernel_size: IntPair, stride: IntPair = 1, padding: In
     b = _bias_arg(bias, x.device)
     if b is not None and b.numel() != C_out:
         raise ValueError(f"bias has {b.numel()} values, expected {C_out}")
+    if epilogue is not None:
+        st, ydt, keep = _epilogue_args(epilogue, C_out, x.device)
+        y = torch.empty((N, C_out, OH, OW), dtype=ydt, device=x.device)
+        check(_lib.load().novaq_conv2d_forward_ex(
+            x.data_ptr(), DTYPES["f32"], None, N, C, H, W, w.data_ptr(), wdt,
+            None if ws is None else ws.data_ptr(), C_out, KH, KW, sh, sw, ph, pw,
+            PAD_MODES[padding_mode], None if b is None else b.data_ptr(), ctypes.byref(st),
+            y.data_ptr(), _stream(x.device)), "conv2d")
+        return _finish(y, epilogue, was_numpy)
     y = torch.empty((N, C_out, OH, OW), dtype=torch.float32, device=x.device)
     check(_lib.load().novaq_conv2d_forward(
         x.data_ptr(), N, C, H, W, w.data_ptr(), wdt, None if ws is None else ws.data_ptr(),

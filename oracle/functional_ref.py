@@ -11,6 +11,10 @@ Restates, with this build's own code, the arithmetic of
     grad (C_out, N*OH*OW) @ col.T, grad_bias = row sums, grad_col = w_col.T @
     grad scattered with np.add.at into a zero-padded (N, C, H_p, W_p) buffer
     whose border is then cropped;
+  - ``novann.functional.relu`` (novann/functional.py:8-22): ``x * (x > 0)``;
+  - eval-mode ``BatchNorm2d`` / ``BatchNorm1d`` (batchnorm2d.py:98-102,
+    batchnorm1d.py:138-149): ``gamma * (x - mean) / sqrt(var + eps) + beta``
+    per channel, in fp64 as the reference's float64 running statistics make it;
   - ``novann.functional.conv2d``  (novann/functional.py:275-385):
     pad with numpy.pad (constant / reflect / edge / wrap, :325-344), take
     (N, C, OH, OW, KH, KW) windows with ``as_strided`` (:358-364), reorder
@@ -115,3 +119,37 @@ def conv2d_backward(grad: np.ndarray, x: np.ndarray, w: np.ndarray, stride=(1, 1
     grad_col = w.reshape(C_out, -1).T @ g
     grad_input = col2im(grad_col, x.shape, KH, KW, stride, padding)
     return grad_input, grad_weight, grad_bias
+
+
+def relu(x: np.ndarray) -> np.ndarray:
+    """functional.py:19-20: the mask as x's dtype, then a multiply (negative
+    values give -0, NaN stays NaN, -Inf gives NaN)."""
+    return x * (x > 0).astype(x.dtype, copy=False)
+
+
+def batchnorm_eval(x: np.ndarray, gamma, beta, running_mean, running_var, eps: float = 1e-5,
+                   axis: int = 1) -> np.ndarray:
+    """Eval-mode batch norm over channel axis ``axis`` in fp64
+    (batchnorm2d.py:98-102; batchnorm1d.py:138-149 with axis 1 of a 2-D x)."""
+    shape = [1] * x.ndim
+    shape[axis] = -1
+    r = lambda a: np.asarray(a, dtype=np.float64).reshape(shape)  # noqa: E731
+    x_hat = (x.astype(np.float64) - r(running_mean)) / np.sqrt(r(running_var) + eps)
+    return r(gamma) * x_hat + r(beta)
+
+
+def epilogue_f32(y: np.ndarray, mul=None, add=None, do_relu: bool = False,
+                 axis: int = 1) -> np.ndarray:
+    """The fused epilogue's fp32 steps on an fp32 product output y (each one
+    rounded fp32 operation, in the kernels' order): y * mul[c], + add[c],
+    then relu."""
+    shape = [1] * y.ndim
+    shape[axis] = -1
+    v = np.asarray(y, dtype=np.float32)
+    if mul is not None:
+        v = v * np.asarray(mul, np.float32).reshape(shape)
+    if add is not None:
+        v = v + np.asarray(add, np.float32).reshape(shape)
+    if do_relu:
+        v = relu(v)
+    return v

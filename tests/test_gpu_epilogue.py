@@ -1,0 +1,255 @@
+"""Fused epilogues of the forward products on the GPU (through the C ABI).
+
+Bit-exact checks: the epilogue's fp32 steps equal the oracle's fp32 restatement
+applied to the unfused kernel output (every Linear and Conv2d kernel path);
+bf16 / f16 / FP8 stores equal the oracle cast of those fp32 values; the output
+amax equals max |v|.  Reference-path check: conv / linear -> eval BatchNorm
+(fp64, the reference's formula) -> ReLU within normwise 1e-2 of the fused
+result (the BASELINE tolerance of the products)."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from oracle import functional_ref as R
+from novann_amd import _lib
+from novann_amd import functional as F
+from novann_amd.module import QuantizedParameters
+from tests.gpu_util import to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2
+OUT = {"f32": O.F32, "f16": O.F16, "bf16": O.BF16, "e4m3": O.E4M3, "e5m2": O.E5M2}
+TORCH_OUT = {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16,
+             "e4m3": torch.uint8, "e5m2": torch.uint8}
+
+
+def stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def quantized_codes(w, wdt, rng):
+    """Raw codes (device) of a weight, its scale tensor and the dequantized fp64 matrix."""
+    if wdt in ("e4m3", "e5m2", "e2m1"):
+        c = {"e4m3": O.E4M3, "e5m2": O.E5M2, "e2m1": O.E2M1}[wdt]
+        s = O.scale_from_amax(O.amax(w), c)
+        codes = O.cast(w.reshape(-1), O.F32, c, scale=s)
+        deq = O.cast(codes, c, O.F32, n=w.size, scale=s).reshape(w.shape)
+        return to_dev(codes, c), torch.tensor([s], dtype=torch.float32, device="cuda"), deq
+    if wdt in ("bf16", "f16"):
+        c = O.BF16 if wdt == "bf16" else O.F16
+        codes = O.cast(w.reshape(-1), O.F32, c)
+        return to_dev(codes, c), None, O.cast(codes, c, O.F32).reshape(w.shape)
+    return torch.from_numpy(w).cuda(), None, w
+
+
+class Epi:
+    """ctypes epilogue + the device tensors it points at."""
+
+    def __init__(self, C, rng, relu=True, out="f32", out_scale=None, amax=True, mul=True,
+                 add=True, mul_vals=None, add_vals=None):
+        self.mul = None if not mul else torch.from_numpy(
+            mul_vals if mul_vals is not None
+            else rng.uniform(-2.0, 2.0, C).astype(np.float32)).cuda()
+        self.add = None if not add else torch.from_numpy(
+            add_vals if add_vals is not None
+            else rng.standard_normal(C).astype(np.float32)).cuda()
+        self.scale = None if out_scale is None else torch.tensor([out_scale], device="cuda")
+        self.amax = torch.full((1,), 123.0, device="cuda") if amax else None
+        p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+        self.st = _lib.Epilogue(p(self.mul), p(self.add), p(self.scale), p(self.amax),
+                                1 if relu else 0, _lib.DTYPES[out])
+        self.relu, self.out = relu, out
+
+    def host(self):
+        return (None if self.mul is None else self.mul.cpu().numpy(),
+                None if self.add is None else self.add.cpu().numpy())
+
+
+def linear_ex(x, wd, wdt, ws, D_out, ep=None, bias=None):
+    N, D_in = x.shape
+    xd = torch.from_numpy(x).cuda()
+    out = ep.out if ep is not None else "f32"
+    y = torch.empty((N, D_out), dtype=TORCH_OUT[out], device="cuda")
+    bd = None if bias is None else torch.from_numpy(bias).cuda()
+    _lib.check(_lib.load().novaq_linear_forward_ex(
+        xd.data_ptr(), O.F32, None, N, D_in, wd.data_ptr(), _lib.DTYPES[wdt],
+        None if ws is None else ws.data_ptr(), None if bd is None else bd.data_ptr(), D_out,
+        None if ep is None else ctypes.byref(ep.st), y.data_ptr(), stream()), "linear_ex")
+    torch.cuda.synchronize()
+    return to_host(y).reshape(N, D_out)
+
+
+def conv_ex(x, wd, wdt, ws, wshape, stride, pad, mode="zeros", ep=None, bias=None):
+    N, C, H, W = x.shape
+    C_out, _, KH, KW = wshape
+    OH, OW = (H + 2 * pad[0] - KH) // stride[0] + 1, (W + 2 * pad[1] - KW) // stride[1] + 1
+    xd = torch.from_numpy(x).cuda()
+    out = ep.out if ep is not None else "f32"
+    y = torch.empty((N, C_out, OH, OW), dtype=TORCH_OUT[out], device="cuda")
+    bd = None if bias is None else torch.from_numpy(bias).cuda()
+    _lib.check(_lib.load().novaq_conv2d_forward_ex(
+        xd.data_ptr(), O.F32, None, N, C, H, W, wd.data_ptr(), _lib.DTYPES[wdt],
+        None if ws is None else ws.data_ptr(), C_out, KH, KW, stride[0], stride[1], pad[0],
+        pad[1], _lib.PAD_MODES[mode], None if bd is None else bd.data_ptr(),
+        None if ep is None else ctypes.byref(ep.st), y.data_ptr(), stream()), "conv2d_ex")
+    torch.cuda.synchronize()
+    return to_host(y).reshape(N, C_out, OH, OW)
+
+
+def check_all_outputs(run, y0_bits, C, rng, axis=1):
+    """Epilogue fp32 bit-exact vs the oracle on the unfused output, amax exact,
+    and every narrower store equal to the oracle cast of the fp32 values."""
+    y0 = y0_bits.view(np.float32)
+    ep = Epi(C, rng)
+    y1 = run(ep).view(np.float32)
+    mul, add = ep.host()
+    want = R.epilogue_f32(y0, mul, add, True, axis=axis)
+    assert np.array_equal(y1.view(np.uint32), want.view(np.uint32)), \
+        f"{np.count_nonzero(y1.view(np.uint32) != want.view(np.uint32))} epilogue mismatches"
+    am = float(ep.amax.cpu()[0])
+    assert am == float(np.abs(want).max())
+    flat = want.reshape(-1)
+    for out in ("bf16", "f16"):
+        got = run(Epi(C, rng, out=out, mul_vals=mul, add_vals=add, amax=False)).reshape(-1)
+        assert np.array_equal(got, O.cast(flat, O.F32, OUT[out])), out
+    for out in ("e4m3", "e5m2"):
+        s = O.scale_from_amax(np.float32(am), OUT[out])
+        got = run(Epi(C, rng, out=out, out_scale=s, mul_vals=mul, add_vals=add,
+                      amax=False)).reshape(-1)
+        assert np.array_equal(got, O.cast(flat, O.F32, OUT[out], scale=s)), out
+
+
+LINEAR_CASES = [
+    ("e4m3", 256, 512, 256),   # linear_wide_kernel
+    ("e2m1", 128, 256, 512),   # linear_wide_kernel, FP4
+    ("bf16", 128, 128, 256),   # linear_pipe_kernel
+    ("f16", 128, 64, 128),     # linear_pipe_kernel, 128-wide tiles
+    ("e5m2", 33, 70, 46),      # linear_kernel (ragged)
+    ("f32", 64, 96, 40),       # linear_kernel (fp32 weights)
+]
+
+
+@pytest.mark.parametrize("wdt,N,D_in,D_out", LINEAR_CASES)
+def test_linear_epilogue_bit_exact(wdt, N, D_in, D_out):
+    print(f"linear epilogue {wdt} {N}x{D_in}x{D_out}", flush=True)
+    rng = np.random.default_rng(N + D_in + D_out)
+    x = rng.standard_normal((N, D_in)).astype(np.float32)
+    w = (rng.standard_normal((D_out, D_in)) * np.sqrt(2.0 / D_in)).astype(np.float32)
+    bias = rng.standard_normal(D_out).astype(np.float32)
+    wd, ws, _ = quantized_codes(w, wdt, rng)
+    y0 = linear_ex(x, wd, wdt, ws, D_out, None, bias)
+    check_all_outputs(lambda ep: linear_ex(x, wd, wdt, ws, D_out, ep, bias), y0, D_out, rng)
+
+
+CONV_CASES = [
+    # wdt, (N, C, H, W), C_out, (KH, KW), stride, pad, mode
+    ("e2m1", (3, 8, 12, 12), 16, (3, 3), (1, 1), (1, 1), "zeros"),     # band, K9
+    ("e4m3", (2, 3, 10, 11), 20, (5, 5), (1, 1), (2, 2), "reflect"),   # band, generic regroup
+    ("bf16", (2, 4, 9, 9), 70, (3, 3), (2, 2), (1, 1), "replicate"),  # band, 2 co blocks
+    ("e5m2", (2, 65, 7, 7), 24, (3, 3), (1, 1), (1, 1), "circular"),  # conv2d_kernel (C > 64)
+    ("f32", (1, 2, 6, 301), 5, (1, 3), (1, 1), (0, 1), "zeros"),      # conv2d_kernel (OW > 256)
+]
+
+
+@pytest.mark.parametrize("wdt,xs,C_out,k,stride,pad,mode", CONV_CASES)
+def test_conv2d_epilogue_bit_exact(wdt, xs, C_out, k, stride, pad, mode):
+    print(f"conv epilogue {wdt} {xs} -> {C_out} k={k} s={stride} p={pad} {mode}", flush=True)
+    rng = np.random.default_rng(sum(xs) + C_out)
+    x = rng.standard_normal(xs).astype(np.float32)
+    wshape = (C_out, xs[1]) + k
+    w = (rng.standard_normal(wshape) * np.sqrt(2.0 / (xs[1] * k[0] * k[1]))).astype(np.float32)
+    bias = rng.standard_normal(C_out).astype(np.float32)
+    wd, ws, _ = quantized_codes(w, wdt, rng)
+    y0 = conv_ex(x, wd, wdt, ws, wshape, stride, pad, mode, None, bias)
+    check_all_outputs(lambda ep: conv_ex(x, wd, wdt, ws, wshape, stride, pad, mode, ep, bias),
+                      y0, C_out, rng)
+
+
+def test_relu_special_values():
+    """ReLU keeps the reference's rules: -0 for negative values, NaN for NaN
+    and -Inf, +Inf kept; the amax ignores NaN and takes Inf."""
+    rng = np.random.default_rng(11)
+    N, D_in, D_out = 64, 64, 8
+    x = rng.standard_normal((N, D_in)).astype(np.float32)
+    w = rng.standard_normal((D_out, D_in)).astype(np.float32) * 0.1
+    wd, ws, _ = quantized_codes(w, "f32", rng)
+    add = np.array([np.inf, -np.inf, np.nan, -1e30, 1e30, 0.0, -0.0, -5.0], np.float32)
+    y0 = linear_ex(x, wd, "f32", ws, D_out).view(np.float32)
+    ep = Epi(D_out, rng, mul=False, add_vals=add)
+    y1 = linear_ex(x, wd, "f32", ws, D_out, ep).view(np.float32)
+    want = R.epilogue_f32(y0, None, add, True, axis=1)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(y1), nan)
+    assert np.array_equal(y1[~nan].view(np.uint32), want[~nan].view(np.uint32))
+    assert np.signbit(y1[:, 3]).all() and (y1[:, 3] == 0).all()  # -1e30 -> -0
+    assert np.isnan(y1[:, 1]).all()                               # -inf * 0
+    assert float(ep.amax.cpu()[0]) == np.inf
+
+
+def bn_params(C, rng):
+    return (rng.uniform(0.5, 1.5, C), rng.standard_normal(C) * 0.1, rng.standard_normal(C) * 0.2,
+            rng.uniform(0.5, 2.0, C))
+
+
+@pytest.mark.parametrize("wdt", ["e2m1", "e4m3"])
+def test_conv_bn_relu_matches_reference_path(wdt):
+    """Conv2d -> BatchNorm2d (eval) -> ReLU of novann main.py's first block on
+    an MNIST-shaped batch, fused, against the reference's formulas in fp64."""
+    rng = np.random.default_rng(21)
+    x = rng.uniform(0, 1, (64, 1, 28, 28)).astype(np.float32)
+    w = (rng.standard_normal((16, 1, 3, 3)) * np.sqrt(2.0 / 9)).astype(np.float32)
+    q = QuantizedParameters.from_float(w, wdt)
+    wdeq = q.dequantize().cpu().numpy().astype(np.float64).reshape(w.shape)
+    g, b, m, v = bn_params(16, rng)
+    y = F.conv2d(torch.from_numpy(x).cuda(), q, 3, 1, 1,
+                 epilogue=F.Epilogue.batchnorm(g, b, m, v, 1e-5, relu=True))
+    ref = R.relu(R.batchnorm_eval(R.conv2d(x.astype(np.float64), wdeq, (1, 1), (1, 1)), g, b, m, v))
+    got = y.cpu().numpy()
+    assert np.abs(got - ref).max() / np.abs(ref).max() <= TOL
+
+
+def test_linear_bn_relu_bf16_store_matches_reference_path():
+    """Linear -> BatchNorm1d (eval) -> ReLU with a bf16 output (main.py's
+    classifier block), against the reference's formulas in fp64."""
+    rng = np.random.default_rng(22)
+    x = rng.standard_normal((256, 512)).astype(np.float32)
+    w = (rng.standard_normal((256, 512)) * np.sqrt(2.0 / 512)).astype(np.float32)
+    q = QuantizedParameters.from_float(w, "e4m3")
+    wdeq = q.dequantize().cpu().numpy().astype(np.float64).reshape(w.shape)
+    g, b, m, v = bn_params(256, rng)
+    y = F.linear(torch.from_numpy(x).cuda(), q,
+                 epilogue=F.Epilogue.batchnorm(g, b, m, v, 1e-5, relu=True, out_dtype="bf16"))
+    assert y.dtype == torch.bfloat16 and y.shape == (256, 256)
+    ref = R.relu(R.batchnorm_eval(R.linear(x.astype(np.float64), wdeq), g, b, m, v))
+    got = y.float().cpu().numpy()
+    assert np.abs(got - ref).max() / np.abs(ref).max() <= TOL
+
+
+def test_fp8_store_returns_quantized_with_its_scale():
+    rng = np.random.default_rng(23)
+    x = rng.standard_normal((128, 256)).astype(np.float32)
+    w = (rng.standard_normal((256, 256)) * 0.05).astype(np.float32)
+    q = QuantizedParameters.from_float(w, "e4m3")
+    amax = torch.zeros(1, device="cuda")
+    y32 = F.linear(torch.from_numpy(x).cuda(), q, epilogue=F.Epilogue(relu=True, out_amax=amax))
+    scale = torch.tensor([float(amax.cpu()[0]) / 448.0], device="cuda")
+    y8 = F.linear(torch.from_numpy(x).cuda(), q,
+                  epilogue=F.Epilogue(relu=True, out_dtype="e4m3", out_scale=scale))
+    assert y8.dtype == "e4m3" and y8.shape == (128, 256)
+    want = O.cast(y32.cpu().numpy().reshape(-1), O.F32, O.E4M3, scale=float(scale.cpu()[0]))
+    assert np.array_equal(to_host(y8.data), want)
+
+
+def test_epilogue_rejects_bad_arguments():
+    lib = _lib.load()
+    x = torch.zeros((4, 8), device="cuda")
+    w = torch.zeros((8, 8), device="cuda")
+    y = torch.zeros((4, 8), device="cuda")
+    bad = _lib.Epilogue(None, None, None, None, 0, _lib.DTYPES["e2m1"])
+    assert lib.novaq_linear_forward_ex(x.data_ptr(), O.F32, None, 4, 8, w.data_ptr(), O.F32,
+                                       None, None, 8, ctypes.byref(bad), y.data_ptr(),
+                                       stream()) == _lib.EDTYPE
