@@ -188,9 +188,7 @@ int novaq_linear_forward_ex(const void* x, int x_dtype, const float* x_scale, in
                             int64_t D_in, const void* w_q, int w_dtype, const float* w_scale,
                             const float* bias, int64_t D_out, const novaq_epilogue* epi,
                             void* y, void* stream) {
-  if (!valid_dtype(w_dtype) || !valid_dtype(x_dtype)) return NOVAQ_EDTYPE;
-  if (x_dtype != F32) return NOVAQ_EDTYPE;
-  (void)x_scale;
+  if (!valid_dtype(w_dtype) || !valid_dtype(x_dtype) || x_dtype == E2M1) return NOVAQ_EDTYPE;
   if (N < 0 || D_in < 0 || D_out < 0) return NOVAQ_EINVAL;
   if (epi && (epi->out_dtype == E2M1 || !valid_dtype(epi->out_dtype))) return NOVAQ_EDTYPE;
   if (N == 0 || D_out == 0) return NOVAQ_OK;
@@ -202,8 +200,7 @@ int novaq_linear_forward_ex(const void* x, int x_dtype, const float* x_scale, in
   Epilogue ep;
   const int rc = make_epilogue(bias, epi, &ep, st);
   if (rc != NOVAQ_OK) return rc;
-  return linear_launch(static_cast<const float*>(x), N, D_in, w_q, w_dtype, w_scale, ep, D_out,
-                       y, st);
+  return linear_launch(x, x_dtype, x_scale, N, D_in, w_q, w_dtype, w_scale, ep, D_out, y, st);
 }
 
 int novaq_conv2d_forward_ex(const void* x, int x_dtype, const float* x_scale, int64_t N,
@@ -211,9 +208,7 @@ int novaq_conv2d_forward_ex(const void* x, int x_dtype, const float* x_scale, in
                             const float* w_scale, int64_t C_out, int KH, int KW, int sh, int sw,
                             int ph, int pw, int pad_mode, const float* bias,
                             const novaq_epilogue* epi, void* y, void* stream) {
-  if (!valid_dtype(w_dtype) || !valid_dtype(x_dtype)) return NOVAQ_EDTYPE;
-  if (x_dtype != F32) return NOVAQ_EDTYPE;
-  (void)x_scale;
+  if (!valid_dtype(w_dtype) || !valid_dtype(x_dtype) || x_dtype == E2M1) return NOVAQ_EDTYPE;
   if (pad_mode < NOVAQ_PAD_ZEROS || pad_mode > NOVAQ_PAD_CIRCULAR) return NOVAQ_EPADMODE;
   if (N < 0 || C <= 0 || H <= 0 || W <= 0 || C_out <= 0 || KH <= 0 || KW <= 0 || sh <= 0 ||
       sw <= 0 || ph < 0 || pw < 0)
@@ -227,8 +222,8 @@ int novaq_conv2d_forward_ex(const void* x, int x_dtype, const float* x_scale, in
   Epilogue ep;
   const int rc = make_epilogue(bias, epi, &ep, st);
   if (rc != NOVAQ_OK) return rc;
-  return conv2d_launch(static_cast<const float*>(x), N, C, H, W, w_q, w_dtype, w_scale, C_out,
-                       KH, KW, sh, sw, ph, pw, pad_mode, ep, y, st);
+  return conv2d_launch(x, x_dtype, x_scale, N, C, H, W, w_q, w_dtype, w_scale, C_out, KH, KW, sh,
+                       sw, ph, pw, pad_mode, ep, y, st);
 }
 
 int novaq_transpose(const void* src, int src_dtype, int64_t rows, int64_t cols, void* dst,

@@ -1,896 +1,54 @@
-// Quantized-weight Conv2d forward (NCHW, implicit im2col) on bf16 MFMA.
-//
-//   y[n, co, oh, ow] = bias[co] + s * sum_{c, kh, kw} dec(w[co, c, kh, kw]) *
-//                      xpad[n, c, oh*sh + kh - ph, ow*sw + kw - pw]
-//
-// GEMM view: M = output channels, N = output pixels of one image, K = the
-// (kh, kw, c) window.  NovaNN materialises the (C*KH*KW, N*OH*OW) column
-// matrix (novann/functional.py:346-368); here no column matrix exists:
-//   - a workgroup owns 64 output channels and a run of 256 consecutive output
-//     pixels of one image (4 waves x 64 pixels);
-//   - the input rows that run touches are staged in LDS channel-last,
-//     [row][col][c] in bf16, with the padding mode (zeros / reflect /
-//     replicate / circular, numpy.pad's index rules) resolved while staging,
-//     so the MFMA loop has no bounds logic;
-//   - K is ordered (kh, kw, c) with c padded to a multiple of 8, so the 8
-//     consecutive K values an MFMA lane needs are 8 channels of one input
-//     pixel: one 16-byte LDS read;
-//   - the weights are decoded once per workgroup into LDS as a [co][k] bf16
-//     matrix (exact for E4M3 / E5M2 / E2M1) and the scale and bias are
-//     applied in fp32 after accumulation;
-//   - the result is written straight to contiguous NCHW (32 consecutive
-//     pixels of one channel per store instruction).
-// Workgroups loop over pixel tiles (grid sized to the CU count) so the weight
-// decode is paid once per workgroup, not once per tile.  More than 64 input
-// channels are processed in blocks of 64 (weights then restaged per block).
-#include <hip/hip_runtime.h>
-#include <stdint.h>
-
-#include <algorithm>
-
-#include "novaq_convert.h"
-#include "novaq_epilogue.h"
-#include "novaq_internal.h"
+// Conv2d forward: fp32 x kernels and the dispatch over the stored dtype of x
+// (the other x dtypes are instantiated in conv2d_x*.hip).
+#include "conv2d_impl.h"
 
 namespace novaq {
-namespace {
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
+template int conv2d_launch_xt<F32>(const uint8_t*, const float*, int64_t, int64_t, int64_t,
+                                   int64_t, const void*, int, const float*, int64_t, int, int, int,
+                                   int, int, int, int, const Epilogue&, void*, hipStream_t);
+extern template int conv2d_launch_xt<BF16>(const uint8_t*, const float*, int64_t, int64_t, int64_t,
+                                           int64_t, const void*, int, const float*, int64_t, int,
+                                           int, int, int, int, int, int, const Epilogue&, void*,
+                                           hipStream_t);
+extern template int conv2d_launch_xt<F16>(const uint8_t*, const float*, int64_t, int64_t, int64_t,
+                                          int64_t, const void*, int, const float*, int64_t, int,
+                                          int, int, int, int, int, int, const Epilogue&, void*,
+                                          hipStream_t);
+extern template int conv2d_launch_xt<E4M3>(const uint8_t*, const float*, int64_t, int64_t, int64_t,
+                                           int64_t, const void*, int, const float*, int64_t, int,
+                                           int, int, int, int, int, int, const Epilogue&, void*,
+                                           hipStream_t);
+extern template int conv2d_launch_xt<E5M2>(const uint8_t*, const float*, int64_t, int64_t, int64_t,
+                                           int64_t, const void*, int, const float*, int64_t, int,
+                                           int, int, int, int, int, int, const Epilogue&, void*,
+                                           hipStream_t);
 
-constexpr int THREADS = 256;
-constexpr int CO_TILE = 64;
-constexpr int PIX_WAVE = 64;
-constexpr int PIX_TILE = PIX_WAVE * (THREADS / 64);
-constexpr int MAX_CB = 64;
-// workgroups per CU the registers are sized for (the grid is CUs x this), and
-// input-staging items per thread whose loads are issued together
-#ifndef CONV_OCC
-#define CONV_OCC 2
-#endif
-#ifndef CONV_IB
-#define CONV_IB 4
-#endif
-constexpr size_t LDS_LIMIT = 160 * 1024;
-
-struct ConvGeom {
-  int N, C, H, W, C_out, KH, KW, sh, sw, ph, pw, pad_mode;
-  int OH, OW;
-  int CB;        // channels per block (multiple of 8, <= 64)
-  int cstride;   // bf16 per staged input pixel (CB, +8 if CB/8 is even)
-  int groups;    // K groups of 8 per channel block = KH*KW*CB/8
-  int ksteps;    // ceil(groups / 2)
-  int wrow;      // bytes per weight LDS row (2*ksteps K groups, padded for banks)
-  int rows;      // staged input rows per tile
-  int wp;        // staged input columns
-  int tiles_per_image;
-  int raw_in_lds;  // weights staged through a raw LDS copy (one channel block, fits)
-  int64_t tiles;
-};
-
-__device__ __forceinline__ int pad_index(int i, int n, int mode) {
-  if (i >= 0 && i < n) return i;
-  if (mode == NOVAQ_PAD_ZEROS) return -1;
-  if (mode == NOVAQ_PAD_REPLICATE) return i < 0 ? 0 : n - 1;
-  if (mode == NOVAQ_PAD_CIRCULAR) {
-    int r = i % n;
-    return r < 0 ? r + n : r;
+int conv2d_launch(const void* x, int x_dtype, const float* x_scale, int64_t N, int64_t C,
+                  int64_t H, int64_t W, const void* w_q, int w_dtype, const float* w_scale,
+                  int64_t C_out, int KH, int KW, int sh, int sw, int ph, int pw, int pad_mode,
+                  const Epilogue& ep, void* y, hipStream_t stream) {
+  const auto* xb = static_cast<const uint8_t*>(x);
+#define NOVAQ_CONV_XT(T)                                                                    \
+  conv2d_launch_xt<T>(xb, x_scale, N, C, H, W, w_q, w_dtype, w_scale, C_out, KH, KW, sh, sw, \
+                      ph, pw, pad_mode, ep, y, stream)
+  switch (x_dtype) {
+    case F32: return NOVAQ_CONV_XT(F32);
+    case BF16: return NOVAQ_CONV_XT(BF16);
+    case F16: return NOVAQ_CONV_XT(F16);
+    case E4M3: return NOVAQ_CONV_XT(E4M3);
+    case E5M2: return NOVAQ_CONV_XT(E5M2);
+    default: return NOVAQ_EDTYPE;
   }
-  if (n == 1) return 0;  // reflect, period 2(n-1)
-  int p = 2 * (n - 1);
-  int r = i % p;
-  if (r < 0) r += p;
-  return r >= n ? p - r : r;
+#undef NOVAQ_CONV_XT
 }
-
-__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
-  return (uint16_t)enc_bf16(__float_as_uint(f));
-}
-
-// Bytes of one 8-wide K group of a weight row in LDS: the packed codes for
-// E2M1 (4 B) and E4M3 / E5M2 (8 B), decoded bf16 otherwise (16 B).
-template <int WT>
-__host__ __device__ constexpr int group_bytes() {
-  return WT == E2M1 ? 4 : (WT == E4M3 || WT == E5M2) ? 8 : 16;
-}
-
-// Stored code of weight element e (E2M1 nibble or FP8 byte).
-template <int WT>
-__device__ __forceinline__ uint32_t weight_code(const uint8_t* __restrict__ w, int64_t e) {
-  if constexpr (WT == E2M1) return (w[e >> 1] >> ((e & 1) * 4)) & 0xFu;
-  else return w[e];
-}
-
-typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
-
-// One lane's A fragment (8 weights of one K group) from LDS as 8 bf16; FP8
-// and FP4 codes are decoded exactly with gfx950's packed converts.
-template <int WT>
-__device__ __forceinline__ bf16x8 weight_frag(const uint8_t* p) {
-  if constexpr (WT == E2M1) {
-    const uint32_t v = *reinterpret_cast<const uint32_t*>(p);
-    uint32_t o[4];
-    o[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, 1.0f, 0));
-    o[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, 1.0f, 1));
-    o[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, 1.0f, 2));
-    o[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, 1.0f, 3));
-    return __builtin_bit_cast(bf16x8, make_uint4(o[0], o[1], o[2], o[3]));
-  } else if constexpr (WT == E4M3 || WT == E5M2) {
-    const u32x2v v = *reinterpret_cast<const u32x2v*>(p);
-    const uint32_t lo = v[0], hi = v[1];
-    uint32_t o[4];
-    if constexpr (WT == E4M3) {
-      o[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, false));
-      o[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, true));
-      o[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, false));
-      o[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, true));
-    } else {
-      o[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(lo, 1.0f, false));
-      o[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(lo, 1.0f, true));
-      o[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(hi, 1.0f, false));
-      o[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(hi, 1.0f, true));
-    }
-    return __builtin_bit_cast(bf16x8, make_uint4(o[0], o[1], o[2], o[3]));
-  } else {
-    return *reinterpret_cast<const bf16x8*>(p);
-  }
-}
-
-// Decoded weight element e (flat (co, c, kh, kw) index) as bf16 bits.
-template <int WT>
-__device__ __forceinline__ uint16_t weight_bf16(const uint8_t* __restrict__ w, int64_t e) {
-  uint32_t f;
-  if constexpr (WT == E4M3) f = dec_e4m3(w[e]);
-  else if constexpr (WT == E5M2) f = dec_e5m2(w[e]);
-  else if constexpr (WT == E2M1) f = dec_e2m1((w[e >> 1] >> ((e & 1) * 4)) & 0xFu);
-  else if constexpr (WT == BF16) return reinterpret_cast<const uint16_t*>(w)[e];
-  else if constexpr (WT == F16) f = dec_f16(reinterpret_cast<const uint16_t*>(w)[e]);
-  else f = reinterpret_cast<const uint32_t*>(w)[e];
-  // FP8 / FP4 values are exact in bf16; fp16 / fp32 weights round to nearest even
-  return (uint16_t)enc_bf16(f);
-}
-
-template <int WT>
-__global__ __launch_bounds__(THREADS, CONV_OCC) void conv2d_kernel(
-    const float* __restrict__ x, const uint8_t* __restrict__ w, const float* __restrict__ w_scale,
-    Epilogue ep, void* __restrict__ y, ConvGeom g) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-  constexpr int GB = group_bytes<WT>();
-  uint8_t* wl = lds;                                                     // [CO_TILE][g.wrow B]
-  uint16_t* xl = reinterpret_cast<uint16_t*>(lds + CO_TILE * g.wrow);    // [rows][wp][cstride]
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, half = lane >> 5;
-  const int co0 = blockIdx.y * CO_TILE;
-  const int cblocks = (g.C + g.CB - 1) / g.CB;
-  const int npix = g.OH * g.OW;
-  const int c8 = g.CB / 8;
-  const bool two_m = co0 + 32 < g.C_out;
-  const float s = w_scale ? *w_scale : 1.0f;
-  const float inv_o = epi_inv_scale(ep);
-  uint32_t am = 0;
-
-  // Weights: one item = (output channel, group of 8 consecutive K values), i.e.
-  // 8 channels of one (kh, kw) tap, written as one LDS group: 8 packed E2M1
-  // nibbles (4 B), 8 FP8 bytes (8 B) or 8 decoded bf16 (16 B).  Channels
-  // past C and K groups past the window are zeros (code 0 is +0 in every
-  // format).  `src` holds the (co, c, kh, kw) weights in storage order
-  // starting at output channel `cofs` (the global tensor, or its raw copy).
-  auto stage_weights = [&](int cb, const uint8_t* src, int cofs) {
-    const int gpr = 2 * g.ksteps;  // 8-wide K groups per LDS row
-    const int cstep = g.KH * g.KW;
-    for (int it = tid; it < CO_TILE * gpr; it += THREADS) {
-      const int co = it / gpr, grp = it - co * gpr;
-      uint32_t p[4] = {0u, 0u, 0u, 0u};
-      if (grp < g.groups && co0 + co < g.C_out) {
-        const int khkw = grp / c8;
-        const int cbase = cb * g.CB + (grp - khkw * c8) * 8;
-        const int64_t e0 = ((int64_t)(co0 + co - cofs) * g.C + cbase) * cstep + khkw;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          if (cbase + j >= g.C) continue;
-          if constexpr (GB == 4) {
-            p[0] |= weight_code<WT>(src, e0 + j * cstep) << (4 * j);
-          } else if constexpr (GB == 8) {
-            p[j >> 2] |= weight_code<WT>(src, e0 + j * cstep) << (8 * (j & 3));
-          } else {
-            p[j >> 1] |= (uint32_t)weight_bf16<WT>(src, e0 + j * cstep) << ((j & 1) * 16);
-          }
-        }
-      }
-      uint8_t* d = wl + co * g.wrow + grp * GB;
-      if constexpr (GB == 4) *reinterpret_cast<uint32_t*>(d) = p[0];
-      else if constexpr (GB == 8) *reinterpret_cast<u32x2v*>(d) = u32x2v{p[0], p[1]};
-      else *reinterpret_cast<uint4*>(d) = make_uint4(p[0], p[1], p[2], p[3]);
-    }
-  };
-  // Raw copy of this workgroup's weight rows into the (not yet used) input
-  // tile region with coalesced dword loads, all in flight at once; the
-  // decode above then reads LDS instead of issuing dependent global loads.
-  // Used when all channels fit one block and the raw rows fit the region.
-  auto stage_weights_via_lds = [&]() {
-    const int rows = min(CO_TILE, g.C_out - co0);
-    const int64_t row_elems = (int64_t)g.C * g.KH * g.KW;
-    const int64_t first = (int64_t)co0 * row_elems;  // first element (even: co0 % 64 == 0)
-    const int nbytes = (int)(rows * row_elems * dtype_bits(WT) / 8 + (dtype_bits(WT) == 4 ? (rows * row_elems) & 1 : 0));
-    const uint8_t* gsrc = w + first * dtype_bits(WT) / 8;  // 4-byte aligned (row_elems * 64 elems)
-    uint8_t* raw = reinterpret_cast<uint8_t*>(xl);
-    const int nwords = nbytes >> 2;
-#pragma unroll 8
-    for (int i = tid; i < nwords; i += THREADS)
-      reinterpret_cast<uint32_t*>(raw)[i] = reinterpret_cast<const uint32_t*>(gsrc)[i];
-    for (int i = (nwords << 2) + tid; i < nbytes; i += THREADS) raw[i] = gsrc[i];
-    __syncthreads();
-    stage_weights(0, raw, co0);
-  };
-
-  // window offset (in staged-input elements) of each 8-wide K group, -1 for
-  // the padding group past the window
-  int* ktab = reinterpret_cast<int*>(xl + g.rows * g.wp * g.cstride);
-  for (int i = tid; i < 2 * g.ksteps; i += THREADS) {
-    int koff = -1;
-    if (i < g.groups) {
-      const int khkw = i / c8;
-      const int kh = khkw / g.KW, kw = khkw - kh * g.KW;
-      koff = (kh * g.wp + kw) * g.cstride + (i - khkw * c8) * 8;
-    }
-    ktab[i] = koff;
-  }
-
-  if (cblocks == 1) {
-    if (g.raw_in_lds) stage_weights_via_lds();
-    else stage_weights(0, w, 0);
-  }
-
-  for (int64_t tile = blockIdx.x; tile < g.tiles; tile += gridDim.x) {
-    const int n = (int)(tile / g.tiles_per_image);
-    const int p0 = (int)(tile - (int64_t)n * g.tiles_per_image) * PIX_TILE;
-    const int oh_first = p0 / g.OW;
-    const int ih0 = oh_first * g.sh - g.ph;
-
-    // per-lane pixel bases (in staged-input elements) for the two 32-pixel blocks
-    int pbase[2];
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      int p = p0 + wave * PIX_WAVE + nt * 32 + (lane & 31);
-      if (p >= npix) p = p0;  // read something valid; never stored
-      const int oh = p / g.OW, ow = p - oh * g.OW;
-      pbase[nt] = (((oh - oh_first) * g.sh) * g.wp + ow * g.sw) * g.cstride;
-    }
-
-    f32x16 acc[2][2];
-#pragma unroll
-    for (int a = 0; a < 2; ++a)
-#pragma unroll
-      for (int b = 0; b < 2; ++b)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.0f;
-
-    for (int cb = 0; cb < cblocks; ++cb) {
-      __syncthreads();  // previous readers of the LDS tile are done
-      if (cblocks > 1) stage_weights(cb, w, 0);
-      // Stage input rows [ih0, ih0 + rows) x cols [-pw, -pw + wp) of channel
-      // block cb.  One item = one staged pixel x 8 channels: 8 independent
-      // loads (consecutive lanes take consecutive pixels, so each load
-      // instruction reads a contiguous row segment), 4 packed bf16 converts
-      // (RNE) and one 16-byte LDS write.
-      const int pix = g.rows * g.wp;
-      const int total = pix * c8;
-      const int64_t hw = (int64_t)g.H * g.W;
-      // batches of IB items per thread: all 8*IB loads are issued before the
-      // first conversion
-      constexpr int IB = CONV_IB;
-      for (int base = 0; base < total; base += IB * THREADS) {
-        float v[IB][8];
-        int dst[IB];
-#pragma unroll
-        for (int b = 0; b < IB; ++b) {
-          const int it = base + b * THREADS + tid;
-          dst[b] = -1;
-#pragma unroll
-          for (int j = 0; j < 8; ++j) v[b][j] = 0.0f;
-          if (it < total) {
-            const int cgi = it / pix, p = it - cgi * pix;
-            const int r = p / g.wp, col = p - r * g.wp;
-            const int hi = pad_index(ih0 + r, g.H, g.pad_mode);
-            const int wi = pad_index(col - g.pw, g.W, g.pad_mode);
-            const int cbase = cb * g.CB + cgi * 8;
-            dst[b] = (r * g.wp + col) * g.cstride + cgi * 8;
-            if (hi >= 0 && wi >= 0) {
-              const float* src = x + ((int64_t)n * g.C + cbase) * hw + (int64_t)hi * g.W + wi;
-#pragma unroll
-              for (int j = 0; j < 8; ++j)
-                if (cbase + j < g.C) v[b][j] = src[j * hw];
-            }
-          }
-        }
-#pragma unroll
-        for (int b = 0; b < IB; ++b) {
-          if (dst[b] < 0) continue;
-          uint32_t q[4];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            f32x2 f = {v[b][2 * j], v[b][2 * j + 1]};
-            q[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));
-          }
-          *reinterpret_cast<uint4*>(&xl[dst[b]]) = make_uint4(q[0], q[1], q[2], q[3]);
-        }
-      }
-      __syncthreads();
-
-      // fragments of K step st into register set `buf`; the window offset
-      // of each 8-wide K group comes from the per-workgroup table (-1: the
-      // zero padding group past the window)
-      bf16x8 fa0[2], fa1[2], fb[2][2];
-      auto load = [&](int st, int buf) {
-        const int koff = ktab[2 * st + half];
-        const int kbyte = (2 * st + half) * GB;
-        fa0[buf] = weight_frag<WT>(wl + (lane & 31) * g.wrow + kbyte);
-        fa1[buf] = weight_frag<WT>(wl + (32 + (lane & 31)) * g.wrow + kbyte);
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
-          if (koff >= 0) {
-            fb[buf][nt] = *reinterpret_cast<const bf16x8*>(&xl[pbase[nt] + koff]);
-          } else {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) fb[buf][nt][j] = (__bf16)0.0f;
-          }
-        }
-      };
-      auto mfma = [&](int buf) {
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
-          acc[0][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa0[buf], fb[buf][nt], acc[0][nt], 0, 0, 0);
-          if (two_m)
-            acc[1][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa1[buf], fb[buf][nt], acc[1][nt], 0, 0, 0);
-        }
-      };
-      // the next step's fragments are read while the current step multiplies
-      load(0, 0);
-      for (int st = 0; st < g.ksteps; st += 2) {
-        if (st + 1 < g.ksteps) load(st + 1, 1);
-        mfma(0);
-        if (st + 1 < g.ksteps) {
-          if (st + 2 < g.ksteps) load(st + 2, 0);
-          mfma(1);
-        }
-      }
-    }
-
-    // epilogue: lane holds pixel (lane & 31) of each 32-block and channels
-    // 8*(r/4) + 4*half + r%4 of each 32-channel block
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      if (mt == 1 && !two_m) break;
-#pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        const int p = p0 + wave * PIX_WAVE + nt * 32 + (lane & 31);
-        if (p >= npix) continue;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int co = co0 + mt * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-          if (co < g.C_out) {
-            const float v = epi_value(ep, epi_chan(ep, co), acc[mt][nt][r], s);
-            am = epi_track(am, v);
-            epi_store(ep.out_dtype, y, ((int64_t)n * g.C_out + co) * npix + p, v, inv_o);
-          }
-        }
-      }
-    }
-  }
-  epi_amax_commit(ep, am);
-}
-
-// ---------------------------------------------------------------------------
-// Band kernel (C <= 64 input channels, at most 256 output pixels per band).
-//
-// A workgroup owns up to 64 output channels of one band of R whole output
-// rows of one image; the band's output is R*OW consecutive floats of each
-// channel plane.  GEMM orientation per band: M = the band's pixels in
-// 16-pixel tiles, N = output channels in 16-channel tiles, K = (kh, kw, c) in
-// 8-channel groups, on v_mfma_f32_16x16x32_bf16.  With pixels as rows, a
-// lane's four accumulators are four consecutive pixels of one channel: one
-// 16-byte store.
-//   - the weights of the workgroup's output channels are regrouped once from
-//     (co, c, kh, kw) order into (co, [kh, kw, 8 channels]) groups in LDS,
-//     FP8 / FP4 codes kept packed and decoded per MFMA fragment (exact);
-//   - the band's input rows are staged in LDS channel-last in bf16 (RNE);
-//     whole 4-column groups of the interior come in as 16-byte loads of 8
-//     channels, issued into registers before the weights are regrouped (when
-//     there is at most one such item per thread) so their latency overlaps
-//     that work, and are transposed in registers; padding columns are
-//     resolved element-wise with numpy.pad's index rules;
-//   - many small workgroups per CU: one's loads overlap another's MFMAs and
-//     stores.
-
-struct BandGeom {
-  int N, C, H, W, C_out, KH, KW, sh, sw, ph, pw, pad_mode, OH, OW;
-  int c8;        // 8-channel groups (C padded to a multiple of 8)
-  int cstride;   // bf16 per staged pixel
-  int taps;      // KH * KW
-  int groups;    // taps * c8 K groups of 8
-  int gpr;       // groups rounded up to whole MFMA K steps (4 groups)
-  int wrow;      // bytes per weight row in LDS
-  int R;         // output rows per band
-  int bands;     // bands per image
-  int rows_in;   // staged input rows per band
-  int wp;        // staged input columns
-  int nborder;   // staged columns outside [0, W) (element-wise path)
-  int vec;       // interior columns staged with 16-byte loads (W % 4 == 0)
-  int vitems;    // 16-byte-load items per band (rows_in * W/4 * c8)
-  int raw_ok;    // packed weights copied to LDS before regrouping
-  int x_off;     // LDS byte offset of the staged input
-  int x_bytes;   // bytes of the staged input
-};
-
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-
-// 16-byte-load items of one band held in registers: IPT items per thread,
-// each 8 channels x 4 columns.
-template <int IPT>
-struct BandRegs {
-  f32x4 v[IPT > 0 ? IPT : 1][8];
-};
-
-// K9: 3x3 window, C a multiple of 8 and packed FP8 / FP4 codes copied to LDS:
-// the 8 channels x 9 taps of one (co, channel group) are 72 consecutive codes
-// (aligned 32-bit words), regrouped with constant shifts.
-template <int WT, int IPT, bool K9>
-__global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
-    const float* __restrict__ x, const uint8_t* __restrict__ w, const float* __restrict__ w_scale,
-    Epilogue ep, void* __restrict__ y, BandGeom g) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-  constexpr int GB = group_bytes<WT>();
-  uint8_t* wl = lds;                                           // [64][g.wrow]
-  int* ktab = reinterpret_cast<int*>(lds + CO_TILE * g.wrow);  // [g.gpr]
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int lr = lane & 15, lg = lane >> 4;
-  const int band = blockIdx.x % g.bands, n = blockIdx.x / g.bands;
-  const int co0 = blockIdx.y * CO_TILE;
-  const int64_t HW = (int64_t)g.H * g.W;
-  const float* xn = x + (int64_t)n * g.C * HW;
-  const int W4 = g.W >> 2;
-
-  // 16-byte-load item `it` of band b: (row r, column group cg, channel group q)
-  auto vload = [&](int b, int it, f32x4* v) {
-    const int q = it % g.c8, rest = it / g.c8;
-    const int cg = rest % W4, r = rest / W4;
-    const int hi = pad_index(b * g.R * g.sh - g.ph + r, g.H, g.pad_mode);
-    const bool used = cg * 4 + g.pw < g.wp;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int c = q * 8 + j;
-      v[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-      if (used && hi >= 0 && c < g.C)
-        v[j] = *reinterpret_cast<const f32x4*>(xn + c * HW + (int64_t)hi * g.W + cg * 4);
-    }
-  };
-  // the band's 16-byte loads go out first
-  BandRegs<IPT> r0;
-  if constexpr (IPT > 0) {
-    if (tid < g.vitems) vload(band, tid, r0.v[0]);
-  }
-
-  // --- weights: (co, c, kh, kw) -> [co][K group] ---------------------------
-  const int row_elems = g.C * g.taps;
-  const uint8_t* src = w;
-  int cofs = 0;
-  if (g.raw_ok) {
-    // packed codes of rows co0 .. co0+63 (the first element is even, so the
-    // E2M1 byte boundary matches), coalesced dwords then bytes, into the
-    // staged-input region
-    const int rows = min(CO_TILE, g.C_out - co0);
-    const int64_t first = (int64_t)co0 * row_elems;
-    const int nbytes = (int)(((int64_t)rows * row_elems * dtype_bits(WT) + 7) / 8);
-    const uint8_t* gsrc = w + first * dtype_bits(WT) / 8;
-    uint8_t* raw = lds + g.x_off;
-    const int nwords = (reinterpret_cast<uintptr_t>(gsrc) & 3) ? 0 : nbytes >> 2;
-    for (int i = tid; i < nwords; i += THREADS)
-      reinterpret_cast<uint32_t*>(raw)[i] = reinterpret_cast<const uint32_t*>(gsrc)[i];
-    for (int i = (nwords << 2) + tid; i < nbytes; i += THREADS) raw[i] = gsrc[i];
-    __syncthreads();
-    src = raw;
-    cofs = co0;
-  }
-  if constexpr (K9 && GB < 16) {
-    constexpr int BITS = dtype_bits(WT);
-    constexpr int NW = 72 * BITS / 32;  // words of one (co, q) run
-    for (int item = tid; item < CO_TILE * g.c8; item += THREADS) {
-      const int co = item / g.c8, q = item - co * g.c8;
-      uint32_t o[9][GB / 4];
-      if (co0 + co < g.C_out) {
-        const uint32_t* run = reinterpret_cast<const uint32_t*>(
-            src + (size_t)(co * g.C + q * 8) * 9 * BITS / 8);
-        uint32_t wv[NW];
-#pragma unroll
-        for (int i = 0; i < NW; ++i) wv[i] = run[i];
-#pragma unroll
-        for (int t = 0; t < 9; ++t) {
-#pragma unroll
-          for (int k = 0; k < GB / 4; ++k) o[t][k] = 0u;
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            constexpr uint32_t mask = (1u << BITS) - 1u;
-            const int e = 9 * j + t;
-            const uint32_t code = (wv[e * BITS / 32] >> ((e * BITS) % 32)) & mask;
-            o[t][(j * BITS) / 32] |= code << ((j * BITS) % 32);
-          }
-        }
-      } else {
-#pragma unroll
-        for (int t = 0; t < 9; ++t)
-#pragma unroll
-          for (int k = 0; k < GB / 4; ++k) o[t][k] = 0u;
-      }
-#pragma unroll
-      for (int t = 0; t < 9; ++t) {
-        uint8_t* d = wl + co * g.wrow + (t * g.c8 + q) * GB;
-        if constexpr (GB == 4) *reinterpret_cast<uint32_t*>(d) = o[t][0];
-        else *reinterpret_cast<u32x2v*>(d) = u32x2v{o[t][0], o[t][1]};
-      }
-    }
-    // zero groups past the window (K padding to whole MFMA steps)
-    const int pad = g.gpr - g.groups;
-    for (int item = tid; item < CO_TILE * pad; item += THREADS) {
-      const int co = item / pad, gi = g.groups + (item - co * pad);
-      uint8_t* d = wl + co * g.wrow + gi * GB;
-      if constexpr (GB == 4) *reinterpret_cast<uint32_t*>(d) = 0u;
-      else *reinterpret_cast<u32x2v*>(d) = u32x2v{0u, 0u};
-    }
-  } else {
-    // four threads per output channel row, each taking every fourth group
-    const int co = tid >> 2;
-    const bool live = co0 + co < g.C_out;
-    int tap = 0, q = tid & 3;
-    while (q >= g.c8) { q -= g.c8; ++tap; }
-    for (int gi = tid & 3; gi < g.gpr; gi += 4) {
-      uint32_t p[4] = {0u, 0u, 0u, 0u};
-      if (live && gi < g.groups) {
-        const int cbase = q * 8;
-        const int64_t e0 = ((int64_t)(co0 + co - cofs) * g.C + cbase) * g.taps + tap;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          if (cbase + j >= g.C) break;
-          if constexpr (GB == 4) {
-            p[0] |= weight_code<WT>(src, e0 + j * g.taps) << (4 * j);
-          } else if constexpr (GB == 8) {
-            p[j >> 2] |= weight_code<WT>(src, e0 + j * g.taps) << (8 * (j & 3));
-          } else {
-            p[j >> 1] |= (uint32_t)weight_bf16<WT>(src, e0 + j * g.taps) << ((j & 1) * 16);
-          }
-        }
-      }
-      uint8_t* d = wl + co * g.wrow + gi * GB;
-      if constexpr (GB == 4) *reinterpret_cast<uint32_t*>(d) = p[0];
-      else if constexpr (GB == 8) *reinterpret_cast<u32x2v*>(d) = u32x2v{p[0], p[1]};
-      else *reinterpret_cast<uint4*>(d) = make_uint4(p[0], p[1], p[2], p[3]);
-      // advance (tap, q) by four groups
-      q += 4;
-      while (q >= g.c8) { q -= g.c8; ++tap; }
-    }
-  }
-  // window offset (staged elements) of each K group; -1 past the window
-  for (int gi = tid; gi < g.gpr; gi += THREADS) {
-    int koff = -1;
-    if (gi < g.groups) {
-      const int tap = gi / g.c8, q = gi - tap * g.c8;
-      const int kh = tap / g.KW, kw = tap - kh * g.KW;
-      koff = (kh * g.wp + kw) * g.cstride + q * 8;
-    }
-    ktab[gi] = koff;
-  }
-  __syncthreads();  // weights regrouped; the raw copy region is free
-
-  auto vstore = [&](uint16_t* xl, int it, const f32x4* v) {
-    const int q = it % g.c8, rest = it / g.c8;
-    const int cg = rest % W4, r = rest / W4;
-    const int col0 = cg * 4 + g.pw;  // staged column of input column 4*cg
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int col = col0 + i;
-      if (col >= g.wp) break;
-      uint32_t pk[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        f32x2 f = {v[2 * j][i], v[2 * j + 1][i]};
-        pk[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));
-      }
-      *reinterpret_cast<uint4*>(&xl[(r * g.wp + col) * g.cstride + q * 8]) =
-          make_uint4(pk[0], pk[1], pk[2], pk[3]);
-    }
-  };
-  // stage band b into buffer xl (from the registers when IPT > 0)
-  auto stage = [&](const BandRegs<IPT>& rg, int b, uint16_t* xl) {
-    if (g.vec) {
-      if constexpr (IPT > 0) {
-#pragma unroll
-        for (int k = 0; k < IPT; ++k) {
-          const int it = tid + k * THREADS;
-          if (it < g.vitems) vstore(xl, it, rg.v[k]);
-        }
-      } else {
-        for (int it = tid; it < g.vitems; it += THREADS) {
-          f32x4 v[8];
-          vload(b, it, v);
-          vstore(xl, it, v);
-        }
-      }
-    }
-    // element-wise columns: the padding columns, or every column when the
-    // rows are not 16-byte aligned
-    const int ncols = g.vec ? g.nborder : g.wp;
-    const int left = min(g.pw, g.wp);
-    const int items = g.rows_in * ncols * g.c8;
-    const int ih0 = b * g.R * g.sh - g.ph;
-    for (int it = tid; it < items; it += THREADS) {
-      const int q = it % g.c8, rest = it / g.c8;
-      const int bi = rest % ncols, r = rest / ncols;
-      const int col = !g.vec ? bi : (bi < left ? bi : g.pw + g.W + (bi - left));
-      const int hi = pad_index(ih0 + r, g.H, g.pad_mode);
-      const int wi = pad_index(col - g.pw, g.W, g.pad_mode);
-      float v[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int c = q * 8 + j;
-        v[j] = (hi >= 0 && wi >= 0 && c < g.C) ? xn[c * HW + (int64_t)hi * g.W + wi] : 0.0f;
-      }
-      uint32_t pk[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        f32x2 f = {v[2 * j], v[2 * j + 1]};
-        pk[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));
-      }
-      *reinterpret_cast<uint4*>(&xl[(r * g.wp + col) * g.cstride + q * 8]) =
-          make_uint4(pk[0], pk[1], pk[2], pk[3]);
-    }
-  };
-
-  const float s = w_scale ? *w_scale : 1.0f;
-  const float inv_o = epi_inv_scale(ep);
-  uint32_t am = 0;
-  const int64_t npix = (int64_t)g.OH * g.OW;
-  const int nt_live = min(4, (min(CO_TILE, g.C_out - co0) + 15) >> 4);
-  const uint8_t* wfrag = wl + lr * g.wrow + lg * GB;
-  const int steps = g.gpr >> 2;
-  const bf16x8 zero8 = __builtin_bit_cast(bf16x8, make_uint4(0u, 0u, 0u, 0u));
-
-  // MFMA and store of band b from buffer xl; wave w takes M tiles w, w+4, ...
-  auto compute = [&](int b, const uint16_t* xl) {
-    const int oh0 = b * g.R;
-    const int P = min(g.R, g.OH - oh0) * g.OW;
-    const int mtiles = (P + 15) >> 4;
-    const int my_mt = wave < mtiles ? (mtiles - wave + 3) >> 2 : 0;
-    int pb[4];
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      int p = (wave + 4 * m) * 16 + lr;
-      if (p >= P) p = 0;  // a valid address; the product is never stored
-      const int ohr = p / g.OW, ow = p - ohr * g.OW;
-      pb[m] = ((ohr * g.sh) * g.wp + ow * g.sw) * g.cstride;
-    }
-    f32x4 acc[4][4];
-#pragma unroll
-    for (int m = 0; m < 4; ++m)
-#pragma unroll
-      for (int t = 0; t < 4; ++t) acc[m][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    // (the fragments are not double-buffered: the extra registers would cost
-    // a workgroup per CU, and other workgroups hide the LDS latency)
-    auto frags = [&](int st, bf16x8* af, bf16x8* bf) {
-      const int koff = ktab[st * 4 + lg];
-#pragma unroll
-      for (int t = 0; t < 4; ++t)
-        if (t < nt_live) bf[t] = weight_frag<WT>(wfrag + t * 16 * g.wrow + st * 4 * GB);
-#pragma unroll
-      for (int m = 0; m < 4; ++m)
-        if (m < my_mt) af[m] = koff >= 0 ? *reinterpret_cast<const bf16x8*>(&xl[pb[m] + koff]) : zero8;
-    };
-    auto mma = [&](const bf16x8* af, const bf16x8* bf) {
-#pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        if (m >= my_mt) break;
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-          if (t < nt_live)
-            acc[m][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[m], bf[t], acc[m][t], 0, 0, 0);
-      }
-    };
-    for (int st = 0; st < steps; ++st) {
-      bf16x8 af[4], bf[4];
-      frags(st, af, bf);
-      mma(af, bf);
-    }
-    // lane holds pixels 4*lg .. 4*lg+3 of channel lr of each tile
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      if (m >= my_mt) break;
-      const int p = (wave + 4 * m) * 16 + 4 * lg;
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const int co = co0 + t * 16 + lr;
-        if (t >= nt_live || co >= g.C_out) continue;
-        const EpiChan k = epi_chan(ep, co);
-        const int64_t di = ((int64_t)n * g.C_out + co) * npix + (int64_t)oh0 * g.OW + p;
-        float v[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          v[i] = epi_value(ep, k, acc[m][t][i], s);
-          if (p + i < P) am = epi_track(am, v[i]);
-        }
-        // plain stores: the 64-byte pieces of a line written by neighbouring
-        // lanes and waves merge in L2 before they reach HBM
-        if (p + 3 < P && (di & 3) == 0) {
-          epi_store4(ep.out_dtype, y, di, v, inv_o);
-        } else {
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            if (p + i < P) epi_store(ep.out_dtype, y, di + i, v[i], inv_o);
-        }
-      }
-    }
-  };
-
-  uint16_t* xl = reinterpret_cast<uint16_t*>(lds + g.x_off);
-  stage(r0, band, xl);
-  __syncthreads();
-  compute(band, xl);
-  epi_amax_commit(ep, am);
-}
-
-// Band geometry for this convolution, or false when the band kernel does not
-// apply (too many channels, rows too wide, or LDS too small).  *ipt is the
-// number of 16-byte-load items per thread held in registers (0: loaded while
-// staging).
-template <int WT>
-bool band_geometry(const ConvGeom& cg, BandGeom& b, size_t& lds, int* ipt) {
-  if (cg.C > MAX_CB || cg.OW > 256) return false;
-  b = BandGeom{};
-  b.N = cg.N; b.C = cg.C; b.H = cg.H; b.W = cg.W; b.C_out = cg.C_out; b.KH = cg.KH;
-  b.KW = cg.KW; b.sh = cg.sh; b.sw = cg.sw; b.ph = cg.ph; b.pw = cg.pw; b.pad_mode = cg.pad_mode;
-  b.OH = cg.OH; b.OW = cg.OW;
-  b.c8 = (cg.C + 7) / 8;
-  // pixel stride in LDS of 8 mod 16 bf16 (4 mod 8 banks): the 16 pixels of a
-  // fragment read fall in distinct banks
-  b.cstride = (b.c8 % 2 == 0) ? b.c8 * 8 + 8 : b.c8 * 8;
-  b.taps = cg.KH * cg.KW;
-  b.groups = b.taps * b.c8;
-  b.gpr = (b.groups + 3) / 4 * 4;
-  // bands of whole output rows, at most 256 pixels, balanced across the image
-  const int64_t npix = (int64_t)cg.OH * cg.OW;
-  const int nb = (int)((npix + 255) / 256);
-  b.R = (cg.OH + nb - 1) / nb;
-  while ((int64_t)b.R * cg.OW > 256) --b.R;
-  if (b.R < 1) return false;
-  b.bands = (cg.OH + b.R - 1) / b.R;
-  b.rows_in = (b.R - 1) * cg.sh + cg.KH;
-  b.wp = (cg.OW - 1) * cg.sw + cg.KW;
-  b.vec = (cg.W % 4) == 0;
-  b.nborder = std::min(cg.pw, b.wp) + std::max(0, b.wp - cg.pw - cg.W);
-  b.vitems = b.vec ? b.rows_in * (cg.W / 4) * b.c8 : 0;
-  *ipt = (b.vec && b.vitems <= THREADS) ? 1 : 0;
-  // weight row: gpr groups of GB bytes, stride padded so the 16 rows a
-  // fragment read touches fall in distinct banks
-  constexpr int GB = group_bytes<WT>();
-  int stride_dw = b.gpr * GB / 4;
-  while ((GB == 4 && stride_dw % 2 != 1) || (GB == 8 && stride_dw % 4 != 2) ||
-         (GB == 16 && stride_dw % 8 != 4))
-    stride_dw += GB / 4;
-  b.wrow = stride_dw * 4;
-  b.x_off = (CO_TILE * b.wrow + 4 * b.gpr + 15) / 16 * 16;
-  b.x_bytes = (int)(((size_t)b.rows_in * b.wp * b.cstride * 2 + 15) / 16 * 16);
-  const size_t raw_bytes = ((size_t)CO_TILE * cg.C * b.taps * dtype_bits(WT) + 7) / 8;
-  b.raw_ok = dtype_bits(WT) <= 8 && raw_bytes <= (size_t)b.x_bytes;
-  lds = b.x_off + (size_t)b.x_bytes;
-  return lds <= 80 * 1024;
-}
-
-template <int WT, int IPT, bool K9>
-int launch_band(const float* x, const void* w, const float* w_scale, const Epilogue& ep, void* y,
-                const BandGeom& b, size_t lds, int64_t co_blocks, hipStream_t stream) {
-  auto kern = conv2d_band_kernel<WT, IPT, K9>;
-  static size_t lds_enabled = 64 * 1024;  // per instantiation: raise the limit once
-  if (lds > lds_enabled) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_LIMIT);
-    if (e != hipSuccess) return hip_fail(e);
-    lds_enabled = LDS_LIMIT;
-  }
-  const int64_t blocks = (int64_t)b.N * b.bands;
-  if (blocks > 0x7FFFFFFF) return NOVAQ_EINVAL;
-  hipLaunchKernelGGL(kern, dim3((unsigned)blocks, (unsigned)co_blocks), dim3(THREADS), lds, stream,
-                     x, static_cast<const uint8_t*>(w), w_scale, ep, y, b);
-  return check_launch();
-}
-
-template <int WT>
-int launch(const float* x, const void* w, const float* w_scale, const Epilogue& ep, void* y,
-           ConvGeom g, hipStream_t stream) {
-  {
-    BandGeom b;
-    size_t lds = 0;
-    int ipt = 0;
-    if (band_geometry<WT>(g, b, lds, &ipt)) {
-      const int64_t co_blocks = (g.C_out + CO_TILE - 1) / CO_TILE;
-      if constexpr (group_bytes<WT>() < 16) {
-        if (b.taps == 9 && g.C % 8 == 0 && b.raw_ok) {
-          if (ipt == 1) return launch_band<WT, 1, true>(x, w, w_scale, ep, y, b, lds, co_blocks, stream);
-          return launch_band<WT, 0, true>(x, w, w_scale, ep, y, b, lds, co_blocks, stream);
-        }
-      }
-      if (ipt == 1) return launch_band<WT, 1, false>(x, w, w_scale, ep, y, b, lds, co_blocks, stream);
-      return launch_band<WT, 0, false>(x, w, w_scale, ep, y, b, lds, co_blocks, stream);
-    }
-  }
-  // staged rows for a run of PIX_TILE pixels: it spans at most
-  // ceil((PIX_TILE - 1) / OW) + 1 output rows
-  const int out_rows = (PIX_TILE - 1) / g.OW + 2;
-  g.rows = (out_rows - 1) * g.sh + g.KH;
-  g.wp = (g.OW - 1) * g.sw + g.KW;
-  // weight row: 2*ksteps groups of GB bytes, padded so the 32 rows one
-  // fragment read touches fall in distinct LDS banks (row stride in dwords
-  // odd for 4-byte reads, 2 mod 4 for 8-byte reads, 4 mod 8 for 16-byte reads)
-  constexpr int GB = group_bytes<WT>();
-  int stride_dw = 2 * g.ksteps * GB / 4;
-  while ((GB == 4 && stride_dw % 2 != 1) || (GB == 8 && stride_dw % 4 != 2) ||
-         (GB == 16 && stride_dw % 8 != 4))
-    stride_dw += GB / 4;
-  g.wrow = stride_dw * 4;
-  const size_t xl_bytes = (size_t)g.rows * g.wp * g.cstride * 2;
-  // weights, staged input, then the K-group offset table (2*ksteps ints)
-  const size_t lds = (size_t)CO_TILE * g.wrow + xl_bytes + (size_t)8 * g.ksteps;
-  const size_t raw_bytes = ((size_t)CO_TILE * g.C * g.KH * g.KW * dtype_bits(WT) + 7) / 8;
-  g.raw_in_lds = g.C <= g.CB && raw_bytes <= xl_bytes;
-  if (lds > LDS_LIMIT) return NOVAQ_ENOTSUP;  // rows too wide for one LDS tile
-  auto kern = conv2d_kernel<WT>;
-  static size_t lds_enabled = 64 * 1024;  // per instantiation: raise the limit once
-  if (lds > lds_enabled) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)LDS_LIMIT);
-    if (e != hipSuccess) return hip_fail(e);
-    lds_enabled = LDS_LIMIT;
-  }
-  const int64_t co_blocks = (g.C_out + CO_TILE - 1) / CO_TILE;
-  int64_t grid = (int64_t)device_cu_count() * CONV_OCC;
-  if (grid > g.tiles) grid = g.tiles;
-  if (grid < 1) grid = 1;
-  hipLaunchKernelGGL(kern, dim3((unsigned)grid, (unsigned)co_blocks), dim3(THREADS), lds, stream, x,
-                     static_cast<const uint8_t*>(w), w_scale, ep, y, g);
-  return check_launch();
-}
-
-}  // namespace
 
 int conv2d_launch(const float* x, int64_t N, int64_t C, int64_t H, int64_t W, const void* w_q,
                   int w_dtype, const float* w_scale, int64_t C_out, int KH, int KW, int sh,
                   int sw, int ph, int pw, int pad_mode, const Epilogue& ep, void* y,
                   hipStream_t stream) {
-  const int64_t OH = (H + 2 * (int64_t)ph - KH) / sh + 1;
-  const int64_t OW = (W + 2 * (int64_t)pw - KW) / sw + 1;
-  if (OH <= 0 || OW <= 0) return NOVAQ_ESHAPE;
-  if (N > 0x7FFFFFFF || C > 0x7FFFFFFF || H * W > 0x7FFFFFFF || C_out > 65535 * CO_TILE ||
-      OH * OW > 0x7FFFFFFF)
-    return NOVAQ_EINVAL;
-  ConvGeom g{};
-  g.N = (int)N; g.C = (int)C; g.H = (int)H; g.W = (int)W; g.C_out = (int)C_out;
-  g.KH = KH; g.KW = KW; g.sh = sh; g.sw = sw; g.ph = ph; g.pw = pw; g.pad_mode = pad_mode;
-  g.OH = (int)OH; g.OW = (int)OW;
-  const int cpad = (int)((C + 7) / 8 * 8);
-  g.CB = cpad < MAX_CB ? cpad : MAX_CB;
-  g.cstride = ((g.CB / 8) % 2 == 0) ? g.CB + 8 : g.CB;
-  g.groups = KH * KW * g.CB / 8;
-  g.ksteps = (g.groups + 1) / 2;
-  g.tiles_per_image = (int)((OH * OW + PIX_TILE - 1) / PIX_TILE);
-  g.tiles = (int64_t)N * g.tiles_per_image;
-  switch (w_dtype) {
-    case E4M3: return launch<E4M3>(x, w_q, w_scale, ep, y, g, stream);
-    case E5M2: return launch<E5M2>(x, w_q, w_scale, ep, y, g, stream);
-    case E2M1: return launch<E2M1>(x, w_q, w_scale, ep, y, g, stream);
-    case BF16: return launch<BF16>(x, w_q, w_scale, ep, y, g, stream);
-    case F16: return launch<F16>(x, w_q, w_scale, ep, y, g, stream);
-    case F32: return launch<F32>(x, w_q, w_scale, ep, y, g, stream);
-    default: return NOVAQ_EDTYPE;
-  }
+  return conv2d_launch(x, F32, nullptr, N, C, H, W, w_q, w_dtype, w_scale, C_out, KH, KW, sh, sw,
+                       ph, pw, pad_mode, ep, y, stream);
 }
 
 int conv2d_launch(const float* x, int64_t N, int64_t C, int64_t H, int64_t W, const void* w_q,
@@ -900,8 +58,8 @@ int conv2d_launch(const float* x, int64_t N, int64_t C, int64_t H, int64_t W, co
   Epilogue ep{};
   ep.bias = bias;
   ep.out_dtype = F32;
-  return conv2d_launch(x, N, C, H, W, w_q, w_dtype, w_scale, C_out, KH, KW, sh, sw, ph, pw,
-                       pad_mode, ep, y, stream);
+  return conv2d_launch(x, F32, nullptr, N, C, H, W, w_q, w_dtype, w_scale, C_out, KH, KW, sh, sw,
+                       ph, pw, pad_mode, ep, y, stream);
 }
 
 }  // namespace novaq

@@ -1,0 +1,751 @@
+// Quantized-weight Linear forward on bf16 MFMA (gfx950) -- kernels, included
+// by one translation unit per x dtype (linear.hip: fp32 x and the dispatch;
+// linear_x*.hip: the others), so each file compiles in about the time one did.
+//
+//   y[M, N] = epilogue(x[M, K] . (s_w * dec(W[N, K]))^T * s_x + bias[N])
+//
+// Both operands are K-contiguous ("NT" GEMM).  x (fp32, or bf16 / f16 / FP8
+// as a fused epilogue stored it) becomes bf16 on its way into LDS (fp32 and
+// f16 rounded to nearest even, FP8 decoded exactly); W is read in its stored
+// format (E4M3 / E5M2 / E2M1 / bf16 / f16 / f32) and decoded to bf16 with
+// gfx950's packed converts (v_cvt_scalef32_pk_bf16_{fp8,bf8,fp4}, scale 1.0),
+// which are exact: every E4M3, E5M2 and E2M1 value is a bf16 value.  Products
+// run on v_mfma_f32_32x32x16_bf16 with fp32 accumulation; the per-tensor scale
+// s and the bias are applied in fp32 after accumulation.
+//
+// Three kernels, chosen by shape and weight format:
+//   - linear_wide_kernel (FP8 / FP4 weights, M % 128, N % 256, K % 128): one
+//     128 x 256 tile per workgroup of 8 waves, K blocks of 128 (one 128-byte
+//     line of an FP8 W row), W raw in LDS and decoded per MFMA fragment,
+//     buffer loads with SGPR offsets;
+//   - linear_pipe_kernel (whole 128-row tiles, K % 64): W decoded once per
+//     workgroup into bf16 LDS tiles, loads kept up to 3 K blocks ahead;
+//   - linear_kernel: any shape (guarded edge tiles) and fp32 weights.
+// Tiles are numbered so that the workgroups the hardware sends to one XCD
+// (block id mod 8) cover a compact 4-row group of tiles, so their x rows and W
+// rows are shared through that XCD's L2.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "novaq_convert.h"
+#include "novaq_epilogue.h"
+#include "novaq_internal.h"
+#include "novaq_xload.h"
+
+namespace novaq {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int BM = 128, BN = 256, BK = 64;
+constexpr int LDS_ROW = BK + 8;  // bf16 per LDS row
+constexpr int THREADS = 256;
+constexpr int WM = 64, WN = 128;  // per-wave sub-tile
+constexpr int MT = WM / 32, NT = WN / 32;
+constexpr int XCH = BM * BK / 4 / THREADS;  // x 16-byte chunks per thread
+
+template <int WT>
+struct W {
+  static constexpr int bits = dtype_bits(WT);
+  static constexpr int epc = 128 / bits;           // elements per 16-byte chunk
+  static constexpr int chunks = BN * BK / epc / THREADS;  // per thread per K block
+  static constexpr int words = epc / 2;            // bf16 pairs per chunk
+};
+
+__device__ __forceinline__ uint32_t bf16_pair(bf16x2 v) { return __builtin_bit_cast(uint32_t, v); }
+
+__device__ __forceinline__ uint32_t f32x2_to_bf16(uint32_t lo, uint32_t hi) {
+  f32x2 f = {__uint_as_float(lo), __uint_as_float(hi)};
+  return bf16_pair(__builtin_convertvector(f, bf16x2));
+}
+
+// Decode one 16-byte chunk of W (epc elements) into epc/2 bf16 pairs.
+template <int WT>
+__device__ __forceinline__ void decode_chunk(const u32x4& c, uint32_t* out) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    uint32_t v = c[i];
+    if constexpr (WT == E4M3) {
+      out[2 * i] = bf16_pair(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v, 1.0f, false));
+      out[2 * i + 1] = bf16_pair(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v, 1.0f, true));
+    } else if constexpr (WT == E5M2) {
+      out[2 * i] = bf16_pair(__builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(v, 1.0f, false));
+      out[2 * i + 1] = bf16_pair(__builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(v, 1.0f, true));
+    } else if constexpr (WT == E2M1) {
+      out[4 * i] = bf16_pair(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, 1.0f, 0));
+      out[4 * i + 1] = bf16_pair(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, 1.0f, 1));
+      out[4 * i + 2] = bf16_pair(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, 1.0f, 2));
+      out[4 * i + 3] = bf16_pair(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, 1.0f, 3));
+    } else if constexpr (WT == BF16) {
+      out[i] = v;
+    } else if constexpr (WT == F16) {
+      f16x2 h = __builtin_bit_cast(f16x2, v);
+      f32x2 f = __builtin_convertvector(h, f32x2);  // exact widening
+      out[i] = bf16_pair(__builtin_convertvector(f, bf16x2));
+    } else {  // F32: two chunk words per bf16 pair
+      if (i % 2 == 0) out[i / 2] = f32x2_to_bf16(c[i], c[i + 1]);
+    }
+  }
+}
+
+// Element e of a row of W in storage order, for the guarded (edge) loads.
+template <int WT>
+__device__ __forceinline__ uint32_t load_w_elem(const uint8_t* row, int e) {
+  if constexpr (W<WT>::bits == 32) return reinterpret_cast<const uint32_t*>(row)[e];
+  else if constexpr (W<WT>::bits == 16) return reinterpret_cast<const uint16_t*>(row)[e];
+  else if constexpr (W<WT>::bits == 8) return row[e];
+  else return (row[e >> 1] >> ((e & 1) * 4)) & 0xFu;
+}
+
+// 16-byte chunk of row `r` (< rows) starting at element k (multiple of epc):
+// one vector load when it lies inside the row and rows are 16-byte aligned,
+// element loads with zero fill otherwise.
+template <int WT>
+__device__ __forceinline__ u32x4 load_w_chunk(const uint8_t* __restrict__ w, int r, int rows,
+                                              int k, int K, size_t row_bytes, bool vec_ok) {
+  constexpr int EPC = W<WT>::epc;
+  u32x4 v = {0u, 0u, 0u, 0u};
+  if (r >= rows) return v;
+  const uint8_t* row = w + (size_t)r * row_bytes;
+  if (vec_ok && k + EPC <= K) return *reinterpret_cast<const u32x4*>(row + (size_t)k * W<WT>::bits / 8);
+  constexpr int bits = W<WT>::bits;
+#pragma unroll
+  for (int e = 0; e < EPC; ++e) {
+    if (k + e < K) {
+      uint32_t c = load_w_elem<WT>(row, k + e);
+      v[(e * bits) / 32] |= c << ((e * bits) % 32);
+    }
+  }
+  return v;
+}
+
+// Raw codes of x elements k .. k+3 of row r (zeros past the row or matrix).
+template <int XT>
+__device__ __forceinline__ u32x4 load_x_chunk(const uint8_t* __restrict__ x, int r, int rows,
+                                              int k, int K, bool vec_ok) {
+  if (r >= rows) return u32x4{0u, 0u, 0u, 0u};
+  const int64_t e = (int64_t)r * K + k;
+  if (vec_ok && k + 4 <= K) return x4_raw<XT>(x, e);
+  return x4_raw_guarded<XT>(x, e, (int64_t)r * K + K);
+}
+
+template <int WT, int XT>
+__global__ __launch_bounds__(THREADS, 1) void linear_kernel(
+    const uint8_t* __restrict__ x, const float* __restrict__ x_scale, const uint8_t* __restrict__ w,
+    const float* __restrict__ w_scale,
+    Epilogue ep, void* __restrict__ y, int M, int N, int K, int tiles_m,
+    int tiles_n, int x_vec, int w_vec) {
+  __shared__ __attribute__((aligned(16))) __bf16 As[2][BM * LDS_ROW];
+  __shared__ __attribute__((aligned(16))) __bf16 Bs[2][BN * LDS_ROW];
+  using WTr = W<WT>;
+  constexpr int WCPR = BK / WTr::epc;  // W chunks per tile row
+  const size_t w_row_bytes = (size_t)K * WTr::bits / 8;
+
+  // tile index: XCD-contiguous, then 4-row groups walked column by column
+  const int T = tiles_m * tiles_n;
+  int t = blockIdx.x;
+  if ((T & 7) == 0) t = (t & 7) * (T >> 3) + (t >> 3);
+  constexpr int GM = 4;
+  const int group = t / (GM * tiles_n);
+  const int first_m = group * GM;
+  const int gm = min(tiles_m - first_m, GM);
+  const int rem = t - group * GM * tiles_n;
+  const int m0 = (first_m + rem % gm) * BM;
+  const int n0 = (rem / gm) * BN;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = (wave & 1) * WM, wn = (wave >> 1) * WN;
+
+  u32x4 xr[XCH];
+  u32x4 wr[WTr::chunks];
+  auto fetch = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < XCH; ++i) {
+      int c = tid + THREADS * i;
+      xr[i] = load_x_chunk<XT>(x, m0 + (c >> 4), M, k0 + (c & 15) * 4, K, x_vec);
+    }
+#pragma unroll
+    for (int i = 0; i < WTr::chunks; ++i) {
+      int c = tid + THREADS * i;
+      wr[i] = load_w_chunk<WT>(w, n0 + c / WCPR, N, k0 + (c % WCPR) * WTr::epc, K, w_row_bytes,
+                               w_vec);
+    }
+  };
+  auto stage = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < XCH; ++i) {
+      int c = tid + THREADS * i;
+      const xl_u32x2 pr = x4_bf16<XT>(xr[i]);
+      *reinterpret_cast<uint2*>(&As[buf][(c >> 4) * LDS_ROW + (c & 15) * 4]) = make_uint2(pr[0], pr[1]);
+    }
+#pragma unroll
+    for (int i = 0; i < WTr::chunks; ++i) {
+      int c = tid + THREADS * i;
+      uint32_t words[WTr::words];
+      decode_chunk<WT>(wr[i], words);
+      uint32_t* dst = reinterpret_cast<uint32_t*>(&Bs[buf][(c / WCPR) * LDS_ROW + (c % WCPR) * WTr::epc]);
+      if constexpr (WTr::words == 2) {
+        *reinterpret_cast<uint2*>(dst) = make_uint2(words[0], words[1]);
+      } else {
+#pragma unroll
+        for (int q = 0; q < WTr::words; q += 4)
+          *reinterpret_cast<uint4*>(dst + q) =
+              make_uint4(words[q], words[q + 1], words[q + 2], words[q + 3]);
+      }
+    }
+  };
+
+  f32x16 acc[MT][NT];
+#pragma unroll
+  for (int a = 0; a < MT; ++a)
+#pragma unroll
+    for (int b = 0; b < NT; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.0f;
+
+  const int kblocks = (K + BK - 1) / BK;
+  fetch(0);
+  stage(0);
+  __syncthreads();
+  for (int kb = 0; kb < kblocks; ++kb) {
+    const int buf = kb & 1;
+    const bool more = kb + 1 < kblocks;
+    if (more) fetch((kb + 1) * BK);
+#pragma unroll
+    for (int s = 0; s < BK / 16; ++s) {
+      const int kk = s * 16 + (lane >> 5) * 8;
+      bf16x8 a[MT], b[NT];
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+        a[i] = *reinterpret_cast<const bf16x8*>(&As[buf][(wm + i * 32 + (lane & 31)) * LDS_ROW + kk]);
+#pragma unroll
+      for (int j = 0; j < NT; ++j)
+        b[j] = *reinterpret_cast<const bf16x8*>(&Bs[buf][(wn + j * 32 + (lane & 31)) * LDS_ROW + kk]);
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+    }
+    if (more) stage(buf ^ 1);
+    __syncthreads();
+  }
+
+  // epilogue: lane holds column (lane & 31) and rows 8*(r/4) + 4*(lane/32) + r%4
+  const float s = product_scale(w_scale, x_scale);
+  const float inv_o = epi_inv_scale(ep);
+  uint32_t am = 0;
+#pragma unroll
+  for (int j = 0; j < NT; ++j) {
+    const int col = n0 + wn + j * 32 + (lane & 31);
+    if (col >= N) continue;
+    const EpiChan k = epi_chan(ep, col);
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (row < M) {
+          const float v = epi_value(ep, k, acc[i][j][r], s);
+          am = epi_track(am, v);
+          epi_store(ep.out_dtype, y, (size_t)row * N + col, v, inv_o);
+        }
+      }
+    }
+  }
+  epi_amax_commit(ep, am);
+}
+
+constexpr int A_PITCH = BK + 8;                      // bf16 per A row in LDS
+constexpr int A_STAGE = BM * A_PITCH * 2;            // bytes
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// 8 stored W elements (one lane's fragment) -> 8 bf16 for the MFMA B operand
+template <int WT>
+__device__ __forceinline__ bf16x8 frag_to_bf16(const uint8_t* p) {
+  uint32_t o[4];
+  if constexpr (WT == E4M3 || WT == E5M2) {
+    u32x2 v = *reinterpret_cast<const u32x2*>(p);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      if constexpr (WT == E4M3) {
+        o[2 * i] = bf16_pair(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v[i], 1.0f, false));
+        o[2 * i + 1] = bf16_pair(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v[i], 1.0f, true));
+      } else {
+        o[2 * i] = bf16_pair(__builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(v[i], 1.0f, false));
+        o[2 * i + 1] = bf16_pair(__builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(v[i], 1.0f, true));
+      }
+    }
+  } else if constexpr (WT == E2M1) {
+    uint32_t v = *reinterpret_cast<const uint32_t*>(p);
+    o[0] = bf16_pair(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, 1.0f, 0));
+    o[1] = bf16_pair(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, 1.0f, 1));
+    o[2] = bf16_pair(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, 1.0f, 2));
+    o[3] = bf16_pair(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(v, 1.0f, 3));
+  } else if constexpr (WT == BF16) {
+    return *reinterpret_cast<const bf16x8*>(p);
+  } else {  // F16
+    u32x4 v = *reinterpret_cast<const u32x4*>(p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      // the element goes through a scalar first: bit-casting v[i] directly
+      // makes this compiler (ROCm 7.2 clang) reuse element 0 for every i
+      const uint32_t word = v[i];
+      f32x2 f = __builtin_convertvector(__builtin_bit_cast(f16x2, word), f32x2);
+      o[i] = bf16_pair(__builtin_convertvector(f, bf16x2));
+    }
+  }
+  u32x4 r = {o[0], o[1], o[2], o[3]};
+  return __builtin_bit_cast(bf16x8, r);
+}
+
+constexpr int B_PITCH = BK + 8;  // bf16 per W row in LDS (144 B, conflict-free fragment reads)
+
+// ---------------------------------------------------------------------------
+// Pipelined staged-decode kernel (whole tiles, any weight format but fp32):
+// W is decoded to bf16 once per workgroup while it is written to LDS, so the
+// MFMA loop is only 16-byte LDS reads and MFMAs.  NW waves (2 along M x NW/2
+// along N, each 64 x FBN*2/NW); PF register sets keep global loads PF K
+// blocks ahead: block kb+PF is loaded while block kb+1 (loaded PF-1 blocks
+// earlier) is converted into the idle LDS buffer after MFMA steps 1..3.
+
+template <int WT, int XT, int FBN, int NW, int OCC, int PF>
+__global__ __launch_bounds__(NW * 64, OCC) void linear_pipe_kernel(
+    const uint8_t* __restrict__ x, const float* __restrict__ x_scale, const uint8_t* __restrict__ w,
+    const float* __restrict__ w_scale,
+    Epilogue ep, void* __restrict__ y, int M, int N, int K, int tiles_m,
+    int tiles_n) {
+  using WTr = W<WT>;
+  constexpr int NTH = NW * 64;
+  constexpr int FWN = FBN * 2 / NW;
+  constexpr int FNT = FWN / 32;
+  constexpr int B_STAGE = FBN * B_PITCH * 2;
+  constexpr int STAGE = A_STAGE + B_STAGE;
+  constexpr int XC = BM * BK / 4 / NTH;               // x chunks per thread
+  constexpr int WCPR = BK / WTr::epc;                 // W chunks per row
+  constexpr int WC = FBN * BK / WTr::epc / NTH;       // W chunks per thread
+  constexpr int UNITS = XC + WC;
+  static_assert(FNT >= 1 && XC >= 1 && WC >= 1 && NTH % WCPR == 0, "tile shape");
+  static_assert(PF >= 1 && PF <= 3, "prefetch distance");
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * STAGE];
+
+  const int T = tiles_m * tiles_n;
+  int t = blockIdx.x;
+  if ((T & 7) == 0) t = (t & 7) * (T >> 3) + (t >> 3);
+  constexpr int GM = 4;
+  const int group = t / (GM * tiles_n);
+  const int first_m = group * GM;
+  const int gm = min(tiles_m - first_m, GM);
+  const int rem = t - group * GM * tiles_n;
+  const int m0 = (first_m + rem % gm) * BM;
+  const int n0 = (rem / gm) * FBN;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, half = lane >> 5;
+  const int wm = (wave & 1) * WM, wn = (wave >> 1) * FWN;
+  const size_t w_row_bytes = (size_t)K * WTr::bits / 8;
+
+  const uint8_t* xtile = x + (size_t)m0 * K * XL<XT>::bytes;
+  const uint32_t xlane = (uint32_t)((tid >> 4) * K + (tid & 15) * 4);
+  const size_t xstep = (size_t)(NTH / 16) * K;
+  const int xdst0 = ((tid >> 4) * A_PITCH + (tid & 15) * 4) * 2;
+  constexpr int XDST_STEP = (NTH / 16) * A_PITCH * 2;
+  const uint8_t* wtile = w + (size_t)n0 * w_row_bytes;
+  const uint32_t wlane = (uint32_t)((tid / WCPR) * w_row_bytes + (tid % WCPR) * 16);
+  const size_t wstep = (size_t)(NTH / WCPR) * w_row_bytes;
+  const int wdst0 = A_STAGE + ((tid / WCPR) * B_PITCH + (tid % WCPR) * WTr::epc) * 2;
+  constexpr int WDST_STEP = (NTH / WCPR) * B_PITCH * 2;
+
+  struct Regs {
+    u32x4 x[XC];
+    u32x4 w[WC];
+  };
+  auto fetch = [&](Regs& r, int kb) {
+    const size_t xk = (size_t)kb * BK;
+    const uint8_t* wk = wtile + (size_t)kb * (BK * WTr::bits / 8);
+#pragma unroll
+    for (int i = 0; i < XC; ++i) r.x[i] = x4_raw<XT>(xtile, xk + i * xstep + xlane);
+#pragma unroll
+    for (int i = 0; i < WC; ++i) r.w[i] = *reinterpret_cast<const u32x4*>(wk + i * wstep + wlane);
+  };
+  // staging units u in [u0, u1): x chunks first, then W chunks
+  auto stage_units = [&](const Regs& r, uint8_t* S, int u0, int u1) {
+#pragma unroll
+    for (int u = 0; u < UNITS; ++u) {
+      if (u < u0 || u >= u1) continue;
+      if (u < XC) {
+        const xl_u32x2 pr = x4_bf16<XT>(r.x[u]);
+        *reinterpret_cast<u32x2*>(S + xdst0 + u * XDST_STEP) = u32x2{pr[0], pr[1]};
+      } else {
+        const int i = u - XC;
+        uint32_t words[WTr::words];
+        decode_chunk<WT>(r.w[i], words);
+        uint8_t* d = S + wdst0 + i * WDST_STEP;
+#pragma unroll
+        for (int q = 0; q < WTr::words; q += 4)
+          *reinterpret_cast<u32x4*>(d + 4 * q) = u32x4{words[q], words[q + 1], words[q + 2], words[q + 3]};
+      }
+    }
+  };
+
+  f32x16 acc[MT][FNT];
+#pragma unroll
+  for (int a = 0; a < MT; ++a)
+#pragma unroll
+    for (int b = 0; b < FNT; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.0f;
+
+  int aoff[MT], boff[FNT];
+#pragma unroll
+  for (int i = 0; i < MT; ++i) aoff[i] = ((wm + i * 32 + (lane & 31)) * A_PITCH + half * 8) * 2;
+#pragma unroll
+  for (int j = 0; j < FNT; ++j) boff[j] = A_STAGE + ((wn + j * 32 + (lane & 31)) * B_PITCH + half * 8) * 2;
+
+  const int kblocks = K / BK;
+  // One K block: fetch block kb+PF into `rf` (free: its previous block is
+  // already in LDS), multiply the LDS buffer of block kb, and convert block
+  // kb+1 from `rs` into the other buffer after MFMA steps 1..3.  Past the end
+  // the last block is fetched and staged again into the idle buffer, so the
+  // body has no branch.
+  auto body = [&](int kb, Regs& rf, const Regs& rs) {
+    const uint8_t* S = lds + (kb & 1) * STAGE;
+    uint8_t* Snext = lds + ((kb + 1) & 1) * STAGE;
+    fetch(rf, min(kb + PF, kblocks - 1));
+    bf16x8 a[2][MT], b[2][FNT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) a[0][i] = *reinterpret_cast<const bf16x8*>(S + aoff[i]);
+#pragma unroll
+    for (int j = 0; j < FNT; ++j) b[0][j] = *reinterpret_cast<const bf16x8*>(S + boff[j]);
+#pragma unroll
+    for (int s = 0; s < BK / 16; ++s) {
+      const int cur = s & 1, nxt = cur ^ 1;
+      if (s + 1 < BK / 16) {
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+          a[nxt][i] = *reinterpret_cast<const bf16x8*>(S + aoff[i] + (s + 1) * 32);
+#pragma unroll
+        for (int j = 0; j < FNT; ++j)
+          b[nxt][j] = *reinterpret_cast<const bf16x8*>(S + boff[j] + (s + 1) * 32);
+      }
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < FNT; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[cur][i], b[cur][j], acc[i][j], 0, 0, 0);
+      if (s >= 1) stage_units(rs, Snext, (s - 1) * UNITS / 3, s * UNITS / 3);
+    }
+    __syncthreads();
+  };
+
+  Regs r0, r1, r2;
+  fetch(r0, 0);
+  if constexpr (PF >= 2) fetch(r1, min(1, kblocks - 1));
+  if constexpr (PF >= 3) fetch(r2, min(2, kblocks - 1));
+  stage_units(r0, lds, 0, UNITS);
+  __syncthreads();
+  if constexpr (PF == 1) {
+    for (int kb = 0; kb < kblocks; ++kb) body(kb, r0, r0);
+  } else if constexpr (PF == 2) {
+    for (int kb = 0; kb < kblocks; kb += 2) {
+      body(kb, r0, r1);
+      if (kb + 1 < kblocks) body(kb + 1, r1, r0);
+    }
+  } else {
+    for (int kb = 0; kb < kblocks; kb += 3) {
+      body(kb, r0, r1);
+      if (kb + 1 < kblocks) body(kb + 1, r1, r2);
+      if (kb + 2 < kblocks) body(kb + 2, r2, r0);
+    }
+  }
+
+  const float s = product_scale(w_scale, x_scale);
+  const float inv_o = epi_inv_scale(ep);
+  uint32_t am = 0;
+#pragma unroll
+  for (int j = 0; j < FNT; ++j) {
+    const int col = n0 + wn + j * 32 + (lane & 31);
+    const EpiChan k = epi_chan(ep, col);
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+        const float v = epi_value(ep, k, acc[i][j][r], s);
+        am = epi_track(am, v);
+        if (ep.out_dtype == F32)
+          __builtin_nontemporal_store(v, reinterpret_cast<float*>(y) + (size_t)row * N + col);
+        else
+          epi_store(ep.out_dtype, y, (size_t)row * N + col, v, inv_o);
+      }
+    }
+  }
+  epi_amax_commit(ep, am);
+}
+
+// ---------------------------------------------------------------------------
+// Wide-K kernel (E4M3 / E5M2 / E2M1 weights, K % 128 == 0): K blocks of 128,
+// so one K block of a W row is a whole 128-byte line for FP8 (64 bytes for
+// E2M1) and each W load fetches no line it uses only half of; barriers are
+// half as many.  W stays in its stored format in LDS (decoded per fragment),
+// x is rounded to bf16 on the way in; two LDS stages, two register sets
+// (block kb+2 is loaded while block kb+1 is staged).
+
+template <int WT>
+struct Wide {
+  static constexpr int KB = 128;                        // K per block
+  static constexpr int bits = dtype_bits(WT);
+  static constexpr int row_bytes = KB * bits / 8;       // W bytes per row per block
+  static constexpr int pitch = bits == 8 ? 136 : 68;    // W LDS row pitch (bytes)
+  static constexpr int a_pitch = KB + 8;                // bf16 per x row in LDS
+  static constexpr int frag_bytes = 8 * bits / 8;
+  static constexpr int cpr = row_bytes / 16;            // W 16-byte chunks per row
+};
+
+template <int WT, int XT>
+__global__ __launch_bounds__(512, 1) void linear_wide_kernel(
+    const uint8_t* __restrict__ x, const float* __restrict__ x_scale, const uint8_t* __restrict__ w,
+    const float* __restrict__ w_scale,
+    Epilogue ep, void* __restrict__ y, int M, int N, int K, int tiles_m,
+    int tiles_n) {
+  using F = Wide<WT>;
+  constexpr int KB = F::KB;
+  constexpr int FBN = 256, NTH = 512;
+  constexpr int FWN = 64, FNT = 2;
+  constexpr int A_ST = BM * F::a_pitch * 2;
+  constexpr int STAGE = A_ST + FBN * F::pitch;
+  constexpr int XC = BM * KB / 4 / NTH;                 // 8 x chunks per thread
+  constexpr int WC = FBN * F::row_bytes / 16 / NTH;     // 4 (FP8) or 2 (E2M1) W chunks
+  constexpr int UNITS = XC + WC;
+  constexpr int STEPS = KB / 16;
+  static_assert(F::bits <= 8 && NTH % F::cpr == 0, "tile shape");
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * STAGE];
+
+  const int T = tiles_m * tiles_n;
+  int t = blockIdx.x;
+  if ((T & 7) == 0) t = (t & 7) * (T >> 3) + (t >> 3);
+  constexpr int GM = 4;
+  const int group = t / (GM * tiles_n);
+  const int first_m = group * GM;
+  const int gm = min(tiles_m - first_m, GM);
+  const int rem = t - group * GM * tiles_n;
+  const int m0 = (first_m + rem % gm) * BM;
+  const int n0 = (rem / gm) * FBN;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, half = lane >> 5;
+  const int wm = (wave & 1) * WM, wn = (wave >> 1) * FWN;
+
+  // Global loads are buffer loads through per-tile descriptors: a 32-bit
+  // per-lane byte offset in one VGPR, block and chunk offsets in SGPRs.
+  // x: 32 chunks (512 B) per row, 16 rows per pass of the workgroup;
+  // W: cpr chunks per row, NTH / cpr rows per pass.
+  constexpr int XB = XL<XT>::bytes;
+  const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(x + (size_t)m0 * K * XB), (short)0, BM * K * XB, 0x00020000);
+  const uint32_t xlane = (uint32_t)((tid >> 5) * K + (tid & 31) * 4) * (uint32_t)XB;
+  const uint32_t xstep = 16u * (uint32_t)K * (uint32_t)XB;
+  const uint32_t w_row_bytes = (uint32_t)K * F::bits / 8;
+  const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(w + (size_t)n0 * w_row_bytes), (short)0, (int)(FBN * w_row_bytes),
+      0x00020000);
+  const uint32_t wlane = (uint32_t)(tid / F::cpr) * w_row_bytes + (uint32_t)(tid % F::cpr) * 16u;
+  const uint32_t wstep = (uint32_t)(NTH / F::cpr) * w_row_bytes;
+
+  // LDS: [A0 | A1 | B0 | B1].  Per-lane bases below; every other offset is a
+  // compile-time constant that fits a ds instruction's 16-bit offset field.
+  constexpr int B_ST = FBN * F::pitch;
+  constexpr int XDST_STEP = 16 * F::a_pitch * 2;
+  constexpr int WDST_STEP = (NTH / F::cpr) * F::pitch;
+  constexpr int A_ROWS32 = 32 * F::a_pitch * 2;
+  constexpr int B_ROWS32 = 32 * F::pitch;
+  const int xw = ((tid >> 5) * F::a_pitch + (tid & 31) * 4) * 2;
+  const int ww0 = 2 * A_ST + (tid / F::cpr) * F::pitch + (tid % F::cpr) * 16, ww1 = ww0 + B_ST;
+  const int ar = ((wm + (lane & 31)) * F::a_pitch + half * 8) * 2;
+  const int br0 = 2 * A_ST + (wn + (lane & 31)) * F::pitch + half * F::frag_bytes, br1 = br0 + B_ST;
+
+  struct Regs {
+    u32x4 x[XC];
+    u32x4 w[WC];
+  };
+  auto fetch = [&](Regs& r, int kb) {
+    const uint32_t xk = (uint32_t)kb * (KB * XB), wk = (uint32_t)kb * F::row_bytes;
+#pragma unroll
+    for (int i = 0; i < XC; ++i) {
+      if constexpr (XB == 4) {
+        r.x[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xlane, xk + i * xstep, 0);
+      } else if constexpr (XB == 2) {
+        const xl_u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(xrs, xlane, xk + i * xstep, 0);
+        r.x[i] = u32x4{v[0], v[1], 0u, 0u};
+      } else {
+        r.x[i] = u32x4{__builtin_amdgcn_raw_buffer_load_b32(xrs, xlane, xk + i * xstep, 0), 0u,
+                       0u, 0u};
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < WC; ++i) r.w[i] = __builtin_amdgcn_raw_buffer_load_b128(wrs, wlane, wk + i * wstep, 0);
+  };
+  auto stage_units = [&](const Regs& r, const int BUF, int u0, int u1) {
+#pragma unroll
+    for (int u = 0; u < UNITS; ++u) {
+      if (u < u0 || u >= u1) continue;
+      if (u < XC) {
+        const xl_u32x2 pr = x4_bf16<XT>(r.x[u]);
+        *reinterpret_cast<u32x2*>(lds + xw + BUF * A_ST + u * XDST_STEP) = u32x2{pr[0], pr[1]};
+      } else {
+        const int i = u - XC;
+        uint8_t* d = lds + (BUF ? ww1 : ww0) + i * WDST_STEP;
+        if constexpr (F::pitch % 8 == 0) {
+          *reinterpret_cast<u32x2*>(d) = u32x2{r.w[i][0], r.w[i][1]};
+          *reinterpret_cast<u32x2*>(d + 8) = u32x2{r.w[i][2], r.w[i][3]};
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) *reinterpret_cast<uint32_t*>(d + 4 * q) = r.w[i][q];
+        }
+      }
+    }
+  };
+
+  f32x16 acc[MT][FNT];
+#pragma unroll
+  for (int a = 0; a < MT; ++a)
+#pragma unroll
+    for (int b = 0; b < FNT; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.0f;
+
+  const int kblocks = K / KB;
+  // Block kb in buffer BUF: fetch block kb+2 into `rf` (its block kb is in
+  // LDS already), multiply, and stage block kb+1 from `rs` into buffer BUF^1
+  // after MFMA steps 1..6.  Past the end the last block is fetched and staged
+  // again into the idle buffer, so the body has no branch.
+  auto body = [&](int kb, const int BUF, Regs& rf, const Regs& rs) {
+    const uint8_t* SA = lds + ar + BUF * A_ST;
+    const uint8_t* SB = lds + (BUF ? br1 : br0);
+    fetch(rf, min(kb + 2, kblocks - 1));
+    bf16x8 a[2][MT], b[2][FNT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) a[0][i] = *reinterpret_cast<const bf16x8*>(SA + i * A_ROWS32);
+#pragma unroll
+    for (int j = 0; j < FNT; ++j) b[0][j] = frag_to_bf16<WT>(SB + j * B_ROWS32);
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s) {
+      const int cur = s & 1, nxt = cur ^ 1;
+      if (s + 1 < STEPS) {
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+          a[nxt][i] = *reinterpret_cast<const bf16x8*>(SA + i * A_ROWS32 + (s + 1) * 32);
+#pragma unroll
+        for (int j = 0; j < FNT; ++j)
+          b[nxt][j] = frag_to_bf16<WT>(SB + j * B_ROWS32 + (s + 1) * 2 * F::frag_bytes);
+      }
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int j = 0; j < FNT; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[cur][i], b[cur][j], acc[i][j], 0, 0, 0);
+      if (s >= 1 && s <= 6) stage_units(rs, BUF ^ 1, (s - 1) * UNITS / 6, s * UNITS / 6);
+    }
+    __syncthreads();
+  };
+
+  Regs r0, r1;
+  fetch(r0, 0);
+  fetch(r1, min(1, kblocks - 1));
+  stage_units(r0, 0, 0, UNITS);
+  __syncthreads();
+  for (int kb = 0; kb < kblocks; kb += 2) {
+    body(kb, 0, r0, r1);
+    if (kb + 1 < kblocks) body(kb + 1, 1, r1, r0);
+  }
+
+  const float s = product_scale(w_scale, x_scale);
+  const float inv_o = epi_inv_scale(ep);
+  uint32_t am = 0;
+#pragma unroll
+  for (int j = 0; j < FNT; ++j) {
+    const int col = n0 + wn + j * 32 + (lane & 31);
+    const EpiChan k = epi_chan(ep, col);
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+        const float v = epi_value(ep, k, acc[i][j][r], s);
+        am = epi_track(am, v);
+        if (ep.out_dtype == F32)
+          __builtin_nontemporal_store(v, reinterpret_cast<float*>(y) + (size_t)row * N + col);
+        else
+          epi_store(ep.out_dtype, y, (size_t)row * N + col, v, inv_o);
+      }
+    }
+  }
+  epi_amax_commit(ep, am);
+}
+
+template <int WT, int XT>
+int launch(const uint8_t* x, const float* x_scale, int64_t M, int64_t K, const void* w,
+           const float* w_scale, const Epilogue& ep, int64_t N, void* y, hipStream_t stream) {
+  const int64_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+  const int64_t T = tiles_m * tiles_n;
+  if (T > 0x7FFFFFFF || M > 0x7FFFFFFF || N > 0x7FFFFFFF || K > 0x7FFFFFFF) return NOVAQ_EINVAL;
+  const auto* wq = static_cast<const uint8_t*>(w);
+  const bool rows_whole = M % BM == 0 && K > 0;
+  if constexpr (dtype_bits(WT) <= 8) {
+    // tile byte sizes (BM * K * bytes(x) for x) must fit the 31-bit buffer range
+    if (rows_whole && N % 256 == 0 && K % 128 == 0 && K <= (1 << 21)) {
+      hipLaunchKernelGGL((linear_wide_kernel<WT, XT>), dim3((unsigned)(tiles_m * (N / 256))),
+                         dim3(512), 0, stream, x, x_scale, wq, w_scale, ep, y, (int)M, (int)N,
+                         (int)K, (int)tiles_m, (int)(N / 256));
+      return check_launch();
+    }
+  }
+  if constexpr (WT != F32) {
+    if (rows_whole && N % 256 == 0 && K % BK == 0) {
+      hipLaunchKernelGGL((linear_pipe_kernel<WT, XT, 256, 8, 1, 3>),
+                         dim3((unsigned)(tiles_m * (N / 256))), dim3(512), 0, stream, x, x_scale,
+                         wq, w_scale, ep, y, (int)M, (int)N, (int)K, (int)tiles_m, (int)(N / 256));
+      return check_launch();
+    }
+    if (rows_whole && N % 128 == 0 && K % BK == 0) {
+      hipLaunchKernelGGL((linear_pipe_kernel<WT, XT, 128, 4, 2, 2>),
+                         dim3((unsigned)(tiles_m * (N / 128))), dim3(256), 0, stream, x, x_scale,
+                         wq, w_scale, ep, y, (int)M, (int)N, (int)K, (int)tiles_m, (int)(N / 128));
+      return check_launch();
+    }
+  }
+  const int x_vec = (K % 4) == 0;
+  const int w_vec = ((K * W<WT>::bits / 8) % 16) == 0 && (K * W<WT>::bits) % 8 == 0;
+  hipLaunchKernelGGL((linear_kernel<WT, XT>), dim3((unsigned)T), dim3(THREADS), 0, stream, x,
+                     x_scale, wq, w_scale, ep, y, (int)M, (int)N, (int)K, (int)tiles_m,
+                     (int)tiles_n, x_vec, w_vec);
+  return check_launch();
+}
+
+}  // namespace
+
+// The product for x stored as XT (one translation unit per XT instantiates it).
+template <int XT>
+int linear_launch_xt(const uint8_t* x, const float* x_scale, int64_t N, int64_t D_in,
+                     const void* w_q, int w_dtype, const float* w_scale, const Epilogue& ep,
+                     int64_t D_out, void* y, hipStream_t stream) {
+  switch (w_dtype) {
+    case E4M3: return launch<E4M3, XT>(x, x_scale, N, D_in, w_q, w_scale, ep, D_out, y, stream);
+    case E5M2: return launch<E5M2, XT>(x, x_scale, N, D_in, w_q, w_scale, ep, D_out, y, stream);
+    case E2M1: return launch<E2M1, XT>(x, x_scale, N, D_in, w_q, w_scale, ep, D_out, y, stream);
+    case BF16: return launch<BF16, XT>(x, x_scale, N, D_in, w_q, w_scale, ep, D_out, y, stream);
+    case F16: return launch<F16, XT>(x, x_scale, N, D_in, w_q, w_scale, ep, D_out, y, stream);
+    case F32: return launch<F32, XT>(x, x_scale, N, D_in, w_q, w_scale, ep, D_out, y, stream);
+    default: return NOVAQ_EDTYPE;
+  }
+}
+
+}  // namespace novaq

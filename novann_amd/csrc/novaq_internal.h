@@ -33,6 +33,10 @@ int linear_launch(const float* x, int64_t N, int64_t D_in, const void* w_q, int 
 int linear_launch(const float* x, int64_t N, int64_t D_in, const void* w_q, int w_dtype,
                   const float* w_scale, const Epilogue& ep, int64_t D_out, void* y,
                   hipStream_t stream);
+// x stored as x_dtype (F32, BF16, F16, E4M3, E5M2) with per-tensor scale x_scale (NULL = 1).
+int linear_launch(const void* x, int x_dtype, const float* x_scale, int64_t N, int64_t D_in,
+                  const void* w_q, int w_dtype, const float* w_scale, const Epilogue& ep,
+                  int64_t D_out, void* y, hipStream_t stream);
 int conv2d_launch(const float* x, int64_t N, int64_t C, int64_t H, int64_t W, const void* w_q,
                   int w_dtype, const float* w_scale, int64_t C_out, int KH, int KW, int sh,
                   int sw, int ph, int pw, int pad_mode, const float* bias, float* y,
@@ -41,6 +45,10 @@ int conv2d_launch(const float* x, int64_t N, int64_t C, int64_t H, int64_t W, co
                   int w_dtype, const float* w_scale, int64_t C_out, int KH, int KW, int sh,
                   int sw, int ph, int pw, int pad_mode, const Epilogue& ep, void* y,
                   hipStream_t stream);
+int conv2d_launch(const void* x, int x_dtype, const float* x_scale, int64_t N, int64_t C,
+                  int64_t H, int64_t W, const void* w_q, int w_dtype, const float* w_scale,
+                  int64_t C_out, int KH, int KW, int sh, int sw, int ph, int pw, int pad_mode,
+                  const Epilogue& ep, void* y, hipStream_t stream);
 
 // Sets count 32-bit words at p to v (a kernel, so it may be captured in graphs).
 int fill_u32_launch(uint32_t* p, uint32_t v, int count, hipStream_t stream);

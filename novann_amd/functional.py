@@ -42,6 +42,26 @@ def _to_device_f32(a, what: str) -> Tuple[torch.Tensor, bool]:
     raise TypeError(f"{what} must be a numpy array or a torch tensor")
 
 
+_X_DTYPES = {torch.float16: "f16", torch.bfloat16: "bf16", torch.float8_e4m3fn: "e4m3",
+             torch.float8_e5m2: "e5m2"}
+
+
+def _x_arg(a, what: str):
+    """(device tensor, dtype name, scale tensor or None, logical shape, was_numpy)
+    for a product input: fp32 (numpy or tensors of other float types are
+    converted), a bf16 / f16 / FP8 device tensor as stored, or a
+    quant.Quantized E4M3 / E5M2 activation (codes + its scale)."""
+    from . import quant
+    if isinstance(a, quant.Quantized):
+        if a.dtype not in ("e4m3", "e5m2"):
+            raise TypeError(f"{what}: a quantized input must be e4m3 or e5m2, got {a.dtype}")
+        return a.data.contiguous(), a.dtype, a.scale, tuple(a.shape), False
+    if isinstance(a, torch.Tensor) and a.is_cuda and a.dtype in _X_DTYPES:
+        return a.contiguous(), _X_DTYPES[a.dtype], None, tuple(a.shape), False
+    t, was_numpy = _to_device_f32(a, what)
+    return t, "f32", None, tuple(t.shape), was_numpy
+
+
 def _weight_args(weight, dev: torch.device):
     """(codes tensor, dtype code, scale tensor or None) for a weight."""
     if isinstance(weight, QuantizedParameters):
@@ -158,26 +178,27 @@ def linear(input, weight, bias: Optional[Parameters] = None, *,
     (N, D_out) fp32: an ndarray when input was an ndarray.  ``epilogue``
     (keyword only, not in the reference) fuses what follows the layer (eval
     BatchNorm1d, ReLU, a cast of y) into the product; see Epilogue."""
-    x, was_numpy = _to_device_f32(input, "input")
-    if x.dim() != 2:
-        raise ValueError(f"linear expects a 2-D input, got shape {tuple(x.shape)}")
+    x, xdt, xs, xshape, was_numpy = _x_arg(input, "input")
+    if len(xshape) != 2:
+        raise ValueError(f"linear expects a 2-D input, got shape {xshape}")
     wshape = weight.shape if isinstance(weight, QuantizedParameters) else tuple(
         (weight.data if isinstance(weight, Parameters) else weight).shape)
-    if len(wshape) != 2 or wshape[1] != x.shape[1]:
-        raise ValueError(f"matmul: input {tuple(x.shape)} does not match weight {wshape}")
-    N, D_in = x.shape
+    if len(wshape) != 2 or wshape[1] != xshape[1]:
+        raise ValueError(f"matmul: input {xshape} does not match weight {wshape}")
+    N, D_in = xshape
     D_out = wshape[0]
     w, wdt, ws = _weight_args(weight, x.device)
     b = _bias_arg(bias, x.device)
     if b is not None and b.numel() != D_out:
         raise ValueError(f"bias has {b.numel()} values, expected {D_out}")
-    if epilogue is not None:
+    if epilogue is not None or xdt != "f32":
         st, ydt, keep = _epilogue_args(epilogue, D_out, x.device)
         y = torch.empty((N, D_out), dtype=ydt, device=x.device)
         check(_lib.load().novaq_linear_forward_ex(
-            x.data_ptr(), DTYPES["f32"], None, N, D_in, w.data_ptr(), wdt,
+            x.data_ptr(), DTYPES[xdt], None if xs is None else xs.data_ptr(), N, D_in,
+            w.data_ptr(), wdt,
             None if ws is None else ws.data_ptr(), None if b is None else b.data_ptr(), D_out,
-            ctypes.byref(st), y.data_ptr(), _stream(x.device)), "linear")
+            None if st is None else ctypes.byref(st), y.data_ptr(), _stream(x.device)), "linear")
         return _finish(y, epilogue, was_numpy)
     y = torch.empty((N, D_out), dtype=torch.float32, device=x.device)
     check(_lib.load().novaq_linear_forward(
@@ -259,10 +280,10 @@ def conv2d(input, weight, kernel_size: IntPair, stride: IntPair = 1, padding: In
     if extras:
         raise NotImplementedError("conv2d(extras=True): the im2col matrix is never "
                                   "materialised on this path")
-    x, was_numpy = _to_device_f32(input, "input")
-    if x.dim() != 4:
-        raise ValueError(f"conv2d expects (N, C, H, W), got {tuple(x.shape)}")
-    N, C, H, W = x.shape
+    x, xdt, xs, xshape, was_numpy = _x_arg(input, "input")
+    if len(xshape) != 4:
+        raise ValueError(f"conv2d expects (N, C, H, W), got {xshape}")
+    N, C, H, W = xshape
     wshape = weight.shape if isinstance(weight, QuantizedParameters) else tuple(
         (weight.data if isinstance(weight, Parameters) else weight).shape)
     if len(wshape) != 4 or wshape[1] != C or (wshape[2], wshape[3]) != (KH, KW):
@@ -277,14 +298,15 @@ def conv2d(input, weight, kernel_size: IntPair, stride: IntPair = 1, padding: In
     b = _bias_arg(bias, x.device)
     if b is not None and b.numel() != C_out:
         raise ValueError(f"bias has {b.numel()} values, expected {C_out}")
-    if epilogue is not None:
+    if epilogue is not None or xdt != "f32":
         st, ydt, keep = _epilogue_args(epilogue, C_out, x.device)
         y = torch.empty((N, C_out, OH, OW), dtype=ydt, device=x.device)
         check(_lib.load().novaq_conv2d_forward_ex(
-            x.data_ptr(), DTYPES["f32"], None, N, C, H, W, w.data_ptr(), wdt,
-            None if ws is None else ws.data_ptr(), C_out, KH, KW, sh, sw, ph, pw,
-            PAD_MODES[padding_mode], None if b is None else b.data_ptr(), ctypes.byref(st),
-            y.data_ptr(), _stream(x.device)), "conv2d")
+            x.data_ptr(), DTYPES[xdt], None if xs is None else xs.data_ptr(), N, C, H, W,
+            w.data_ptr(), wdt, None if ws is None else ws.data_ptr(), C_out, KH, KW, sh, sw, ph,
+            pw, PAD_MODES[padding_mode], None if b is None else b.data_ptr(),
+            None if st is None else ctypes.byref(st), y.data_ptr(), _stream(x.device)),
+            "conv2d")
         return _finish(y, epilogue, was_numpy)
     y = torch.empty((N, C_out, OH, OW), dtype=torch.float32, device=x.device)
     check(_lib.load().novaq_conv2d_forward(

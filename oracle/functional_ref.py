@@ -124,7 +124,8 @@ def conv2d_backward(grad: np.ndarray, x: np.ndarray, w: np.ndarray, stride=(1, 1
 def relu(x: np.ndarray) -> np.ndarray:
     """functional.py:19-20: the mask as x's dtype, then a multiply (negative
     values give -0, NaN stays NaN, -Inf gives NaN)."""
-    return x * (x > 0).astype(x.dtype, copy=False)
+    with np.errstate(invalid="ignore"):  # -Inf * 0 is NaN, as in the reference
+        return x * (x > 0).astype(x.dtype, copy=False)
 
 
 def batchnorm_eval(x: np.ndarray, gamma, beta, running_mean, running_var, eps: float = 1e-5,
