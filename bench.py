@@ -393,6 +393,107 @@ def bench_conv_backward(dev, iters: int = 20, warmup: int = 5):
     return {"workload": "BASELINE config [5] shapes, backward", "layers": out}
 
 
+def bench_epilogue(dev, iters: int = 20, warmup: int = 5):
+    """Fused epilogues (eval BatchNorm + ReLU + bf16 store) on config [5]'s
+    conv2 and config [4]'s Linear, each reading its input as the bf16 a
+    previous fused layer stores; beside them the unfused equivalent of the
+    same layer: the fp32-input product with an fp32 output, then a separate
+    fp32 -> bf16 cast of y (the HBM round trip the fusion removes; the
+    BatchNorm and ReLU would cost another such pass).  A 512 MiB write evicts
+    the MALL before every timed launch."""
+    import ctypes
+
+    import torch
+
+    from novann_amd import _lib, quant
+    lib = _lib.load()
+    g = torch.Generator(device=dev)
+    g.manual_seed(8)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    flush = torch.empty(1 << 27, dtype=torch.float32, device=dev)
+
+    def timed(fn):
+        for _ in range(warmup):
+            fn()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(iters)]
+        torch.cuda.synchronize(dev)
+        for e0, e1 in ev:
+            flush.zero_()
+            e0.record()
+            fn()
+            e1.record()
+        torch.cuda.synchronize(dev)
+        return sum(e0.elapsed_time(e1) for e0, e1 in ev) / iters
+
+    def bn_epilogue(C, out_dtype):
+        mul = (torch.rand(C, generator=g, device=dev) + 0.5).contiguous()
+        add = (torch.randn(C, generator=g, device=dev) * 0.1).contiguous()
+        return _lib.Epilogue(mul.data_ptr(), add.data_ptr(), None, None, 1,
+                             _lib.DTYPES[out_dtype]), (mul, add)
+
+    out = {}
+    # conv2 of config [5]: (256, 32, 28, 28) -> (256, 64, 28, 28), 3x3/s1/p1, E2M1
+    N, C, Co, H = 256, 32, 64, 28
+    x32 = torch.rand((N, C, H, H), generator=g, device=dev)
+    x16 = x32.to(torch.bfloat16)
+    w = torch.randn((Co, C, 3, 3), generator=g, device=dev) * (2.0 / (C * 9)) ** 0.5
+    q = quant.quantize(w.contiguous(), "e2m1")
+    y16 = torch.empty((N, Co, H, H), dtype=torch.bfloat16, device=dev)
+    y32 = torch.empty((N, Co, H, H), dtype=torch.float32, device=dev)
+    ep, keep = bn_epilogue(Co, "bf16")
+
+    def conv_fused():
+        _lib.check(lib.novaq_conv2d_forward_ex(
+            x16.data_ptr(), _lib.BF16, None, N, C, H, H, q.data.data_ptr(), _lib.E2M1,
+            q.scale.data_ptr(), Co, 3, 3, 1, 1, 1, 1, 0, None, ctypes.byref(ep), y16.data_ptr(),
+            stream), "conv2d fused")
+
+    def conv_unfused():
+        _lib.check(lib.novaq_conv2d_forward(x32.data_ptr(), N, C, H, H, q.data.data_ptr(),
+                                            _lib.E2M1, q.scale.data_ptr(), Co, 3, 3, 1, 1, 1,
+                                            1, 0, None, y32.data_ptr(), stream), "conv2d")
+        _lib.check(lib.novaq_cast(y32.data_ptr(), _lib.F32, y16.data_ptr(), _lib.BF16,
+                                  y32.numel(), None, stream), "cast")
+    ms_f, ms_u = timed(conv_fused), timed(conv_unfused)
+    nb = (x16.numel() + y16.numel()) * 2
+    out["conv2"] = {"layer": "conv 32->64 + BN + ReLU, bf16 in / bf16 out",
+                    "ms": round(ms_f, 4), "GB/s": round(nb / (ms_f * 1e-3) / 1e9, 1),
+                    "frac_hbm": round(nb / (ms_f * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "bytes": nb,
+                    "unfused_ms": round(ms_u, 4),
+                    "unfused": "fp32 conv (fp32 in / out) + fp32->bf16 cast of y"}
+    del x32, x16, y16, y32
+    # Linear of config [4]: x (2048, 4096) bf16, W (4096, 4096) E4M3
+    M_, K, Nn = 2048, 4096, 4096
+    x32 = torch.randn((M_, K), generator=g, device=dev)
+    x16 = x32.to(torch.bfloat16)
+    w = torch.randn((Nn, K), generator=g, device=dev) * (2.0 / K) ** 0.5
+    wq = quant.quantize(w, "e4m3")
+    y16 = torch.empty((M_, Nn), dtype=torch.bfloat16, device=dev)
+    y32 = torch.empty((M_, Nn), dtype=torch.float32, device=dev)
+    ep2, keep2 = bn_epilogue(Nn, "bf16")
+
+    def lin_fused():
+        _lib.check(lib.novaq_linear_forward_ex(
+            x16.data_ptr(), _lib.BF16, None, M_, K, wq.data.data_ptr(), _lib.E4M3,
+            wq.scale.data_ptr(), None, Nn, ctypes.byref(ep2), y16.data_ptr(), stream),
+            "linear fused")
+
+    def lin_unfused():
+        _lib.check(lib.novaq_linear_forward(x32.data_ptr(), M_, K, wq.data.data_ptr(), _lib.E4M3,
+                                            wq.scale.data_ptr(), None, Nn, y32.data_ptr(),
+                                            stream), "linear")
+        _lib.check(lib.novaq_cast(y32.data_ptr(), _lib.F32, y16.data_ptr(), _lib.BF16,
+                                  y32.numel(), None, stream), "cast")
+    ms_f, ms_u = timed(lin_fused), timed(lin_unfused)
+    tf = 2.0 * M_ * Nn * K / (ms_f * 1e-3) / 1e12
+    out["linear"] = {"layer": "Linear 4096x4096 E4M3 + BN1d + ReLU, bf16 in / bf16 out",
+                     "ms": round(ms_f, 4), "TFLOP/s": round(tf, 1),
+                     "frac_mfma": round(tf / BF16_PEAK_TFLOPS, 4), "unfused_ms": round(ms_u, 4),
+                     "unfused": "fp32-input Linear (fp32 y) + fp32->bf16 cast of y"}
+    return {"workload": "BASELINE configs [5] (conv2) and [4] with fused epilogues", **out}
+
+
 def cpu_baseline(sample: int, min_seconds: float = 10.0):
     """The C oracle running the same sweep on a bounded sample (all host cores)."""
     import numpy as np
@@ -468,6 +569,8 @@ def main() -> int:
     log(f"conv2d: {conv}")
     conv_bwd = None if args.no_conv else bench_conv_backward(dev)
     log(f"conv2d backward: {conv_bwd}")
+    epi = None if args.no_conv else bench_epilogue(dev)
+    log(f"fused epilogues: {epi}")
     fp4 = None if args.no_fp4 else bench_fp4(dev)
     log(f"fp4: {fp4}")
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_sample)
@@ -490,6 +593,7 @@ def main() -> int:
         "linear_backward": lin_bwd,
         "conv2d": conv,
         "conv2d_backward": conv_bwd,
+        "epilogue": epi,
         "fp4": fp4,
         "cpu_baseline": cpu,
     }

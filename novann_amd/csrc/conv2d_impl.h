@@ -383,7 +383,7 @@ __global__ __launch_bounds__(THREADS, CONV_OCC) void conv2d_kernel(
           const int co = co0 + mt * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
           if (co < g.C_out) {
             const float v = epi_value(ep, epi_chan(ep, co), acc[mt][nt][r], s);
-            am = epi_track(am, v);
+            if (ep.amax) am = epi_track(am, v);
             epi_store(ep.out_dtype, y, ((int64_t)n * g.C_out + co) * npix + p, v, inv_o);
           }
         }
@@ -663,6 +663,7 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
   const float s = product_scale(w_scale, x_scale);
   const float inv_o = epi_inv_scale(ep);
   uint32_t am = 0;
+  const bool plain = !ep.mul && !ep.add && !ep.relu && !ep.amax && ep.out_dtype == F32;
   const int64_t npix = (int64_t)g.OH * g.OW;
   const int nt_live = min(4, (min(CO_TILE, g.C_out - co0) + 15) >> 4);
   const uint8_t* wfrag = wl + lr * g.wrow + lg * GB;
@@ -723,13 +724,27 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
       for (int t = 0; t < 4; ++t) {
         const int co = co0 + t * 16 + lr;
         if (t >= nt_live || co >= g.C_out) continue;
-        const EpiChan k = epi_chan(ep, co);
         const int64_t di = ((int64_t)n * g.C_out + co) * npix + (int64_t)oh0 * g.OW + p;
+        if (plain) {
+          // bias only, fp32 output: one 16-byte store of the four pixels
+          const float bv = ep.bias ? ep.bias[co] : 0.0f;
+          float* dst = reinterpret_cast<float*>(y) + di;
+          const f32x4 v = acc[m][t] * s + bv;
+          if (p + 3 < P && (di & 3) == 0) {
+            *reinterpret_cast<f32x4*>(dst) = v;
+          } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (p + i < P) dst[i] = v[i];
+          }
+          continue;
+        }
+        const EpiChan k = epi_chan(ep, co);
         float v[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           v[i] = epi_value(ep, k, acc[m][t][i], s);
-          if (p + i < P) am = epi_track(am, v[i]);
+          if (ep.amax && p + i < P) am = epi_track(am, v[i]);
         }
         // plain stores: the 64-byte pieces of a line written by neighbouring
         // lanes and waves merge in L2 before they reach HBM

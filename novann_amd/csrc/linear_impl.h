@@ -256,7 +256,7 @@ __global__ __launch_bounds__(THREADS, 1) void linear_kernel(
         const int row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
         if (row < M) {
           const float v = epi_value(ep, k, acc[i][j][r], s);
-          am = epi_track(am, v);
+          if (ep.amax) am = epi_track(am, v);
           epi_store(ep.out_dtype, y, (size_t)row * N + col, v, inv_o);
         }
       }
@@ -481,7 +481,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void linear_pipe_kernel(
       for (int r = 0; r < 16; ++r) {
         const int row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
         const float v = epi_value(ep, k, acc[i][j][r], s);
-        am = epi_track(am, v);
+        if (ep.amax) am = epi_track(am, v);
         if (ep.out_dtype == F32)
           __builtin_nontemporal_store(v, reinterpret_cast<float*>(y) + (size_t)row * N + col);
         else
@@ -680,7 +680,7 @@ __global__ __launch_bounds__(512, 1) void linear_wide_kernel(
       for (int r = 0; r < 16; ++r) {
         const int row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
         const float v = epi_value(ep, k, acc[i][j][r], s);
-        am = epi_track(am, v);
+        if (ep.amax) am = epi_track(am, v);
         if (ep.out_dtype == F32)
           __builtin_nontemporal_store(v, reinterpret_cast<float*>(y) + (size_t)row * N + col);
         else

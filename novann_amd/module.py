@@ -6,7 +6,10 @@ for quantized weights: device codes (E4M3 / E5M2 / E2M1) plus a per-tensor
 scale.  ``Linear`` mirrors novann/layers/linear/linear.py:10-108 and
 ``Conv2d`` novann/layers/convolutional/conv2d.py:9-207 (same constructor
 arguments, parameter shapes and defaults, forward and backward); both call the
-GPU operators in ``functional``.
+GPU operators in ``functional``.  ``BatchNorm2d`` / ``BatchNorm1d`` hold the
+reference's parameters and running statistics (batchnorm2d.py:33-55,
+batchnorm1d.py:33-55) and ``ReLU`` stands for novann's ReLU layer; on this
+path they run fused into the product before them (``fuse``), in eval mode.
 """
 from __future__ import annotations
 
@@ -192,3 +195,92 @@ class Conv2d:
 
     def parameters(self):
         return [self.weight] + ([self.bias] if self.bias is not None else [])
+
+
+class _BatchNorm:
+    """Parameters and running statistics of novann's BatchNorm layers, used
+    as an eval-mode epilogue of the product before them."""
+
+    _shape_tail: tuple = ()
+
+    def __init__(self, num_features: int, momentum: float = 0.1, eps: float = 1e-5) -> None:
+        self.num_features = int(num_features)
+        self.momentum, self.eps = float(momentum), float(eps)
+        shape = (1, self.num_features) + self._shape_tail
+        self.gamma = Parameters(np.ones(shape))
+        self.beta = Parameters(np.zeros(shape))
+        self.gamma.name, self.beta.name = "gamma", "beta"
+        self.running_mean = np.zeros(shape)
+        self.running_var = np.ones(shape)
+
+    def epilogue(self, relu: bool = False, **kw):
+        """The fused epilogue gamma * (v - mean) / sqrt(var + eps) + beta
+        (batchnorm2d.py:98-102), then ReLU when ``relu``."""
+        from .functional import Epilogue
+        return Epilogue.batchnorm(self.gamma.data, self.beta.data, self.running_mean,
+                                  self.running_var, self.eps, relu=relu, **kw)
+
+    def parameters(self):
+        return [self.gamma, self.beta]
+
+
+class BatchNorm2d(_BatchNorm):
+    """novann BatchNorm2d's state (batchnorm2d.py:33-55): (1, C, 1, 1) arrays."""
+    _shape_tail = (1, 1)
+
+
+class BatchNorm1d(_BatchNorm):
+    """novann BatchNorm1d's state (batchnorm1d.py:33-55): (1, C) arrays."""
+    _shape_tail = ()
+
+
+class ReLU:
+    """novann's ReLU layer (relu.py:8-48): x * (x > 0), fused into the
+    product before it."""
+
+
+class Fused:
+    """A Linear or Conv2d followed by an eval-mode BatchNorm and / or a ReLU,
+    run as one product whose epilogue applies them (the layers that follow a
+    product on novann's main path, main.py:24-46).  ``out_dtype`` 'bf16',
+    'f16', 'e4m3' or 'e5m2' stores the activation narrow for the next product
+    (FP8 with ``out_scale``, e.g. from a calibration pass's ``out_amax``)."""
+
+    def __init__(self, layer, bn: Optional[_BatchNorm] = None, relu: bool = False,
+                 out_dtype: str = "f32", out_scale=None) -> None:
+        if not isinstance(layer, (Linear, Conv2d)):
+            raise TypeError("fuse: the first layer must be a Linear or a Conv2d")
+        want = BatchNorm2d if isinstance(layer, Conv2d) else BatchNorm1d
+        if bn is not None and not isinstance(bn, want):
+            raise TypeError(f"fuse: {type(layer).__name__} is followed by {want.__name__}")
+        self.layer, self.bn, self.relu = layer, bn, relu
+        self.out_dtype, self.out_scale = out_dtype, out_scale
+
+    def __call__(self, x, out_amax=None):
+        return self.forward(x, out_amax)
+
+    def forward(self, x, out_amax=None):
+        from . import functional as F
+        kw = dict(relu=self.relu, out_dtype=self.out_dtype, out_scale=self.out_scale,
+                  out_amax=out_amax)
+        ep = self.bn.epilogue(**kw) if self.bn is not None else F.Epilogue(**kw)
+        L = self.layer
+        if isinstance(L, Linear):
+            return F.linear(x, L.weight, L.bias, epilogue=ep)
+        return F.conv2d(x, L.weight, (L.KH, L.KW), (L.sh, L.sw), (L.ph, L.pw), bias=L.bias,
+                        padding_mode=L.pm, epilogue=ep)
+
+
+def fuse(*layers, out_dtype: str = "f32", out_scale=None) -> Fused:
+    """Fuse [Linear | Conv2d] [BatchNorm1d | BatchNorm2d] [ReLU] into one layer."""
+    if not layers:
+        raise ValueError("fuse: no layers")
+    head, rest = layers[0], list(layers[1:])
+    bn = rest.pop(0) if rest and isinstance(rest[0], _BatchNorm) else None
+    relu = bool(rest) and isinstance(rest[0], ReLU)
+    if relu:
+        rest.pop(0)
+    if rest:
+        raise ValueError(f"fuse: cannot fuse {type(rest[0]).__name__} after "
+                         f"{type(head).__name__}")
+    return Fused(head, bn, relu, out_dtype, out_scale)

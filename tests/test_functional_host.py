@@ -48,3 +48,20 @@ def test_kaiming_normal_statistics():
     assert abs(w.std() - np.sqrt(2.0 / 288)) < 0.01 * np.sqrt(2.0 / 288) * 5
     w = kaiming_normal_((4096, 4096), rng=rng)
     assert abs(w.std() - np.sqrt(2.0 / 4096)) < 1e-3
+
+
+def test_fuse_validates_the_layer_sequence():
+    """fuse() takes [Linear|Conv2d] [BatchNorm] [ReLU], in that order (host logic)."""
+    from novann_amd import module as M
+    conv = M.Conv2d.__new__(M.Conv2d)   # no weights needed to check the sequence
+    lin = M.Linear.__new__(M.Linear)
+    f = M.fuse(conv, M.BatchNorm2d(4), M.ReLU())
+    assert f.bn is not None and f.relu
+    assert M.fuse(lin, M.ReLU()).bn is None
+    with pytest.raises(TypeError):
+        M.fuse(conv, M.BatchNorm1d(4))
+    with pytest.raises(ValueError):
+        M.fuse(conv, M.ReLU(), M.BatchNorm2d(4))
+    bn = M.BatchNorm2d(3)
+    assert bn.gamma.data.shape == (1, 3, 1, 1) and bn.running_var.shape == (1, 3, 1, 1)
+    assert M.BatchNorm1d(5).running_mean.shape == (1, 5)

@@ -391,3 +391,50 @@ def test_main_py_blocks_chained_through_narrow_activations():
 def F_dequant(q):
     from novann_amd import quant
     return quant.dequantize(q).cpu().numpy()
+
+
+def test_fused_layers_from_the_module_api():
+    """novann main.py:24-46's blocks built from this package's layers and
+    fused (conv+BN+ReLU x2 with bf16 activations, then a Linear+BN1d+ReLU on
+    a pooled vector), against the reference formulas in fp64."""
+    from novann_amd import module as M
+    rng = np.random.default_rng(41)
+    conv1 = M.Conv2d(1, 16, 3, padding=1, bias=False, weight_dtype="e2m1")
+    conv2 = M.Conv2d(16, 32, 3, padding=1, stride=2, bias=False, weight_dtype="e2m1")
+    bns = [M.BatchNorm2d(16), M.BatchNorm2d(32)]
+    for bn in bns:
+        g, b, m, v = bn_params(bn.num_features, rng)
+        bn.gamma.data = g.reshape(bn.gamma.data.shape)
+        bn.beta.data = b.reshape(bn.beta.data.shape)
+        bn.running_mean = m.reshape(bn.running_mean.shape)
+        bn.running_var = v.reshape(bn.running_var.shape)
+    block1 = M.fuse(conv1, bns[0], M.ReLU(), out_dtype="bf16")
+    block2 = M.fuse(conv2, bns[1], M.ReLU())
+    x = rng.uniform(0, 1, (32, 1, 28, 28)).astype(np.float32)
+    y1 = block1(torch.from_numpy(x).cuda())
+    y2 = block2(y1)
+    assert y1.dtype == torch.bfloat16 and tuple(y2.shape) == (32, 32, 14, 14)
+
+    def ref(a, conv, bn):
+        wdeq = conv.weight.dequantize().cpu().numpy().astype(np.float64).reshape(conv.weight.shape)
+        return R.relu(R.batchnorm_eval(R.conv2d(a, wdeq, (conv.sh, conv.sw), (conv.ph, conv.pw)),
+                                       bn.gamma.data, bn.beta.data, bn.running_mean,
+                                       bn.running_var, bn.eps))
+    a1 = y1.float().cpu().numpy()
+    r1 = ref(x.astype(np.float64), conv1, bns[0])
+    assert np.abs(a1 - r1).max() / np.abs(r1).max() <= TOL
+    r2 = ref(a1.astype(np.float64), conv2, bns[1])
+    got = y2.cpu().numpy()
+    assert np.abs(got - r2).max() / np.abs(r2).max() <= TOL
+    # classifier block: Linear(32 -> 16, no bias) + BatchNorm1d + ReLU on pooled features
+    lin = M.Linear(32, 16, bias=False, weight_dtype="e4m3")
+    bn1 = M.BatchNorm1d(16)
+    g, b, m, v = bn_params(16, rng)
+    bn1.gamma.data, bn1.beta.data = g.reshape(1, 16), b.reshape(1, 16)
+    bn1.running_mean, bn1.running_var = m.reshape(1, 16), v.reshape(1, 16)
+    feat = got.mean(axis=(2, 3)).astype(np.float32)
+    out = M.fuse(lin, bn1, M.ReLU())(feat)
+    wdeq = lin.weight.dequantize().cpu().numpy().astype(np.float64).reshape(16, 32)
+    r3 = R.relu(R.batchnorm_eval(R.linear(feat.astype(np.float64), wdeq), g, b, m, v))
+    assert isinstance(out, np.ndarray) and out.shape == (32, 16)
+    assert np.abs(out - r3).max() / np.abs(r3).max() <= TOL
