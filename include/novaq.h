@@ -195,6 +195,40 @@ int novaq_conv2d_forward_ex(const void *x, int x_dtype, const float *x_scale, in
                             int ph, int pw, int pad_mode, const float *bias,
                             const novaq_epilogue *epi, void *y, void *stream);
 
+/* Hyper-parameters of one AdamW step (novann AdamW, adamw.py:17-38): Python
+ * floats there, doubles here; step is the 1-based step count t; decay = 0
+ * marks a parameter the reference never decays (BatchNorm gamma / beta,
+ * adamw.py:50). */
+typedef struct novaq_adamw {
+  double lr, beta1, beta2, eps, weight_decay;
+  int64_t step;
+  int decay;
+} novaq_adamw;
+
+/* One AdamW step on n fp32 weights w with gradient grad and moment buffers
+ * m, v (all device, updated in place):
+ *   m = b1 m + (1 - b1) g;  v = b2 v + (1 - b2) g^2
+ *   w -= lr (m / (1 - b1^t)) / (sqrt(v / (1 - b2^t)) + eps)
+ *   w -= (lr wd) w                      (if weight_decay > 0 and decay)
+ * each a float32 operation with the hyper-parameter rounded to float32, as
+ * numpy evaluates the reference's statements on its float32 arrays, so the
+ * result equals the reference's bit for bit.  w_amax (optional, device)
+ * receives max |w| of the updated weights (NaN ignored).
+ * Replaces: AdamW.step for one parameter (novann/optim/adamw.py:41-65). */
+int novaq_adamw_step(float *w, const float *grad, float *m, float *v, int64_t n,
+                     const novaq_adamw *hp, float *w_amax, void *stream);
+
+/* novaq_adamw_step on fp32 master weights, then their re-quantization into
+ * codes (q_dtype E4M3, E5M2 or E2M1) with a fresh per-tensor scale:
+ * amax_scale[0] = max |w|, amax_scale[1] = s = amax / fmt_max, codes =
+ * enc(w * (1/s)), exactly as novaq_quantize of the updated w.  The packed
+ * weight a quantized layer multiplies with follows each optimizer step.
+ * No reference counterpart as one call: the reference steps float32 weights
+ * (adamw.py:41-65) and has no quantized storage (module.py:20-23). */
+int novaq_adamw_requantize(float *w, const float *grad, float *m, float *v, int64_t n,
+                           const novaq_adamw *hp, void *codes, int q_dtype, float *amax_scale,
+                           void *stream);
+
 /* dst (cols x rows, dst_dtype) = src (rows x cols, src_dtype) transposed, both
  * row-major.  src_dtype == dst_dtype permutes the stored values (quantized
  * codes are never re-encoded; E2M1 needs even rows and cols, both sides

@@ -27,6 +27,14 @@ class Epilogue(ctypes.Structure):
                 ("relu", ctypes.c_int), ("out_dtype", ctypes.c_int)]
 
 
+class AdamW(ctypes.Structure):
+    """struct novaq_adamw (include/novaq.h)."""
+    _fields_ = [("lr", ctypes.c_double), ("beta1", ctypes.c_double),
+                ("beta2", ctypes.c_double), ("eps", ctypes.c_double),
+                ("weight_decay", ctypes.c_double), ("step", ctypes.c_int64),
+                ("decay", ctypes.c_int)]
+
+
 # Every symbol include/novaq.h declares, with its ctypes signature.
 _vp, _i32, _i64, _f32p = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_void_p
 _epip = ctypes.POINTER(Epilogue)
@@ -50,6 +58,10 @@ SIGNATURES = {
     "novaq_conv2d_forward_ex": (_i32, [_vp, _i32, _f32p, _i64, _i64, _i64, _i64, _vp, _i32,
                                        _f32p, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
                                        _f32p, _epip, _vp, _vp]),
+    "novaq_adamw_step": (_i32, [_f32p, _f32p, _f32p, _f32p, _i64, ctypes.POINTER(AdamW), _f32p,
+                                _vp]),
+    "novaq_adamw_requantize": (_i32, [_f32p, _f32p, _f32p, _f32p, _i64, ctypes.POINTER(AdamW),
+                                      _vp, _i32, _f32p, _vp]),
     "novaq_transpose": (_i32, [_vp, _i32, _i64, _i64, _vp, _i32, _vp]),
     "novaq_colsum": (_i32, [_f32p, _i64, _i64, _f32p, _vp]),
     "novaq_linear_backward_workspace": (ctypes.c_size_t, [_i64, _i64, _i64, _i32]),

@@ -226,6 +226,31 @@ int novaq_conv2d_forward_ex(const void* x, int x_dtype, const float* x_scale, in
                        sw, ph, pw, pad_mode, ep, y, st);
 }
 
+int novaq_adamw_step(float* w, const float* grad, float* m, float* v, int64_t n,
+                     const novaq_adamw* hp, float* w_amax, void* stream) {
+  if (!hp || n < 0 || hp->step < 1) return NOVAQ_EINVAL;
+  if (n > 0 && (!w || !grad || !m || !v)) return NOVAQ_EINVAL;
+  for (const void* p : {(const void*)w, (const void*)grad, (const void*)m, (const void*)v})
+    if (p && !aligned16(p)) return NOVAQ_EALIGN;
+  if (w_amax && (reinterpret_cast<uintptr_t>(w_amax) & 3)) return NOVAQ_EALIGN;
+  return adamw_launch(w, grad, m, v, n, hp->lr, hp->beta1, hp->beta2, hp->eps, hp->weight_decay,
+                      hp->step, hp->decay, w_amax, static_cast<hipStream_t>(stream));
+}
+
+int novaq_adamw_requantize(float* w, const float* grad, float* m, float* v, int64_t n,
+                           const novaq_adamw* hp, void* codes, int q_dtype, float* amax_scale,
+                           void* stream) {
+  if (q_dtype != E4M3 && q_dtype != E5M2 && q_dtype != E2M1) return NOVAQ_EDTYPE;
+  if (!amax_scale || (n > 0 && !codes)) return NOVAQ_EINVAL;
+  if ((codes && !aligned16(codes)) || (reinterpret_cast<uintptr_t>(amax_scale) & 3))
+    return NOVAQ_EALIGN;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  int rc = novaq_adamw_step(w, grad, m, v, n, hp, amax_scale, stream);
+  if (rc != NOVAQ_OK) return rc;
+  // the amax-scaled cast: s = amax / fmt_max (block 0 writes it), codes = enc(w * (1/s))
+  return cast_launch(w, F32, codes, q_dtype, n, 2, amax_scale, amax_scale + 1, st);
+}
+
 int novaq_transpose(const void* src, int src_dtype, int64_t rows, int64_t cols, void* dst,
                     int dst_dtype, void* stream) {
   if (!valid_dtype(src_dtype) || !valid_dtype(dst_dtype)) return NOVAQ_EDTYPE;

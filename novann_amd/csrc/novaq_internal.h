@@ -50,6 +50,11 @@ int conv2d_launch(const void* x, int x_dtype, const float* x_scale, int64_t N, i
                   int64_t C_out, int KH, int KW, int sh, int sw, int ph, int pw, int pad_mode,
                   const Epilogue& ep, void* y, hipStream_t stream);
 
+// One AdamW step of n fp32 weights (adamw.py:41-65); amax (optional) gets max |w|.
+int adamw_launch(float* w, const float* g, float* m, float* v, int64_t n, double lr, double beta1,
+                 double beta2, double eps, double weight_decay, int64_t step, int decay,
+                 float* amax, hipStream_t stream);
+
 // Sets count 32-bit words at p to v (a kernel, so it may be captured in graphs).
 int fill_u32_launch(uint32_t* p, uint32_t v, int count, hipStream_t stream);
 

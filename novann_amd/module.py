@@ -35,40 +35,61 @@ class Parameters:
         if set_to_none:
             self.grad = None
         elif self.grad is None:
-            self.grad = np.zeros_like(self.data)
+            self.grad = (torch.zeros_like(self.data) if isinstance(self.data, torch.Tensor)
+                         else np.zeros_like(self.data))
+        elif isinstance(self.grad, torch.Tensor):
+            self.grad.zero_()
         else:
             self.grad.fill(0.0)
 
 
 class QuantizedParameters:
-    """Per-tensor quantized weight resident on the device.
+    """Per-tensor quantized weight resident on the device: the packed
+    replacement of ``Parameters.data`` (module.py:20-23).
 
     codes: flat device tensor of codes (E2M1: two per byte, element 2i in the
     low nibble, rows of the innermost dimension packed contiguously); shape:
     logical shape; dtype: 'e4m3' | 'e5m2' | 'e2m1'; scale: one fp32 device
-    value s, the weight being s * decode(codes)."""
+    value s, the weight being s * decode(codes); amax: max |w| the scale was
+    derived from.  For training, ``master`` holds the fp32 weights the
+    optimizer steps (the codes are re-quantized from them after each step)
+    and ``grad`` the gradient of the dequantized weight."""
 
     def __init__(self, codes: torch.Tensor, shape, dtype: str, scale: torch.Tensor,
-                 amax: Optional[torch.Tensor] = None, name: Optional[str] = None):
+                 amax: Optional[torch.Tensor] = None, name: Optional[str] = None,
+                 master: Optional[torch.Tensor] = None):
         self.codes = codes
         self.shape = tuple(int(d) for d in shape)
         self.dtype = dtype
         self.scale = scale
         self.amax = amax
         self.name = name
+        self.master = master
         self.grad = None
 
     @classmethod
-    def from_float(cls, w, dtype: str, device=None) -> "QuantizedParameters":
-        """Quantize an fp32 array with per-tensor amax scaling on the GPU."""
+    def from_float(cls, w, dtype: str, device=None,
+                   keep_master: bool = False) -> "QuantizedParameters":
+        """Quantize an fp32 array with per-tensor amax scaling on the GPU
+        (keeping an fp32 device copy as ``master`` when asked)."""
         from . import quant
         if isinstance(w, Parameters):
             w = w.data
         if isinstance(w, np.ndarray):
             dev = device or torch.device("cuda", torch.cuda.current_device())
             w = torch.from_numpy(np.ascontiguousarray(w, dtype=np.float32)).to(dev)
-        q = quant.quantize(w.contiguous(), dtype)
-        return cls(q.data, q.shape, dtype, q.scale, q.amax)
+        w = w.to(torch.float32).contiguous()
+        q = quant.quantize(w, dtype)
+        master = w.clone() if keep_master else None
+        return cls(q.data, q.shape, dtype, q.scale, q.amax, master=master)
+
+    def zero_grad(self, set_to_none: bool = True) -> None:
+        if set_to_none or self.grad is None:
+            self.grad = None
+        elif isinstance(self.grad, torch.Tensor):
+            self.grad.zero_()
+        else:
+            self.grad.fill(0.0)
 
     def dequantize(self) -> torch.Tensor:
         """s * decode(codes) as an fp32 device tensor of the logical shape."""
@@ -112,7 +133,8 @@ class Linear:
         self.weight = Parameters(np.asarray(w, dtype=np.float32))
         self.weight.name = "linear weight"
         if weight_dtype is not None:
-            self.weight = QuantizedParameters.from_float(self.weight, weight_dtype)
+            self.weight = QuantizedParameters.from_float(self.weight, weight_dtype,
+                                                         keep_master=True)
             self.weight.name = "linear weight"
         self.bias = None
         if bias:
@@ -163,7 +185,8 @@ class Conv2d:
         self.weight = Parameters(np.asarray(w, dtype=np.float32))
         self.weight.name = "conv2d weight"
         if weight_dtype is not None:
-            self.weight = QuantizedParameters.from_float(self.weight, weight_dtype)
+            self.weight = QuantizedParameters.from_float(self.weight, weight_dtype,
+                                                         keep_master=True)
             self.weight.name = "conv2d weight"
         self.bias = None
         if bias:
