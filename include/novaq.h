@@ -195,6 +195,29 @@ int novaq_conv2d_forward_ex(const void *x, int x_dtype, const float *x_scale, in
                             int ph, int pw, int pad_mode, const float *bias,
                             const novaq_epilogue *epi, void *y, void *stream);
 
+/* y (N, C, OH, OW) = the max of each KH x KW window of x (N, C, H, W) padded
+ * (ph, pw) in pad_mode with numpy.pad's rules (zeros pads +0), stride
+ * (sh, sw); OH = (H + 2ph - KH)/sh + 1.  x and y in x_dtype (F32, or BF16 /
+ * F16 / E4M3 / E5M2 as an epilogue stores activations; FP8 codes keep their
+ * scale): the result is one of the window's values, the later one in
+ * row-major window order when two are equal (the sign of a zero maximum),
+ * NaN when the window holds one.
+ * Replaces: novann.functional.max_pool2d (novann/functional.py:450-532),
+ * called by MaxPool2d.forward (layers/pooling/maxpool/maxpool2d.py:51-79). */
+int novaq_max_pool2d(const void *x, int x_dtype, int64_t N, int64_t C, int64_t H, int64_t W,
+                     int KH, int KW, int sh, int sw, int ph, int pw, int pad_mode, void *y,
+                     void *stream);
+
+/* y[n, c] = mean over H, W of x[n, c] (x_dtype as above, times x_scale for
+ * FP8 when given), fp32, evaluated as numpy's np.mean does on float32: 0 plus
+ * numpy's pairwise sums of the plane's 8192-element blocks (its ufunc buffer
+ * size), divided by H*W, so bit for bit equal.
+ * Replaces: novann.functional.avg_pool2d (novann/functional.py:548-559),
+ * called by GlobalAvgPool2d.forward (layers/pooling/gap/global_avg_pool2d.py:19-32);
+ * y is the reference's (N, C, 1, 1) output. */
+int novaq_global_avg_pool2d(const void *x, int x_dtype, const float *x_scale, int64_t N,
+                            int64_t C, int64_t H, int64_t W, float *y, void *stream);
+
 /* Hyper-parameters of one AdamW step (novann AdamW, adamw.py:17-38): Python
  * floats there, doubles here; step is the 1-based step count t; decay = 0
  * marks a parameter the reference never decays (BatchNorm gamma / beta,

@@ -226,6 +226,32 @@ int novaq_conv2d_forward_ex(const void* x, int x_dtype, const float* x_scale, in
                        sw, ph, pw, pad_mode, ep, y, st);
 }
 
+int novaq_max_pool2d(const void* x, int x_dtype, int64_t N, int64_t C, int64_t H, int64_t W,
+                     int KH, int KW, int sh, int sw, int ph, int pw, int pad_mode, void* y,
+                     void* stream) {
+  if (!valid_dtype(x_dtype) || x_dtype == E2M1) return NOVAQ_EDTYPE;
+  if (pad_mode < NOVAQ_PAD_ZEROS || pad_mode > NOVAQ_PAD_CIRCULAR) return NOVAQ_EPADMODE;
+  if (N < 0 || C <= 0 || H <= 0 || W <= 0 || KH <= 0 || KW <= 0 || sh <= 0 || sw <= 0 ||
+      ph < 0 || pw < 0)
+    return NOVAQ_EINVAL;
+  if (H + 2 * (int64_t)ph < KH || W + 2 * (int64_t)pw < KW) return NOVAQ_ESHAPE;
+  if (H > 0x7FFFFFFF || W > 0x7FFFFFFF) return NOVAQ_EINVAL;
+  if (N == 0) return NOVAQ_OK;
+  if (!x || !y) return NOVAQ_EINVAL;
+  return max_pool2d_launch(x, x_dtype, N, C, H, W, KH, KW, sh, sw, ph, pw, pad_mode, y,
+                           static_cast<hipStream_t>(stream));
+}
+
+int novaq_global_avg_pool2d(const void* x, int x_dtype, const float* x_scale, int64_t N,
+                            int64_t C, int64_t H, int64_t W, float* y, void* stream) {
+  if (!valid_dtype(x_dtype) || x_dtype == E2M1) return NOVAQ_EDTYPE;
+  if (N < 0 || C <= 0 || H <= 0 || W <= 0) return NOVAQ_EINVAL;
+  if (N == 0) return NOVAQ_OK;
+  if (!x || !y) return NOVAQ_EINVAL;
+  return global_avg_pool2d_launch(x, x_dtype, x_scale, N * C, H * W, y,
+                                  static_cast<hipStream_t>(stream));
+}
+
 int novaq_adamw_step(float* w, const float* grad, float* m, float* v, int64_t n,
                      const novaq_adamw* hp, float* w_amax, void* stream) {
   if (!hp || n < 0 || hp->step < 1) return NOVAQ_EINVAL;

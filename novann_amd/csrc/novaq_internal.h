@@ -55,6 +55,12 @@ int adamw_launch(float* w, const float* g, float* m, float* v, int64_t n, double
                  double beta2, double eps, double weight_decay, int64_t step, int decay,
                  float* amax, hipStream_t stream);
 
+int max_pool2d_launch(const void* x, int x_dtype, int64_t N, int64_t C, int64_t H, int64_t W,
+                      int KH, int KW, int sh, int sw, int ph, int pw, int pad_mode, void* y,
+                      hipStream_t stream);
+int global_avg_pool2d_launch(const void* x, int x_dtype, const float* x_scale, int64_t planes,
+                             int64_t hw, float* y, hipStream_t stream);
+
 // Sets count 32-bit words at p to v (a kernel, so it may be captured in graphs).
 int fill_u32_launch(uint32_t* p, uint32_t v, int count, hipStream_t stream);
 

@@ -1,0 +1,241 @@
+// MaxPool2d and GlobalAvgPool2d forward for gfx950 (restate
+// novann.functional.max_pool2d, functional.py:450-532, and avg_pool2d,
+// :548-559), on x stored as F32 or as a fused epilogue stores activations
+// (BF16, F16, E4M3, E5M2).
+//
+// max_pool2d: the input padded with numpy.pad's rules (zeros pads +0), then
+// the max of each KH x KW window.  The reference reduces a strided window
+// view with numpy's maximum; its result is the window's largest value, a
+// later element in row-major window order replacing an equal one (so the sign
+// of a zero maximum is that of the last zero), and NaN once a NaN is met.
+// The kernel walks the window in the same order with the same rule; the
+// result is one of the input codes, so every x dtype is exact (FP8 codes
+// keep their per-tensor scale).  One lane per output element, consecutive
+// lanes on consecutive output columns.  HBM-bound: read x ~once (the windows
+// of a row overlap in L1/L2), write y once.
+//
+// global_avg_pool2d: np.mean over H and W of each (n, c) plane, which numpy
+// evaluates in float32 as 0 plus, block by block of its default ufunc buffer
+// size (8192 elements), the pairwise_sum of the block, followed by one float32
+// division by H*W.  pairwise_sum is numpy's published algorithm: fewer than
+// 8 elements summed in order from 0; up to 128 with 8 interleaved partial
+// sums combined as ((r0+r1)+(r2+r3))+((r4+r5)+(r6+r7)) plus the remainder in
+// order; longer runs split at n/2 rounded down to a multiple of 8 and the two
+// halves added.  The kernel evaluates exactly that, so the result equals the
+// reference's bit for bit; narrow x is decoded and multiplied by its scale
+// first (the dequantized array the reference would average).  One lane per
+// plane.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "novaq_convert.h"
+#include "novaq_internal.h"
+#include "novaq_xload.h"
+
+namespace novaq {
+namespace {
+
+struct PoolGeom {
+  int64_t N, C;
+  int H, W, KH, KW, sh, sw, ph, pw, pad_mode, OH, OW;
+};
+
+__device__ __forceinline__ int pool_pad_index(int i, int n, int mode) {
+  if (i >= 0 && i < n) return i;
+  if (mode == NOVAQ_PAD_ZEROS) return -1;
+  if (mode == NOVAQ_PAD_REPLICATE) return i < 0 ? 0 : n - 1;
+  if (mode == NOVAQ_PAD_CIRCULAR) {
+    int r = i % n;
+    return r < 0 ? r + n : r;
+  }
+  if (n == 1) return 0;  // reflect, period 2(n-1)
+  const int p = 2 * (n - 1);
+  int r = i % p;
+  if (r < 0) r += p;
+  return r >= n ? p - r : r;
+}
+
+template <int XT>
+__device__ __forceinline__ void store_code(uint8_t* __restrict__ y, int64_t i, uint32_t c) {
+  if constexpr (XL<XT>::bits == 32) reinterpret_cast<uint32_t*>(y)[i] = c;
+  else if constexpr (XL<XT>::bits == 16) reinterpret_cast<uint16_t*>(y)[i] = (uint16_t)c;
+  else y[i] = (uint8_t)c;
+}
+
+template <int XT>
+__global__ __launch_bounds__(256) void max_pool2d_kernel(const uint8_t* __restrict__ x,
+                                                        uint8_t* __restrict__ y, PoolGeom g) {
+  const int64_t total = g.N * g.C * g.OH * g.OW;
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= total) return;
+  const int ow = (int)(t % g.OW);
+  int64_t r = t / g.OW;
+  const int oh = (int)(r % g.OH);
+  const int64_t plane = r / g.OH;  // n * C + c
+  const int64_t base = plane * g.H * g.W;
+  uint32_t best = 0;
+  float bv = 0.0f;
+  bool first = true;
+  for (int kh = 0; kh < g.KH; ++kh) {
+    const int hi = pool_pad_index(oh * g.sh + kh - g.ph, g.H, g.pad_mode);
+    for (int kw = 0; kw < g.KW; ++kw) {
+      const int wi = pool_pad_index(ow * g.sw + kw - g.pw, g.W, g.pad_mode);
+      uint32_t c = 0;  // the zero padding's +0
+      if (hi >= 0 && wi >= 0) c = x_code<XT>(x, base + (int64_t)hi * g.W + wi);
+      const float v = u2f(decode<XT>(c));
+      if (first) {
+        best = c;
+        bv = v;
+        first = false;
+      } else if (!isnan(bv) && (v >= bv || isnan(v))) {
+        best = c;
+        bv = v;
+      }
+    }
+  }
+  store_code<XT>(y, t, best);
+}
+
+template <int XT>
+__device__ __forceinline__ float elem(const uint8_t* __restrict__ x, int64_t i, float s,
+                                      bool scaled) {
+  const float v = x_val<XT>(x, i);
+  return scaled ? v * s : v;
+}
+
+// numpy's pairwise_sum of n <= 128 elements starting at element b.
+template <int XT>
+__device__ float pw_leaf(const uint8_t* __restrict__ x, int64_t b, int n, float s, bool scaled) {
+  if (n < 8) {
+    float res = 0.0f;
+    for (int i = 0; i < n; ++i) res += elem<XT>(x, b + i, s, scaled);
+    return res;
+  }
+  float r[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) r[j] = elem<XT>(x, b + j, s, scaled);
+  int i = 8;
+  for (; i < n - (n % 8); i += 8) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r[j] += elem<XT>(x, b + i + j, s, scaled);
+  }
+  float res = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
+  for (; i < n; ++i) res += elem<XT>(x, b + i, s, scaled);
+  return res;
+}
+
+// numpy's pairwise_sum of n <= 8192 elements starting at element b: the
+// recursion pw(a, n) = pw(a, n2) + pw(a + n2, n - n2), n2 = n/2 - (n/2) % 8,
+// for n > 128, walked with an explicit stack (at most 7 frames: 8192 halves
+// to a leaf of <= 128 in 6 splits).
+template <int XT>
+__device__ float pw_sum(const uint8_t* __restrict__ x, int64_t b, int64_t n, float s,
+                        bool scaled) {
+  if (n <= 128) return pw_leaf<XT>(x, b, (int)n, s, scaled);
+  struct Frame {
+    int64_t off, len, n2;
+    float left;
+    int stage;
+  };
+  Frame st[8];
+  int sp = 0;
+  st[0] = Frame{b, n, 0, 0.0f, 0};
+  float ret = 0.0f;
+  while (sp >= 0) {
+    Frame& f = st[sp];
+    if (f.stage == 0) {
+      if (f.len <= 128) {
+        ret = pw_leaf<XT>(x, f.off, (int)f.len, s, scaled);
+        --sp;
+        continue;
+      }
+      f.n2 = f.len / 2;
+      f.n2 -= f.n2 % 8;
+      f.stage = 1;
+      st[sp + 1] = Frame{f.off, f.n2, 0, 0.0f, 0};
+      ++sp;
+    } else if (f.stage == 1) {
+      f.left = ret;
+      f.stage = 2;
+      st[sp + 1] = Frame{f.off + f.n2, f.len - f.n2, 0, 0.0f, 0};
+      ++sp;
+    } else {
+      ret = f.left + ret;
+      --sp;
+    }
+  }
+  return ret;
+}
+
+constexpr int64_t NP_BUFSIZE = 8192;  // numpy's default ufunc buffer (np.getbufsize())
+
+template <int XT>
+__global__ __launch_bounds__(256) void global_avg_pool2d_kernel(const uint8_t* __restrict__ x,
+                                                               const float* __restrict__ x_scale,
+                                                               float* __restrict__ y,
+                                                               int64_t planes, int64_t hw) {
+  const int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (p >= planes) return;
+  const bool scaled = x_scale != nullptr;
+  const float s = scaled ? *x_scale : 1.0f;
+  // numpy's reduction hands the inner loop blocks of its ufunc buffer size
+  float sum = 0.0f;
+  for (int64_t b = 0; b < hw; b += NP_BUFSIZE)
+    sum = sum + pw_sum<XT>(x, p * hw + b, hw - b < NP_BUFSIZE ? hw - b : NP_BUFSIZE, s, scaled);
+  y[p] = sum / (float)hw;
+}
+
+template <int XT>
+int launch_max(const void* x, void* y, const PoolGeom& g, hipStream_t stream) {
+  const int64_t total = g.N * g.C * g.OH * g.OW;
+  const int64_t blocks = (total + 255) / 256;
+  if (blocks > 0x7FFFFFFF) return NOVAQ_EINVAL;
+  hipLaunchKernelGGL(max_pool2d_kernel<XT>, dim3((unsigned)blocks), dim3(256), 0, stream,
+                     static_cast<const uint8_t*>(x), static_cast<uint8_t*>(y), g);
+  return check_launch();
+}
+
+template <int XT>
+int launch_gap(const void* x, const float* x_scale, float* y, int64_t planes, int64_t hw,
+               hipStream_t stream) {
+  const int64_t blocks = (planes + 255) / 256;
+  if (blocks > 0x7FFFFFFF) return NOVAQ_EINVAL;
+  hipLaunchKernelGGL(global_avg_pool2d_kernel<XT>, dim3((unsigned)blocks), dim3(256), 0, stream,
+                     static_cast<const uint8_t*>(x), x_scale, y, planes, hw);
+  return check_launch();
+}
+
+}  // namespace
+
+int max_pool2d_launch(const void* x, int x_dtype, int64_t N, int64_t C, int64_t H, int64_t W,
+                      int KH, int KW, int sh, int sw, int ph, int pw, int pad_mode, void* y,
+                      hipStream_t stream) {
+  PoolGeom g{};
+  g.N = N; g.C = C; g.H = (int)H; g.W = (int)W; g.KH = KH; g.KW = KW; g.sh = sh; g.sw = sw;
+  g.ph = ph; g.pw = pw; g.pad_mode = pad_mode;
+  g.OH = (int)((H + 2 * (int64_t)ph - KH) / sh + 1);
+  g.OW = (int)((W + 2 * (int64_t)pw - KW) / sw + 1);
+  switch (x_dtype) {
+    case F32: return launch_max<F32>(x, y, g, stream);
+    case F16: return launch_max<F16>(x, y, g, stream);
+    case BF16: return launch_max<BF16>(x, y, g, stream);
+    case E4M3: return launch_max<E4M3>(x, y, g, stream);
+    case E5M2: return launch_max<E5M2>(x, y, g, stream);
+    default: return NOVAQ_EDTYPE;
+  }
+}
+
+int global_avg_pool2d_launch(const void* x, int x_dtype, const float* x_scale, int64_t planes,
+                             int64_t hw, float* y, hipStream_t stream) {
+  switch (x_dtype) {
+    case F32: return launch_gap<F32>(x, x_scale, y, planes, hw, stream);
+    case F16: return launch_gap<F16>(x, x_scale, y, planes, hw, stream);
+    case BF16: return launch_gap<BF16>(x, x_scale, y, planes, hw, stream);
+    case E4M3: return launch_gap<E4M3>(x, x_scale, y, planes, hw, stream);
+    case E5M2: return launch_gap<E5M2>(x, x_scale, y, planes, hw, stream);
+    default: return NOVAQ_EDTYPE;
+  }
+}
+
+}  // namespace novaq

@@ -361,3 +361,59 @@ def conv2d_backward(grad, input, weight, kernel_size: IntPair, stride: IntPair =
     if was_numpy:
         return (gi.cpu().numpy(), gw.cpu().numpy(), None if gb is None else gb.cpu().numpy())
     return gi, gw, gb
+
+
+def _narrow_out(y: torch.Tensor, xdt: str, xs, was_numpy: bool, shape):
+    """A pooled result in the input's storage: ndarray for numpy callers,
+    quant.Quantized (same scale) for FP8 inputs, the device tensor otherwise."""
+    from . import quant
+    if xdt in ("e4m3", "e5m2"):
+        scale = xs if xs is not None else torch.ones(1, dtype=torch.float32, device=y.device)
+        return quant.Quantized(data=y.reshape(-1), shape=tuple(shape), dtype=xdt, scale=scale)
+    return y.cpu().numpy() if was_numpy else y
+
+
+def max_pool2d(input, kernel_size: IntPair, stride: IntPair, padding: IntPair = 0,
+               padding_mode: str = "zeros", extras: bool = False):
+    """2-D max pooling (novann/functional.py:450-532): the input padded with
+    numpy.pad's rules (zeros pads 0), the max of each window.  Returns
+    (N, C, OH, OW) in the input's storage (fp32 ndarray for numpy input; bf16
+    / f16 tensors and FP8 Quantized activations pool without decoding: the
+    result is one of the input values).  ``extras=True`` (the window view,
+    a training cache of the reference) is not available."""
+    KH, KW = _pair(kernel_size)
+    ph, pw = _pair(padding)
+    sh, sw = _pair(stride)
+    if padding_mode not in PAD_MODES:
+        raise ValueError(f"padding_mode Only accept {tuple(PAD_MODES)} not '{padding_mode}'")
+    if extras:
+        raise NotImplementedError("max_pool2d(extras=True): the window view is never "
+                                  "materialised on this path")
+    x, xdt, xs, xshape, was_numpy = _x_arg(input, "input")
+    if len(xshape) != 4:
+        raise ValueError(f"max_pool2d expects (N, C, H, W), got {xshape}")
+    N, C, H, W = xshape
+    OH = (H + 2 * ph - KH) // sh + 1
+    OW = (W + 2 * pw - KW) // sw + 1
+    if OH <= 0 or OW <= 0:
+        raise ValueError(f"output size {(OH, OW)} is empty")
+    y = torch.empty(N * C * OH * OW, dtype=x.dtype, device=x.device)
+    check(_lib.load().novaq_max_pool2d(x.data_ptr(), DTYPES[xdt], N, C, H, W, KH, KW, sh, sw,
+                                       ph, pw, PAD_MODES[padding_mode], y.data_ptr(),
+                                       _stream(x.device)), "max_pool2d")
+    return _narrow_out(y.view(N, C, OH, OW), xdt, xs, was_numpy, (N, C, OH, OW))
+
+
+def avg_pool2d(input):
+    """Global average over H and W (novann/functional.py:548-559): returns
+    (N, C, 1, 1) fp32, equal bit for bit to the reference's np.mean on the
+    same float32 values (narrow inputs are decoded, FP8 times its scale)."""
+    x, xdt, xs, xshape, was_numpy = _x_arg(input, "input")
+    if len(xshape) != 4:
+        raise ValueError(f"avg_pool2d expects (N, C, H, W), got {xshape}")
+    N, C, H, W = xshape
+    y = torch.empty((N, C, 1, 1), dtype=torch.float32, device=x.device)
+    check(_lib.load().novaq_global_avg_pool2d(x.data_ptr(), DTYPES[xdt],
+                                              None if xs is None else xs.data_ptr(), N, C, H, W,
+                                              y.data_ptr(), _stream(x.device)), "avg_pool2d")
+    return y.cpu().numpy() if was_numpy else y

@@ -307,3 +307,34 @@ def fuse(*layers, out_dtype: str = "f32", out_scale=None) -> Fused:
         raise ValueError(f"fuse: cannot fuse {type(rest[0]).__name__} after "
                          f"{type(head).__name__}")
     return Fused(head, bn, relu, out_dtype, out_scale)
+
+
+class MaxPool2d:
+    """novann MaxPool2d (layers/pooling/maxpool/maxpool2d.py:8-79): kernel,
+    stride (None = kernel size), padding, padding_mode; forward on the GPU."""
+
+    def __init__(self, kernel_size, stride=None, padding=0, padding_mode: str = "zeros") -> None:
+        self.KH, self.KW = _pair(kernel_size)
+        self.sh, self.sw = _pair(stride if stride is not None else kernel_size)
+        self.ph, self.pw = _pair(padding)
+        self.pm = padding_mode
+
+    def __call__(self, x):
+        return self.forward(x)
+
+    def forward(self, x):
+        from . import functional as F
+        return F.max_pool2d(x, (self.KH, self.KW), (self.sh, self.sw), (self.ph, self.pw),
+                            padding_mode=self.pm)
+
+
+class GlobalAvgPool2d:
+    """novann GlobalAvgPool2d (layers/pooling/gap/global_avg_pool2d.py:7-32):
+    (N, C, H, W) -> (N, C, 1, 1) means, on the GPU."""
+
+    def __call__(self, x):
+        return self.forward(x)
+
+    def forward(self, x):
+        from . import functional as F
+        return F.avg_pool2d(x)
