@@ -494,6 +494,106 @@ def bench_epilogue(dev, iters: int = 20, warmup: int = 5):
     return {"workload": "BASELINE configs [5] (conv2) and [4] with fused epilogues", **out}
 
 
+def _timed_flush(dev, fn, iters, warmup):
+    """Average ms of fn over iters launches, the MALL evicted before each."""
+    import torch
+    flush = torch.empty(1 << 27, dtype=torch.float32, device=dev)
+    for _ in range(warmup):
+        fn()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(iters)]
+    torch.cuda.synchronize(dev)
+    for e0, e1 in ev:
+        flush.zero_()
+        e0.record()
+        fn()
+        e1.record()
+    torch.cuda.synchronize(dev)
+    return sum(e0.elapsed_time(e1) for e0, e1 in ev) / iters
+
+
+def bench_optim(dev, iters: int = 20, warmup: int = 3):
+    """AdamW (adamw.py:41-65) on config [4]'s 4096 x 4096 weight: the fp32
+    step alone (28 algorithmic bytes per element: w, g, m, v read, w, m, v
+    written) and the step with re-quantization to E4M3 (+ 4 B read and 1 B
+    written by the amax-scaled cast)."""
+    import ctypes
+
+    import torch
+
+    from novann_amd import _lib
+    lib = _lib.load()
+    n = 4096 * 4096
+    g = torch.Generator(device=dev)
+    g.manual_seed(9)
+    w = torch.randn(n, generator=g, device=dev) * 0.02
+    grad = torch.randn(n, generator=g, device=dev)
+    m = torch.zeros(n, device=dev)
+    v = torch.zeros(n, device=dev)
+    codes = torch.empty(n, dtype=torch.uint8, device=dev)
+    st = torch.empty(2, device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    hp = _lib.AdamW(1e-3, 0.9, 0.999, 1e-8, 1e-2, 1, 1)
+
+    def step():
+        hp.step += 1
+        _lib.check(lib.novaq_adamw_step(w.data_ptr(), grad.data_ptr(), m.data_ptr(),
+                                        v.data_ptr(), n, ctypes.byref(hp), None, stream), "adamw")
+
+    def requant():
+        hp.step += 1
+        _lib.check(lib.novaq_adamw_requantize(w.data_ptr(), grad.data_ptr(), m.data_ptr(),
+                                              v.data_ptr(), n, ctypes.byref(hp),
+                                              codes.data_ptr(), _lib.E4M3, st.data_ptr(),
+                                              stream), "adamw requantize")
+    ms_s = _timed_flush(dev, step, iters, warmup)
+    ms_r = _timed_flush(dev, requant, iters, warmup)
+    gs = 28.0 * n / (ms_s * 1e-3) / 1e9
+    gr = 33.0 * n / (ms_r * 1e-3) / 1e9
+    return {"workload": "AdamW on BASELINE config [4]'s 4096x4096 weight", "elements": n,
+            "step": {"ms": round(ms_s, 4), "GB/s": round(gs, 1),
+                     "frac": round(gs / HBM_PEAK_GBS, 4), "bytes_per_element": 28},
+            "step_requantize_e4m3": {"ms": round(ms_r, 4), "GB/s": round(gr, 1),
+                                     "frac": round(gr / HBM_PEAK_GBS, 4),
+                                     "bytes_per_element": 33}}
+
+
+def bench_pool(dev, iters: int = 20, warmup: int = 3):
+    """MaxPool2d(2, 2) and GlobalAvgPool2d on a config [5]-sized activation
+    (256, 64, 28, 28) in fp32 and bf16, and GlobalAvgPool2d on main.py's 7x7
+    map at batch 256: algorithmic bytes = read x once + write y once."""
+    import torch
+
+    from novann_amd import _lib
+    lib = _lib.load()
+    g = torch.Generator(device=dev)
+    g.manual_seed(10)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    out = []
+    x32 = torch.randn((256, 64, 28, 28), generator=g, device=dev)
+    for name, x, dt in (("f32", x32, _lib.F32), ("bf16", x32.to(torch.bfloat16), _lib.BF16)):
+        y = torch.empty((256, 64, 14, 14), dtype=x.dtype, device=dev)
+        fn = lambda x=x, y=y, dt=dt: _lib.check(lib.novaq_max_pool2d(  # noqa: E731
+            x.data_ptr(), dt, 256, 64, 28, 28, 2, 2, 2, 2, 0, 0, 0, y.data_ptr(), stream),
+            "max_pool2d")
+        ms = _timed_flush(dev, fn, iters, warmup)
+        nb = (x.numel() + y.numel()) * x.element_size()
+        out.append({"op": f"max_pool2d 2x2/2 (256,64,28,28) {name}", "ms": round(ms, 4),
+                    "GB/s": round(nb / (ms * 1e-3) / 1e9, 1),
+                    "frac": round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
+    for shape in ((256, 64, 28, 28), (256, 64, 7, 7)):
+        x = torch.randn(shape, generator=g, device=dev)
+        y = torch.empty(shape[:2], device=dev)
+        fn = lambda x=x, y=y, s=shape: _lib.check(lib.novaq_global_avg_pool2d(  # noqa: E731
+            x.data_ptr(), _lib.F32, None, *s, y.data_ptr(), stream), "avg_pool2d")
+        ms = _timed_flush(dev, fn, iters, warmup)
+        nb = (x.numel() + y.numel()) * 4
+        out.append({"op": f"global_avg_pool2d {shape} f32", "ms": round(ms, 4),
+                    "GB/s": round(nb / (ms * 1e-3) / 1e9, 1),
+                    "frac": round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
+    return {"workload": "pools on config [5]-sized and main.py activations", "kernels": out}
+
+
 def cpu_baseline(sample: int, min_seconds: float = 10.0):
     """The C oracle running the same sweep on a bounded sample (all host cores)."""
     import numpy as np
@@ -571,6 +671,10 @@ def main() -> int:
     log(f"conv2d backward: {conv_bwd}")
     epi = None if args.no_conv else bench_epilogue(dev)
     log(f"fused epilogues: {epi}")
+    opt = None if args.no_conv else bench_optim(dev)
+    log(f"adamw: {opt}")
+    pool = None if args.no_conv else bench_pool(dev)
+    log(f"pools: {pool}")
     fp4 = None if args.no_fp4 else bench_fp4(dev)
     log(f"fp4: {fp4}")
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_sample)
@@ -594,6 +698,8 @@ def main() -> int:
         "conv2d": conv,
         "conv2d_backward": conv_bwd,
         "epilogue": epi,
+        "adamw": opt,
+        "pool": pool,
         "fp4": fp4,
         "cpu_baseline": cpu,
     }

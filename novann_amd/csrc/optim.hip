@@ -28,6 +28,8 @@
 namespace novaq {
 namespace {
 
+typedef float f4 __attribute__((ext_vector_type(4)));
+
 struct AdamHP {
   float b1, omb1, b2, omb2, bc1, bc2, lr, eps, lrwd;
   int decay;
@@ -50,30 +52,58 @@ __device__ __forceinline__ uint32_t abs_max(uint32_t am, float w) {
 
 constexpr int ADAM_THREADS = 256;
 
-// Lane i of the grid takes the 4-element groups i, i + stride, ...; the
-// ragged tail (n % 4 elements) goes to the first lanes of the grid.
+// Lane i of the grid takes the 4-element groups i, i + stride, i + 2 stride,
+// ..., two per iteration with all eight 16-byte non-temporal loads issued
+// first; the
+// ragged tail (n % 4 elements) goes to the first lanes of the grid.  The
+// amax is reduced per workgroup (waves, then LDS) with one atomic each.
 __global__ __launch_bounds__(ADAM_THREADS) void adamw_kernel(float* __restrict__ w,
                                                             const float* __restrict__ g,
                                                             float* __restrict__ m,
                                                             float* __restrict__ v, int64_t n,
                                                             AdamHP h, uint32_t* __restrict__ amax) {
+  __shared__ uint32_t wave_max[ADAM_THREADS / 64];
   const int64_t n4 = n >> 2;
   const int64_t stride = (int64_t)gridDim.x * ADAM_THREADS;
   const int64_t t0 = (int64_t)blockIdx.x * ADAM_THREADS + threadIdx.x;
+  f4* W4 = reinterpret_cast<f4*>(w);
+  const f4* G4 = reinterpret_cast<const f4*>(g);
+  f4* M4 = reinterpret_cast<f4*>(m);
+  f4* V4 = reinterpret_cast<f4*>(v);
   uint32_t am = 0;
-  for (int64_t i = t0; i < n4; i += stride) {
-    float4 wv = reinterpret_cast<const float4*>(w)[i];
-    const float4 gv = reinterpret_cast<const float4*>(g)[i];
-    float4 mv = reinterpret_cast<const float4*>(m)[i];
-    float4 vv = reinterpret_cast<const float4*>(v)[i];
-    wv.x = adam_elem(wv.x, gv.x, mv.x, vv.x, h);
-    wv.y = adam_elem(wv.y, gv.y, mv.y, vv.y, h);
-    wv.z = adam_elem(wv.z, gv.z, mv.z, vv.z, h);
-    wv.w = adam_elem(wv.w, gv.w, mv.w, vv.w, h);
-    reinterpret_cast<float4*>(w)[i] = wv;
-    reinterpret_cast<float4*>(m)[i] = mv;
-    reinterpret_cast<float4*>(v)[i] = vv;
-    if (amax) am = abs_max(abs_max(abs_max(abs_max(am, wv.x), wv.y), wv.z), wv.w);
+  auto update = [&](f4& wv, const f4& gv, f4& mv, f4& vv) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      float mq = mv[q], vq = vv[q];
+      wv[q] = adam_elem(wv[q], gv[q], mq, vq, h);
+      mv[q] = mq;
+      vv[q] = vq;
+      if (amax) am = abs_max(am, wv[q]);
+    }
+  };
+  int64_t i = t0;
+  // every element is read and written once: non-temporal accesses
+#define LD(p) __builtin_nontemporal_load(&(p))
+#define ST(p, v) __builtin_nontemporal_store((v), &(p))
+  for (; i + stride < n4; i += 2 * stride) {
+    const int64_t j = i + stride;
+    f4 wa = LD(W4[i]), wb = LD(W4[j]);
+    const f4 ga = LD(G4[i]), gb = LD(G4[j]);
+    f4 ma = LD(M4[i]), mb = LD(M4[j]);
+    f4 va = LD(V4[i]), vb = LD(V4[j]);
+    update(wa, ga, ma, va);
+    update(wb, gb, mb, vb);
+    ST(W4[i], wa); ST(M4[i], ma); ST(V4[i], va);
+    ST(W4[j], wb); ST(M4[j], mb); ST(V4[j], vb);
+  }
+#undef LD
+#undef ST
+  if (i < n4) {
+    f4 wa = W4[i];
+    const f4 ga = G4[i];
+    f4 ma = M4[i], va = V4[i];
+    update(wa, ga, ma, va);
+    W4[i] = wa; M4[i] = ma; V4[i] = va;
   }
   const int64_t e = (n4 << 2) + t0;
   if (e < n) {
@@ -90,7 +120,14 @@ __global__ __launch_bounds__(ADAM_THREADS) void adamw_kernel(float* __restrict__
       const uint32_t t = (uint32_t)__shfl_xor((int)am, o);
       am = t > am ? t : am;
     }
-    if ((threadIdx.x & 63) == 0 && am) atomicMax(amax, am);
+    if ((threadIdx.x & 63) == 0) wave_max[threadIdx.x >> 6] = am;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      uint32_t b = wave_max[0];
+#pragma unroll
+      for (int k = 1; k < ADAM_THREADS / 64; ++k) b = wave_max[k] > b ? wave_max[k] : b;
+      if (b) atomicMax(amax, b);
+    }
   }
 }
 
@@ -117,7 +154,8 @@ int adamw_launch(float* w, const float* g, float* m, float* v, int64_t n, double
   if (n == 0) return NOVAQ_OK;
   const int64_t n4 = n >> 2;
   int64_t blocks = (std::max<int64_t>(n4, n & 3) + ADAM_THREADS - 1) / ADAM_THREADS;
-  const int64_t cap = (int64_t)device_cu_count() * 32;  // grid-stride beyond this
+  // grid-stride beyond 8 workgroups per CU (also bounds the amax atomics)
+  const int64_t cap = (int64_t)device_cu_count() * 8;
   if (blocks > cap) blocks = cap;
   if (blocks < 1) blocks = 1;
   hipLaunchKernelGGL(adamw_kernel, dim3((unsigned)blocks), dim3(ADAM_THREADS), 0, stream, w, g, m,

@@ -63,16 +63,17 @@ __device__ __forceinline__ void store_code(uint8_t* __restrict__ y, int64_t i, u
   else y[i] = (uint8_t)c;
 }
 
+// Lane t of the grid makes output element t (planes of OH x OW outputs back
+// to back), so workgroups are full whatever the plane size.
 template <int XT>
 __global__ __launch_bounds__(256) void max_pool2d_kernel(const uint8_t* __restrict__ x,
                                                         uint8_t* __restrict__ y, PoolGeom g) {
-  const int64_t total = g.N * g.C * g.OH * g.OW;
+  const int npix = g.OH * g.OW;
   const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (t >= total) return;
-  const int ow = (int)(t % g.OW);
-  int64_t r = t / g.OW;
-  const int oh = (int)(r % g.OH);
-  const int64_t plane = r / g.OH;  // n * C + c
+  if (t >= g.N * g.C * npix) return;
+  const int64_t plane = t / npix;  // n * C + c
+  const int pix = (int)(t - plane * npix);
+  const int oh = pix / g.OW, ow = pix - oh * g.OW;
   const int64_t base = plane * g.H * g.W;
   uint32_t best = 0;
   float bv = 0.0f;
@@ -95,6 +96,74 @@ __global__ __launch_bounds__(256) void max_pool2d_kernel(const uint8_t* __restri
     }
   }
   store_code<XT>(y, t, best);
+}
+
+// The window rule: v replaces the running maximum bv when it is larger or
+// equal, or NaN, unless bv is NaN already.
+__device__ __forceinline__ void take_max(uint32_t c, float v, uint32_t& best, float& bv) {
+  if (!isnan(bv) && (v >= bv || isnan(v))) {
+    best = c;
+    bv = v;
+  }
+}
+
+// 2-wide windows with stride 2 along W and no W padding (MaxPool2d(2, 2) and
+// its (k, 2) / (k, 2) relatives): a lane makes the two adjacent outputs
+// 2u, 2u+1 of one output row from 4 consecutive inputs per window row, read
+// with one 16 / 8 / 4-byte load when W is a multiple of 4.
+template <int XT>
+__global__ __launch_bounds__(256) void max_pool2d_w2_kernel(const uint8_t* __restrict__ x,
+                                                           uint8_t* __restrict__ y, PoolGeom g) {
+  const int OU = (g.OW + 1) / 2;  // output pairs per row
+  const int per = g.OH * OU;
+  const int64_t t0 = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t0 >= g.N * g.C * per) return;
+  const int64_t plane = t0 / per;
+  const int item = (int)(t0 - plane * per);
+  const int oh = item / OU, u = item - oh * OU;
+  const int64_t base = plane * g.H * g.W;
+  const bool two = 2 * u + 1 < g.OW;
+  const bool vec = (g.W & 3) == 0;
+  constexpr int B = XL<XT>::bits;
+  uint32_t best[2] = {0u, 0u};
+  float bv[2] = {0.0f, 0.0f};
+  for (int kh = 0; kh < g.KH; ++kh) {
+    const int hi = pool_pad_index(oh * g.sh + kh - g.ph, g.H, g.pad_mode);
+    uint32_t c[4] = {0u, 0u, 0u, 0u};  // the zero padding's +0
+    if (hi >= 0) {
+      const int64_t e = base + (int64_t)hi * g.W + 4 * u;
+      if (vec) {
+        const xl_u32x4 r = x4_raw<XT>(x, e);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          c[q] = B == 32 ? r[q] : (r[(q * B) / 32] >> ((q * B) % 32)) & ((1u << (B & 31)) - 1u);
+      } else {
+        c[0] = x_code<XT>(x, e);
+        c[1] = x_code<XT>(x, e + 1);
+        if (two) {
+          c[2] = x_code<XT>(x, e + 2);
+          c[3] = x_code<XT>(x, e + 3);
+        }
+      }
+    }
+#pragma unroll
+    for (int o = 0; o < 2; ++o) {
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const uint32_t code = c[2 * o + q];
+        const float v = u2f(decode<XT>(code));
+        if (kh == 0 && q == 0) {
+          best[o] = code;
+          bv[o] = v;
+        } else {
+          take_max(code, v, best[o], bv[o]);
+        }
+      }
+    }
+  }
+  const int64_t t = plane * g.OH * g.OW + (int64_t)oh * g.OW + 2 * u;
+  store_code<XT>(y, t, best[0]);
+  if (two) store_code<XT>(y, t + 1, best[1]);
 }
 
 template <int XT>
@@ -188,8 +257,17 @@ __global__ __launch_bounds__(256) void global_avg_pool2d_kernel(const uint8_t* _
 
 template <int XT>
 int launch_max(const void* x, void* y, const PoolGeom& g, hipStream_t stream) {
-  const int64_t total = g.N * g.C * g.OH * g.OW;
-  const int64_t blocks = (total + 255) / 256;
+  const int64_t npix = (int64_t)g.OH * g.OW;
+  if (npix > 0x7FFFFFFF) return NOVAQ_EINVAL;
+  if (g.KW == 2 && g.sw == 2 && g.pw == 0) {
+    const int64_t items = g.N * g.C * (int64_t)g.OH * ((g.OW + 1) / 2);
+    const int64_t blocks = (items + 255) / 256;
+    if (blocks > 0x7FFFFFFF) return NOVAQ_EINVAL;
+    hipLaunchKernelGGL(max_pool2d_w2_kernel<XT>, dim3((unsigned)blocks), dim3(256), 0, stream,
+                       static_cast<const uint8_t*>(x), static_cast<uint8_t*>(y), g);
+    return check_launch();
+  }
+  const int64_t blocks = (g.N * g.C * npix + 255) / 256;
   if (blocks > 0x7FFFFFFF) return NOVAQ_EINVAL;
   hipLaunchKernelGGL(max_pool2d_kernel<XT>, dim3((unsigned)blocks), dim3(256), 0, stream,
                      static_cast<const uint8_t*>(x), static_cast<uint8_t*>(y), g);

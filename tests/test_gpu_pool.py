@@ -46,6 +46,9 @@ GEOMS = [
     ((1, 5, 7, 6), (2, 3), (1, 2), (1, 0), "replicate"),
     ((3, 2, 8, 8), (3, 3), (2, 2), (1, 2), "circular"),
     ((128, 32, 14, 14), (2, 2), (2, 2), (0, 0), "zeros"),   # main.py:35 (block 2 output)
+    ((2, 3, 8, 12), (2, 2), (2, 2), (0, 0), "zeros"),       # 2-wide path, vector loads
+    ((2, 2, 9, 16), (3, 2), (1, 2), (1, 0), "reflect"),     # 2-wide path, padded rows
+    ((1, 2, 6, 7), (2, 2), (2, 2), (0, 0), "zeros"),        # 2-wide path, odd OW
 ]
 
 
@@ -59,8 +62,9 @@ def test_max_pool2d_f32_bit_exact(xs, k, s, p, mode):
     same_bits_or_nan(got, R.max_pool2d(x, k, s, p, mode))
 
 
+@pytest.mark.parametrize("ksp", [(3, 2, 1), (2, 2, 0)])
 @pytest.mark.parametrize("xt", ["bf16", "f16", "e4m3", "e5m2"])
-def test_max_pool2d_narrow_codes(xt):
+def test_max_pool2d_narrow_codes(xt, ksp):
     """Pooling codes equals encoding the pooled decoded values (the max is
     one of the inputs); FP8 keeps its scale."""
     rng = np.random.default_rng(3)
@@ -74,8 +78,9 @@ def test_max_pool2d_narrow_codes(xt):
     if scale:
         xd = quant.Quantized(xd, xs, xt, torch.tensor([scale], dtype=torch.float32,
                                                        device="cuda"))
-    y = F.max_pool2d(xd, 3, 2, 1, "zeros")
-    want = R.max_pool2d(dec, 3, 2, 1, "zeros")
+    k, st, pd = ksp
+    y = F.max_pool2d(xd, k, st, pd, "zeros")
+    want = R.max_pool2d(dec, k, st, pd, "zeros")
     ycodes = to_host(y.data if scale else y).reshape(-1)
     assert np.array_equal(O.cast(ycodes, CODE[xt], O.F32).view(np.uint32),
                           want.reshape(-1).view(np.uint32))
