@@ -45,7 +45,7 @@ KERNEL_OF = {
     "f32->e5m2 scaled": "cast_kernel<0, 4, 1>", "e5m2->f32 scaled": "cast_kernel<4, 0, 1>",
 }
 FP4_KERNEL = {"pack f32->e2m1": "cast_kernel<0, 5, 1>", "unpack e2m1->f32": "cast_kernel<5, 0, 1>"}
-CONV_KERNEL = {1: "conv2d_band_kernel<5, 1, false>", 32: "conv2d_band_kernel<5, 1, true>"}
+CONV_KERNEL = {1: "conv2d_band_kernel<5, 0, 1, false>", 32: "conv2d_band_kernel<5, 0, 1, true>"}
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 
 
@@ -189,7 +189,7 @@ def bench_linear(dev, iters: int = 20, warmup: int = 5):
             "roofline": {"bound": "mfma", "achieved": round(tflops, 1),
                          "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
-                         "traffic": measured_traffic("linear_wide_kernel<3>")}}
+                         "traffic": measured_traffic("linear_wide_kernel<3, 0>")}}
 
 
 def bench_linear_backward(dev, iters: int = 10, warmup: int = 3):
