@@ -255,6 +255,117 @@ __global__ __launch_bounds__(256) void global_avg_pool2d_kernel(const uint8_t* _
   y[p] = sum / (float)hw;
 }
 
+// --- global average, wave-parallel (planes of at most 8192 elements) -------
+//
+// numpy's pairwise recursion on a plane of n <= 8192 elements (one buffer
+// block) splits it into leaves of <= 128 elements (at most 64) combined by a
+// fixed binary tree; the host works both out once per launch (every plane
+// has the same n) into a GapPlan: the leaves in order and the tree as a
+// postfix program (bit 1: push the next leaf's sum, bit 0: add the two top
+// values).  8 lanes make a leaf's 8 interleaved partial sums (lane j:
+// elements j, j+8, ... of the leaf's whole groups of 8, in order), shuffles
+// combine them as ((r0+r1)+(r2+r3))+((r4+r5)+(r6+r7)), lane 0 of the 8 adds
+// the leaf's remainder in order; the plane's first lane then runs the program
+// over the leaf sums with an 8-deep register stack (the tree is at most 7
+// levels deep).  Same operations in the same association as numpy.
+constexpr int GAP_MAX_LEAVES = 64;
+
+struct GapPlan {
+  int L, nops;
+  uint32_t prog[4];  // 2L - 1 <= 127 postfix bits
+  int2 leaf[GAP_MAX_LEAVES];  // (offset, length)
+};
+
+template <int XT>
+__global__ __launch_bounds__(256) void global_avg_pool2d_wave_kernel(
+    const uint8_t* __restrict__ x, const float* __restrict__ x_scale, float* __restrict__ y,
+    int64_t planes, int hw, GapPlan plan) {
+  __shared__ float sums[4][GAP_MAX_LEAVES];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int L = plan.L;
+  const int G = L < 8 ? L : 8;         // leaves per pass
+  const int ppw = 64 / (8 * G);        // planes per wave
+  const int pi = lane / (8 * G), rem = lane - pi * 8 * G;
+  const int li = rem >> 3, j = rem & 7;
+  const int64_t plane = ((int64_t)blockIdx.x * 4 + wave) * ppw + pi;
+  const bool live = pi < ppw && plane < planes;
+  const int64_t base = plane * hw;
+  const bool scaled = x_scale != nullptr;
+  const float s = scaled ? *x_scale : 1.0f;
+  for (int p0 = 0; p0 < L; p0 += G) {
+    const int leaf = p0 + li;
+    const bool on = live && leaf < L;
+    const int2 lt = on ? plan.leaf[leaf] : make_int2(0, 0);
+    const int64_t b = base + lt.x;
+    const int main = lt.y - (lt.y & 7);
+    // a leaf holds at most 16 groups of 8: every load of the lane goes out
+    // before the in-order sum
+    float v[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const int i = j + 8 * k;
+      v[k] = (on && i < main) ? elem<XT>(x, b + i, s, scaled) : 0.0f;
+    }
+    float r = 0.0f;
+    if (on && lt.y >= 8) {
+      r = v[0];
+#pragma unroll
+      for (int k = 1; k < 16; ++k)
+        if (j + 8 * k < main) r += v[k];
+    }
+    // ((r0+r1)+(r2+r3))+((r4+r5)+(r6+r7)) across the 8 lanes of the leaf
+    r = r + __shfl_down(r, 1, 8);
+    r = r + __shfl_down(r, 2, 8);
+    r = r + __shfl_down(r, 4, 8);
+    if (on && j == 0) {
+      // the leaf's remainder (or, below 8 elements, the whole leaf) in order
+      const int e0 = lt.y < 8 ? 0 : main;
+      float t[7];
+#pragma unroll
+      for (int q = 0; q < 7; ++q) t[q] = e0 + q < lt.y ? elem<XT>(x, b + e0 + q, s, scaled) : 0.0f;
+      float res = lt.y < 8 ? 0.0f : r;
+#pragma unroll
+      for (int q = 0; q < 7; ++q)
+        if (e0 + q < lt.y) res += t[q];
+      sums[wave][pi * L + leaf] = res;
+    }
+  }
+  __syncthreads();
+  if (live && rem == 0) {
+    const float* ls = &sums[wave][pi * L];
+    float st[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    int next = 0;
+    for (int k = 0; k < plan.nops; ++k) {
+      if ((plan.prog[k >> 5] >> (k & 31)) & 1u) {
+        const float v = ls[next++];
+#pragma unroll
+        for (int d = 7; d > 0; --d) st[d] = st[d - 1];
+        st[0] = v;
+      } else {
+        st[0] = st[1] + st[0];
+#pragma unroll
+        for (int d = 1; d < 7; ++d) st[d] = st[d + 1];
+      }
+    }
+    y[plane] = (0.0f + st[0]) / (float)hw;
+  }
+}
+
+// Leaves and postfix program of numpy's pairwise recursion on n elements.
+void gap_plan(int n, int off, GapPlan& p) {
+  if (n <= 128) {
+    p.leaf[p.L++] = make_int2(off, n);
+    p.prog[p.nops >> 5] |= 1u << (p.nops & 31);
+    ++p.nops;
+    return;
+  }
+  int n2 = n / 2;
+  n2 -= n2 % 8;
+  gap_plan(n2, off, p);
+  gap_plan(n - n2, off + n2, p);
+  ++p.nops;  // bit 0: add
+}
+
 template <int XT>
 int launch_max(const void* x, void* y, const PoolGeom& g, hipStream_t stream) {
   const int64_t npix = (int64_t)g.OH * g.OW;
@@ -277,6 +388,20 @@ int launch_max(const void* x, void* y, const PoolGeom& g, hipStream_t stream) {
 template <int XT>
 int launch_gap(const void* x, const float* x_scale, float* y, int64_t planes, int64_t hw,
                hipStream_t stream) {
+  if (hw <= NP_BUFSIZE) {
+    GapPlan plan{};
+    gap_plan((int)hw, 0, plan);
+    const int leaves = plan.L;
+    const int G = leaves < 8 ? leaves : 8;
+    const int64_t ppw = 64 / (8 * G);
+    const int64_t waves = (planes + ppw - 1) / ppw;
+    const int64_t blocks = (waves + 3) / 4;
+    if (blocks > 0x7FFFFFFF) return NOVAQ_EINVAL;
+    hipLaunchKernelGGL(global_avg_pool2d_wave_kernel<XT>, dim3((unsigned)blocks), dim3(256), 0,
+                       stream, static_cast<const uint8_t*>(x), x_scale, y, planes, (int)hw,
+                       plan);
+    return check_launch();
+  }
   const int64_t blocks = (planes + 255) / 256;
   if (blocks > 0x7FFFFFFF) return NOVAQ_EINVAL;
   hipLaunchKernelGGL(global_avg_pool2d_kernel<XT>, dim3((unsigned)blocks), dim3(256), 0, stream,
