@@ -715,21 +715,29 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
       frags(st, af, bf);
       mma(af, bf);
     }
-    // lane holds pixels 4*lg .. 4*lg+3 of channel lr of each tile
+    // lane holds pixels 4*lg .. 4*lg+3 of channel lr of each tile; its four
+    // channels' epilogue constants are loaded once
+    EpiChan kc[4];
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      if (m >= my_mt) break;
-      const int p = (wave + 4 * m) * 16 + 4 * lg;
+    for (int t = 0; t < 4; ++t) {
+      const int co = co0 + t * 16 + lr;
+      kc[t] = (t < nt_live && co < g.C_out) ? epi_chan(ep, co) : EpiChan{0.0f, 1.0f, 0.0f};
+    }
+    if (plain) {
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const int co = co0 + t * 16 + lr;
-        if (t >= nt_live || co >= g.C_out) continue;
-        const int64_t di = ((int64_t)n * g.C_out + co) * npix + (int64_t)oh0 * g.OW + p;
-        if (plain) {
+      for (int m = 0; m < 4; ++m) {
+        if (m >= my_mt) break;
+        const int p = (wave + 4 * m) * 16 + 4 * lg;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int co = co0 + t * 16 + lr;
+          if (t >= nt_live || co >= g.C_out) continue;
           // bias only, fp32 output: one 16-byte store of the four pixels
-          const float bv = ep.bias ? ep.bias[co] : 0.0f;
+          // (plain stores: the 64-byte pieces of a line written by
+          // neighbouring lanes and waves merge in L2 before they reach HBM)
+          const int64_t di = ((int64_t)n * g.C_out + co) * npix + (int64_t)oh0 * g.OW + p;
           float* dst = reinterpret_cast<float*>(y) + di;
-          const f32x4 v = acc[m][t] * s + bv;
+          const f32x4 v = acc[m][t] * s + kc[t].bias;
           if (p + 3 < P && (di & 3) == 0) {
             *reinterpret_cast<f32x4*>(dst) = v;
           } else {
@@ -737,25 +745,44 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
             for (int i = 0; i < 4; ++i)
               if (p + i < P) dst[i] = v[i];
           }
-          continue;
-        }
-        const EpiChan k = epi_chan(ep, co);
-        float v[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          v[i] = epi_value(ep, k, acc[m][t][i], s);
-          if (ep.amax && p + i < P) am = epi_track(am, v[i]);
-        }
-        // plain stores: the 64-byte pieces of a line written by neighbouring
-        // lanes and waves merge in L2 before they reach HBM
-        if (p + 3 < P && (di & 3) == 0) {
-          epi_store4(ep.out_dtype, y, di, v, inv_o);
-        } else {
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            if (p + i < P) epi_store(ep.out_dtype, y, di + i, v[i], inv_o);
         }
       }
+      return;
+    }
+    // the epilogue, with the output dtype fixed per copy of the loop
+    auto store_all = [&](auto od) {
+      constexpr int OD = decltype(od)::value;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        if (m >= my_mt) break;
+        const int p = (wave + 4 * m) * 16 + 4 * lg;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int co = co0 + t * 16 + lr;
+          if (t >= nt_live || co >= g.C_out) continue;
+          const int64_t di = ((int64_t)n * g.C_out + co) * npix + (int64_t)oh0 * g.OW + p;
+          float v[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            v[i] = epi_value(ep, kc[t], acc[m][t][i], s);
+            if (ep.amax && p + i < P) am = epi_track(am, v[i]);
+          }
+          if (p + 3 < P && (di & 3) == 0) {
+            epi_store4_t<OD>(y, di, v, inv_o);
+          } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (p + i < P) epi_store_t<OD>(y, di + i, v[i], inv_o);
+          }
+        }
+      }
+    };
+    switch (ep.out_dtype) {
+      case F16: store_all(OutDtype<F16>{}); break;
+      case BF16: store_all(OutDtype<BF16>{}); break;
+      case E4M3: store_all(OutDtype<E4M3>{}); break;
+      case E5M2: store_all(OutDtype<E5M2>{}); break;
+      default: store_all(OutDtype<F32>{}); break;
     }
   };
 

@@ -119,4 +119,44 @@ __device__ __forceinline__ void epi_store4(int dt, void* y, int64_t i, const flo
   }
 }
 
+// The same encode / stores with the output dtype fixed at compile time.
+template <int OD>
+__device__ __forceinline__ uint32_t epi_encode_t(float v, float inv_s) {
+  if constexpr (OD == F16) return enc_f16(f2u(v));
+  else if constexpr (OD == BF16) return enc_bf16(f2u(v));
+  else if constexpr (OD == E4M3) return enc_e4m3(scale_mul(f2u(v), inv_s));
+  else if constexpr (OD == E5M2) return enc_e5m2(scale_mul(f2u(v), inv_s));
+  else return f2u(v);
+}
+
+template <int OD>
+__device__ __forceinline__ void epi_store_t(void* y, int64_t i, float v, float inv_s) {
+  if constexpr (OD == F32) reinterpret_cast<float*>(y)[i] = v;
+  else if constexpr (OD == F16 || OD == BF16)
+    reinterpret_cast<uint16_t*>(y)[i] = (uint16_t)epi_encode_t<OD>(v, inv_s);
+  else reinterpret_cast<uint8_t*>(y)[i] = (uint8_t)epi_encode_t<OD>(v, inv_s);
+}
+
+template <int OD>
+__device__ __forceinline__ void epi_store4_t(void* y, int64_t i, const float* v, float inv_s) {
+  if constexpr (OD == F32) {
+    *reinterpret_cast<float4*>(reinterpret_cast<float*>(y) + i) = make_float4(v[0], v[1], v[2], v[3]);
+  } else if constexpr (OD == F16 || OD == BF16) {
+    const uint32_t c0 = epi_encode_t<OD>(v[0], inv_s), c1 = epi_encode_t<OD>(v[1], inv_s);
+    const uint32_t c2 = epi_encode_t<OD>(v[2], inv_s), c3 = epi_encode_t<OD>(v[3], inv_s);
+    *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(y) + i) =
+        make_uint2(c0 | (c1 << 16), c2 | (c3 << 16));
+  } else {
+    uint32_t w = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) w |= epi_encode_t<OD>(v[q], inv_s) << (8 * q);
+    *reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(y) + i) = w;
+  }
+}
+
+template <int OD>
+struct OutDtype {
+  static constexpr int value = OD;
+};
+
 }  // namespace novaq
