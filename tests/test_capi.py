@@ -135,3 +135,77 @@ def test_status_maps_to_reference_exceptions():
     with pytest.raises(NotImplementedError):
         _lib.check(_lib.ENOTSUP, "x")
     _lib.check(_lib.OK, "x")
+
+
+def test_fused_forward_validation():
+    """novaq_*_forward_ex reject bad x / output dtypes, padding modes, shapes
+    and misaligned epilogue pointers before any launch."""
+    lib = _lib.load()
+    ep = _lib.Epilogue(None, None, None, None, 1, _lib.BF16)
+    bad_out = _lib.Epilogue(None, None, None, None, 0, _lib.E2M1)
+    odd = _lib.Epilogue(FAKE + 2, None, None, None, 0, _lib.F32)
+    lin = lib.novaq_linear_forward_ex
+    largs = [FAKE, _lib.F32, None, 4, 8, FAKE, _lib.E4M3, None, None, 8, None, FAKE, None]
+
+    def lcall(**kw):
+        a = list(largs)
+        for i, v in kw.items():
+            a[int(i[1:])] = v
+        return lin(*a)
+    assert lcall(a1=_lib.E2M1) == _lib.EDTYPE              # x cannot be FP4
+    assert lcall(a1=9) == _lib.EDTYPE
+    assert lcall(a6=9) == _lib.EDTYPE                      # weight dtype
+    assert lcall(a10=ctypes.byref(bad_out)) == _lib.EDTYPE  # FP4 output
+    assert lcall(a3=-1) == _lib.EINVAL
+    assert lcall(a6=_lib.E2M1, a4=7) == _lib.ESHAPE        # odd D_in for E2M1 rows
+    assert lcall(a0=FAKE + 4) == _lib.EALIGN
+    assert lcall(a10=ctypes.byref(odd)) == _lib.EALIGN      # epilogue pointer
+    assert lcall(a3=0, a10=ctypes.byref(ep)) == _lib.OK     # empty batch
+    conv = lib.novaq_conv2d_forward_ex
+    cargs = [FAKE, _lib.BF16, None, 2, 3, 8, 8, FAKE, _lib.E2M1, None, 4, 3, 3, 1, 1, 1, 1, 0,
+             None, None, FAKE, None]
+
+    def ccall(**kw):
+        a = list(cargs)
+        for i, v in kw.items():
+            a[int(i[1:])] = v
+        return conv(*a)
+    assert ccall(a17=4) == _lib.EPADMODE
+    assert ccall(a1=_lib.E2M1) == _lib.EDTYPE
+    assert ccall(a11=12) == _lib.ESHAPE
+    assert ccall(a13=0) == _lib.EINVAL
+    assert ccall(a19=ctypes.byref(bad_out)) == _lib.EDTYPE
+    assert ccall(a3=0) == _lib.OK
+
+
+def test_optimizer_and_pool_validation():
+    lib = _lib.load()
+    hp = _lib.AdamW(1e-3, 0.9, 0.999, 1e-8, 0.0, 1, 1)
+    bad = _lib.AdamW(1e-3, 0.9, 0.999, 1e-8, 0.0, 0, 1)   # steps count from 1
+    step = lib.novaq_adamw_step
+    assert step(FAKE, FAKE, FAKE, FAKE, 8, ctypes.byref(bad), None, None) == _lib.EINVAL
+    assert step(FAKE, FAKE, FAKE, FAKE, 8, None, None, None) == _lib.EINVAL
+    assert step(FAKE + 4, FAKE, FAKE, FAKE, 8, ctypes.byref(hp), None, None) == _lib.EALIGN
+    assert step(None, FAKE, FAKE, FAKE, 8, ctypes.byref(hp), None, None) == _lib.EINVAL
+    rq = lib.novaq_adamw_requantize
+    assert rq(FAKE, FAKE, FAKE, FAKE, 8, ctypes.byref(hp), FAKE, _lib.F16, FAKE,
+              None) == _lib.EDTYPE                         # codes must be FP8 / FP4
+    assert rq(FAKE, FAKE, FAKE, FAKE, 8, ctypes.byref(hp), FAKE, _lib.E4M3, None,
+              None) == _lib.EINVAL                         # amax_scale is required
+    mp = lib.novaq_max_pool2d
+    margs = [FAKE, _lib.F32, 2, 3, 8, 8, 2, 2, 2, 2, 0, 0, 0, FAKE, None]
+
+    def mcall(**kw):
+        a = list(margs)
+        for i, v in kw.items():
+            a[int(i[1:])] = v
+        return mp(*a)
+    assert mcall(a1=_lib.E2M1) == _lib.EDTYPE
+    assert mcall(a12=5) == _lib.EPADMODE
+    assert mcall(a6=11) == _lib.ESHAPE
+    assert mcall(a8=0) == _lib.EINVAL
+    assert mcall(a2=0) == _lib.OK
+    gap = lib.novaq_global_avg_pool2d
+    assert gap(FAKE, _lib.E2M1, None, 2, 3, 4, 4, FAKE, None) == _lib.EDTYPE
+    assert gap(FAKE, _lib.F32, None, 2, 0, 4, 4, FAKE, None) == _lib.EINVAL
+    assert gap(FAKE, _lib.F32, None, 0, 3, 4, 4, FAKE, None) == _lib.OK
