@@ -330,6 +330,221 @@ __global__ __launch_bounds__(DW_THREADS, 2) void dweight_kernel(
   }
 }
 
+// grad_weight for stride 1 and output rows of at most 64 pixels, one wave
+// per window tap.  A workgroup owns 64 output channels (two 32-row MFMA
+// tiles) and 32 input channels, and walks a chunk of (image, band of R output
+// rows) stages.  Per stage it stages in LDS, as bf16:
+//   - Gs[co][k]: grad of the band, k = r * OWP + ow (rows padded to OWP, a
+//     multiple of 16, with zeros; R * OWP = 128 = 8 MFMA k-steps);
+//   - Xs[c][rr][col] = xpad[c][oh0 + rr - ph][col - pw]: the band's R + KH - 1
+//     input rows, XW = OWP + 8 columns each, the padding mode resolved (zero
+//     rows and columns past what the band's outputs read),
+// so wave t = (kh, kw) multiplies A = Gs (8 consecutive pixels of one channel,
+// a 16-byte LDS read) by B = Xs[c][r + kh][ow + kw ..] (8 consecutive
+// columns; for odd kw the 16 bytes sit across 5 dwords and v_alignbit
+// realigns them) with v_mfma_f32_32x32x16_bf16 into the (co, c) block of its
+// tap.  The Xs channel pitch is an odd number of dwords, so the 32 channels
+// of a fragment read fall in distinct banks.
+//
+// Staging is one contiguous run per channel: a band's R * OW grad values and
+// a channel's rows_in * XW staged slots are spread over the 64 lanes (GJ = 2
+// and XJ slots per lane), whose byte offsets each lane forms once per stage.
+// The loads are buffer loads: a masked slot (padding, rows past the image,
+// channels past the tensor) carries an offset beyond the buffer's size and
+// reads 0, so no lane branches.  A stage's loads (KH * KW >= 8 makes one step
+// per wave enough) are issued into registers while the previous stage's
+// products run.  Each workgroup writes its chunk's partial as [tap][co][c];
+// the column sum adds the chunks and permutes to [co][c][kh][kw].
+constexpr int DR_K = 128;          // pixels per stage
+constexpr uint32_t DR_OOB = 0x80000000u;  // byte offset past any buffer (reads 0)
+constexpr uint32_t DR_BUF3 = 0x00020000u;  // buffer resource word 3 (raw, 32-bit data)
+
+struct RowsGeom {
+  int OWP, R, XW, rows_in, taps, cp, spi;  // padded output row, rows per stage, staged row
+                                           // width, staged rows, KH*KW, Xs channel pitch
+                                           // (bf16), stages per image
+};
+
+template <int XJ>
+__global__ __launch_bounds__(1024) void dweight_rows_kernel(
+    const float* __restrict__ grad, const float* __restrict__ x, float* __restrict__ part,
+    BwdGeom g, RowsGeom rg, int chunks, int co_blocks, int c_blocks) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t dr_lds[];
+  constexpr int GP = DR_K + 8;  // Gs row pitch (bf16); slot DR_K takes masked lanes
+  __bf16* Gs = reinterpret_cast<__bf16*>(dr_lds);
+  __bf16* Xs = Gs + 64 * GP;
+  const int tid = threadIdx.x, lane = tid & 63, half = lane >> 5;
+  const int tap = __builtin_amdgcn_readfirstlane(tid >> 6), nthreads = rg.taps * 64;
+  const int kh = tap / g.KW, kw = tap - kh * g.KW;
+  int bid = blockIdx.x;
+  const int cb = bid % c_blocks;
+  bid /= c_blocks;
+  const int cob = bid % co_blocks;
+  const int chunk = bid / co_blocks;
+  const int co0 = cob * 64, c0 = cb * 32;
+  const int64_t T = (int64_t)g.N * rg.spi;
+  const int64_t t_begin = T * chunk / chunks, t_end = T * (chunk + 1) / chunks;
+  const int HW = g.H * g.W;
+  const int P = g.OH * g.OW;
+  const int xslots = rg.rows_in * rg.XW;
+
+  f32x16 acc[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[i][r] = 0.0f;
+
+  // Gs padding columns (ow >= OW) are zeroed once and never written again.
+  {
+    uint32_t* z = reinterpret_cast<uint32_t*>(dr_lds);
+    for (int i = tid; i < 64 * GP / 2; i += nthreads) z[i] = 0u;
+  }
+  // Gs slot j of this lane: grad value m = lane + 64 j of the band, its row
+  // and Gs column (DR_K when m is past the band)
+  int gr[2], gk[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int m = lane + 64 * j;
+    gr[j] = m / g.OW;
+    gk[j] = m < rg.R * g.OW ? gr[j] * rg.OWP + (m - gr[j] * g.OW) : DR_K;
+  }
+  // Xs slot j of this lane: staged row xr and input column xw (-1: zero; also
+  // for columns no output of the band reads); slots past the channel's
+  // xslots go to the pitch's spare slot
+  int xr[XJ], xw[XJ], xk[XJ];
+#pragma unroll
+  for (int j = 0; j < XJ; ++j) {
+    const int e = lane + 64 * j;
+    xr[j] = e / rg.XW;
+    const int col = e - xr[j] * rg.XW;
+    xw[j] = (e < xslots && col < g.OW + g.KW - 1) ? pad_idx(col - g.pw, g.W, g.pad_mode) : -1;
+    xk[j] = e < xslots ? e : xslots;
+  }
+  const bool odd = kw & 1;
+
+  // Stage t's loads: 8 grad channels (16 slots) and 4 input channels (4 XJ
+  // slots) per wave, which covers the 64 + 32 channels for KH * KW >= 8; all
+  // in flight together, into registers.
+  float gv[16], xv[4 * XJ];
+  auto load_stage = [&](int64_t t) {
+    const int n = (int)(t / rg.spi);
+    const int oh0 = (int)(t - (int64_t)n * rg.spi) * rg.R;
+    const int rows_left = g.OH - oh0;
+    const int rows_read = (rows_left < rg.R ? rows_left : rg.R) + g.KH - 1;
+    const __amdgpu_buffer_rsrc_t gbuf = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(grad + (int64_t)n * g.C_out * P), (short)0, g.C_out * P * 4, DR_BUF3);
+    const __amdgpu_buffer_rsrc_t xbuf = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(x + (int64_t)n * g.C * HW), (short)0, g.C * HW * 4, DR_BUF3);
+    // byte offsets of this lane's slots within a channel
+    uint32_t goff[2], xoff[XJ];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      goff[j] = (gk[j] < DR_K && gr[j] < rows_left)
+                    ? (uint32_t)(oh0 * g.OW + lane + 64 * j) * 4u : DR_OOB;
+    // input row of staged row rr (lane rr holds it; -1: a zero row)
+    const int hi_l = lane < rows_read ? pad_idx(oh0 + lane - g.ph, g.H, g.pad_mode) : -1;
+#pragma unroll
+    for (int j = 0; j < XJ; ++j) {
+      const int hi = __shfl(hi_l, xr[j] < 63 ? xr[j] : 63);
+      xoff[j] = (hi >= 0 && xw[j] >= 0) ? (uint32_t)(hi * g.W + xw[j]) * 4u : DR_OOB;
+    }
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const int co_l = tap + (k >> 1) * rg.taps;
+      const uint32_t coff = (co_l < 64 && co0 + co_l < g.C_out)
+                                ? (uint32_t)(co0 + co_l) * (uint32_t)P * 4u : 0x40000000u;
+      gv[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                            gbuf, goff[k & 1] + coff, 0, 0));
+    }
+#pragma unroll
+    for (int k = 0; k < 4 * XJ; ++k) {
+      const int c_l = tap + (k / XJ) * rg.taps;
+      const uint32_t coff = (c_l < 32 && c0 + c_l < g.C)
+                                ? (uint32_t)(c0 + c_l) * (uint32_t)HW * 4u : 0x40000000u;
+      xv[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                            xbuf, xoff[k % XJ] + coff, 0, 0));
+    }
+  };
+
+  if (t_begin < t_end) load_stage(t_begin);
+  for (int64_t t = t_begin; t < t_end; ++t) {
+    __syncthreads();  // the previous stage's fragment reads are done
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const int co_l = tap + (k >> 1) * rg.taps;
+      if (co_l < 64) Gs[co_l * GP + gk[k & 1]] = (__bf16)gv[k];
+    }
+#pragma unroll
+    for (int k = 0; k < 4 * XJ; ++k) {
+      const int c_l = tap + (k / XJ) * rg.taps;
+      if (c_l < 32) Xs[c_l * rg.cp + xk[k % XJ]] = (__bf16)xv[k];
+    }
+    // the next stage's loads overlap this stage's products
+    if (t + 1 < t_end) load_stage(t + 1);
+    __syncthreads();
+    // wave `tap`: 8 k-steps of 16 pixels, both 32-channel co tiles
+    const uint32_t* xd = reinterpret_cast<const uint32_t*>(Xs) + (lane & 31) * (rg.cp >> 1) +
+                         (kw >> 1);
+#pragma unroll
+    for (int st = 0; st < DR_K / 16; ++st) {
+      const int k0 = st * 16 + half * 8;
+      const int r = (st * 16) / rg.OWP, ow0 = st * 16 - r * rg.OWP + half * 8;
+      const uint32_t* p = xd + (((r + kh) * rg.XW + ow0) >> 1);
+      uint32_t d[5];
+#pragma unroll
+      for (int i = 0; i < 5; ++i) d[i] = p[i];
+      uint32_t bw[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) bw[i] = odd ? __builtin_amdgcn_alignbit(d[i + 1], d[i], 16) : d[i];
+      const bf16x8 b = __builtin_bit_cast(bf16x8, bw);
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const bf16x8 a = *reinterpret_cast<const bf16x8*>(Gs + (i * 32 + (lane & 31)) * GP + k0);
+        acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[i], 0, 0, 0);
+      }
+    }
+  }
+  // lane holds input channel c0 + (lane & 31), output channel rows
+  // 8*(r/4) + 4*half + r%4 of tile i; the partial is stored as
+  // [chunk][tap][co][c] (a half-wave writes 32 consecutive c), which the
+  // column sum permutes into [co][c][kh][kw]
+  float* pc = part + ((int64_t)chunk * rg.taps + tap) * g.C_out * g.C;
+  const int c = c0 + (lane & 31);
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int co = co0 + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+      if (co < g.C_out && c < g.C) pc[(int64_t)co * g.C + c] = acc[i][r];
+    }
+}
+
+constexpr int DR_MAX_XJ = 8;
+
+// The stride-1 rows path applies (its LDS bytes and slots per lane XJ), or 0.
+size_t rows_geometry(const BwdGeom& g, RowsGeom& rg, int& xj) {
+  const int taps = g.KH * g.KW;
+  // (fewer than 16 input channels leave most of the 32-channel tile idle)
+  if (g.sh != 1 || g.sw != 1 || taps < 8 || taps > 16 || g.KW > 8 || g.OW > 64 || g.C < 16)
+    return 0;
+  // 32-bit buffer offsets: an image's grad and input stay below 1 GiB
+  if ((int64_t)g.C_out * g.OH * g.OW * 4 >= (1 << 30) || (int64_t)g.C * g.H * g.W * 4 >= (1 << 30))
+    return 0;
+  rg.OWP = g.OW <= 16 ? 16 : g.OW <= 32 ? 32 : 64;
+  rg.R = DR_K / rg.OWP;
+  rg.XW = rg.OWP + 8;
+  rg.rows_in = rg.R + g.KH - 1;
+  if (rg.rows_in > 64) return 0;
+  rg.taps = taps;
+  const int xslots = rg.rows_in * rg.XW;
+  rg.cp = xslots + 2;  // odd dword pitch; slot xslots is the spare
+  rg.spi = (g.OH + rg.R - 1) / rg.R;
+  xj = (xslots + 63) / 64;
+  if (xj < 2 || xj > DR_MAX_XJ) return 0;
+  const size_t bytes = (size_t)64 * (DR_K + 8) * 2 + (size_t)32 * rg.cp * 2;
+  return bytes <= 150 * 1024 ? bytes : 0;
+}
+
 template <int WT>
 int launch_flip(const void* w, void* wf, const BwdGeom& g, hipStream_t stream) {
   const int64_t total = (int64_t)g.C_out * g.C * g.KH * g.KW;
@@ -424,6 +639,45 @@ int conv2d_backward_launch(const float* grad, const float* x, int64_t N, int64_t
   }
   const int64_t ckk = C * KH * KW;
   if (!grad_weight && !grad_bias) return rc;
+  // stride-1 convolutions with short rows: grad_weight on the rows kernel, and
+  // grad_bias (when asked) on dweight_kernel's bias-only pass, whose bits a
+  // bias-only call reproduces
+  RowsGeom rg{};
+  int xj = 0;
+  const size_t rows_lds = grad_weight ? rows_geometry(g, rg, xj) : 0;
+  if (rows_lds) {
+    float* part = reinterpret_cast<float*>(base + ws.part);
+    const int64_t co_blocks = (C_out + 63) / 64, c_blocks = (C + 31) / 32;
+    const int64_t units = (int64_t)g.N * rg.spi;
+    // about one workgroup per CU: the chunk partials cost HBM traffic
+    int64_t rchunks = std::max<int64_t>(1, device_cu_count() / (co_blocks * c_blocks));
+    rchunks = std::min<int64_t>(std::min<int64_t>(rchunks, ws.chunks), std::max<int64_t>(units, 1));
+    const int64_t blocks = rchunks * co_blocks * c_blocks;
+    if (blocks > 0x7FFFFFFF) return NOVAQ_EINVAL;
+    using RowsKernel = void (*)(const float*, const float*, float*, BwdGeom, RowsGeom, int, int,
+                                int);
+    static const RowsKernel kerns[DR_MAX_XJ + 1] = {
+        nullptr, nullptr, dweight_rows_kernel<2>, dweight_rows_kernel<3>, dweight_rows_kernel<4>,
+        dweight_rows_kernel<5>, dweight_rows_kernel<6>, dweight_rows_kernel<7>,
+        dweight_rows_kernel<8>};
+    static bool lds_raised[DR_MAX_XJ + 1] = {};
+    const RowsKernel kern = kerns[xj];
+    if (!lds_raised[xj]) {
+      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize,
+                                               150 * 1024);
+      if (e != hipSuccess) return hip_fail(e);
+      lds_raised[xj] = true;
+    }
+    hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(rg.taps * 64), rows_lds, stream, grad,
+                       x, part, g, rg, (int)rchunks, (int)co_blocks, (int)c_blocks);
+    rc = check_launch();
+    if (rc != NOVAQ_OK) return rc;
+    rc = colsum_launch(part, rchunks, C_out * ckk, grad_weight, stream, (int)rg.taps, (int)C_out,
+                       (int)C);
+    if (rc != NOVAQ_OK || !grad_bias) return rc;
+    grad_weight = nullptr;  // the bias pass below
+  }
   float* part = reinterpret_cast<float*>(base + ws.part);
   float* bpart = grad_bias ? reinterpret_cast<float*>(base + ws.bpart) : nullptr;
   const int64_t co_blocks = (C_out + DW_M - 1) / DW_M;

@@ -82,12 +82,16 @@ __global__ __launch_bounds__(TT) void transpose_kernel(const uint8_t* __restrict
   }
 }
 
+// Column sums: out[c] = sum over r of x[r * cols + c] in a fixed order (with
+// pt > 0 the columns are a (pt, pco, pc) array and column (t, co, c) is
+// stored at out[(co * pc + c) * pt + t]).
 constexpr int CS_COLS = 64;    // columns per workgroup
 constexpr int CS_SLICES = 16;  // row slices per workgroup (one wave each)
 
 __global__ __launch_bounds__(CS_COLS * CS_SLICES) void colsum_kernel(const float* __restrict__ x,
                                                                     int64_t rows, int64_t cols,
-                                                                    float* __restrict__ out) {
+                                                                    float* __restrict__ out,
+                                                                    int pt, int pco, int pc) {
   __shared__ float part[CS_SLICES][CS_COLS];
   const int tx = threadIdx.x % CS_COLS, ty = threadIdx.x / CS_COLS;
   const int64_t c = (int64_t)blockIdx.x * CS_COLS + tx;
@@ -113,7 +117,13 @@ __global__ __launch_bounds__(CS_COLS * CS_SLICES) void colsum_kernel(const float
     float t = part[0][tx];
 #pragma unroll
     for (int k = 1; k < CS_SLICES; ++k) t += part[k][tx];
-    out[c] = t;
+    int64_t o = c;
+    if (pt > 0) {
+      const int64_t per_t = (int64_t)pco * pc;
+      const int64_t tt = c / per_t, rest = c - tt * per_t;
+      o = rest * pt + tt;  // rest = co * pc + c
+    }
+    out[o] = t;
   }
 }
 
@@ -150,12 +160,13 @@ int transpose_launch(const void* src, int st, int64_t rows, int64_t cols, void* 
   return NOVAQ_EDTYPE;
 }
 
-int colsum_launch(const float* x, int64_t rows, int64_t cols, float* out, hipStream_t stream) {
+int colsum_launch(const float* x, int64_t rows, int64_t cols, float* out, hipStream_t stream,
+                  int pt, int pco, int pc) {
   if (cols == 0) return NOVAQ_OK;
   const int64_t blocks = (cols + CS_COLS - 1) / CS_COLS;
   if (blocks > 0x7FFFFFFF) return NOVAQ_EINVAL;
   hipLaunchKernelGGL(colsum_kernel, dim3((unsigned)blocks), dim3(CS_COLS * CS_SLICES), 0, stream,
-                     x, rows, cols, out);
+                     x, rows, cols, out, pt, pco, pc);
   return check_launch();
 }
 

@@ -81,6 +81,10 @@ int conv2d_backward_launch(const float* grad, const float* x, int64_t N, int64_t
                            int64_t C_out, int KH, int KW, int sh, int sw, int ph, int pw,
                            int pad_mode, float* grad_input, float* grad_weight,
                            float* grad_bias, void* workspace, hipStream_t stream);
-int colsum_launch(const float* x, int64_t rows, int64_t cols, float* out, hipStream_t stream);
+// out[c] = sum over r of x[r * cols + c] in a fixed order; with pt > 0 the
+// columns form a (pt, pco, pc) array and column (t, co, c) goes to
+// out[(co * pc + c) * pt + t].
+int colsum_launch(const float* x, int64_t rows, int64_t cols, float* out, hipStream_t stream,
+                  int pt = 0, int pco = 0, int pc = 0);
 
 }  // namespace novaq

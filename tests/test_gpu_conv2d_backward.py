@@ -72,10 +72,29 @@ def test_conv2d_backward_vs_oracle(geom, wdt):
     check_case(*geom, wdt)
 
 
+# grad_weight on the stride-1 rows kernel (8 to 16 taps, at most 8 columns,
+# output rows of at most 64 pixels, 16 or more input channels)
+ROWS_GEOMETRIES = [
+    (2, 40, 13, 15, 70, 3, 3, (1, 1), (1, 1)),   # 16-pixel rows, last band partial, both channel blocks partial
+    (2, 17, 9, 50, 33, 3, 3, (1, 1), (0, 2)),    # 52-pixel rows (two per band)
+    (3, 16, 10, 12, 8, 4, 4, (1, 1), (2, 1)),    # 4x4: even and odd column shifts
+    (2, 16, 9, 9, 8, 2, 4, (1, 1), (1, 2)),      # 8 taps
+    (1, 16, 6, 20, 8, 2, 8, (1, 1), (0, 3)),     # 8 columns
+    (2, 96, 7, 30, 130, 3, 3, (1, 1), (1, 1)),   # three input and three output channel blocks
+]
+
+
+@pytest.mark.parametrize("wdt", ["e4m3", "e2m1"])
+@pytest.mark.parametrize("geom", ROWS_GEOMETRIES, ids=lambda g: "x".join(map(str, g[:7])))
+def test_conv2d_backward_rows_path(geom, wdt):
+    check_case(*geom, wdt)
+
+
 @pytest.mark.parametrize("mode", ["zeros", "reflect", "replicate", "circular"])
 @pytest.mark.parametrize("geom", [(2, 3, 8, 9, 5, 3, 3, (1, 1), (1, 2)),
-                                  (2, 4, 11, 10, 6, 3, 3, (2, 1), (2, 1))],
-                         ids=["s1", "s2"])
+                                  (2, 4, 11, 10, 6, 3, 3, (2, 1), (2, 1)),
+                                  (2, 16, 8, 9, 5, 3, 3, (1, 1), (1, 2))],
+                         ids=["s1", "s2", "s1rows"])
 def test_conv2d_backward_padding_modes(geom, mode):
     """grad_weight reads the input padded in the forward's mode; grad_input is
     the cropped col2im, the same in every mode (conv2d.py:141-148)."""
