@@ -27,6 +27,7 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+FP8_PEAK_TFLOPS = 5000.0
 BF16_PEAK_TFLOPS = 2500.0
 METRIC = "cast GB/s (% HBM peak) at 256M elems; FP8-weight Linear TFLOP/s at 4096^2"
 
@@ -179,11 +180,35 @@ def bench_linear(dev, iters: int = 20, warmup: int = 5):
     e1.record()
     torch.cuda.synchronize(dev)
     vms = e0.elapsed_time(e1) / iters
+    # the same product on x stored as E4M3 (amax-scaled, as a fused epilogue
+    # writes activations): both operands' codes go to the FP8 MFMA
+    xq = quant.quantize(x, "e4m3")
+
+    def run8():
+        _lib.check(lib.novaq_linear_forward_ex(
+            xq.data.data_ptr(), _lib.E4M3, xq.scale.data_ptr(), M, K, wq.data.data_ptr(), 3,
+            wq.scale.data_ptr(), b.data_ptr(), N, None, y.data_ptr(), stream), "linear fp8 x")
+    for _ in range(warmup):
+        run8()
+    torch.cuda.synchronize(dev)
+    e0.record()
+    for _ in range(iters):
+        run8()
+    e1.record()
+    torch.cuda.synchronize(dev)
+    ms8 = e0.elapsed_time(e1) / iters
+    tf8 = flops / (ms8 * 1e-3) / 1e12
     return {"metric": "FP8-weight Linear TFLOP/s at 4096^2", "value": round(tflops, 1),
             "unit": "TFLOP/s", "ms": round(ms, 4),
             "vendor_bf16_gemm": {"what": "torch.nn.functional.linear, bf16 x and W in HBM",
                                  "ms": round(vms, 4),
                                  "TFLOP/s": round(flops / (vms * 1e-3) / 1e12, 1)},
+            "e4m3_x": {"what": "config [4] with x stored as E4M3 (amax-scaled): "
+                               "linear_f8_kernel, both operands on the FP8 MFMA",
+                       "ms": round(ms8, 4), "TFLOP/s": round(tf8, 1),
+                       "frac_bf16_peak": round(tf8 / BF16_PEAK_TFLOPS, 4),
+                       "frac_fp8_peak": round(tf8 / FP8_PEAK_TFLOPS, 4),
+                       "traffic": measured_traffic("linear_f8_kernel<3, 3>")},
             "config": {"workload": "BASELINE config [4]", "M": M, "K": K, "N": N,
                        "w_dtype": "e4m3", "mfma": "bf16"},
             "roofline": {"bound": "mfma", "achieved": round(tflops, 1),

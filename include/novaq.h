@@ -178,7 +178,10 @@ typedef struct novaq_epilogue {
 /* novaq_linear_forward with a fused epilogue (epi NULL: none, fp32 output).
  * x is (N, D_in) in x_dtype: F32, or BF16 / F16 / E4M3 / E5M2 as a previous
  * epilogue stored it, x_scale its per-tensor scale for FP8 (NULL = 1; the
- * product uses s_x * dec(x)).  y is (N, D_out) in epi->out_dtype.
+ * product uses s_x * dec(x)).  y is (N, D_out) in epi->out_dtype.  With
+ * FP8 x and FP8 / FP4 weights (N % 128, D_out % 256, D_in % 128) both
+ * operands' codes go to the FP8 MFMA: exact products whose sums are not
+ * rounded as fp32 additions are (about 1e-5 normwise against fp64).
  * No reference counterpart as one call: it replaces F.linear followed by the
  * BatchNorm / ReLU layers' forward (see novaq_epilogue). */
 int novaq_linear_forward_ex(const void *x, int x_dtype, const float *x_scale, int64_t N,

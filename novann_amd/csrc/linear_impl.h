@@ -13,7 +13,10 @@
 // run on v_mfma_f32_32x32x16_bf16 with fp32 accumulation; the per-tensor scale
 // s and the bias are applied in fp32 after accumulation.
 //
-// Three kernels, chosen by shape and weight format:
+// Four kernels, chosen by shape and the operands' formats:
+//   - linear_f8_kernel (x stored as E4M3 / E5M2 and FP8 / FP4 weights, M % 128,
+//     N % 256, K % 128): both operands' codes on the FP8 MFMA
+//     (v_mfma_f32_32x32x64_f8f6f4), loaded straight into LDS;
 //   - linear_wide_kernel (FP8 / FP4 weights, M % 128, N % 256, K % 128): one
 //     128 x 256 tile per workgroup of 8 waves, K blocks of 128 (one 128-byte
 //     line of an FP8 W row), W raw in LDS and decoded per MFMA fragment,
@@ -691,6 +694,265 @@ __global__ __launch_bounds__(512, 1) void linear_wide_kernel(
   epi_amax_commit(ep, am);
 }
 
+// ---------------------------------------------------------------------------
+// FP8 product for x stored as E4M3 / E5M2 (the narrow activations a fused
+// epilogue writes) with E4M3 / E5M2 / E2M1 weights; M % 128, N % 256,
+// K % 128.  gfx950's v_mfma_f32_32x32x64_f8f6f4 takes both operands' codes
+// as they are stored: every product is exact and sums in fp32, and the
+// per-tensor scales s_x * s_w are applied in the epilogue, as on the other
+// paths.  The MFMA runs FP8 at over twice the bf16 rate under the chip's
+// power limit, and nothing is converted per fragment.
+//
+// The kernel keeps the 128 x 256 tile and 8 waves (2 x 4, 64 x 64 per wave)
+// of the wide kernel.  x and W go from HBM straight into LDS with
+// global_load_lds_dwordx4 (no staging registers) through a ring of 3 stages
+// of 128 K (x 16 KB + W 32 / 16 KB each: whole 128-byte lines), each issued
+// 2 stages ahead.  Rows are stored in 16-byte chunks XOR-swizzled by row so
+// the 16 rows one fragment read touches per LDS cycle fall in distinct
+// banks; a wave's load writes 64 consecutive chunk slots and each lane
+// fetches the global chunk that belongs in its slot.  The operands' lane
+// halves hold the K ranges the instruction pairs up (F8::x_chunk).  Fragments
+// are read one 64-K step ahead of the MFMAs that use them.  Synchronisation:
+// s_waitcnt vmcnt (this wave's loads of the next stage have landed) and
+// lgkmcnt (its fragment reads are done), then s_barrier (every wave's loads
+// have, and every wave is done with the slot the next load overwrites).
+
+template <int WT, int XT>
+struct F8 {
+  static_assert(XT == E4M3 || XT == E5M2, "x codes feed the FP8 MFMA as stored");
+  static constexpr int KS = 128;                         // K per stage: whole 128-byte lines
+  static constexpr int w_row = KS * dtype_bits(WT) / 8;  // 128 (FP8) or 64 (E2M1)
+  static constexpr int w_chunks = w_row / 16;            // 8 or 4
+  static constexpr int x_bytes = BM * KS;                // 128 rows x 128 B
+  static constexpr int w_bytes = 256 * w_row;
+  static constexpr int stage = x_bytes + w_bytes;         // 48 KB (FP8 W) or 32 KB (E2M1)
+  static constexpr int NS = 150 * 1024 / stage >= 3 ? 3 : 2;
+  static constexpr int X_PER = BM * 8 / 512;              // x loads per lane per stage
+  static constexpr int W_PER = 256 * w_chunks / 512;      // W loads per lane per stage
+  static constexpr int L = X_PER + W_PER;                 // loads per lane per stage
+  static constexpr int lds = NS * stage;
+  static constexpr int fmt = WT == E4M3 ? 0 : WT == E5M2 ? 1 : 4;  // f8f6f4 format codes
+  static constexpr int fmt_x = XT == E5M2 ? 1 : 0;
+  // The instruction's K order within a 64-K step: an FP8 operand's lane half
+  // h holds K [32h, 32h + 32); an E2M1 operand's holds K [16h, 16h + 16) then
+  // [32 + 16h, 32 + 16h + 16).  W keeps its order (in step s, lane half h
+  // reads chunk 2s + h for E2M1, chunks 4s + 2h and 4s + 2h + 1 for FP8), so
+  // the x operand's two 16-byte chunks u = 0, 1 are chunks 4s + 2h + u
+  // against FP8 W and 4s + h + 2u against E2M1 W.
+  __device__ static constexpr int x_chunk(int s, int h, int u) {
+    return 4 * s + (w_chunks == 8 ? 2 * h + u : h + 2 * u);
+  }
+  __device__ static constexpr int w_chunk(int s, int h, int u) {
+    return w_chunks == 8 ? 4 * s + 2 * h + u : 2 * s + h;
+  }
+  // chunk c of row r sits at slot c ^ swz(r): the 16 rows one fragment read
+  // touches per LDS cycle fall in distinct banks
+  __device__ static constexpr int swz_x(int r) { return (r >> 1) & 7; }
+  __device__ static constexpr int swz_w(int r) {
+    return w_chunks == 8 ? ((r >> 1) & 7) : ((r >> 2) & 3);
+  }
+};
+
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+
+// 16 bytes per lane from global memory straight into LDS at lds + 16 * lane
+// (lds is wave-uniform).  A plain device function: inside a kernel template
+// the builtin's host-side checks would drop the kernel's host stub.
+__device__ __forceinline__ void lds_dma16(const void* g, void* lds) {
+  __builtin_amdgcn_global_load_lds(g, lds, 16, 0, 0);
+}
+
+template <int WT, int XT>
+__global__ __launch_bounds__(512, 1) void linear_f8_kernel(
+    const uint8_t* __restrict__ x, const float* __restrict__ x_scale,
+    const uint8_t* __restrict__ w, const float* __restrict__ w_scale, Epilogue ep,
+    void* __restrict__ y, int M, int N, int K, int tiles_m, int tiles_n) {
+  using D = F8<WT, XT>;
+  constexpr int NS = D::NS, FBN = 256, FWN = 64, FNT = 2;
+  extern __shared__ __attribute__((aligned(16))) uint8_t dl[];
+
+  const int T = tiles_m * tiles_n;
+  int t = blockIdx.x;
+  if ((T & 7) == 0) t = (t & 7) * (T >> 3) + (t >> 3);
+  constexpr int GM = 4;
+  const int group = t / (GM * tiles_n);
+  const int first_m = group * GM;
+  const int gm = min(tiles_m - first_m, GM);
+  const int rem = t - group * GM * tiles_n;
+  const int m0 = (first_m + rem % gm) * BM;
+  const int n0 = (rem / gm) * FBN;
+
+  const int tid = threadIdx.x, lane = tid & 63, half = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = (wave & 1) * WM, wn = (wave >> 1) * FWN;
+
+  // this lane's load sources (stage 0): slot q = i * 512 + tid of x or W,
+  // row q / chunks
+  const size_t w_row_bytes = (size_t)K * dtype_bits(WT) / 8;
+  const uint8_t* xsrc[D::X_PER];
+#pragma unroll
+  for (int i = 0; i < D::X_PER; ++i) {
+    const int q = i * 512 + tid, r = q >> 3, c = (q & 7) ^ D::swz_x(r);
+    xsrc[i] = x + (size_t)(m0 + r) * K + c * 16;
+  }
+  const uint8_t* wsrc[D::W_PER];
+#pragma unroll
+  for (int i = 0; i < D::W_PER; ++i) {
+    const int q = i * 512 + tid, r = q / D::w_chunks, c = (q % D::w_chunks) ^ D::swz_w(r);
+    wsrc[i] = w + (size_t)(n0 + r) * w_row_bytes + c * 16;
+  }
+  const int kblocks = K / D::KS;
+  auto issue = [&](int kb) {
+    uint8_t* base = dl + (kb % NS) * D::stage + wave * 64 * 16;
+    const size_t xk = (size_t)kb * D::KS, wk = (size_t)kb * D::w_row;
+#pragma unroll
+    for (int i = 0; i < D::X_PER; ++i) lds_dma16(xsrc[i] + xk, base + i * 512 * 16);
+#pragma unroll
+    for (int i = 0; i < D::W_PER; ++i)
+      lds_dma16(wsrc[i] + wk, base + D::x_bytes + i * 512 * 16);
+  };
+
+  // fragment read offsets within a stage (bytes), per 64-K step; rows are
+  // lane-fixed, so their swizzles are too
+  const int ra = lane & 31;
+  int xoff[2][MT][2], woff[2][FNT][2];
+#pragma unroll
+  for (int st = 0; st < 2; ++st)
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+        xoff[st][i][u] =
+            (wm + i * 32 + ra) * D::KS + ((D::x_chunk(st, half, u) ^ D::swz_x(ra)) << 4);
+#pragma unroll
+      for (int j = 0; j < FNT; ++j)
+        woff[st][j][u] = D::x_bytes + (wn + j * 32 + ra) * D::w_row +
+                         ((D::w_chunk(st, half, u) ^ D::swz_w(ra)) << 4);
+    }
+
+  f32x16 acc[MT][FNT];
+#pragma unroll
+  for (int a = 0; a < MT; ++a)
+#pragma unroll
+    for (int b = 0; b < FNT; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.0f;
+
+  // one 64-K step's operands: x per M tile, W per N tile
+  struct Frags {
+    i32x8 a[MT];
+    i32x8 b[FNT];
+  };
+  auto cat = [](const u32x4& p, const u32x4& q) {
+    return __builtin_bit_cast(i32x8, (uint32_t __attribute__((ext_vector_type(8)))){
+                                         p[0], p[1], p[2], p[3], q[0], q[1], q[2], q[3]});
+  };
+  auto read = [&](Frags& f, int kb, const int st) {
+    const uint8_t* sb = dl + (kb % NS) * D::stage;
+#pragma unroll
+    for (int j = 0; j < FNT; ++j) {
+      const u32x4 p = *reinterpret_cast<const u32x4*>(sb + woff[st][j][0]);
+      u32x4 q = u32x4{0u, 0u, 0u, 0u};
+      if constexpr (D::w_chunks == 8) q = *reinterpret_cast<const u32x4*>(sb + woff[st][j][1]);
+      f.b[j] = cat(p, q);
+    }
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+      f.a[i] = cat(*reinterpret_cast<const u32x4*>(sb + xoff[st][i][0]),
+                   *reinterpret_cast<const u32x4*>(sb + xoff[st][i][1]));
+  };
+  auto multiply = [&](const Frags& f) {
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int j = 0; j < FNT; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+            f.a[i], f.b[j], acc[i][j], D::fmt_x, D::fmt, 0, 0, 0, 0);
+  };
+  // Wait until stage kb + 1 has landed (at most `ahead` later stages still
+  // in flight) and this wave's fragment reads are done, then the barrier:
+  // after it every wave's loads of stage kb + 1 are in LDS and every wave is
+  // done reading stage kb, whose slot the next load may overwrite.
+  auto wait_next = [&](int ahead) {
+    if (NS == 3 && ahead >= 1)
+      asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(D::L) : "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  };
+  // Stage kb in two 64-K steps: step 0's fragments were read one step
+  // earlier; read step 1's and multiply step 0; then (wait for stage kb + 1,
+  // barrier, refill stage kb's slot with stage kb + NS) read stage kb + 1's
+  // step 0 and multiply step 1.  The loop runs while a next stage exists, so
+  // its body has no branch around the reads (a join there costs a full LDS
+  // wait).
+  Frags f0, f1;
+#pragma unroll
+  for (int k = 0; k < NS; ++k)
+    if (k < kblocks) issue(k);
+  {
+    const int ahead = min(NS - 1, kblocks - 1);  // stages in flight beyond stage 0
+    if (ahead >= 2) asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(2 * D::L) : "memory");
+    else if (ahead == 1) asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(D::L) : "memory");
+    else asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+  }
+  read(f0, 0, 0);
+  int kb = 0;
+  for (; kb + 1 < kblocks; ++kb) {
+    read(f1, kb, 1);
+    multiply(f0);
+    wait_next(min(NS - 2, kblocks - 2 - kb));
+    if (kb + NS < kblocks) issue(kb + NS);
+    read(f0, kb + 1, 0);
+    multiply(f1);
+  }
+  read(f1, kb, 1);
+  multiply(f0);
+  multiply(f1);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  const float s = product_scale(w_scale, x_scale);
+  const float inv_o = epi_inv_scale(ep);
+  uint32_t am = 0;
+#pragma unroll
+  for (int j = 0; j < FNT; ++j) {
+    const int col = n0 + wn + j * 32 + (lane & 31);
+    const EpiChan k = epi_chan(ep, col);
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+        const float v = epi_value(ep, k, acc[i][j][r], s);
+        if (ep.amax) am = epi_track(am, v);
+        if (ep.out_dtype == F32)
+          __builtin_nontemporal_store(v, reinterpret_cast<float*>(y) + (size_t)row * N + col);
+        else
+          epi_store(ep.out_dtype, y, (size_t)row * N + col, v, inv_o);
+      }
+    }
+  }
+  epi_amax_commit(ep, am);
+}
+
+template <int WT, int XT>
+int launch_f8(const uint8_t* x, const float* x_scale, int64_t M, int64_t K, const uint8_t* w,
+              const float* w_scale, const Epilogue& ep, int64_t N, void* y, hipStream_t stream) {
+  using D = F8<WT, XT>;
+  static bool lds_raised = false;
+  if (!lds_raised) {
+    const hipError_t e = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(&linear_f8_kernel<WT, XT>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, D::lds);
+    if (e != hipSuccess) return hip_fail(e);
+    lds_raised = true;
+  }
+  const int64_t tiles_m = M / BM, tiles_n = N / 256;
+  hipLaunchKernelGGL((linear_f8_kernel<WT, XT>), dim3((unsigned)(tiles_m * tiles_n)), dim3(512),
+                     D::lds, stream, x, x_scale, w, w_scale, ep, y, (int)M, (int)N, (int)K,
+                     (int)tiles_m, (int)tiles_n);
+  return check_launch();
+}
+
 template <int WT, int XT>
 int launch(const uint8_t* x, const float* x_scale, int64_t M, int64_t K, const void* w,
            const float* w_scale, const Epilogue& ep, int64_t N, void* y, hipStream_t stream) {
@@ -699,6 +961,10 @@ int launch(const uint8_t* x, const float* x_scale, int64_t M, int64_t K, const v
   if (T > 0x7FFFFFFF || M > 0x7FFFFFFF || N > 0x7FFFFFFF || K > 0x7FFFFFFF) return NOVAQ_EINVAL;
   const auto* wq = static_cast<const uint8_t*>(w);
   const bool rows_whole = M % BM == 0 && K > 0;
+  if constexpr (dtype_bits(WT) <= 8 && (XT == E4M3 || XT == E5M2)) {
+    if (rows_whole && N % 256 == 0 && K % F8<WT, XT>::KS == 0)
+      return launch_f8<WT, XT>(x, x_scale, M, K, wq, w_scale, ep, N, y, stream);
+  }
   if constexpr (dtype_bits(WT) <= 8) {
     // tile byte sizes (BM * K * bytes(x) for x) must fit the 31-bit buffer range
     if (rows_whole && N % 256 == 0 && K % 128 == 0 && K <= (1 << 21)) {

@@ -292,9 +292,12 @@ def linear_x(xd, xt, sx, N, D_in, wd, wdt, ws, D_out, bias):
 @pytest.mark.parametrize("xt", ["bf16", "f16", "e4m3", "e5m2"])
 @pytest.mark.parametrize("wdt,N,D_in,D_out", LINEAR_CASES)
 def test_linear_reads_stored_activations(xt, wdt, N, D_in, D_out):
-    """A product on x stored as xt equals, bit for bit, the fp32-input product
-    on the decoded x with the scale folded into the weight scale (the bf16
-    operands and the fp32 epilogue are the same)."""
+    """A product on x stored as xt equals the fp32-input product on the
+    decoded x with the scale folded into the weight scale: bit for bit for
+    bf16 / f16 x (the same operands and order).  FP8 x on the FP8 product path
+    multiplies its codes directly: the same exact products, summed by the
+    FP8 MFMA (whose sums are not rounded as fp32 additions are: ~1e-5
+    normwise at these sizes), so within 1e-4."""
     print(f"linear x={xt} {wdt} {N}x{D_in}x{D_out}", flush=True)
     rng = np.random.default_rng(N * 3 + D_in + D_out)
     x = rng.standard_normal((N, D_in)).astype(np.float32)
@@ -305,7 +308,14 @@ def test_linear_reads_stored_activations(xt, wdt, N, D_in, D_out):
     got = linear_x(xd, xt, sx, N, D_in, wd, wdt, ws, D_out, bias)
     want = linear_x(torch.from_numpy(np.ascontiguousarray(xdec)).cuda(), "f32", None, N, D_in,
                     wd, wdt, combined_scale(ws, sx), D_out, bias)
-    assert np.array_equal(got, want)
+    fp8_path = (xt in ("e4m3", "e5m2") and wdt in ("e4m3", "e5m2", "e2m1") and N % 128 == 0
+                and D_out % 256 == 0 and D_in % 128 == 0)
+    if fp8_path:
+        g, r = got.view(np.float32).astype(np.float64), want.view(np.float32).astype(np.float64)
+        err = np.abs(g - r).max() / np.abs(r).max()
+        assert err <= 1e-4, err
+    else:
+        assert np.array_equal(got, want)
 
 
 def conv_x(xd, xt, sx, xs, wd, wdt, ws, wshape, stride, pad, mode, bias):

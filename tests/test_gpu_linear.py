@@ -196,3 +196,113 @@ def test_layer_shape_contracts_like_reference():
     out = layer(x)
     ref = x.astype(np.float64) @ layer.weight.data.T.astype(np.float64)
     assert normwise(out, ref) <= TOL
+
+
+# ---------------------------------------------------------------------------
+
+def identity_e4m3(n, rows=None):
+    """E4M3 codes of an (rows, n) weight whose first n rows are I (1.0 =
+    0x38) and the rest zero."""
+    rows = n if rows is None else rows
+    codes = np.zeros(rows * n, np.uint8)
+    codes[: n * n : n + 1] = 0x38
+    return codes
+
+
+def test_identity_weight_reproduces_bf16_rounded_input():
+    """W = I: y = x rounded to bf16 (nearest even) exactly, the operand the
+    bf16 product multiplies; rows holding Inf or NaN give the IEEE results of
+    the fp32 product (Inf * 0 = NaN)."""
+    K = N = 256
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((128, K)).astype(np.float32)
+    x *= (2.0 ** rng.integers(-40, 41, size=(128, 1))).astype(np.float32)
+    x[1, 5] = np.inf
+    x[2, 7] = -np.inf
+    x[3, 9] = np.nan
+    x[4, 1], x[4, 2] = np.inf, -np.inf
+    y = run_linear(x, identity_e4m3(K), "e4m3", 1.0, None, N, K)
+    xb = O.cast(O.cast(x, O.F32, O.BF16), O.BF16, O.F32).reshape(x.shape)
+    with np.errstate(invalid="ignore"):
+        want = xb @ np.eye(K, dtype=np.float32)
+    assert np.array_equal(np.isnan(y), np.isnan(want))
+    fin = ~np.isnan(want)
+    assert np.array_equal(y[fin], want[fin])
+    assert np.array_equal(y[5:], xb[5:])
+
+
+@pytest.mark.parametrize("wdt", ["e4m3", "e5m2", "e2m1"])
+def test_wide_dynamic_range_vs_oracle(wdt):
+    """Rows whose magnitudes span 2^-60 .. 2^60, against the fp64 product,
+    each row on its own scale."""
+    rng = np.random.default_rng(11)
+    M, K, N = 256, 512, 512
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    x *= (2.0 ** rng.integers(-60, 61, size=(M, 1))).astype(np.float32)
+    w = (rng.standard_normal((N, K)) * np.sqrt(2.0 / K)).astype(np.float32)
+    q = quant.quantize(torch.from_numpy(w).cuda(), wdt)
+    codes = q.data.view(torch.uint8).cpu().numpy().reshape(-1)
+    s = float(q.scale.cpu().reshape(-1)[0])
+    y = run_linear(x, codes, wdt, s, None, N, K)
+    wd = dequant(codes, wdt, N * K, s).reshape(N, K).astype(np.float64)
+    r = x.astype(np.float64) @ wd.T
+    for i in range(M):
+        assert normwise(y[i : i + 1], r[i : i + 1]) <= TOL, i
+
+
+# ---------------------------------------------------------------------------
+# x stored as E4M3 / E5M2 (M % 128, N % 256, K % 128 with FP8 / FP4 weights):
+# the codes of both operands go to gfx950's FP8 MFMA as they are stored.
+
+def run_linear_x(xcodes, xdt, sx, M, K, codes, wdt, sw, N):
+    xd = to_dev(xcodes, QCODE[xdt])
+    wd = to_dev(codes, QCODE[wdt])
+    sxd = torch.tensor([sx], dtype=torch.float32, device="cuda")
+    swd = torch.tensor([sw], dtype=torch.float32, device="cuda")
+    yd = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    _lib.check(_lib.load().novaq_linear_forward_ex(
+        xd.data_ptr(), _lib.DTYPES[xdt], sxd.data_ptr(), M, K, wd.data_ptr(), _lib.DTYPES[wdt],
+        swd.data_ptr(), None, N, None, yd.data_ptr(), torch.cuda.current_stream().cuda_stream),
+        "linear_ex")
+    torch.cuda.synchronize()
+    return yd.cpu().numpy()
+
+
+@pytest.mark.parametrize("xdt", ["e4m3", "e5m2"])
+def test_fp8_x_identity_weight_exact(xdt):
+    """W = I: y = s_x * dec(x) exactly for every code of x, Inf and NaN codes
+    (E5M2) included, with the IEEE results of the fp32 product (Inf * 0 =
+    NaN in the other columns of the row)."""
+    K = N = 256
+    M = 256
+    rng = np.random.default_rng(5)
+    xc = rng.integers(0, 256, size=M * K, dtype=np.uint8)
+    xc[:256] = np.arange(256, dtype=np.uint8)  # every code
+    sx = 0.375
+    y = run_linear_x(xc, xdt, sx, M, K, identity_e4m3(K), "e4m3", 1.0, N)
+    xv = (O.cast(xc, QCODE[xdt], O.F32).astype(np.float32) * np.float32(sx)).reshape(M, K)
+    with np.errstate(invalid="ignore"):
+        want = xv @ np.eye(K, dtype=np.float32)
+    assert np.array_equal(np.isnan(y), np.isnan(want))
+    fin = ~np.isnan(want)
+    assert np.array_equal(y[fin], want[fin])
+
+
+@pytest.mark.parametrize("xdt", ["e4m3", "e5m2"])
+@pytest.mark.parametrize("wdt", ["e4m3", "e5m2", "e2m1"])
+def test_fp8_x_vs_oracle(xdt, wdt):
+    """Quantized activations times quantized weights, against the fp64
+    product of the two dequantized operands, with a bias."""
+    rng = np.random.default_rng(17)
+    M, K, N = 256, 768, 512
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    w = (rng.standard_normal((N, K)) * np.sqrt(2.0 / K)).astype(np.float32)
+    qx = quant.quantize(torch.from_numpy(x).cuda(), xdt)
+    qw = quant.quantize(torch.from_numpy(w).cuda(), wdt)
+    xc = qx.data.view(torch.uint8).cpu().numpy().reshape(-1)
+    wc = qw.data.view(torch.uint8).cpu().numpy().reshape(-1)
+    sx, sw = float(qx.scale.cpu().reshape(-1)[0]), float(qw.scale.cpu().reshape(-1)[0])
+    y = run_linear_x(xc, xdt, sx, M, K, wc, wdt, sw, N)
+    xd = dequant(xc, xdt, M * K, sx).reshape(M, K).astype(np.float64)
+    wd = dequant(wc, wdt, N * K, sw).reshape(N, K).astype(np.float64)
+    assert normwise(y, xd @ wd.T) <= 1e-4
