@@ -107,63 +107,143 @@ __device__ __forceinline__ void take_max(uint32_t c, float v, uint32_t& best, fl
   }
 }
 
+// n / d for n < 2^31 by a multiply and a shift (Granlund and Montgomery,
+// "Division by invariant integers using multiplication", 1994): with
+// l = ceil(log2 d) and m = floor(2^32 (2^l - d) / d) + 1, n / d =
+// (mulhi(n, m) + n) >> l; the sum stays below 2^32 because n < 2^31.
+struct FastDiv {
+  uint32_t m;
+  int l;
+};
+
+FastDiv fast_div(uint32_t d) {
+  FastDiv f;
+  f.l = 0;
+  while (((uint64_t)1 << f.l) < d) ++f.l;
+  f.m = (uint32_t)((((uint64_t)1 << 32) * (((uint64_t)1 << f.l) - d)) / d + 1);
+  return f;
+}
+
+__device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) {
+  return (__umulhi(n, f.m) + n) >> f.l;
+}
+
 // 2-wide windows with stride 2 along W and no W padding (MaxPool2d(2, 2) and
-// its (k, 2) / (k, 2) relatives): a lane makes the two adjacent outputs
+// its (k, 2) / (k, 2) relatives): an item makes the two adjacent outputs
 // 2u, 2u+1 of one output row from 4 consecutive inputs per window row, read
-// with one 16 / 8 / 4-byte load when W is a multiple of 4.
-template <int XT>
+// with one 16 / 8 / 4-byte load when W is a multiple of 4.  Items t (planes
+// of OH x ceil(OW/2) back to back, t < 2^31) go two per lane per step, grid-
+// strided, all their window rows' loads issued before the first compare
+// (KH2: the 2-row window, unrolled).
+template <int XT, bool KH2>
 __global__ __launch_bounds__(256) void max_pool2d_w2_kernel(const uint8_t* __restrict__ x,
-                                                           uint8_t* __restrict__ y, PoolGeom g) {
+                                                           uint8_t* __restrict__ y, PoolGeom g,
+                                                           FastDiv dper, FastDiv dou,
+                                                           uint32_t total) {
   const int OU = (g.OW + 1) / 2;  // output pairs per row
-  const int per = g.OH * OU;
-  const int64_t t0 = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (t0 >= g.N * g.C * per) return;
-  const int64_t plane = t0 / per;
-  const int item = (int)(t0 - plane * per);
-  const int oh = item / OU, u = item - oh * OU;
-  const int64_t base = plane * g.H * g.W;
-  const bool two = 2 * u + 1 < g.OW;
+  const uint32_t per = (uint32_t)(g.OH * OU);
   const bool vec = (g.W & 3) == 0;
+  const bool pair_store = (g.OW & 1) == 0;
   constexpr int B = XL<XT>::bits;
-  uint32_t best[2] = {0u, 0u};
-  float bv[2] = {0.0f, 0.0f};
-  for (int kh = 0; kh < g.KH; ++kh) {
-    const int hi = pool_pad_index(oh * g.sh + kh - g.ph, g.H, g.pad_mode);
-    uint32_t c[4] = {0u, 0u, 0u, 0u};  // the zero padding's +0
-    if (hi >= 0) {
-      const int64_t e = base + (int64_t)hi * g.W + 4 * u;
-      if (vec) {
-        const xl_u32x4 r = x4_raw<XT>(x, e);
+  constexpr int KR = KH2 ? 2 : 1;  // window rows loaded at once
+  const uint32_t stride = gridDim.x * 256u;
+  struct Item {
+    bool live, two;
+    int oh;
+    int64_t base, out;
+    int u;
+  };
+  auto locate = [&](uint32_t t) {
+    Item it;
+    it.live = t < total;
+    const uint32_t plane = fdiv(t, dper), item = t - plane * per;
+    it.oh = (int)fdiv(item, dou);
+    it.u = (int)item - it.oh * OU;
+    it.base = (int64_t)plane * g.H * g.W;
+    it.out = (int64_t)plane * g.OH * g.OW + (int64_t)it.oh * g.OW + 2 * it.u;
+    it.two = 2 * it.u + 1 < g.OW;
+    return it;
+  };
+  auto load = [&](const Item& it, int kh, uint32_t* c) {
+    c[0] = c[1] = c[2] = c[3] = 0u;  // the zero padding's +0
+    if (!it.live) return;
+    const int hi = pool_pad_index(it.oh * g.sh + kh - g.ph, g.H, g.pad_mode);
+    if (hi < 0) return;
+    const int64_t e = it.base + (int64_t)hi * g.W + 4 * it.u;
+    if (vec) {
+      const xl_u32x4 r = x4_raw<XT>(x, e);
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-          c[q] = B == 32 ? r[q] : (r[(q * B) / 32] >> ((q * B) % 32)) & ((1u << (B & 31)) - 1u);
-      } else {
-        c[0] = x_code<XT>(x, e);
-        c[1] = x_code<XT>(x, e + 1);
-        if (two) {
-          c[2] = x_code<XT>(x, e + 2);
-          c[3] = x_code<XT>(x, e + 3);
-        }
+      for (int q = 0; q < 4; ++q)
+        c[q] = B == 32 ? r[q] : (r[(q * B) / 32] >> ((q * B) % 32)) & ((1u << (B & 31)) - 1u);
+    } else {
+      c[0] = x_code<XT>(x, e);
+      c[1] = x_code<XT>(x, e + 1);
+      if (it.two) {
+        c[2] = x_code<XT>(x, e + 2);
+        c[3] = x_code<XT>(x, e + 3);
       }
     }
+  };
+  auto fold = [&](const uint32_t* c, bool first, uint32_t* best, float* bv) {
 #pragma unroll
-    for (int o = 0; o < 2; ++o) {
+    for (int o = 0; o < 2; ++o)
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
         const uint32_t code = c[2 * o + q];
         const float v = u2f(decode<XT>(code));
-        if (kh == 0 && q == 0) {
+        if (first && q == 0) {
           best[o] = code;
           bv[o] = v;
         } else {
           take_max(code, v, best[o], bv[o]);
         }
       }
+  };
+  auto store = [&](const Item& it, const uint32_t* best) {
+    if (!it.live) return;
+    if (it.two && pair_store) {
+      if constexpr (B == 32) {
+        *reinterpret_cast<uint2*>(reinterpret_cast<uint32_t*>(y) + it.out) =
+            make_uint2(best[0], best[1]);
+      } else if constexpr (B == 16) {
+        reinterpret_cast<uint32_t*>(y)[it.out >> 1] = best[0] | (best[1] << 16);
+      } else {
+        reinterpret_cast<uint16_t*>(y)[it.out >> 1] = (uint16_t)(best[0] | (best[1] << 8));
+      }
+    } else {
+      store_code<XT>(y, it.out, best[0]);
+      if (it.two) store_code<XT>(y, it.out + 1, best[1]);
     }
+  };
+  constexpr int IT = 2;  // items per lane per step
+  for (uint32_t t = blockIdx.x * 256u + threadIdx.x; t < total; t += IT * stride) {
+    Item it[IT];
+    uint32_t best[IT][2];
+    float bv[IT][2];
+#pragma unroll
+    for (int k = 0; k < IT; ++k) {
+      // t + k * stride < 2^31 + IT * 2^31 would wrap; items past the end are
+      // dead (locate's division needs n < 2^31)
+      const uint64_t tk = (uint64_t)t + (uint64_t)k * stride;
+      it[k] = locate(tk < total ? (uint32_t)tk : 0u);
+      it[k].live = tk < total;
+      best[k][0] = best[k][1] = 0u;
+      bv[k][0] = bv[k][1] = 0.0f;
+    }
+    for (int kh0 = 0; kh0 < g.KH; kh0 += KR) {
+      uint32_t c[IT][KR][4];
+#pragma unroll
+      for (int r = 0; r < KR; ++r)
+#pragma unroll
+        for (int k = 0; k < IT; ++k) load(it[k], kh0 + r, c[k][r]);
+#pragma unroll
+      for (int r = 0; r < KR; ++r)
+#pragma unroll
+        for (int k = 0; k < IT; ++k) fold(c[k][r], kh0 + r == 0, best[k], bv[k]);
+    }
+#pragma unroll
+    for (int k = 0; k < IT; ++k) store(it[k], best[k]);
   }
-  const int64_t t = plane * g.OH * g.OW + (int64_t)oh * g.OW + 2 * u;
-  store_code<XT>(y, t, best[0]);
-  if (two) store_code<XT>(y, t + 1, best[1]);
 }
 
 template <int XT>
@@ -371,12 +451,21 @@ int launch_max(const void* x, void* y, const PoolGeom& g, hipStream_t stream) {
   const int64_t npix = (int64_t)g.OH * g.OW;
   if (npix > 0x7FFFFFFF) return NOVAQ_EINVAL;
   if (g.KW == 2 && g.sw == 2 && g.pw == 0) {
-    const int64_t items = g.N * g.C * (int64_t)g.OH * ((g.OW + 1) / 2);
-    const int64_t blocks = (items + 255) / 256;
-    if (blocks > 0x7FFFFFFF) return NOVAQ_EINVAL;
-    hipLaunchKernelGGL(max_pool2d_w2_kernel<XT>, dim3((unsigned)blocks), dim3(256), 0, stream,
-                       static_cast<const uint8_t*>(x), static_cast<uint8_t*>(y), g);
-    return check_launch();
+    const int64_t per = (int64_t)g.OH * ((g.OW + 1) / 2);
+    const int64_t items = g.N * g.C * per;
+    if (items < ((int64_t)1 << 31)) {
+      // two items per lane per step, about 8 workgroups per CU
+      int64_t blocks = (items + 511) / 512;
+      const int64_t cap = (int64_t)device_cu_count() * 8;
+      if (blocks > cap) blocks = cap;
+      if (blocks < 1) blocks = 1;
+      const FastDiv dper = fast_div((uint32_t)per), dou = fast_div((uint32_t)((g.OW + 1) / 2));
+      auto kern = g.KH == 2 ? max_pool2d_w2_kernel<XT, true> : max_pool2d_w2_kernel<XT, false>;
+      hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), 0, stream,
+                         static_cast<const uint8_t*>(x), static_cast<uint8_t*>(y), g, dper, dou,
+                         (uint32_t)items);
+      return check_launch();
+    }
   }
   const int64_t blocks = (g.N * g.C * npix + 255) / 256;
   if (blocks > 0x7FFFFFFF) return NOVAQ_EINVAL;
