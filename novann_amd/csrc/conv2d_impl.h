@@ -721,7 +721,7 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       const int co = co0 + t * 16 + lr;
-      kc[t] = (t < nt_live && co < g.C_out) ? epi_chan(ep, co) : EpiChan{0.0f, 1.0f, 0.0f};
+      kc[t] = (t < nt_live && co < g.C_out) ? epi_chan(ep, co) : EpiChan{0.0f, 1.0f, -0.0f};
     }
     if (plain) {
 #pragma unroll
@@ -749,7 +749,9 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
       }
       return;
     }
-    // the epilogue, with the output dtype fixed per copy of the loop
+    // the epilogue, with the output dtype fixed per copy of the loop and no
+    // branch on the epilogue's fields per element
+    const float z = epi_relu_factor(ep);
     auto store_all = [&](auto od) {
       constexpr int OD = decltype(od)::value;
 #pragma unroll
@@ -764,8 +766,8 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
           float v[4];
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            v[i] = epi_value(ep, kc[t], acc[m][t][i], s);
-            if (ep.amax && p + i < P) am = epi_track(am, v[i]);
+            v[i] = epi_value_nb(kc[t], acc[m][t][i], s, z);
+            if (p + i < P) am = epi_track(am, v[i]);  // committed only with ep.amax
           }
           if (p + 3 < P && (di & 3) == 0) {
             epi_store4_t<OD>(y, di, v, inv_o);

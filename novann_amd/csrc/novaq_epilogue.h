@@ -42,11 +42,12 @@ struct EpiChan {
   float bias, mul, add;
 };
 
+// (an absent mul / add is 1 / -0: the identities epi_value_nb relies on)
 __device__ __forceinline__ EpiChan epi_chan(const Epilogue& e, int c) {
   EpiChan k;
   k.bias = e.bias ? e.bias[c] : 0.0f;
   k.mul = e.mul ? e.mul[c] : 1.0f;
-  k.add = e.add ? e.add[c] : 0.0f;
+  k.add = e.add ? e.add[c] : -0.0f;
   return k;
 }
 
@@ -62,6 +63,21 @@ __device__ __forceinline__ float epi_value(const Epilogue& e, const EpiChan& k, 
   if (e.add) v = v + k.add;
   if (e.relu) v = v * (v > 0.0f ? 1.0f : 0.0f);
   return v;
+}
+
+// epi_value without branches on the epilogue's fields: an absent step is an
+// exact identity (v * 1 = v and v + (-0) = v for every v, -0 and NaN
+// included; the ReLU factor is z = 1 when relu is off, 0 when on), so the
+// result has the same bits (NaN stays NaN).
+__device__ __forceinline__ float epi_relu_factor(const Epilogue& e) {
+  return e.relu ? 0.0f : 1.0f;
+}
+
+__device__ __forceinline__ float epi_value_nb(const EpiChan& k, float acc, float s, float z) {
+  float v = acc * s + k.bias;
+  v = v * k.mul;
+  v = v + k.add;
+  return v * (v > 0.0f ? 1.0f : z);
 }
 
 // Running max of |v| bits, NaN ignored (0 is the identity).
