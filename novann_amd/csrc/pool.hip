@@ -356,27 +356,63 @@ struct GapPlan {
   int2 leaf[GAP_MAX_LEAVES];  // (offset, length)
 };
 
-template <int XT>
+constexpr int GAP_STAGE = 2048;  // at most this many elements of a wave's planes staged in LDS
+
+// STAGED (a wave's planes hold at most GAP_STAGE elements): the wave first
+// copies its planes, which are contiguous in memory, into LDS with coalesced
+// loads (4 elements per load when the planes start on a multiple of 4),
+// decoded and scaled, and the leaf sums read them from there.
+template <int XT, bool STAGED>
 __global__ __launch_bounds__(256) void global_avg_pool2d_wave_kernel(
     const uint8_t* __restrict__ x, const float* __restrict__ x_scale, float* __restrict__ y,
     int64_t planes, int hw, GapPlan plan) {
   __shared__ float sums[4][GAP_MAX_LEAVES];
+  extern __shared__ float gap_stage[];  // STAGED: 4 waves x ppw * hw elements
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int L = plan.L;
   const int G = L < 8 ? L : 8;         // leaves per pass
   const int ppw = 64 / (8 * G);        // planes per wave
   const int pi = lane / (8 * G), rem = lane - pi * 8 * G;
   const int li = rem >> 3, j = rem & 7;
-  const int64_t plane = ((int64_t)blockIdx.x * 4 + wave) * ppw + pi;
+  const int64_t plane0 = ((int64_t)blockIdx.x * 4 + wave) * ppw;
+  const int64_t plane = plane0 + pi;
   const bool live = pi < ppw && plane < planes;
   const int64_t base = plane * hw;
   const bool scaled = x_scale != nullptr;
   const float s = scaled ? *x_scale : 1.0f;
+  if constexpr (STAGED) {
+    const int64_t left = planes - plane0;
+    const int np = left <= 0 ? 0 : (left < ppw ? (int)left : ppw);
+    const int n = np * hw;
+    const int64_t e0 = plane0 * hw;
+    float* st = gap_stage + wave * ppw * hw;
+    if ((e0 & 3) == 0) {
+      for (int g4 = lane; 4 * g4 < n; g4 += 64) {
+        const int64_t e = e0 + 4 * g4;
+        const xl_u32x4 r = 4 * g4 + 3 < n ? x4_raw<XT>(x, e) : x4_raw_guarded<XT>(x, e, e0 + n);
+        constexpr int B = XL<XT>::bits;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t c =
+              B == 32 ? r[q] : (r[(q * B) / 32] >> ((q * B) % 32)) & ((1u << (B & 31)) - 1u);
+          const float v = u2f(decode<XT>(c));
+          if (4 * g4 + q < n) st[4 * g4 + q] = scaled ? v * s : v;
+        }
+      }
+    } else {
+      for (int i = lane; i < n; i += 64) st[i] = elem<XT>(x, e0 + i, s, scaled);
+    }
+    __syncthreads();
+  }
+  // element i of leaf lt of this lane's plane
+  auto val = [&](const int2& lt, int i) {
+    if constexpr (STAGED) return gap_stage[(wave * ppw + pi) * hw + lt.x + i];
+    else return elem<XT>(x, base + lt.x + i, s, scaled);
+  };
   for (int p0 = 0; p0 < L; p0 += G) {
     const int leaf = p0 + li;
     const bool on = live && leaf < L;
     const int2 lt = on ? plan.leaf[leaf] : make_int2(0, 0);
-    const int64_t b = base + lt.x;
     const int main = lt.y - (lt.y & 7);
     // a leaf holds at most 16 groups of 8: every load of the lane goes out
     // before the in-order sum
@@ -384,7 +420,7 @@ __global__ __launch_bounds__(256) void global_avg_pool2d_wave_kernel(
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
       const int i = j + 8 * k;
-      v[k] = (on && i < main) ? elem<XT>(x, b + i, s, scaled) : 0.0f;
+      v[k] = (on && i < main) ? val(lt, i) : 0.0f;
     }
     float r = 0.0f;
     if (on && lt.y >= 8) {
@@ -402,7 +438,7 @@ __global__ __launch_bounds__(256) void global_avg_pool2d_wave_kernel(
       const int e0 = lt.y < 8 ? 0 : main;
       float t[7];
 #pragma unroll
-      for (int q = 0; q < 7; ++q) t[q] = e0 + q < lt.y ? elem<XT>(x, b + e0 + q, s, scaled) : 0.0f;
+      for (int q = 0; q < 7; ++q) t[q] = e0 + q < lt.y ? val(lt, e0 + q) : 0.0f;
       float res = lt.y < 8 ? 0.0f : r;
 #pragma unroll
       for (int q = 0; q < 7; ++q)
@@ -486,9 +522,12 @@ int launch_gap(const void* x, const float* x_scale, float* y, int64_t planes, in
     const int64_t waves = (planes + ppw - 1) / ppw;
     const int64_t blocks = (waves + 3) / 4;
     if (blocks > 0x7FFFFFFF) return NOVAQ_EINVAL;
-    hipLaunchKernelGGL(global_avg_pool2d_wave_kernel<XT>, dim3((unsigned)blocks), dim3(256), 0,
-                       stream, static_cast<const uint8_t*>(x), x_scale, y, planes, (int)hw,
-                       plan);
+    const bool staged = ppw * hw <= GAP_STAGE;
+    auto kern = staged ? global_avg_pool2d_wave_kernel<XT, true>
+                       : global_avg_pool2d_wave_kernel<XT, false>;
+    const size_t lds = staged ? (size_t)4 * ppw * hw * sizeof(float) : 0;
+    hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), lds, stream,
+                       static_cast<const uint8_t*>(x), x_scale, y, planes, (int)hw, plan);
     return check_launch();
   }
   const int64_t blocks = (planes + 255) / 256;
