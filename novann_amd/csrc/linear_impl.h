@@ -268,6 +268,54 @@ __global__ __launch_bounds__(THREADS, 1) void linear_kernel(
   epi_amax_commit(ep, am);
 }
 
+// Epilogue of a whole tile of 32 x 32 MFMA accumulators (acc[i][j]: rows
+// row0 + 32 i + 8 (r / 4) + 4 (lane / 32) + r % 4, column col0 + 32 j +
+// lane % 32): one copy of the store loop per output dtype and no branch on
+// the epilogue's fields per element (epi_value_nb, the same bits); fp32 goes
+// out with non-temporal stores.
+template <int OD, int MTn, int NTn>
+__device__ __forceinline__ uint32_t store_tile(const Epilogue& ep, const f32x16 (&acc)[MTn][NTn],
+                                               float s, float inv_o, float z, void* y, int N,
+                                               int row0, int col0, int lane) {
+  uint32_t am = 0;
+  const int half = lane >> 5;
+#pragma unroll
+  for (int j = 0; j < NTn; ++j) {
+    const int col = col0 + j * 32 + (lane & 31);
+    const EpiChan k = epi_chan(ep, col);
+#pragma unroll
+    for (int i = 0; i < MTn; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = row0 + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+        const float v = epi_value_nb(k, acc[i][j][r], s, z);
+        am = epi_track(am, v);  // committed only with ep.amax
+        if constexpr (OD == F32)
+          __builtin_nontemporal_store(v, reinterpret_cast<float*>(y) + (size_t)row * N + col);
+        else
+          epi_store_t<OD>(y, (size_t)row * N + col, v, inv_o);
+      }
+    }
+  }
+  return am;
+}
+
+template <int MTn, int NTn>
+__device__ __forceinline__ void tile_epilogue(const Epilogue& ep, const f32x16 (&acc)[MTn][NTn],
+                                              float s, void* y, int N, int row0, int col0,
+                                              int lane) {
+  const float inv_o = epi_inv_scale(ep), z = epi_relu_factor(ep);
+  uint32_t am;
+  switch (ep.out_dtype) {
+    case F16: am = store_tile<F16>(ep, acc, s, inv_o, z, y, N, row0, col0, lane); break;
+    case BF16: am = store_tile<BF16>(ep, acc, s, inv_o, z, y, N, row0, col0, lane); break;
+    case E4M3: am = store_tile<E4M3>(ep, acc, s, inv_o, z, y, N, row0, col0, lane); break;
+    case E5M2: am = store_tile<E5M2>(ep, acc, s, inv_o, z, y, N, row0, col0, lane); break;
+    default: am = store_tile<F32>(ep, acc, s, inv_o, z, y, N, row0, col0, lane); break;
+  }
+  epi_amax_commit(ep, am);
+}
+
 constexpr int A_PITCH = BK + 8;                      // bf16 per A row in LDS
 constexpr int A_STAGE = BM * A_PITCH * 2;            // bytes
 
@@ -471,28 +519,7 @@ __global__ __launch_bounds__(NW * 64, OCC) void linear_pipe_kernel(
     }
   }
 
-  const float s = product_scale(w_scale, x_scale);
-  const float inv_o = epi_inv_scale(ep);
-  uint32_t am = 0;
-#pragma unroll
-  for (int j = 0; j < FNT; ++j) {
-    const int col = n0 + wn + j * 32 + (lane & 31);
-    const EpiChan k = epi_chan(ep, col);
-#pragma unroll
-    for (int i = 0; i < MT; ++i) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-        const float v = epi_value(ep, k, acc[i][j][r], s);
-        if (ep.amax) am = epi_track(am, v);
-        if (ep.out_dtype == F32)
-          __builtin_nontemporal_store(v, reinterpret_cast<float*>(y) + (size_t)row * N + col);
-        else
-          epi_store(ep.out_dtype, y, (size_t)row * N + col, v, inv_o);
-      }
-    }
-  }
-  epi_amax_commit(ep, am);
+  tile_epilogue(ep, acc, product_scale(w_scale, x_scale), y, N, m0 + wm, n0 + wn, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -670,28 +697,7 @@ __global__ __launch_bounds__(512, 1) void linear_wide_kernel(
     if (kb + 1 < kblocks) body(kb + 1, 1, r1, r0);
   }
 
-  const float s = product_scale(w_scale, x_scale);
-  const float inv_o = epi_inv_scale(ep);
-  uint32_t am = 0;
-#pragma unroll
-  for (int j = 0; j < FNT; ++j) {
-    const int col = n0 + wn + j * 32 + (lane & 31);
-    const EpiChan k = epi_chan(ep, col);
-#pragma unroll
-    for (int i = 0; i < MT; ++i) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-        const float v = epi_value(ep, k, acc[i][j][r], s);
-        if (ep.amax) am = epi_track(am, v);
-        if (ep.out_dtype == F32)
-          __builtin_nontemporal_store(v, reinterpret_cast<float*>(y) + (size_t)row * N + col);
-        else
-          epi_store(ep.out_dtype, y, (size_t)row * N + col, v, inv_o);
-      }
-    }
-  }
-  epi_amax_commit(ep, am);
+  tile_epilogue(ep, acc, product_scale(w_scale, x_scale), y, N, m0 + wm, n0 + wn, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -910,28 +916,7 @@ __global__ __launch_bounds__(512, 1) void linear_f8_kernel(
   multiply(f1);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-  const float s = product_scale(w_scale, x_scale);
-  const float inv_o = epi_inv_scale(ep);
-  uint32_t am = 0;
-#pragma unroll
-  for (int j = 0; j < FNT; ++j) {
-    const int col = n0 + wn + j * 32 + (lane & 31);
-    const EpiChan k = epi_chan(ep, col);
-#pragma unroll
-    for (int i = 0; i < MT; ++i) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = m0 + wm + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-        const float v = epi_value(ep, k, acc[i][j][r], s);
-        if (ep.amax) am = epi_track(am, v);
-        if (ep.out_dtype == F32)
-          __builtin_nontemporal_store(v, reinterpret_cast<float*>(y) + (size_t)row * N + col);
-        else
-          epi_store(ep.out_dtype, y, (size_t)row * N + col, v, inv_o);
-      }
-    }
-  }
-  epi_amax_commit(ep, am);
+  tile_epilogue(ep, acc, product_scale(w_scale, x_scale), y, N, m0 + wm, n0 + wn, lane);
 }
 
 template <int WT, int XT>
