@@ -365,10 +365,16 @@ struct RowsGeom {
                                            // (bf16), stages per image
 };
 
-template <int XJ>
-__global__ __launch_bounds__(1024) void dweight_rows_kernel(
+// MODE 0: grad_weight; 1: grad_weight and grad_bias; 2: grad_bias only (no x,
+// no products).  grad_bias: each lane adds the grad values it loads per
+// channel in stage order, the wave then adds its 64 lanes in a fixed
+// butterfly, and c block 0 writes the chunk's per-channel sum to bpart.
+template <int XJ, int MODE>
+__global__ __launch_bounds__(768) void dweight_rows_kernel(
     const float* __restrict__ grad, const float* __restrict__ x, float* __restrict__ part,
-    BwdGeom g, RowsGeom rg, int chunks, int co_blocks, int c_blocks) {
+    float* __restrict__ bpart, BwdGeom g, RowsGeom rg, int chunks, int co_blocks,
+    int c_blocks) {
+  constexpr bool WGT = MODE != 2, BIAS = MODE != 0;
   extern __shared__ __attribute__((aligned(16))) uint8_t dr_lds[];
   constexpr int GP = DR_K + 8;  // Gs row pitch (bf16); slot DR_K takes masked lanes
   __bf16* Gs = reinterpret_cast<__bf16*>(dr_lds);
@@ -395,10 +401,11 @@ __global__ __launch_bounds__(1024) void dweight_rows_kernel(
     for (int r = 0; r < 16; ++r) acc[i][r] = 0.0f;
 
   // Gs padding columns (ow >= OW) are zeroed once and never written again.
-  {
+  if constexpr (WGT) {
     uint32_t* z = reinterpret_cast<uint32_t*>(dr_lds);
     for (int i = tid; i < 64 * GP / 2; i += nthreads) z[i] = 0u;
   }
+  float bsum[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
   // Gs slot j of this lane: grad value m = lane + 64 j of the band, its row
   // and Gs column (DR_K when m is past the band)
   int gr[2], gk[2];
@@ -458,6 +465,7 @@ __global__ __launch_bounds__(1024) void dweight_rows_kernel(
     }
 #pragma unroll
     for (int k = 0; k < 4 * XJ; ++k) {
+      if constexpr (!WGT) break;
       const int c_l = tap + (k / XJ) * rg.taps;
       const uint32_t coff = (c_l < 32 && c0 + c_l < g.C)
                                 ? (uint32_t)(c0 + c_l) * (uint32_t)HW * 4u : 0x40000000u;
@@ -466,9 +474,21 @@ __global__ __launch_bounds__(1024) void dweight_rows_kernel(
     }
   };
 
-  if (t_begin < t_end) load_stage(t_begin);
-  for (int64_t t = t_begin; t < t_end; ++t) {
+  if constexpr (!WGT) {
+    // grad_bias only: the stages' grad values, no LDS and no products
+    for (int64_t t = t_begin; t < t_end; ++t) {
+      load_stage(t);
+#pragma unroll
+      for (int k = 0; k < 16; ++k) bsum[k >> 1] += gv[k];
+    }
+  }
+  if (WGT && t_begin < t_end) load_stage(t_begin);
+  for (int64_t t = t_begin; WGT && t < t_end; ++t) {
     __syncthreads();  // the previous stage's fragment reads are done
+    if constexpr (BIAS) {
+#pragma unroll
+      for (int k = 0; k < 16; ++k) bsum[k >> 1] += gv[k];
+    }
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
       const int co_l = tap + (k >> 1) * rg.taps;
@@ -504,6 +524,19 @@ __global__ __launch_bounds__(1024) void dweight_rows_kernel(
       }
     }
   }
+  if constexpr (BIAS) {
+    // channel co_l = tap + c * taps of this wave: the wave's 64 lanes added
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      float v = bsum[c];
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+      const int co_l = tap + c * rg.taps;
+      if (cb == 0 && lane == 0 && co_l < 64 && co0 + co_l < g.C_out)
+        bpart[(int64_t)chunk * g.C_out + co0 + co_l] = v;
+    }
+  }
+  if constexpr (!WGT) return;
   // lane holds input channel c0 + (lane & 31), output channel rows
   // 8*(r/4) + 4*half + r%4 of tile i; the partial is stored as
   // [chunk][tap][co][c] (a half-wave writes 32 consecutive c), which the
@@ -519,13 +552,14 @@ __global__ __launch_bounds__(1024) void dweight_rows_kernel(
     }
 }
 
-constexpr int DR_MAX_XJ = 8;
+constexpr int DR_MAX_XJ = 5;
 
 // The stride-1 rows path applies (its LDS bytes and slots per lane XJ), or 0.
 size_t rows_geometry(const BwdGeom& g, RowsGeom& rg, int& xj) {
   const int taps = g.KH * g.KW;
   // (fewer than 16 input channels leave most of the 32-channel tile idle)
-  if (g.sh != 1 || g.sw != 1 || taps < 8 || taps > 16 || g.KW > 8 || g.OW > 64 || g.C < 16)
+  // (at most 12 taps: 12 waves keep ~170 VGPRs a wave)
+  if (g.sh != 1 || g.sw != 1 || taps < 8 || taps > 12 || g.KW > 8 || g.OW > 64 || g.C < 16)
     return 0;
   // 32-bit buffer offsets: an image's grad and input stay below 1 GiB
   if ((int64_t)g.C_out * g.OH * g.OW * 4 >= (1 << 30) || (int64_t)g.C * g.H * g.W * 4 >= (1 << 30))
@@ -540,7 +574,7 @@ size_t rows_geometry(const BwdGeom& g, RowsGeom& rg, int& xj) {
   rg.cp = xslots + 2;  // odd dword pitch; slot xslots is the spare
   rg.spi = (g.OH + rg.R - 1) / rg.R;
   xj = (xslots + 63) / 64;
-  if (xj < 2 || xj > DR_MAX_XJ) return 0;
+  if (xj < 2 || xj > DR_MAX_XJ) return 0;  // (more slots per lane spill registers)
   const size_t bytes = (size_t)64 * (DR_K + 8) * 2 + (size_t)32 * rg.cp * 2;
   return bytes <= 150 * 1024 ? bytes : 0;
 }
@@ -639,44 +673,55 @@ int conv2d_backward_launch(const float* grad, const float* x, int64_t N, int64_t
   }
   const int64_t ckk = C * KH * KW;
   if (!grad_weight && !grad_bias) return rc;
-  // stride-1 convolutions with short rows: grad_weight on the rows kernel, and
-  // grad_bias (when asked) on dweight_kernel's bias-only pass, whose bits a
-  // bias-only call reproduces
+  // stride-1 convolutions with short rows: grad_weight and grad_bias on the
+  // rows kernel (a bias-only call runs its bias-only mode over the same
+  // chunks, so its bits match a full call's)
   RowsGeom rg{};
   int xj = 0;
-  const size_t rows_lds = grad_weight ? rows_geometry(g, rg, xj) : 0;
+  const size_t rows_lds = rows_geometry(g, rg, xj);
   if (rows_lds) {
     float* part = reinterpret_cast<float*>(base + ws.part);
+    float* bpart = reinterpret_cast<float*>(base + ws.bpart);
     const int64_t co_blocks = (C_out + 63) / 64, c_blocks = (C + 31) / 32;
     const int64_t units = (int64_t)g.N * rg.spi;
     // about one workgroup per CU: the chunk partials cost HBM traffic
     int64_t rchunks = std::max<int64_t>(1, device_cu_count() / (co_blocks * c_blocks));
     rchunks = std::min<int64_t>(std::min<int64_t>(rchunks, ws.chunks), std::max<int64_t>(units, 1));
-    const int64_t blocks = rchunks * co_blocks * c_blocks;
+    const int mode = grad_weight ? (grad_bias ? 1 : 0) : 2;
+    const int64_t blocks = rchunks * co_blocks * (mode == 2 ? 1 : c_blocks);
     if (blocks > 0x7FFFFFFF) return NOVAQ_EINVAL;
-    using RowsKernel = void (*)(const float*, const float*, float*, BwdGeom, RowsGeom, int, int,
-                                int);
-    static const RowsKernel kerns[DR_MAX_XJ + 1] = {
-        nullptr, nullptr, dweight_rows_kernel<2>, dweight_rows_kernel<3>, dweight_rows_kernel<4>,
-        dweight_rows_kernel<5>, dweight_rows_kernel<6>, dweight_rows_kernel<7>,
-        dweight_rows_kernel<8>};
-    static bool lds_raised[DR_MAX_XJ + 1] = {};
-    const RowsKernel kern = kerns[xj];
-    if (!lds_raised[xj]) {
-      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                               hipFuncAttributeMaxDynamicSharedMemorySize,
-                                               150 * 1024);
-      if (e != hipSuccess) return hip_fail(e);
-      lds_raised[xj] = true;
+    using RowsKernel = void (*)(const float*, const float*, float*, float*, BwdGeom, RowsGeom,
+                                int, int, int);
+    static const RowsKernel kerns[2][DR_MAX_XJ + 1] = {
+        {nullptr, nullptr, dweight_rows_kernel<2, 0>, dweight_rows_kernel<3, 0>,
+         dweight_rows_kernel<4, 0>, dweight_rows_kernel<5, 0>},
+        {nullptr, nullptr, dweight_rows_kernel<2, 1>, dweight_rows_kernel<3, 1>,
+         dweight_rows_kernel<4, 1>, dweight_rows_kernel<5, 1>}};
+    static bool lds_raised[2][DR_MAX_XJ + 1] = {};
+    if (mode == 2) {
+      hipLaunchKernelGGL((dweight_rows_kernel<2, 2>), dim3((unsigned)blocks), dim3(rg.taps * 64),
+                         0, stream, grad, x, part, bpart, g, rg, (int)rchunks, (int)co_blocks, 1);
+    } else {
+      const RowsKernel kern = kerns[mode][xj];
+      if (!lds_raised[mode][xj]) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 150 * 1024);
+        if (e != hipSuccess) return hip_fail(e);
+        lds_raised[mode][xj] = true;
+      }
+      hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(rg.taps * 64), rows_lds, stream, grad,
+                         x, part, bpart, g, rg, (int)rchunks, (int)co_blocks, (int)c_blocks);
     }
-    hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(rg.taps * 64), rows_lds, stream, grad,
-                       x, part, g, rg, (int)rchunks, (int)co_blocks, (int)c_blocks);
     rc = check_launch();
     if (rc != NOVAQ_OK) return rc;
-    rc = colsum_launch(part, rchunks, C_out * ckk, grad_weight, stream, (int)rg.taps, (int)C_out,
-                       (int)C);
-    if (rc != NOVAQ_OK || !grad_bias) return rc;
-    grad_weight = nullptr;  // the bias pass below
+    if (grad_weight) {
+      rc = colsum_launch(part, rchunks, C_out * ckk, grad_weight, stream, (int)rg.taps,
+                         (int)C_out, (int)C);
+      if (rc != NOVAQ_OK) return rc;
+    }
+    if (grad_bias) rc = colsum_launch(bpart, rchunks, C_out, grad_bias, stream);
+    return rc;
   }
   float* part = reinterpret_cast<float*>(base + ws.part);
   float* bpart = grad_bias ? reinterpret_cast<float*>(base + ws.bpart) : nullptr;

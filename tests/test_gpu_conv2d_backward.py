@@ -72,14 +72,16 @@ def test_conv2d_backward_vs_oracle(geom, wdt):
     check_case(*geom, wdt)
 
 
-# grad_weight on the stride-1 rows kernel (8 to 16 taps, at most 8 columns,
-# output rows of at most 64 pixels, 16 or more input channels)
+# grad_weight and grad_bias on the stride-1 rows kernel (8 to 12 taps, at
+# most 8 columns, output rows of at most 64 pixels, 16 or more input
+# channels, at most 5 staged slots per lane), and shapes just outside it
 ROWS_GEOMETRIES = [
     (2, 40, 13, 15, 70, 3, 3, (1, 1), (1, 1)),   # 16-pixel rows, last band partial, both channel blocks partial
     (2, 17, 9, 50, 33, 3, 3, (1, 1), (0, 2)),    # 52-pixel rows (two per band)
-    (3, 16, 10, 12, 8, 4, 4, (1, 1), (2, 1)),    # 4x4: even and odd column shifts
+    (2, 16, 10, 12, 8, 3, 4, (1, 1), (1, 2)),    # 12 taps: even and odd column shifts
     (2, 16, 9, 9, 8, 2, 4, (1, 1), (1, 2)),      # 8 taps
-    (1, 16, 6, 20, 8, 2, 8, (1, 1), (0, 3)),     # 8 columns
+    (3, 16, 10, 12, 8, 4, 4, (1, 1), (2, 1)),    # 16 taps: the general kernel
+    (1, 16, 6, 20, 8, 2, 8, (1, 1), (0, 3)),     # 8 columns, 16 taps: the general kernel
     (2, 96, 7, 30, 130, 3, 3, (1, 1), (1, 1)),   # three input and three output channel blocks
 ]
 
