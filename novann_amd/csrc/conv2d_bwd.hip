@@ -13,7 +13,7 @@
 //     back onto the pixels the padding copied).
 //
 // Kernels:
-//   - flip_weights_kernel: Wf[c, co, kh, kw] = W[co, c, KH-1-kh, KW-1-kw],
+//   - flip (in finish_kernel): Wf[c, co, kh, kw] = W[co, c, KH-1-kh, KW-1-kw],
 //     codes permuted (exact).  With stride 1 and padding < kernel size,
 //     grad_input is the forward convolution of grad with Wf and zero padding
 //     (KH-1-ph, KW-1-pw), run by conv2d.hip's kernels;
@@ -26,13 +26,16 @@
 //     operand gathered element-wise with the padding mode resolved); each
 //     workgroup writes one partial grad_weight tile to the workspace, and the
 //     first j block also the per-channel grad sums of its chunk (grad_bias);
-//   - layout.hip's column sum then adds the chunk partials in a fixed order,
-//     so results do not depend on scheduling.
+//   - finish_kernel: one launch that adds the chunk partials in a fixed order
+//     (novaq_colsum.h's column sum, so results do not depend on scheduling)
+//     for grad_weight and grad_bias, and flips the weights for grad_input;
+//     grad_input's convolution runs after it.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 #include <algorithm>
 
+#include "novaq_colsum.h"
 #include "novaq_convert.h"
 #include "novaq_internal.h"
 
@@ -67,20 +70,18 @@ __device__ __forceinline__ uint32_t code_at(const uint8_t* __restrict__ w, int64
   else return reinterpret_cast<const uint32_t*>(w)[e];
 }
 
-// Wf[c, co, kh, kw] = W[co, c, KH-1-kh, KW-1-kw]; one thread per output byte
-// (E2M1: two elements; the total is even) or element.
+// Wf[c, co, kh, kw] = W[co, c, KH-1-kh, KW-1-kw]: output byte t (E2M1: two
+// elements; an odd total leaves the last high nibble 0) or element t.
 template <int WT>
-__global__ void flip_weights_kernel(const uint8_t* __restrict__ w, uint8_t* __restrict__ wf,
-                                    int C_out, int C, int KH, int KW) {
+__device__ __forceinline__ void flip_item(const uint8_t* __restrict__ w, uint8_t* __restrict__ wf,
+                                          int64_t t, int C_out, int C, int KH, int KW) {
   constexpr int PER = WT == E2M1 ? 2 : 1;
   const int64_t total = (int64_t)C_out * C * KH * KW;
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (t * PER >= total) return;
   uint32_t out = 0;
 #pragma unroll
   for (int q = 0; q < PER; ++q) {
     const int64_t e = t * PER + q;  // index into Wf (c, co, kh, kw)
-    if (e >= total) break;          // E2M1 with an odd total: the last high nibble is 0
+    if (e >= total) break;
     const int kw = (int)(e % KW);
     int64_t r = e / KW;
     const int kh = (int)(r % KH);
@@ -93,6 +94,37 @@ __global__ void flip_weights_kernel(const uint8_t* __restrict__ w, uint8_t* __re
   if constexpr (dtype_bits(WT) <= 8) wf[t] = (uint8_t)out;
   else if constexpr (dtype_bits(WT) == 16) reinterpret_cast<uint16_t*>(wf)[t] = (uint16_t)out;
   else reinterpret_cast<uint32_t*>(wf)[t] = out;
+}
+
+// The backward's finishing launch (1024-lane workgroups): blocks [0, wb) sum
+// grad_weight's columns over the chunk partials (permuted from (tap, co, c)
+// to (co, c, tap) when pt > 0), [wb, wb + bb) grad_bias's, and the rest flip
+// 1024 weight items each for grad_input.
+struct FinishArgs {
+  const float* part;
+  float* gw;
+  const float* bpart;
+  float* gb;
+  const uint8_t* w;
+  uint8_t* wf;
+  int64_t rows, wcols, bcols, flip_items;
+  int pt, pco, pc;
+  unsigned wb, bb;
+};
+
+template <int WT>
+__global__ __launch_bounds__(CS_COLS * CS_SLICES) void finish_kernel(FinishArgs a, int C_out,
+                                                                     int C, int KH, int KW) {
+  __shared__ float part[CS_SLICES][CS_COLS];
+  const unsigned b = blockIdx.x;
+  if (b < a.wb) {
+    colsum_block(a.part, a.rows, a.wcols, a.gw, a.pt, a.pco, a.pc, b, part);
+  } else if (b < a.wb + a.bb) {
+    colsum_block(a.bpart, a.rows, a.bcols, a.gb, 0, 0, 0, b - a.wb, part);
+  } else {
+    const int64_t t = (int64_t)(b - a.wb - a.bb) * (CS_COLS * CS_SLICES) + threadIdx.x;
+    if (t < a.flip_items) flip_item<WT>(a.w, a.wf, t, C_out, C, KH, KW);
+  }
 }
 
 struct BwdGeom {
@@ -579,28 +611,44 @@ size_t rows_geometry(const BwdGeom& g, RowsGeom& rg, int& xj) {
   return bytes <= 150 * 1024 ? bytes : 0;
 }
 
-template <int WT>
-int launch_flip(const void* w, void* wf, const BwdGeom& g, hipStream_t stream) {
+// grad_input as the forward convolution of grad with the flipped weights
+bool flip_path(const BwdGeom& g) { return g.sh == 1 && g.sw == 1 && g.ph < g.KH && g.pw < g.KW; }
+
+int64_t flip_items(const BwdGeom& g, int wt) {
   const int64_t total = (int64_t)g.C_out * g.C * g.KH * g.KW;
-  const int64_t items = WT == E2M1 ? (total + 1) / 2 : total;
-  const int64_t blocks = (items + 255) / 256;
+  return wt == E2M1 ? (total + 1) / 2 : total;
+}
+
+int launch_finish(FinishArgs a, int wt, const BwdGeom& g, hipStream_t stream) {
+  const int64_t wb = (a.wcols + CS_COLS - 1) / CS_COLS, bb = (a.bcols + CS_COLS - 1) / CS_COLS;
+  const int64_t fb = (a.flip_items + CS_COLS * CS_SLICES - 1) / (CS_COLS * CS_SLICES);
+  const int64_t blocks = wb + bb + fb;
+  if (blocks == 0) return NOVAQ_OK;
   if (blocks > 0x7FFFFFFF) return NOVAQ_EINVAL;
-  hipLaunchKernelGGL(flip_weights_kernel<WT>, dim3((unsigned)blocks), dim3(256), 0, stream,
-                     static_cast<const uint8_t*>(w), static_cast<uint8_t*>(wf), g.C_out, g.C,
-                     g.KH, g.KW);
+  a.wb = (unsigned)wb;
+  a.bb = (unsigned)bb;
+  const dim3 grid((unsigned)blocks), block(CS_COLS * CS_SLICES);
+  switch (wt) {
+    case E4M3: hipLaunchKernelGGL(finish_kernel<E4M3>, grid, block, 0, stream, a, g.C_out, g.C, g.KH, g.KW); break;
+    case E5M2: hipLaunchKernelGGL(finish_kernel<E5M2>, grid, block, 0, stream, a, g.C_out, g.C, g.KH, g.KW); break;
+    case E2M1: hipLaunchKernelGGL(finish_kernel<E2M1>, grid, block, 0, stream, a, g.C_out, g.C, g.KH, g.KW); break;
+    case BF16: hipLaunchKernelGGL(finish_kernel<BF16>, grid, block, 0, stream, a, g.C_out, g.C, g.KH, g.KW); break;
+    case F16: hipLaunchKernelGGL(finish_kernel<F16>, grid, block, 0, stream, a, g.C_out, g.C, g.KH, g.KW); break;
+    case F32: hipLaunchKernelGGL(finish_kernel<F32>, grid, block, 0, stream, a, g.C_out, g.C, g.KH, g.KW); break;
+    default: return NOVAQ_EDTYPE;
+  }
   return check_launch();
 }
 
+// wf holds the flipped weights when flip_path(g) (the finishing launch wrote
+// them); the direct kernel covers the rest.
 template <int WT>
 int launch_dinput(const float* grad, const void* w, const void* wf, const float* w_scale,
                   float* gi, const BwdGeom& g, hipStream_t stream) {
-  // stride 1 and padding below the kernel size: the forward convolution of
-  // grad with the flipped weights and zero padding (KH-1-ph, KW-1-pw)
-  if (g.sh == 1 && g.sw == 1 && g.ph < g.KH && g.pw < g.KW) {
-    int rc = launch_flip<WT>(w, const_cast<void*>(wf), g, stream);
-    if (rc != NOVAQ_OK) return rc;
-    rc = conv2d_launch(grad, g.N, g.C_out, g.OH, g.OW, wf, WT, w_scale, g.C, g.KH, g.KW, 1, 1,
-                       g.KH - 1 - g.ph, g.KW - 1 - g.pw, NOVAQ_PAD_ZEROS, nullptr, gi, stream);
+  if (flip_path(g)) {
+    const int rc = conv2d_launch(grad, g.N, g.C_out, g.OH, g.OW, wf, WT, w_scale, g.C, g.KH, g.KW,
+                                 1, 1, g.KH - 1 - g.ph, g.KW - 1 - g.pw, NOVAQ_PAD_ZEROS, nullptr,
+                                 gi, stream);
     if (rc != NOVAQ_ENOTSUP) return rc;
   }
   const int64_t total = (int64_t)g.N * g.C * g.H * g.W;
@@ -639,40 +687,15 @@ ConvBwdWs conv2d_bwd_workspace(int64_t N, int64_t C, int64_t C_out, int KH, int 
   return ws;
 }
 
-int conv2d_backward_launch(const float* grad, const float* x, int64_t N, int64_t C, int64_t H,
-                           int64_t W, const void* w_q, int w_dtype, const float* w_scale,
-                           int64_t C_out, int KH, int KW, int sh, int sw, int ph, int pw,
-                           int pad_mode, float* grad_input, float* grad_weight,
-                           float* grad_bias, void* workspace, hipStream_t stream) {
-  BwdGeom g{};
-  g.N = (int)N; g.C = (int)C; g.H = (int)H; g.W = (int)W; g.C_out = (int)C_out;
-  g.KH = KH; g.KW = KW; g.sh = sh; g.sw = sw; g.ph = ph; g.pw = pw; g.pad_mode = pad_mode;
-  g.OH = (int)((H + 2 * (int64_t)ph - KH) / sh + 1);
-  g.OW = (int)((W + 2 * (int64_t)pw - KW) / sw + 1);
-  const ConvBwdWs ws = conv2d_bwd_workspace(N, C, C_out, KH, KW, w_dtype, device_cu_count());
-  // chunks for this launch: at most one per (image, stage) pair, rounded up to
-  // a multiple of 8 when at least 8 (never above ws.chunks, itself such a
-  // multiple); chunks past the last stage add zeros
-  const int64_t T = N * (((int64_t)g.OH * g.OW + DW_K - 1) / DW_K);
-  int64_t chunks = std::min<int64_t>(ws.chunks, std::max<int64_t>(T, 1));
-  if (chunks >= 8) chunks = (chunks + 7) / 8 * 8;
-  uint8_t* base = static_cast<uint8_t*>(workspace);
-  int rc = NOVAQ_OK;
-  if (grad_input && N > 0) {
-    void* wf = base + ws.wf;
-    switch (w_dtype) {
-      case E4M3: rc = launch_dinput<E4M3>(grad, w_q, wf, w_scale, grad_input, g, stream); break;
-      case E5M2: rc = launch_dinput<E5M2>(grad, w_q, wf, w_scale, grad_input, g, stream); break;
-      case E2M1: rc = launch_dinput<E2M1>(grad, w_q, wf, w_scale, grad_input, g, stream); break;
-      case BF16: rc = launch_dinput<BF16>(grad, w_q, wf, w_scale, grad_input, g, stream); break;
-      case F16: rc = launch_dinput<F16>(grad, w_q, wf, w_scale, grad_input, g, stream); break;
-      case F32: rc = launch_dinput<F32>(grad, w_q, wf, w_scale, grad_input, g, stream); break;
-      default: return NOVAQ_EDTYPE;
-    }
-    if (rc != NOVAQ_OK) return rc;
-  }
-  const int64_t ckk = C * KH * KW;
-  if (!grad_weight && !grad_bias) return rc;
+// grad_weight and grad_bias partials: the stride-1 rows kernel or the general
+// implicit GEMM, one partial per chunk; fa receives what the finishing
+// launch sums.
+static int dweight_launch(const float* grad, const float* x, const BwdGeom& g, int64_t chunks,
+                          const ConvBwdWs& ws, uint8_t* base, float* grad_weight,
+                          float* grad_bias, FinishArgs& fa, hipStream_t stream) {
+  if (!grad_weight && !grad_bias) return NOVAQ_OK;
+  const int64_t C = g.C, C_out = g.C_out;
+  const int64_t ckk = C * g.KH * g.KW;
   // stride-1 convolutions with short rows: grad_weight and grad_bias on the
   // rows kernel (a bias-only call runs its bias-only mode over the same
   // chunks, so its bits match a full call's)
@@ -713,15 +736,21 @@ int conv2d_backward_launch(const float* grad, const float* x, int64_t N, int64_t
       hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(rg.taps * 64), rows_lds, stream, grad,
                          x, part, bpart, g, rg, (int)rchunks, (int)co_blocks, (int)c_blocks);
     }
-    rc = check_launch();
-    if (rc != NOVAQ_OK) return rc;
+    fa.rows = rchunks;
     if (grad_weight) {
-      rc = colsum_launch(part, rchunks, C_out * ckk, grad_weight, stream, (int)rg.taps,
-                         (int)C_out, (int)C);
-      if (rc != NOVAQ_OK) return rc;
+      fa.part = part;
+      fa.gw = grad_weight;
+      fa.wcols = C_out * ckk;
+      fa.pt = (int)rg.taps;
+      fa.pco = (int)C_out;
+      fa.pc = (int)C;
     }
-    if (grad_bias) rc = colsum_launch(bpart, rchunks, C_out, grad_bias, stream);
-    return rc;
+    if (grad_bias) {
+      fa.bpart = bpart;
+      fa.gb = grad_bias;
+      fa.bcols = C_out;
+    }
+    return check_launch();
   }
   float* part = reinterpret_cast<float*>(base + ws.part);
   float* bpart = grad_bias ? reinterpret_cast<float*>(base + ws.bpart) : nullptr;
@@ -731,20 +760,68 @@ int conv2d_backward_launch(const float* grad, const float* x, int64_t N, int64_t
   const int64_t blocks = chunks * co_blocks * j_blocks;
   if (blocks > 0x7FFFFFFF) return NOVAQ_EINVAL;
   const dim3 grid((unsigned)blocks);
-  const bool zp = pad_mode == NOVAQ_PAD_ZEROS;
+  const bool zp = g.pad_mode == NOVAQ_PAD_ZEROS;
   auto kern = grad_weight ? (zp ? dweight_kernel<true, false> : dweight_kernel<false, false>)
                           : dweight_kernel<true, true>;
   hipLaunchKernelGGL(kern, grid, dim3(DW_THREADS), 0, stream, grad, x, part, bpart, g, (int)ckk,
                      (int)chunks, (int)co_blocks, (int)j_blocks);
-  rc = check_launch();
-  if (rc != NOVAQ_OK) return rc;
-  // partials added over the chunks in a fixed order
+  // partials added over the chunks in a fixed order by the finishing launch
+  fa.rows = chunks;
   if (grad_weight) {
-    rc = colsum_launch(part, chunks, C_out * ckk, grad_weight, stream);
-    if (rc != NOVAQ_OK) return rc;
+    fa.part = part;
+    fa.gw = grad_weight;
+    fa.wcols = C_out * ckk;
   }
-  if (grad_bias) rc = colsum_launch(bpart, chunks, C_out, grad_bias, stream);
-  return rc;
+  if (grad_bias) {
+    fa.bpart = bpart;
+    fa.gb = grad_bias;
+    fa.bcols = C_out;
+  }
+  return check_launch();
+}
+
+int conv2d_backward_launch(const float* grad, const float* x, int64_t N, int64_t C, int64_t H,
+                           int64_t W, const void* w_q, int w_dtype, const float* w_scale,
+                           int64_t C_out, int KH, int KW, int sh, int sw, int ph, int pw,
+                           int pad_mode, float* grad_input, float* grad_weight,
+                           float* grad_bias, void* workspace, hipStream_t stream) {
+  BwdGeom g{};
+  g.N = (int)N; g.C = (int)C; g.H = (int)H; g.W = (int)W; g.C_out = (int)C_out;
+  g.KH = KH; g.KW = KW; g.sh = sh; g.sw = sw; g.ph = ph; g.pw = pw; g.pad_mode = pad_mode;
+  g.OH = (int)((H + 2 * (int64_t)ph - KH) / sh + 1);
+  g.OW = (int)((W + 2 * (int64_t)pw - KW) / sw + 1);
+  const ConvBwdWs ws = conv2d_bwd_workspace(N, C, C_out, KH, KW, w_dtype, device_cu_count());
+  // chunks for this launch: at most one per (image, stage) pair, rounded up to
+  // a multiple of 8 when at least 8 (never above ws.chunks, itself such a
+  // multiple); chunks past the last stage add zeros
+  const int64_t T = N * (((int64_t)g.OH * g.OW + DW_K - 1) / DW_K);
+  int64_t chunks = std::min<int64_t>(ws.chunks, std::max<int64_t>(T, 1));
+  if (chunks >= 8) chunks = (chunks + 7) / 8 * 8;
+  switch (w_dtype) {
+    case E4M3: case E5M2: case E2M1: case BF16: case F16: case F32: break;
+    default: return NOVAQ_EDTYPE;
+  }
+  uint8_t* base = static_cast<uint8_t*>(workspace);
+  void* wf = base + ws.wf;
+  int rc = NOVAQ_OK;
+  // order: the weight-gradient kernel, one finishing launch (its column sums
+  // and the weight flip), then grad_input's convolution
+  FinishArgs fa{};
+  fa.w = static_cast<const uint8_t*>(w_q);
+  fa.wf = static_cast<uint8_t*>(wf);
+  fa.flip_items = grad_input && N > 0 && flip_path(g) ? flip_items(g, w_dtype) : 0;
+  rc = dweight_launch(grad, x, g, chunks, ws, base, grad_weight, grad_bias, fa, stream);
+  if (rc != NOVAQ_OK) return rc;
+  rc = launch_finish(fa, w_dtype, g, stream);
+  if (rc != NOVAQ_OK || !grad_input || N == 0) return rc;
+  switch (w_dtype) {
+    case E4M3: return launch_dinput<E4M3>(grad, w_q, wf, w_scale, grad_input, g, stream);
+    case E5M2: return launch_dinput<E5M2>(grad, w_q, wf, w_scale, grad_input, g, stream);
+    case E2M1: return launch_dinput<E2M1>(grad, w_q, wf, w_scale, grad_input, g, stream);
+    case BF16: return launch_dinput<BF16>(grad, w_q, wf, w_scale, grad_input, g, stream);
+    case F16: return launch_dinput<F16>(grad, w_q, wf, w_scale, grad_input, g, stream);
+    default: return launch_dinput<F32>(grad, w_q, wf, w_scale, grad_input, g, stream);
+  }
 }
 
 }  // namespace novaq

@@ -17,6 +17,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "novaq_colsum.h"
 #include "novaq_convert.h"
 #include "novaq_internal.h"
 
@@ -82,49 +83,13 @@ __global__ __launch_bounds__(TT) void transpose_kernel(const uint8_t* __restrict
   }
 }
 
-// Column sums: out[c] = sum over r of x[r * cols + c] in a fixed order (with
-// pt > 0 the columns are a (pt, pco, pc) array and column (t, co, c) is
-// stored at out[(co * pc + c) * pt + t]).
-constexpr int CS_COLS = 64;    // columns per workgroup
-constexpr int CS_SLICES = 16;  // row slices per workgroup (one wave each)
-
+// Column sums (the fixed summation order is novaq_colsum.h's).
 __global__ __launch_bounds__(CS_COLS * CS_SLICES) void colsum_kernel(const float* __restrict__ x,
                                                                     int64_t rows, int64_t cols,
                                                                     float* __restrict__ out,
                                                                     int pt, int pco, int pc) {
   __shared__ float part[CS_SLICES][CS_COLS];
-  const int tx = threadIdx.x % CS_COLS, ty = threadIdx.x / CS_COLS;
-  const int64_t c = (int64_t)blockIdx.x * CS_COLS + tx;
-  const int64_t per = (rows + CS_SLICES - 1) / CS_SLICES;
-  const int64_t rb = ty * per, re = min(rows, rb + per);
-  float s = 0.0f;
-  if (c < cols) {
-    // four independent chains keep four loads in flight per lane
-    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
-    int64_t r = rb;
-    for (; r + 3 < re; r += 4) {
-      a0 += x[r * cols + c];
-      a1 += x[(r + 1) * cols + c];
-      a2 += x[(r + 2) * cols + c];
-      a3 += x[(r + 3) * cols + c];
-    }
-    for (; r < re; ++r) a0 += x[r * cols + c];
-    s = (a0 + a1) + (a2 + a3);
-  }
-  part[ty][tx] = s;
-  __syncthreads();
-  if (ty == 0 && c < cols) {
-    float t = part[0][tx];
-#pragma unroll
-    for (int k = 1; k < CS_SLICES; ++k) t += part[k][tx];
-    int64_t o = c;
-    if (pt > 0) {
-      const int64_t per_t = (int64_t)pco * pc;
-      const int64_t tt = c / per_t, rest = c - tt * per_t;
-      o = rest * pt + tt;  // rest = co * pc + c
-    }
-    out[o] = t;
-  }
+  colsum_block(x, rows, cols, out, pt, pco, pc, blockIdx.x, part);
 }
 
 template <int ST, int DT>
