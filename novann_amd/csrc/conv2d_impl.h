@@ -423,6 +423,7 @@ struct BandGeom {
   int groups;    // taps * c8 K groups of 8
   int gpr;       // groups rounded up to whole MFMA K steps (4 groups)
   int wrow;      // bytes per weight row in LDS
+  int co_rows;   // weight rows staged in LDS (C_out rounded up to 16, at most 64)
   int R;         // output rows per band
   int bands;     // bands per image
   int rows_in;   // staged input rows per band
@@ -454,8 +455,8 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
     Epilogue ep, void* __restrict__ y, BandGeom g) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   constexpr int GB = group_bytes<WT>();
-  uint8_t* wl = lds;                                           // [64][g.wrow]
-  int* ktab = reinterpret_cast<int*>(lds + CO_TILE * g.wrow);  // [g.gpr]
+  uint8_t* wl = lds;                                           // [g.co_rows][g.wrow]
+  int* ktab = reinterpret_cast<int*>(lds + g.co_rows * g.wrow);  // [g.gpr]
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int lr = lane & 15, lg = lane >> 4;
@@ -509,7 +510,7 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
   if constexpr (K9 && GB < 16) {
     constexpr int BITS = dtype_bits(WT);
     constexpr int NW = 72 * BITS / 32;  // words of one (co, q) run
-    for (int item = tid; item < CO_TILE * g.c8; item += THREADS) {
+    for (int item = tid; item < g.co_rows * g.c8; item += THREADS) {
       const int co = item / g.c8, q = item - co * g.c8;
       uint32_t o[9][GB / 4];
       if (co0 + co < g.C_out) {
@@ -545,7 +546,7 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
     }
     // zero groups past the window (K padding to whole MFMA steps)
     const int pad = g.gpr - g.groups;
-    for (int item = tid; item < CO_TILE * pad; item += THREADS) {
+    for (int item = tid; item < g.co_rows * pad; item += THREADS) {
       const int co = item / pad, gi = g.groups + (item - co * pad);
       uint8_t* d = wl + co * g.wrow + gi * GB;
       if constexpr (GB == 4) *reinterpret_cast<uint32_t*>(d) = 0u;
@@ -553,11 +554,13 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
     }
   } else {
     // four threads per output channel row, each taking every fourth group
+    // (rows past g.co_rows are not staged)
     const int co = tid >> 2;
     const bool live = co0 + co < g.C_out;
+    const int gend = co < g.co_rows ? g.gpr : 0;
     int tap = 0, q = tid & 3;
     while (q >= g.c8) { q -= g.c8; ++tap; }
-    for (int gi = tid & 3; gi < g.gpr; gi += 4) {
+    for (int gi = tid & 3; gi < gend; gi += 4) {
       uint32_t p[4] = {0u, 0u, 0u, 0u};
       if (live && gi < g.groups) {
         const int cbase = q * 8;
@@ -834,9 +837,10 @@ bool band_geometry(const ConvGeom& cg, BandGeom& b, size_t& lds, int* ipt) {
          (GB == 16 && stride_dw % 8 != 4))
     stride_dw += GB / 4;
   b.wrow = stride_dw * 4;
-  b.x_off = (CO_TILE * b.wrow + 4 * b.gpr + 15) / 16 * 16;
+  b.co_rows = std::min(CO_TILE, (cg.C_out + 15) / 16 * 16);
+  b.x_off = (b.co_rows * b.wrow + 4 * b.gpr + 15) / 16 * 16;
   b.x_bytes = (int)(((size_t)b.rows_in * b.wp * b.cstride * 2 + 15) / 16 * 16);
-  const size_t raw_bytes = ((size_t)CO_TILE * cg.C * b.taps * dtype_bits(WT) + 7) / 8;
+  const size_t raw_bytes = ((size_t)b.co_rows * cg.C * b.taps * dtype_bits(WT) + 7) / 8;
   b.raw_ok = dtype_bits(WT) <= 8 && raw_bytes <= (size_t)b.x_bytes;
   lds = b.x_off + (size_t)b.x_bytes;
   return lds <= 80 * 1024;
