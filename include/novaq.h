@@ -281,7 +281,7 @@ size_t novaq_linear_backward_workspace(int64_t N, int64_t D_in, int64_t D_out, i
  * Replaces: Linear.backward (novann/layers/linear/linear.py:85-108).  Any of
  * the three outputs may be NULL (not computed).  The products run on the
  * Linear forward kernels (bf16 MFMA, fp32 accumulation): grad_input on w_q's
- * codes transposed (exact), grad_weight on grad^T in fp32 and x^T rounded to
+ * codes transposed (exact), grad_weight on grad^T and x^T, both rounded to
  * bf16.  workspace: device memory of novaq_linear_backward_workspace() bytes
  * (16-byte aligned) the call may overwrite; it is not used after the call's
  * kernels complete. */

@@ -33,7 +33,7 @@ int device_cu_count() {
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
-// Workspace of novaq_linear_backward: W^T in W's format, grad^T (fp32) and
+// Workspace of novaq_linear_backward: W^T in W's format, grad^T (bf16) and
 // x^T (bf16), each 256-byte aligned.
 struct LinearBwdWs {
   size_t wt, gyt, xt, total;
@@ -42,7 +42,7 @@ static LinearBwdWs linear_bwd_ws(int64_t N, int64_t D_in, int64_t D_out, int w_d
   LinearBwdWs w;
   w.wt = 0;
   w.gyt = align256(((size_t)D_in * (size_t)D_out * dtype_bits(w_dtype) + 7) / 8);
-  w.xt = w.gyt + align256((size_t)D_out * (size_t)N * 4);
+  w.xt = w.gyt + align256((size_t)D_out * (size_t)N * 2);
   w.total = w.xt + align256((size_t)D_in * (size_t)N * 2);
   return w;
 }
@@ -328,15 +328,19 @@ int novaq_linear_backward(const float* grad, const float* x, int64_t N, int64_t 
     rc = linear_launch(grad, N, D_out, wt, w_dtype, w_scale, nullptr, D_in, grad_input, s);
     if (rc != NOVAQ_OK) return rc;
   }
-  // grad_weight = grad^T @ x: the forward product of grad^T (fp32) and x^T (bf16)
+  // grad_weight = grad^T @ x: the forward product of grad^T and x^T, both
+  // transposed straight to bf16 (the fp32 operand would be rounded to bf16 with
+  // the same round-to-nearest-even while staged)
   if (grad_weight && D_out > 0 && D_in > 0) {
-    float* gyt = reinterpret_cast<float*>(base + ws.gyt);
+    void* gyt = base + ws.gyt;
     void* xt = base + ws.xt;
-    rc = transpose_launch(grad, F32, N, D_out, gyt, F32, s);
+    rc = transpose_launch(grad, F32, N, D_out, gyt, BF16, s);
     if (rc != NOVAQ_OK) return rc;
     rc = transpose_launch(x, F32, N, D_in, xt, BF16, s);
     if (rc != NOVAQ_OK) return rc;
-    rc = linear_launch(gyt, D_out, N, xt, BF16, nullptr, nullptr, D_in, grad_weight, s);
+    Epilogue ep{};
+    ep.out_dtype = F32;
+    rc = linear_launch(gyt, BF16, nullptr, D_out, N, xt, BF16, nullptr, ep, D_in, grad_weight, s);
     if (rc != NOVAQ_OK) return rc;
   }
   // grad_bias = grad summed over the batch
