@@ -589,7 +589,8 @@ constexpr int DR_MAX_XJ = 5;
 // The stride-1 rows path applies (its LDS bytes and slots per lane XJ), or 0.
 size_t rows_geometry(const BwdGeom& g, RowsGeom& rg, int& xj) {
   const int taps = g.KH * g.KW;
-  // (fewer than 16 input channels leave most of the 32-channel tile idle)
+  // (fewer than 16 input channels leave most of the 32-channel tile idle: a
+  // 1-channel 28x28 batch of 256 takes ~33 us here against 16.5 on dweight_kernel)
   // (at most 12 taps: 12 waves keep ~170 VGPRs a wave)
   if (g.sh != 1 || g.sw != 1 || taps < 8 || taps > 12 || g.KW > 8 || g.OW > 64 || g.C < 16)
     return 0;
