@@ -83,6 +83,54 @@ __global__ __launch_bounds__(TT) void transpose_kernel(const uint8_t* __restrict
   }
 }
 
+// 8-bit codes with rows and cols multiples of 16: a workgroup moves a
+// 128 x 128 byte tile.  Lane (rb, cb) loads 16 bytes of each of source rows
+// 4rb .. 4rb+3 (a wave's load covers 8 rows x 128 contiguous bytes),
+// transposes the 4 x 16 byte block in registers into 16 dwords (4 source
+// rows of one source column each) and writes them to LDS as tile[col][rb];
+// then 8 lanes per destination row write its 128 bytes with 16-byte stores.
+// Rows and cols being multiples of 16 make every 16-byte access wholly in or
+// out of range.
+constexpr int TB = 128;            // tile edge in bytes
+constexpr int TB_DW = TB / 4 + 1;  // LDS dwords per destination row (padded)
+
+__global__ __launch_bounds__(TT) void transpose_bytes_kernel(const uint8_t* __restrict__ src,
+                                                             uint8_t* __restrict__ dst,
+                                                             int64_t rows, int64_t cols) {
+  __shared__ uint32_t tile[TB][TB_DW];
+  const int64_t r0 = (int64_t)blockIdx.y * TB, c0 = (int64_t)blockIdx.x * TB;
+  const int t = threadIdx.x;
+  const int rb = t >> 3, cb = t & 7;  // 4-row group, 16-byte column chunk
+  uint4 a[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int64_t r = r0 + 4 * rb + k, c = c0 + 16 * cb;
+    a[k] = (r < rows && c < cols) ? *reinterpret_cast<const uint4*>(src + r * cols + c)
+                                  : make_uint4(0u, 0u, 0u, 0u);
+  }
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const uint32_t w0 = (&a[0].x)[d], w1 = (&a[1].x)[d], w2 = (&a[2].x)[d], w3 = (&a[3].x)[d];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      // bytes j of the four rows' dwords: source column 16cb + 4d + j
+      const uint32_t o = ((w0 >> (8 * j)) & 0xFFu) | (((w1 >> (8 * j)) & 0xFFu) << 8) |
+                         (((w2 >> (8 * j)) & 0xFFu) << 16) | (((w3 >> (8 * j)) & 0xFFu) << 24);
+      tile[16 * cb + 4 * d + j][rb] = o;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const int oc = (t >> 3) + 32 * p, chunk = t & 7;  // destination row, 16-byte chunk
+    const int64_t c = c0 + oc, r = r0 + 16 * chunk;
+    if (c < cols && r < rows) {
+      const uint32_t* q = &tile[oc][4 * chunk];
+      *reinterpret_cast<uint4*>(dst + c * rows + r) = make_uint4(q[0], q[1], q[2], q[3]);
+    }
+  }
+}
+
 // Column sums (the fixed summation order is novaq_colsum.h's).
 __global__ __launch_bounds__(CS_COLS * CS_SLICES) void colsum_kernel(const float* __restrict__ x,
                                                                     int64_t rows, int64_t cols,
@@ -108,6 +156,14 @@ int transpose_launch(const void* src, int st, int64_t rows, int64_t cols, void* 
                      hipStream_t stream) {
   if (rows == 0 || cols == 0) return NOVAQ_OK;
   if (st == dt) {
+    if (dtype_bits(st) == 8 && rows % 16 == 0 && cols % 16 == 0) {
+      const int64_t gx = (cols + TB - 1) / TB, gy = (rows + TB - 1) / TB;
+      if (gx > 0x7FFFFFFF || gy > 65535) return NOVAQ_EINVAL;
+      hipLaunchKernelGGL(transpose_bytes_kernel, dim3((unsigned)gx, (unsigned)gy), dim3(TT), 0,
+                         stream, static_cast<const uint8_t*>(src), static_cast<uint8_t*>(dst),
+                         rows, cols);
+      return check_launch();
+    }
     switch (st) {
       case F32: return launch_transpose<F32, F32>(src, dst, rows, cols, stream);
       case F16: return launch_transpose<F16, F16>(src, dst, rows, cols, stream);

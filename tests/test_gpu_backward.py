@@ -54,7 +54,8 @@ def pack_nibbles(c):
     return (c[:, 0] | (c[:, 1] << 4)).astype(np.uint8)
 
 
-@pytest.mark.parametrize("shape", [(1, 1), (3, 5), (64, 64), (65, 130), (200, 77), (128, 4096)])
+@pytest.mark.parametrize("shape", [(1, 1), (3, 5), (64, 64), (65, 130), (200, 77), (128, 4096),
+                                   (16, 16), (48, 272), (400, 144)])
 @pytest.mark.parametrize("dt", [O.F32, O.F16, O.BF16, O.E4M3, O.E5M2])
 def test_transpose_permutes_codes_exactly(shape, dt):
     rows, cols = shape
