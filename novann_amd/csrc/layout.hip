@@ -131,6 +131,49 @@ __global__ __launch_bounds__(TT) void transpose_bytes_kernel(const uint8_t* __re
   }
 }
 
+// fp32 -> bf16 / fp16 with rows a multiple of 8 and cols of 4: a workgroup
+// moves a 64 x 64 tile.  Lane (rb, cb) loads 4 floats of each of source rows
+// 4rb .. 4rb+3 (a wave's load covers 4 rows x 256 contiguous bytes), rounds
+// them and writes each source column's 4 values as two packed dwords to LDS;
+// then 8 lanes per destination row write its 128 bytes with 16-byte stores.
+constexpr int TN = 64;                 // tile edge in elements
+constexpr int TN_DW = TN / 2 + 1;      // LDS dwords per destination row (padded)
+
+template <int DT>
+__global__ __launch_bounds__(TT) void transpose_round_kernel(const float* __restrict__ src,
+                                                             uint16_t* __restrict__ dst,
+                                                             int64_t rows, int64_t cols) {
+  __shared__ uint32_t tile[TN][TN_DW];
+  const int64_t r0 = (int64_t)blockIdx.y * TN, c0 = (int64_t)blockIdx.x * TN;
+  const int t = threadIdx.x;
+  const int rb = t >> 4, cb = t & 15;  // 4-row group, 4-column chunk
+  uint4 a[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int64_t r = r0 + 4 * rb + k, c = c0 + 4 * cb;
+    a[k] = (r < rows && c < cols) ? *reinterpret_cast<const uint4*>(src + r * cols + c)
+                                  : make_uint4(0u, 0u, 0u, 0u);
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    uint32_t e[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) e[k] = convert_code<F32, DT>((&a[k].x)[j]);
+    tile[4 * cb + j][2 * rb] = e[0] | (e[1] << 16);
+    tile[4 * cb + j][2 * rb + 1] = e[2] | (e[3] << 16);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const int oc = (t >> 3) + 32 * p, chunk = t & 7;  // destination row, 8-element chunk
+    const int64_t c = c0 + oc, r = r0 + 8 * chunk;
+    if (c < cols && r < rows) {
+      const uint32_t* q = &tile[oc][4 * chunk];
+      *reinterpret_cast<uint4*>(dst + c * rows + r) = make_uint4(q[0], q[1], q[2], q[3]);
+    }
+  }
+}
+
 // Column sums (the fixed summation order is novaq_colsum.h's).
 __global__ __launch_bounds__(CS_COLS * CS_SLICES) void colsum_kernel(const float* __restrict__ x,
                                                                     int64_t rows, int64_t cols,
@@ -175,6 +218,14 @@ int transpose_launch(const void* src, int st, int64_t rows, int64_t cols, void* 
         return launch_transpose<E2M1, E2M1>(src, dst, rows, cols, stream);
       default: return NOVAQ_EDTYPE;
     }
+  }
+  if (st == F32 && (dt == BF16 || dt == F16) && rows % 8 == 0 && cols % 4 == 0) {
+    const int64_t gx = (cols + TN - 1) / TN, gy = (rows + TN - 1) / TN;
+    if (gx > 0x7FFFFFFF || gy > 65535) return NOVAQ_EINVAL;
+    auto kern = dt == BF16 ? transpose_round_kernel<BF16> : transpose_round_kernel<F16>;
+    hipLaunchKernelGGL(kern, dim3((unsigned)gx, (unsigned)gy), dim3(TT), 0, stream,
+                       static_cast<const float*>(src), static_cast<uint16_t*>(dst), rows, cols);
+    return check_launch();
   }
   if (st == F32 && dt == BF16) return launch_transpose<F32, BF16>(src, dst, rows, cols, stream);
   if (st == F32 && dt == F16) return launch_transpose<F32, F16>(src, dst, rows, cols, stream);

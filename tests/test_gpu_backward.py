@@ -77,9 +77,12 @@ def test_transpose_e2m1_nibbles(shape):
     assert np.array_equal(got, want)
 
 
+# (97, 130): the element tile kernel; the rest (rows % 8 == 0, cols % 4 == 0)
+# the 16-byte tile kernel, partial tiles included
+@pytest.mark.parametrize("shape", [(97, 130), (8, 4), (96, 132), (200, 68), (1024, 256)])
 @pytest.mark.parametrize("dt", [O.BF16, O.F16])
-def test_transpose_rounds_f32_like_the_cast(dt):
-    rows, cols = 97, 130
+def test_transpose_rounds_f32_like_the_cast(dt, shape):
+    rows, cols = shape
     rng = np.random.default_rng(7)
     x = (rng.standard_normal(rows * cols) * np.exp2(rng.integers(-30, 30, rows * cols))
          ).astype(np.float32)
