@@ -7,7 +7,10 @@
 // codes are permuted, never re-encoded (E2M1: both sides nibble-packed along
 // their rows, element 2i in the low nibble; a lane writes one byte, i.e. two
 // consecutive elements of a destination row).  fp32 -> bf16 / fp16 rounds to
-// nearest even with the same rules as the cast kernels.
+// nearest even with the same rules as the cast kernels.  Two shapes take
+// 16-byte accesses instead: 8-bit codes with rows and cols multiples of 16
+// (transpose_bytes_kernel) and fp32 -> bf16 / fp16 with rows % 8 == 0 and
+// cols % 4 == 0 (transpose_round_kernel).
 //
 // Column sum: out[c] = sum over rows of x[r][c] in fp32, in a fixed order
 // (each of 16 row slices summed in four interleaved row chains, the chains
