@@ -1,9 +1,9 @@
 // Cast, amax and scale kernels (HBM-bound streaming) for gfx950.
 //
-// Layout: each thread moves UNITS_PER_THREAD "units"; a unit is EPL
+// Layout: each thread moves a few "units" (4; 2 for 16 -> 32-bit); a unit is EPL
 // consecutive elements, sized so that the wider side of the cast is one
 // 16-byte access per lane (the narrower side is 2 to 8 bytes: fp32 <-> fp4
-// moves 16 bytes against 2).  Unit u of a block sits at (block * UNITS_PER_THREAD + j) *
+// moves 16 bytes against 2).  Unit u of a block sits at (block * units_per_thread + j) *
 // blockDim + tid, so every load and store instruction of a wave covers one
 // contiguous span (fully coalesced).  All loads of a thread are issued before
 // any conversion, to keep several 16-byte requests in flight per lane.  The
@@ -27,6 +27,11 @@ struct CastShape {
   static constexpr int dst_bits = epl * dtype_bits(DT);
   static constexpr int src_words = (src_bits + 31) / 32;  // 32-bit words holding a unit
   static constexpr int dst_words = (dst_bits + 31) / 32;
+  // units per thread: 2 for 16 -> 32-bit widening (twice the workgroups:
+  // bf16 -> fp32 on 2^28 elements 271 -> 255 us; 4 and 8 units and the 8 / 4
+  // -> 32-bit casts at 2 units measured slower)
+  static constexpr int upt =
+      dtype_bits(ST) == 16 && dtype_bits(DT) == 32 ? kUnitsPerThread / 2 : kUnitsPerThread;
 };
 
 template <int N>
@@ -129,16 +134,16 @@ __global__ __launch_bounds__(kCastThreads) void cast_kernel(
     if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = s;
   }
   const int64_t units = n / EPL;
-  const int64_t base = (int64_t)blockIdx.x * kUnitsPerThread * kCastThreads + threadIdx.x;
+  const int64_t base = (int64_t)blockIdx.x * Sh::upt * kCastThreads + threadIdx.x;
 
-  Words<Sh::src_words> in[kUnitsPerThread];
+  Words<Sh::src_words> in[Sh::upt];
 #pragma unroll
-  for (int j = 0; j < kUnitsPerThread; ++j) {
+  for (int j = 0; j < Sh::upt; ++j) {
     int64_t u = base + (int64_t)j * kCastThreads;
     if (u < units) in[j] = load_words<Sh::src_bits>(src + u * (Sh::src_bits / 8));
   }
 #pragma unroll
-  for (int j = 0; j < kUnitsPerThread; ++j) {
+  for (int j = 0; j < Sh::upt; ++j) {
     int64_t u = base + (int64_t)j * kCastThreads;
     if (u < units) {
       Words<Sh::dst_words> out;
@@ -247,7 +252,7 @@ static int launch_cast(const void* src, void* dst, int64_t n, const float* scale
                        float* scale_out, hipStream_t stream) {
   using Sh = CastShape<ST, DT>;
   int64_t units = n / Sh::epl;
-  int64_t per_block = (int64_t)kUnitsPerThread * kCastThreads;
+  int64_t per_block = (int64_t)Sh::upt * kCastThreads;
   int64_t blocks = (units + per_block - 1) / per_block;
   if (blocks < 1) blocks = 1;
   if (blocks > 0x7FFFFFFF) return NOVAQ_EINVAL;
