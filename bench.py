@@ -123,12 +123,22 @@ def bench_sweep(n: int, steps: int, warmup: int, dev):
     t1 = time.perf_counter()
     per_op = []
     for i, (name, b, _) in enumerate(ops):
-        ms = sum(events[s][i][0].elapsed_time(events[s][i][1]) for s in range(steps)) / steps
+        t = [events[s][i][0].elapsed_time(events[s][i][1]) for s in range(steps)]
+        ms = sum(t) / steps
         gbs = b * n / (ms * 1e-3) / 1e9 if b else None
-        per_op.append({"op": name, "ms": round(ms, 4),
+        per_op.append({"op": name, "ms": round(ms, 4), "median_ms": round(_median(t), 4),
                        "GB/s": None if gbs is None else round(gbs, 1),
                        "frac": None if gbs is None else round(gbs / HBM_PEAK_GBS, 4)})
-    del bufs
+    # after the timed steps, each op again with the MALL evicted before every
+    # launch (its inputs then come from HBM, not from the op just before)
+    flush = torch.zeros(1 << 27, dtype=torch.float32, device=dev)
+    for p, (_, b, fn) in zip(per_op, ops):
+        if not b:
+            continue
+        mean, med = _time_launches(dev, fn, max(steps, 5), 0, flush)
+        p["evicted_median_ms"] = round(med, 4)
+        p["evicted_GB/s"] = round(b * n / (med * 1e-3) / 1e9, 1)
+    del bufs, flush
     return (t1 - t0) * 1e3 / steps, per_op
 
 
@@ -156,30 +166,13 @@ def bench_linear(dev, iters: int = 20, warmup: int = 5):
         run()
     except NotImplementedError:
         return None
-    for _ in range(warmup):
-        run()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize(dev)
-    e0.record()
-    for _ in range(iters):
-        run()
-    e1.record()
-    torch.cuda.synchronize(dev)
-    ms = e0.elapsed_time(e1) / iters
+    ms, med = _time_launches(dev, run, iters, warmup)
     flops = 2.0 * M * N * K
     tflops = flops / (ms * 1e-3) / 1e12
     # context: the vendor bf16 GEMM (torch -> hipBLASLt) on the same shape with
     # bf16 operands already in HBM (no fp32 x conversion, no W decode)
     xb, wb = x.to(torch.bfloat16), w.to(torch.bfloat16).contiguous()
-    for _ in range(warmup):
-        torch.nn.functional.linear(xb, wb)
-    torch.cuda.synchronize(dev)
-    e0.record()
-    for _ in range(iters):
-        torch.nn.functional.linear(xb, wb)
-    e1.record()
-    torch.cuda.synchronize(dev)
-    vms = e0.elapsed_time(e1) / iters
+    vms, _ = _time_launches(dev, lambda: torch.nn.functional.linear(xb, wb), iters, warmup)
     # the same product on x stored as E4M3 (amax-scaled, as a fused epilogue
     # writes activations): both operands' codes go to the FP8 MFMA
     xq = quant.quantize(x, "e4m3")
@@ -188,18 +181,10 @@ def bench_linear(dev, iters: int = 20, warmup: int = 5):
         _lib.check(lib.novaq_linear_forward_ex(
             xq.data.data_ptr(), _lib.E4M3, xq.scale.data_ptr(), M, K, wq.data.data_ptr(), 3,
             wq.scale.data_ptr(), b.data_ptr(), N, None, y.data_ptr(), stream), "linear fp8 x")
-    for _ in range(warmup):
-        run8()
-    torch.cuda.synchronize(dev)
-    e0.record()
-    for _ in range(iters):
-        run8()
-    e1.record()
-    torch.cuda.synchronize(dev)
-    ms8 = e0.elapsed_time(e1) / iters
+    ms8, _ = _time_launches(dev, run8, iters, warmup)
     tf8 = flops / (ms8 * 1e-3) / 1e12
     return {"metric": "FP8-weight Linear TFLOP/s at 4096^2", "value": round(tflops, 1),
-            "unit": "TFLOP/s", "ms": round(ms, 4),
+            "unit": "TFLOP/s", "ms": round(ms, 4), "median_ms": round(med, 4),
             "vendor_bf16_gemm": {"what": "torch.nn.functional.linear, bf16 x and W in HBM",
                                  "ms": round(vms, 4),
                                  "TFLOP/s": round(flops / (vms * 1e-3) / 1e12, 1)},
@@ -527,22 +512,38 @@ def _evict(buf):
     buf.amax()
 
 
-def _timed_flush(dev, fn, iters, warmup):
-    """Average ms of fn over iters launches, the MALL evicted before each."""
+def _median(v):
+    s = sorted(v)
+    k = len(s) // 2
+    return s[k] if len(s) % 2 else 0.5 * (s[k - 1] + s[k])
+
+
+def _time_launches(dev, fn, iters, warmup, flush=None):
+    """(mean, median) ms of fn over `iters` launches, each bracketed by HIP
+    events on the current stream (the one every entry point here is given);
+    with `flush`, the MALL is evicted before each launch, outside the events."""
     import torch
-    flush = torch.zeros(1 << 27, dtype=torch.float32, device=dev)
     for _ in range(warmup):
         fn()
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
           for _ in range(iters)]
     torch.cuda.synchronize(dev)
     for e0, e1 in ev:
-        _evict(flush)
+        if flush is not None:
+            _evict(flush)
         e0.record()
         fn()
         e1.record()
     torch.cuda.synchronize(dev)
-    return sum(e0.elapsed_time(e1) for e0, e1 in ev) / iters
+    t = [e0.elapsed_time(e1) for e0, e1 in ev]
+    return sum(t) / len(t), _median(t)
+
+
+def _timed_flush(dev, fn, iters, warmup):
+    """Average ms of fn over iters launches, the MALL evicted before each."""
+    import torch
+    flush = torch.zeros(1 << 27, dtype=torch.float32, device=dev)
+    return _time_launches(dev, fn, iters, warmup, flush)[0]
 
 
 def bench_optim(dev, iters: int = 20, warmup: int = 3):
@@ -656,6 +657,107 @@ def cpu_baseline(sample: int, min_seconds: float = 10.0):
                       f"elements, C oracle, {threads} OpenMP threads, {dt_s:.1f} s"}
 
 
+def _cpu_info():
+    """(BLAS threads numpy uses, CPU model, nproc) of this host."""
+    import numpy as np  # noqa: F401  (loads the BLAS threadpoolctl reports)
+    threads = None
+    try:
+        import threadpoolctl
+        info = [i for i in threadpoolctl.threadpool_info() if i.get("user_api") == "blas"]
+        threads = info[0]["num_threads"] if info else None
+    except ImportError:
+        pass
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((ln.split(":", 1)[1].strip() for ln in f
+                          if ln.startswith("model name")), None)
+    except OSError:
+        pass
+    return threads, model, os.cpu_count()
+
+
+def _cpu_reps(fn, min_reps: int = 5, max_seconds: float = 12.0):
+    """Median and count of repeated host timings of fn (one untimed warm-up)."""
+    fn()
+    t, start = [], time.perf_counter()
+    while len(t) < min_reps or (time.perf_counter() - start < 2.0 and len(t) < 50):
+        t0 = time.perf_counter()
+        fn()
+        t.append(time.perf_counter() - t0)
+        if time.perf_counter() - start > max_seconds and len(t) >= 3:
+            break
+    return _median(t), len(t)
+
+
+def cpu_linear_baseline():
+    """The reference's own Linear arithmetic on the host: numpy
+    ``x @ W.T`` then ``+= b`` (novann/functional.py:160-162, restated in
+    oracle.functional_ref.linear) at config [4], W the E4M3-quantized weight
+    dequantized to fp32 by the C oracle.  Median of >= 5 repetitions."""
+    import numpy as np
+
+    import oracle as O
+    from oracle import functional_ref as R
+    M, K, N = 2048, 4096, 4096
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((M, K), dtype=np.float32)
+    w = rng.standard_normal((N, K), dtype=np.float32) * np.float32((2.0 / K) ** 0.5)
+    s = O.scale_from_amax(O.amax(w), O.E4M3)
+    wd = O.cast(O.cast(w, O.F32, O.E4M3, scale=s), O.E4M3, O.F32, n=w.size,
+                scale=s).reshape(N, K)
+    b = np.zeros((1, N), dtype=np.float32)
+    med, reps = _cpu_reps(lambda: R.linear(x, wd, b))
+    threads, model, ncpu = _cpu_info()
+    return {"value": round(2.0 * M * N * K / med / 1e12, 4), "unit": "TFLOP/s",
+            "ms": round(med * 1e3, 3), "cores": threads, "nproc": ncpu, "cpu": model,
+            "kind": "port",
+            "sample": f"config [4] at full size (x {M}x{K} fp32, dequantized E4M3 W {N}x{K}), "
+                      f"numpy x @ W.T + b (OpenBLAS sgemm, {threads} threads), "
+                      f"median of {reps}"}
+
+
+def cpu_conv_baseline():
+    """The reference's own Conv2d arithmetic on the host: numpy.pad +
+    as_strided im2col + one GEMM + bias + NCHW view (novann/functional.py:
+    346-382, restated in oracle.functional_ref.conv2d) for config [5]'s two
+    layers, E2M1-quantized weights dequantized by the C oracle.  Median of
+    >= 5 repetitions per layer."""
+    import numpy as np
+
+    import oracle as O
+    from oracle import functional_ref as R
+    rng = np.random.default_rng(5)
+    x = rng.random((256, 1, 28, 28), dtype=np.float32)
+    threads, model, ncpu = _cpu_info()
+    out = []
+    for cin, cout in ((1, 32), (32, 64)):
+        w = rng.standard_normal((cout, cin, 3, 3), dtype=np.float32) * np.float32(
+            (2.0 / (cin * 9)) ** 0.5)
+        s = O.scale_from_amax(O.amax(w), O.E2M1)
+        wd = O.cast(O.cast(w, O.F32, O.E2M1, scale=s), O.E2M1, O.F32, n=w.size,
+                    scale=s).reshape(w.shape)
+        b = np.zeros((cout, 1), dtype=np.float32)
+        y = None
+
+        def run(x=x, wd=wd, b=b):
+            nonlocal y
+            y = R.conv2d(x, wd, (1, 1), (1, 1), "zeros", b)
+        med, reps = _cpu_reps(run)
+        nbytes = (x.size + 256 * cout * 28 * 28) * 4
+        out.append({"layer": f"conv {cin}->{cout}", "ms": round(med * 1e3, 3),
+                    "GB/s": round(nbytes / med / 1e9, 3), "reps": reps})
+        x = np.ascontiguousarray(y)
+    return {"layers": out, "unit": "GB/s", "cores": threads, "nproc": ncpu, "cpu": model,
+            "kind": "port",
+            "sample": f"config [5] at full size (batch 256), numpy im2col + GEMM "
+                      f"(OpenBLAS, {threads} threads), median per layer"}
+
+
+LEGS = ("sweep", "linear", "linear_backward", "conv", "conv_backward", "epilogue", "adamw",
+        "pool", "fp4", "cpu")
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -663,6 +765,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--elems", type=int, default=1 << 28)
     ap.add_argument("--cpu-sample", type=int, default=1 << 26)
+    ap.add_argument("--only", default="",
+                    help="comma-separated subset of legs to run (profiling runs): "
+                         + ", ".join(LEGS))
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-linear", action="store_true")
     ap.add_argument("--copy-probe", action="store_true",
@@ -675,10 +780,23 @@ def main() -> int:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
               "(run with --gpus 1)", file=sys.stderr)
         return 2
+    legs = set(args.only.split(",")) if args.only else set(LEGS)
+    unknown = legs - set(LEGS)
+    if unknown:
+        print(f"bench.py: unknown legs {sorted(unknown)}; known: {', '.join(LEGS)}",
+              file=sys.stderr)
+        return 2
+    if args.no_linear:
+        legs -= {"linear", "linear_backward"}
+    if args.no_conv:
+        legs -= {"conv", "conv_backward", "epilogue", "adamw", "pool"}
+    if args.no_fp4:
+        legs.discard("fp4")
+    if args.no_cpu:
+        legs.discard("cpu")
     import torch
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-    log(f"sweep: {args.elems} elements, {args.steps} steps, {args.warmup} warmup")
     if args.copy_probe:
         from novann_amd import _lib
         src = torch.empty(args.elems, dtype=torch.float32, device=dev).fill_(1.0)
@@ -687,53 +805,58 @@ def main() -> int:
                                           torch.cuda.current_stream(dev).cuda_stream), "copy")
         torch.cuda.synchronize(dev)
         del src, dst
-    ms, per_op = bench_sweep(args.elems, args.steps, args.warmup, dev)
-    value = BYTES_PER_ELEM * args.elems / (ms * 1e-3) / 1e9
-    # dominant single-kernel op (the amax op also launches a 1-thread fill kernel)
-    kernels = [p for p in per_op if p["op"] in KERNEL_OF]
-    dom = max(kernels, key=lambda p: p["ms"])
-    dom_bpe = dict(SWEEP)[dom["op"]]
-    log(f"sweep done: {ms:.3f} ms/step, {value:.1f} GB/s")
-    lin = None if args.no_linear else bench_linear(dev)
-    log(f"linear: {lin}")
-    lin_bwd = None if args.no_linear else bench_linear_backward(dev)
-    log(f"linear backward: {lin_bwd}")
-    conv = None if args.no_conv else bench_conv(dev)
-    log(f"conv2d: {conv}")
-    conv_bwd = None if args.no_conv else bench_conv_backward(dev)
-    log(f"conv2d backward: {conv_bwd}")
-    epi = None if args.no_conv else bench_epilogue(dev)
-    log(f"fused epilogues: {epi}")
-    opt = None if args.no_conv else bench_optim(dev)
-    log(f"adamw: {opt}")
-    pool = None if args.no_conv else bench_pool(dev)
-    log(f"pools: {pool}")
-    fp4 = None if args.no_fp4 else bench_fp4(dev)
-    log(f"fp4: {fp4}")
-    cpu = None if args.no_cpu else cpu_baseline(args.cpu_sample)
-    log(f"cpu baseline: {cpu}")
+    ms = value = None
+    per_op, roof = None, None
+    if "sweep" in legs:
+        log(f"sweep: {args.elems} elements, {args.steps} steps, {args.warmup} warmup")
+        ms, per_op = bench_sweep(args.elems, args.steps, args.warmup, dev)
+        value = BYTES_PER_ELEM * args.elems / (ms * 1e-3) / 1e9
+        # dominant single-kernel op (the amax op also launches a 1-thread fill kernel)
+        kernels = [p for p in per_op if p["op"] in KERNEL_OF]
+        dom = max(kernels, key=lambda p: p["ms"])
+        dom_bpe = dict(SWEEP)[dom["op"]]
+        roof = {"bound": "hbm", "kernel": f'{dom["op"]} ({KERNEL_OF[dom["op"]]})',
+                "achieved": dom["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": dom["frac"],
+                "traffic": (measured_traffic(KERNEL_OF[dom["op"]])
+                            if args.elems == 1 << 28 else None),
+                "bytes_per_launch": dom_bpe * args.elems}
+        log(f"sweep done: {ms:.3f} ms/step, {value:.1f} GB/s")
+    run = {}
+    for leg, fn in (("linear", bench_linear), ("linear_backward", bench_linear_backward),
+                    ("conv", bench_conv), ("conv_backward", bench_conv_backward),
+                    ("epilogue", bench_epilogue), ("adamw", bench_optim),
+                    ("pool", bench_pool), ("fp4", bench_fp4)):
+        run[leg] = fn(dev) if leg in legs else None
+        log(f"{leg}: {run[leg]}")
+    cpu = None
+    if "cpu" in legs:
+        cpu = cpu_baseline(args.cpu_sample)
+        log(f"cpu baseline: {cpu}")
+        if run["linear"] is not None:
+            run["linear"]["cpu_baseline"] = cpu_linear_baseline()
+            log(f"linear cpu baseline: {run['linear']['cpu_baseline']}")
+        if run["conv"] is not None:
+            run["conv"]["cpu_baseline"] = cpu_conv_baseline()
+            log(f"conv2d cpu baseline: {run['conv']['cpu_baseline']}")
     out = {
-        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "metric": METRIC, "value": None if value is None else round(value, 1), "unit": "GB/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": None if ms is None else round(ms, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f32<->{f16,bf16,e4m3,e5m2}", "data": "synthetic",
         "config": {"workload": "BASELINE config [2]: cast sweep, amax-scaled FP8",
                    "elements": args.elems, "bytes_per_element": BYTES_PER_ELEM},
-        "roofline": {"bound": "hbm", "kernel": f'{dom["op"]} ({KERNEL_OF[dom["op"]]})',
-                     "achieved": dom["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": dom["frac"],
-                     "traffic": (measured_traffic(KERNEL_OF[dom["op"]])
-                                 if args.elems == 1 << 28 else None),
-                     "bytes_per_launch": dom_bpe * args.elems},
+        "roofline": roof,
         "kernels": per_op,
-        "linear": lin,
-        "linear_backward": lin_bwd,
-        "conv2d": conv,
-        "conv2d_backward": conv_bwd,
-        "epilogue": epi,
-        "adamw": opt,
-        "pool": pool,
-        "fp4": fp4,
+        "linear": run["linear"],
+        "linear_backward": run["linear_backward"],
+        "conv2d": run["conv"],
+        "conv2d_backward": run["conv_backward"],
+        "epilogue": run["epilogue"],
+        "adamw": run["adamw"],
+        "pool": run["pool"],
+        "fp4": run["fp4"],
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
