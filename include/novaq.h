@@ -121,7 +121,9 @@ int novaq_unpack_fp4(const uint8_t *packed, int64_t n, const float *scale, float
  * Replaces: novann.functional.linear(input, weight, bias)
  * (novann/functional.py:147-163), called by Linear.forward
  * (novann/layers/linear/linear.py:70-83).  w_q is (D_out, D_in) row-major in
- * w_dtype (E4M3, E5M2, E2M1 packed along D_in, BF16, F16 or F32); w_scale is
+ * w_dtype (E4M3, E5M2, E2M1 packed along D_in, BF16, F16 or F32; an E2M1 row
+ * holds ceil(D_in / 2) bytes, so with odd D_in each row ends with a pad
+ * nibble, which is never read); w_scale is
  * the per-tensor s (NULL = 1); bias is D_out fp32 values or NULL (the
  * reference's (1, D_out) bias); y is (N, D_out) fp32, freshly written.
  * Products run on bf16 MFMA with fp32 accumulation; the scale and the bias are
@@ -204,7 +206,8 @@ int novaq_conv2d_forward_ex(const void *x, int x_dtype, const float *x_scale, in
  * F16 / E4M3 / E5M2 as an epilogue stores activations; FP8 codes keep their
  * scale): the result is one of the window's values, the later one in
  * row-major window order when two are equal (the sign of a zero maximum),
- * NaN when the window holds one.
+ * NaN when the window holds one.  x and y need only be aligned to their
+ * element size (NOVAQ_EALIGN otherwise): views into a larger tensor work.
  * Replaces: novann.functional.max_pool2d (novann/functional.py:450-532),
  * called by MaxPool2d.forward (layers/pooling/maxpool/maxpool2d.py:51-79). */
 int novaq_max_pool2d(const void *x, int x_dtype, int64_t N, int64_t C, int64_t H, int64_t W,
@@ -243,6 +246,18 @@ typedef struct novaq_adamw {
  * Replaces: AdamW.step for one parameter (novann/optim/adamw.py:41-65). */
 int novaq_adamw_step(float *w, const float *grad, float *m, float *v, int64_t n,
                      const novaq_adamw *hp, float *w_amax, void *stream);
+
+/* novaq_adamw_step on n float64 weights w with float64 moments m, v (all
+ * device, updated in place; 8-byte aligned): the reference's statements on
+ * its float64 parameters (BatchNorm gamma / beta, batchnorm2d.py:33-55, whose
+ * moments np.zeros_like makes float64), evaluated as numpy does: in float64,
+ * except that with grad_f32 != 0 (grad holds float32 values) the products
+ * (1 - b1) * g and (1 - b2) * g^2 are float32 operations, widened for the
+ * float64 sums; with grad_f32 == 0 grad holds float64 values.  Equal to the
+ * reference bit for bit.
+ * Replaces: AdamW.step for one float64 parameter (novann/optim/adamw.py:41-65). */
+int novaq_adamw_step_f64(double *w, const void *grad, int grad_f32, double *m, double *v,
+                         int64_t n, const novaq_adamw *hp, void *stream);
 
 /* novaq_adamw_step on fp32 master weights, then their re-quantization into
  * codes (q_dtype E4M3, E5M2 or E2M1) with a fresh per-tensor scale:

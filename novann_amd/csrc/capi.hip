@@ -128,7 +128,6 @@ int novaq_linear_forward(const float* x, int64_t N, int64_t D_in, const void* w_
   if (N < 0 || D_in < 0 || D_out < 0) return NOVAQ_EINVAL;
   if (N == 0 || D_out == 0) return NOVAQ_OK;
   if (!x || !w_q || !y) return NOVAQ_EINVAL;
-  if (w_dtype == E2M1 && (D_in & 1)) return NOVAQ_ESHAPE;  // rows of whole bytes
   if (!aligned16(x) || !aligned16(w_q) || !aligned16(y) || (bias && !aligned16(bias)))
     return NOVAQ_EALIGN;
   return linear_launch(x, N, D_in, w_q, w_dtype, w_scale, bias, D_out, y,
@@ -193,7 +192,6 @@ int novaq_linear_forward_ex(const void* x, int x_dtype, const float* x_scale, in
   if (epi && (epi->out_dtype == E2M1 || !valid_dtype(epi->out_dtype))) return NOVAQ_EDTYPE;
   if (N == 0 || D_out == 0) return NOVAQ_OK;
   if (!x || !w_q || !y) return NOVAQ_EINVAL;
-  if (w_dtype == E2M1 && (D_in & 1)) return NOVAQ_ESHAPE;  // rows of whole bytes
   if (!aligned16(x) || !aligned16(w_q) || !aligned16(y) || (bias && !aligned16(bias)))
     return NOVAQ_EALIGN;
   const hipStream_t st = static_cast<hipStream_t>(stream);
@@ -238,6 +236,8 @@ int novaq_max_pool2d(const void* x, int x_dtype, int64_t N, int64_t C, int64_t H
   if (H > 0x7FFFFFFF || W > 0x7FFFFFFF) return NOVAQ_EINVAL;
   if (N == 0) return NOVAQ_OK;
   if (!x || !y) return NOVAQ_EINVAL;
+  const uintptr_t eb = (uintptr_t)dtype_bits(x_dtype) / 8;  // element-aligned views only
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) % eb) return NOVAQ_EALIGN;
   return max_pool2d_launch(x, x_dtype, N, C, H, W, KH, KW, sh, sw, ph, pw, pad_mode, y,
                            static_cast<hipStream_t>(stream));
 }
@@ -261,6 +261,18 @@ int novaq_adamw_step(float* w, const float* grad, float* m, float* v, int64_t n,
   if (w_amax && (reinterpret_cast<uintptr_t>(w_amax) & 3)) return NOVAQ_EALIGN;
   return adamw_launch(w, grad, m, v, n, hp->lr, hp->beta1, hp->beta2, hp->eps, hp->weight_decay,
                       hp->step, hp->decay, w_amax, static_cast<hipStream_t>(stream));
+}
+
+int novaq_adamw_step_f64(double* w, const void* grad, int grad_f32, double* m, double* v,
+                         int64_t n, const novaq_adamw* hp, void* stream) {
+  if (!hp || n < 0 || hp->step < 1) return NOVAQ_EINVAL;
+  if (n > 0 && (!w || !grad || !m || !v)) return NOVAQ_EINVAL;
+  for (const void* p : {(const void*)w, (const void*)m, (const void*)v})
+    if (p && (reinterpret_cast<uintptr_t>(p) & 7)) return NOVAQ_EALIGN;
+  if (grad && (reinterpret_cast<uintptr_t>(grad) & (grad_f32 ? 3 : 7))) return NOVAQ_EALIGN;
+  return adamw_f64_launch(w, grad, grad_f32 != 0, m, v, n, hp->lr, hp->beta1, hp->beta2, hp->eps,
+                          hp->weight_decay, hp->step, hp->decay,
+                          static_cast<hipStream_t>(stream));
 }
 
 int novaq_adamw_requantize(float* w, const float* grad, float* m, float* v, int64_t n,

@@ -865,6 +865,52 @@ int launch_band(const uint8_t* x, const float* x_scale, const void* w, const flo
   return check_launch();
 }
 
+// Any geometry whose staged input rows do not fit in LDS (very wide images):
+// one lane per output element (grid-strided over the NCHW output), the window
+// gathered straight from global memory with the padding mode resolved.  The
+// operands are those of the MFMA paths -- x and W rounded to bf16, so every
+// product is exact in fp32 -- summed in fp32 in (c, kh, kw) order, then the
+// same epilogue.
+template <int WT, int XT>
+__global__ __launch_bounds__(256) void conv2d_direct_kernel(
+    const uint8_t* __restrict__ x, const float* __restrict__ x_scale,
+    const uint8_t* __restrict__ w, const float* __restrict__ w_scale, Epilogue ep,
+    void* __restrict__ y, ConvGeom g) {
+  const int64_t total = (int64_t)g.N * g.C_out * g.OH * g.OW;
+  const float s = product_scale(w_scale, x_scale);
+  const float inv_o = epi_inv_scale(ep);
+  const int64_t hw = (int64_t)g.H * g.W;
+  uint32_t am = 0;
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  for (int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x; t < total; t += stride) {
+    const int ow = (int)(t % g.OW);
+    int64_t r = t / g.OW;
+    const int oh = (int)(r % g.OH);
+    r /= g.OH;
+    const int co = (int)(r % g.C_out);
+    const int64_t n = r / g.C_out;
+    float acc = 0.0f;
+    for (int c = 0; c < g.C; ++c) {
+      const int64_t xb = (n * g.C + c) * hw;
+      const int64_t wb = ((int64_t)co * g.C + c) * g.KH * g.KW;
+      for (int kh = 0; kh < g.KH; ++kh) {
+        const int hi = pad_index(oh * g.sh + kh - g.ph, g.H, g.pad_mode);
+        for (int kw = 0; kw < g.KW; ++kw) {
+          const int wi = pad_index(ow * g.sw + kw - g.pw, g.W, g.pad_mode);
+          if (hi < 0 || wi < 0) continue;  // zero padding adds +0 * w
+          const float xv = u2f(enc_bf16(f2u(x_val<XT>(x, xb + (int64_t)hi * g.W + wi))) << 16);
+          const float wv = u2f((uint32_t)weight_bf16<WT>(w, wb + kh * g.KW + kw) << 16);
+          acc = acc + xv * wv;
+        }
+      }
+    }
+    const float v = epi_value(ep, epi_chan(ep, co), acc, s);
+    am = epi_track(am, v);
+    epi_store(ep.out_dtype, y, t, v, inv_o);
+  }
+  epi_amax_commit(ep, am);
+}
+
 template <int WT, int XT>
 int launch(const uint8_t* x, const float* x_scale, const void* w, const float* w_scale,
            const Epilogue& ep, void* y, ConvGeom g, hipStream_t stream) {
@@ -903,7 +949,16 @@ int launch(const uint8_t* x, const float* x_scale, const void* w, const float* w
   const size_t lds = (size_t)CO_TILE * g.wrow + xl_bytes + (size_t)8 * g.ksteps;
   const size_t raw_bytes = ((size_t)CO_TILE * g.C * g.KH * g.KW * dtype_bits(WT) + 7) / 8;
   g.raw_in_lds = g.C <= g.CB && raw_bytes <= xl_bytes;
-  if (lds > LDS_LIMIT) return NOVAQ_ENOTSUP;  // rows too wide for one LDS tile
+  if (lds > LDS_LIMIT) {  // rows too wide for one LDS tile: the direct gather
+    const int64_t total = (int64_t)g.N * g.C_out * g.OH * g.OW;
+    int64_t blocks = (total + 255) / 256;
+    const int64_t cap = (int64_t)device_cu_count() * 16;
+    if (blocks > cap) blocks = cap;
+    if (blocks < 1) blocks = 1;
+    hipLaunchKernelGGL((conv2d_direct_kernel<WT, XT>), dim3((unsigned)blocks), dim3(256), 0,
+                       stream, x, x_scale, static_cast<const uint8_t*>(w), w_scale, ep, y, g);
+    return check_launch();
+  }
   auto kern = conv2d_kernel<WT, XT>;
   static size_t lds_enabled = 64 * 1024;  // per instantiation: raise the limit once
   if (lds > lds_enabled) {

@@ -149,7 +149,8 @@ __global__ __launch_bounds__(THREADS, 1) void linear_kernel(
   __shared__ __attribute__((aligned(16))) __bf16 Bs[2][BN * LDS_ROW];
   using WTr = W<WT>;
   constexpr int WCPR = BK / WTr::epc;  // W chunks per tile row
-  const size_t w_row_bytes = (size_t)K * WTr::bits / 8;
+  // rows of whole bytes: an odd-length E2M1 row ends with a pad nibble
+  const size_t w_row_bytes = ((size_t)K * WTr::bits + 7) / 8;
 
   // tile index: XCD-contiguous, then 4-row groups walked column by column
   const int T = tiles_m * tiles_n;

@@ -54,6 +54,11 @@ int conv2d_launch(const void* x, int x_dtype, const float* x_scale, int64_t N, i
 int adamw_launch(float* w, const float* g, float* m, float* v, int64_t n, double lr, double beta1,
                  double beta2, double eps, double weight_decay, int64_t step, int decay,
                  float* amax, hipStream_t stream);
+// The same step on n float64 weights and moments, the gradient float32
+// (g_f32) or float64, with numpy's promotion rules.
+int adamw_f64_launch(double* w, const void* g, bool g_f32, double* m, double* v, int64_t n,
+                     double lr, double beta1, double beta2, double eps, double weight_decay,
+                     int64_t step, int decay, hipStream_t stream);
 
 int max_pool2d_launch(const void* x, int x_dtype, int64_t N, int64_t C, int64_t H, int64_t W,
                       int KH, int KW, int sh, int sw, int ph, int pw, int pad_mode, void* y,

@@ -131,6 +131,47 @@ __global__ __launch_bounds__(ADAM_THREADS) void adamw_kernel(float* __restrict__
   }
 }
 
+// The same update on a float64 parameter (the reference's BatchNorm gamma /
+// beta are float64 arrays, and np.zeros_like gives their moments that dtype):
+// every operation in float64, except that numpy forms (1 - b1) * g and
+// (1 - b2) * g**2 in float32 when the gradient array is float32 (a Python
+// float does not widen an array) and widens them only for the float64 sums.
+struct AdamHP64 {
+  double b1, omb1, b2, omb2, bc1, bc2, lr, eps, lrwd;
+  float omb1f, omb2f;
+  int decay;
+};
+
+template <bool G32>
+__global__ __launch_bounds__(ADAM_THREADS) void adamw_f64_kernel(double* __restrict__ w,
+                                                                const void* __restrict__ g,
+                                                                double* __restrict__ m,
+                                                                double* __restrict__ v,
+                                                                int64_t n, AdamHP64 h) {
+  const int64_t stride = (int64_t)gridDim.x * ADAM_THREADS;
+  for (int64_t i = (int64_t)blockIdx.x * ADAM_THREADS + threadIdx.x; i < n; i += stride) {
+    double gm, gs;
+    if constexpr (G32) {
+      const float gf = reinterpret_cast<const float*>(g)[i];
+      gm = (double)(h.omb1f * gf);
+      gs = (double)(h.omb2f * (gf * gf));
+    } else {
+      const double gd = reinterpret_cast<const double*>(g)[i];
+      gm = h.omb1 * gd;
+      gs = h.omb2 * (gd * gd);
+    }
+    const double mm = h.b1 * m[i] + gm;
+    const double vv = h.b2 * v[i] + gs;
+    const double m_hat = mm / h.bc1;
+    const double v_hat = vv / h.bc2;
+    double ww = w[i] - (h.lr * m_hat) / (sqrt(v_hat) + h.eps);
+    if (h.decay) ww = ww - h.lrwd * ww;
+    w[i] = ww;
+    m[i] = mm;
+    v[i] = vv;
+  }
+}
+
 }  // namespace
 
 int adamw_launch(float* w, const float* g, float* m, float* v, int64_t n, double lr, double beta1,
@@ -160,6 +201,32 @@ int adamw_launch(float* w, const float* g, float* m, float* v, int64_t n, double
   if (blocks < 1) blocks = 1;
   hipLaunchKernelGGL(adamw_kernel, dim3((unsigned)blocks), dim3(ADAM_THREADS), 0, stream, w, g, m,
                      v, n, h, reinterpret_cast<uint32_t*>(amax));
+  return check_launch();
+}
+
+int adamw_f64_launch(double* w, const void* g, bool g_f32, double* m, double* v, int64_t n,
+                     double lr, double beta1, double beta2, double eps, double weight_decay,
+                     int64_t step, int decay, hipStream_t stream) {
+  if (n == 0) return NOVAQ_OK;
+  AdamHP64 h;
+  h.b1 = beta1;
+  h.omb1 = 1.0 - beta1;
+  h.b2 = beta2;
+  h.omb2 = 1.0 - beta2;
+  h.omb1f = (float)h.omb1;
+  h.omb2f = (float)h.omb2;
+  h.bc1 = 1.0 - pow(beta1, (double)step);
+  h.bc2 = 1.0 - pow(beta2, (double)step);
+  h.lr = lr;
+  h.eps = eps;
+  h.lrwd = lr * weight_decay;
+  h.decay = weight_decay > 0.0 && decay;
+  int64_t blocks = (n + ADAM_THREADS - 1) / ADAM_THREADS;
+  const int64_t cap = (int64_t)device_cu_count() * 8;
+  if (blocks > cap) blocks = cap;
+  auto kern = g_f32 ? adamw_f64_kernel<true> : adamw_f64_kernel<false>;
+  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(ADAM_THREADS), 0, stream, w, g, m, v, n,
+                     h);
   return check_launch();
 }
 

@@ -30,6 +30,7 @@
 #include <stdint.h>
 
 #include "novaq_convert.h"
+#include "novaq_gap_plan.h"
 #include "novaq_internal.h"
 #include "novaq_xload.h"
 
@@ -348,14 +349,6 @@ __global__ __launch_bounds__(256) void global_avg_pool2d_kernel(const uint8_t* _
 // the leaf's remainder in order; the plane's first lane then runs the program
 // over the leaf sums with an 8-deep register stack (the tree is at most 7
 // levels deep).  Same operations in the same association as numpy.
-constexpr int GAP_MAX_LEAVES = 64;
-
-struct GapPlan {
-  int L, nops;
-  uint32_t prog[4];  // 2L - 1 <= 127 postfix bits
-  int2 leaf[GAP_MAX_LEAVES];  // (offset, length)
-};
-
 constexpr int GAP_STAGE = 2048;  // at most this many elements of a wave's planes staged in LDS
 
 // STAGED (a wave's planes hold at most GAP_STAGE elements): the wave first
@@ -405,15 +398,15 @@ __global__ __launch_bounds__(256) void global_avg_pool2d_wave_kernel(
     __syncthreads();
   }
   // element i of leaf lt of this lane's plane
-  auto val = [&](const int2& lt, int i) {
-    if constexpr (STAGED) return gap_stage[(wave * ppw + pi) * hw + lt.x + i];
-    else return elem<XT>(x, base + lt.x + i, s, scaled);
+  auto val = [&](const GapLeaf& lt, int i) {
+    if constexpr (STAGED) return gap_stage[(wave * ppw + pi) * hw + lt.off + i];
+    else return elem<XT>(x, base + lt.off + i, s, scaled);
   };
   for (int p0 = 0; p0 < L; p0 += G) {
     const int leaf = p0 + li;
     const bool on = live && leaf < L;
-    const int2 lt = on ? plan.leaf[leaf] : make_int2(0, 0);
-    const int main = lt.y - (lt.y & 7);
+    const GapLeaf lt = on ? plan.leaf[leaf] : GapLeaf{0, 0};
+    const int main = lt.len - (lt.len & 7);
     // a leaf holds at most 16 groups of 8: every load of the lane goes out
     // before the in-order sum
     float v[16];
@@ -423,7 +416,7 @@ __global__ __launch_bounds__(256) void global_avg_pool2d_wave_kernel(
       v[k] = (on && i < main) ? val(lt, i) : 0.0f;
     }
     float r = 0.0f;
-    if (on && lt.y >= 8) {
+    if (on && lt.len >= 8) {
       r = v[0];
 #pragma unroll
       for (int k = 1; k < 16; ++k)
@@ -435,58 +428,49 @@ __global__ __launch_bounds__(256) void global_avg_pool2d_wave_kernel(
     r = r + __shfl_down(r, 4, 8);
     if (on && j == 0) {
       // the leaf's remainder (or, below 8 elements, the whole leaf) in order
-      const int e0 = lt.y < 8 ? 0 : main;
+      const int e0 = lt.len < 8 ? 0 : main;
       float t[7];
 #pragma unroll
-      for (int q = 0; q < 7; ++q) t[q] = e0 + q < lt.y ? val(lt, e0 + q) : 0.0f;
-      float res = lt.y < 8 ? 0.0f : r;
+      for (int q = 0; q < 7; ++q) t[q] = e0 + q < lt.len ? val(lt, e0 + q) : 0.0f;
+      float res = lt.len < 8 ? 0.0f : r;
 #pragma unroll
       for (int q = 0; q < 7; ++q)
-        if (e0 + q < lt.y) res += t[q];
+        if (e0 + q < lt.len) res += t[q];
       sums[wave][pi * L + leaf] = res;
     }
   }
   __syncthreads();
   if (live && rem == 0) {
     const float* ls = &sums[wave][pi * L];
-    float st[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    float st[GAP_MAX_STACK] = {};  // the plan's tree never needs more
     int next = 0;
     for (int k = 0; k < plan.nops; ++k) {
       if ((plan.prog[k >> 5] >> (k & 31)) & 1u) {
         const float v = ls[next++];
 #pragma unroll
-        for (int d = 7; d > 0; --d) st[d] = st[d - 1];
+        for (int d = GAP_MAX_STACK - 1; d > 0; --d) st[d] = st[d - 1];
         st[0] = v;
       } else {
         st[0] = st[1] + st[0];
 #pragma unroll
-        for (int d = 1; d < 7; ++d) st[d] = st[d + 1];
+        for (int d = 1; d < GAP_MAX_STACK - 1; ++d) st[d] = st[d + 1];
       }
     }
     y[plane] = (0.0f + st[0]) / (float)hw;
   }
 }
 
-// Leaves and postfix program of numpy's pairwise recursion on n elements.
-void gap_plan(int n, int off, GapPlan& p) {
-  if (n <= 128) {
-    p.leaf[p.L++] = make_int2(off, n);
-    p.prog[p.nops >> 5] |= 1u << (p.nops & 31);
-    ++p.nops;
-    return;
-  }
-  int n2 = n / 2;
-  n2 -= n2 % 8;
-  gap_plan(n2, off, p);
-  gap_plan(n - n2, off + n2, p);
-  ++p.nops;  // bit 0: add
-}
-
 template <int XT>
 int launch_max(const void* x, void* y, const PoolGeom& g, hipStream_t stream) {
   const int64_t npix = (int64_t)g.OH * g.OW;
   if (npix > 0x7FFFFFFF) return NOVAQ_EINVAL;
-  if (g.KW == 2 && g.sw == 2 && g.pw == 0) {
+  // the paired kernel reads 4 elements at once when W % 4 == 0 and stores
+  // output pairs when OW is even: it needs x on a 4-element and y on a
+  // 2-element boundary (views into a larger tensor need not be)
+  constexpr uintptr_t EB = XL<XT>::bits / 8;
+  const bool aligned = (reinterpret_cast<uintptr_t>(x) % (4 * EB)) == 0 &&
+                       (reinterpret_cast<uintptr_t>(y) % (2 * EB)) == 0;
+  if (g.KW == 2 && g.sw == 2 && g.pw == 0 && aligned) {
     const int64_t per = (int64_t)g.OH * ((g.OW + 1) / 2);
     const int64_t items = g.N * g.C * per;
     if (items < ((int64_t)1 << 31)) {
@@ -513,9 +497,8 @@ int launch_max(const void* x, void* y, const PoolGeom& g, hipStream_t stream) {
 template <int XT>
 int launch_gap(const void* x, const float* x_scale, float* y, int64_t planes, int64_t hw,
                hipStream_t stream) {
-  if (hw <= NP_BUFSIZE) {
-    GapPlan plan{};
-    gap_plan((int)hw, 0, plan);
+  GapPlan plan;
+  if (hw <= NP_BUFSIZE && gap_plan((int)hw, plan)) {
     const int leaves = plan.L;
     const int G = leaves < 8 ? leaves : 8;
     const int64_t ppw = 64 / (8 * G);

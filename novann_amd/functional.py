@@ -38,8 +38,14 @@ def _to_device_f32(a, what: str) -> Tuple[torch.Tensor, bool]:
     if isinstance(a, torch.Tensor):
         if not a.is_cuda:
             a = a.to(_device())
-        return a.to(torch.float32).contiguous(), False
+        return _aligned(a.to(torch.float32).contiguous()), False
     raise TypeError(f"{what} must be a numpy array or a torch tensor")
+
+
+def _aligned(t: torch.Tensor) -> torch.Tensor:
+    """The kernels read 16-byte vectors: a view that does not start on a
+    16-byte boundary (a slice of a larger tensor) is copied, not refused."""
+    return t if t.data_ptr() % 16 == 0 else t.clone()
 
 
 _X_DTYPES = {torch.float16: "f16", torch.bfloat16: "bf16", torch.float8_e4m3fn: "e4m3",
@@ -55,9 +61,10 @@ def _x_arg(a, what: str):
     if isinstance(a, quant.Quantized):
         if a.dtype not in ("e4m3", "e5m2"):
             raise TypeError(f"{what}: a quantized input must be e4m3 or e5m2, got {a.dtype}")
-        return a.data.contiguous(), a.dtype, a.scale, tuple(a.shape), False
+        a.check(what)
+        return _aligned(a.data.contiguous()), a.dtype, a.scale, tuple(a.shape), False
     if isinstance(a, torch.Tensor) and a.is_cuda and a.dtype in _X_DTYPES:
-        return a.contiguous(), _X_DTYPES[a.dtype], None, tuple(a.shape), False
+        return _aligned(a.contiguous()), _X_DTYPES[a.dtype], None, tuple(a.shape), False
     t, was_numpy = _to_device_f32(a, what)
     return t, "f32", None, tuple(t.shape), was_numpy
 
@@ -65,7 +72,12 @@ def _x_arg(a, what: str):
 def _weight_args(weight, dev: torch.device):
     """(codes tensor, dtype code, scale tensor or None) for a weight."""
     if isinstance(weight, QuantizedParameters):
-        return weight.codes.to(dev), DTYPES[weight.dtype], weight.scale.to(dev)
+        from . import quant
+        n = 1
+        for d in weight.stored_shape:
+            n *= int(d)
+        quant._require_holds(weight.codes, weight.dtype, n, "weight codes")
+        return _aligned(weight.codes.to(dev).contiguous()), DTYPES[weight.dtype], weight.scale.to(dev)
     data = weight.data if isinstance(weight, Parameters) else weight
     w, _ = _to_device_f32(data, "weight")
     return w, DTYPES["f32"], None
@@ -76,7 +88,7 @@ def _bias_arg(bias, dev: torch.device) -> Optional[torch.Tensor]:
         return None
     data = bias.data if isinstance(bias, Parameters) else bias
     b, _ = _to_device_f32(data, "bias")
-    return b.reshape(-1).contiguous()
+    return _aligned(b.reshape(-1).contiguous())
 
 
 def _stream(dev: torch.device) -> int:
@@ -230,6 +242,13 @@ def linear_backward(grad, input, weight, bias: bool = True):
         raise ValueError(f"weight {tuple(wshape)} does not match grad {tuple(g.shape)} and "
                          f"input {tuple(x.shape)}")
     w, wdt, ws = _weight_args(weight, x.device)
+    if wdt == DTYPES["e2m1"] and (D_in % 2 or D_out % 2):
+        # nibble-packed codes transpose only with even sides: decode them to
+        # bf16 (exact for every E2M1 value, no scale) and multiply those same
+        # values, the scale applied after accumulation as for the codes
+        from . import quant
+        rows = quant.cast(w, "bf16", src_dtype="e2m1", n=D_out * weight.padded_cols)
+        w, wdt = rows.view(D_out, weight.padded_cols)[:, :D_in].contiguous(), DTYPES["bf16"]
     lib = _lib.load()
     gi = torch.empty((N, D_in), dtype=torch.float32, device=x.device)
     gw = torch.empty((D_out, D_in), dtype=torch.float32, device=x.device)

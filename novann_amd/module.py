@@ -1,22 +1,31 @@
-"""Parameter containers and layers with NovaNN's interface.
+"""Parameter containers, the module / layer contract, and layers with
+NovaNN's interface.
 
 ``Parameters`` mirrors novann/module/module.py:6-38 (``.data``, ``.grad``,
-``.name``).  ``QuantizedParameters`` is the packed replacement of ``.data``
-for quantized weights: device codes (E4M3 / E5M2 / E2M1) plus a per-tensor
-scale.  ``Linear`` mirrors novann/layers/linear/linear.py:10-108 and
-``Conv2d`` novann/layers/convolutional/conv2d.py:9-207 (same constructor
-arguments, parameter shapes and defaults, forward and backward); both call the
-GPU operators in ``functional``.  ``BatchNorm2d`` / ``BatchNorm1d`` hold the
-reference's parameters and running statistics (batchnorm2d.py:33-55,
-batchnorm1d.py:33-55) and ``ReLU`` stands for novann's ReLU layer; on this
-path they run fused into the product before them (``fuse``), in eval mode.
+``.name``), ``Module`` its train / eval / parameters / zero_grad contract
+(module.py:41-85) and ``Layer`` the callable forward / backward base
+(module/layer.py:6-59).  ``QuantizedParameters`` is the packed replacement of
+``.data`` for quantized weights: device codes (E4M3 / E5M2 / E2M1) plus a
+per-tensor scale.  ``Linear`` mirrors novann/layers/linear/linear.py:10-118
+and ``Conv2d`` novann/layers/convolutional/conv2d.py:9-217: same constructor
+arguments, ``reset_parameters`` with the reference's default initialisers
+drawn from numpy's global generator (so a seeded construction gives the
+reference's weights), parameter shapes, the float32 coercion of numpy inputs,
+forward and backward; both call the GPU operators in ``functional``.
+``BatchNorm2d`` / ``BatchNorm1d`` hold the reference's parameters and running
+statistics (batchnorm2d.py:33-55, batchnorm1d.py:33-55) and ``ReLU`` stands
+for novann's ReLU layer; on this path they run fused into the product before
+them (``fuse``), in eval mode.
 """
 from __future__ import annotations
 
+from abc import ABC, abstractmethod
 from typing import Optional
 
 import numpy as np
 import torch
+
+from .init import DEFAULT_NORMAL_INIT_MAP, DEFAULT_UNIFORM_INIT_MAP
 
 
 class Parameters:
@@ -53,7 +62,12 @@ class QuantizedParameters:
     value s, the weight being s * decode(codes); amax: max |w| the scale was
     derived from.  For training, ``master`` holds the fp32 weights the
     optimizer steps (the codes are re-quantized from them after each step)
-    and ``grad`` the gradient of the dequantized weight."""
+    and ``grad`` the gradient of the dequantized weight.
+
+    A 2-D E2M1 weight (a Linear's (out, in)) with an odd number of columns
+    keeps whole bytes per row: codes and master carry one zero column more
+    (``padded_cols``), whose +0 codes the products never read; a zero column
+    changes neither the amax nor, under AdamW (zero gradient), its value."""
 
     def __init__(self, codes: torch.Tensor, shape, dtype: str, scale: torch.Tensor,
                  amax: Optional[torch.Tensor] = None, name: Optional[str] = None,
@@ -67,6 +81,18 @@ class QuantizedParameters:
         self.master = master
         self.grad = None
 
+    @property
+    def padded_cols(self) -> int:
+        """Columns per stored row: the logical ones, plus one pad column for an
+        odd-width 2-D E2M1 weight."""
+        cols = self.shape[-1] if self.shape else 1
+        pad = self.dtype == "e2m1" and len(self.shape) == 2 and cols % 2 == 1
+        return cols + 1 if pad else cols
+
+    @property
+    def stored_shape(self) -> tuple:
+        return self.shape[:-1] + (self.padded_cols,) if self.shape else self.shape
+
     @classmethod
     def from_float(cls, w, dtype: str, device=None,
                    keep_master: bool = False) -> "QuantizedParameters":
@@ -79,9 +105,12 @@ class QuantizedParameters:
             dev = device or torch.device("cuda", torch.cuda.current_device())
             w = torch.from_numpy(np.ascontiguousarray(w, dtype=np.float32)).to(dev)
         w = w.to(torch.float32).contiguous()
+        shape = tuple(w.shape)
+        if dtype == "e2m1" and w.dim() == 2 and w.shape[1] % 2 == 1:
+            w = torch.nn.functional.pad(w, (0, 1))  # whole bytes per row
         q = quant.quantize(w, dtype)
         master = w.clone() if keep_master else None
-        return cls(q.data, q.shape, dtype, q.scale, q.amax, master=master)
+        return cls(q.data, shape, dtype, q.scale, q.amax, master=master)
 
     def zero_grad(self, set_to_none: bool = True) -> None:
         if set_to_none or self.grad is None:
@@ -94,18 +123,60 @@ class QuantizedParameters:
     def dequantize(self) -> torch.Tensor:
         """s * decode(codes) as an fp32 device tensor of the logical shape."""
         from . import quant
-        return quant.dequantize(quant.Quantized(self.codes, self.shape, self.dtype,
-                                                self.scale), "f32")
+        y = quant.dequantize(quant.Quantized(self.codes, self.stored_shape, self.dtype,
+                                             self.scale), "f32")
+        return y if self.stored_shape == self.shape else y[..., :self.shape[-1]].contiguous()
 
 
-def kaiming_normal_(shape, gain: float = float(np.sqrt(2.0)),
-                    rng: Optional[np.random.RandomState] = None) -> np.ndarray:
-    """N(0, (gain / sqrt(fan_in))^2) as fp32 (novann/core/init.py:155-179 with
-    the fan rules of :55-90: fan_in = shape[1] * prod(shape[2:]))."""
-    fan_in = int(shape[1]) * int(np.prod(shape[2:])) if len(shape) > 2 else int(shape[1])
-    std = gain / np.sqrt(fan_in)
-    gen = rng if rng is not None else np.random
-    return gen.normal(0.0, std, shape).astype(np.float32)
+class Module:
+    """Train / eval mode and parameter access (module.py:41-85): modules start
+    in training mode; ``parameters()`` is empty unless a subclass owns some;
+    ``zero_grad`` clears every parameter's gradient (``set_to_none`` as
+    Parameters.zero_grad)."""
+
+    def __init__(self) -> None:
+        self._training = True
+
+    def train(self) -> None:
+        self._training = True
+
+    def eval(self) -> None:
+        self._training = False
+
+    def parameters(self):
+        return []
+
+    def zero_grad(self) -> None:
+        for p in self.parameters():
+            p.zero_grad()
+
+
+class Layer(Module, ABC):
+    """A module called as ``layer(x)`` -> ``forward(x)``, with ``backward``
+    (module/layer.py:6-59)."""
+
+    def __call__(self, x):
+        return self.forward(x)
+
+    @abstractmethod
+    def forward(self, x):
+        raise NotImplementedError("Layer subclasses must implement forward method")
+
+    @abstractmethod
+    def backward(self, grad):
+        raise NotImplementedError("Layer subclasses must implement backward method")
+
+
+def _as_f32(x):
+    """The reference's layer-entry coercion ``x.astype(np.float32, copy=False)``
+    (linear.py:81, conv2d.py:159) for numpy inputs; device tensors and
+    quantized activations are the products' own input formats and pass as
+    they are, except float64, which becomes float32 as in numpy."""
+    if isinstance(x, np.ndarray):
+        return x.astype(np.float32, copy=False)
+    if isinstance(x, torch.Tensor) and x.dtype == torch.float64:
+        return x.float()
+    return x
 
 
 def _pair(v):
@@ -120,33 +191,46 @@ def _pair(v):
     return tuple(v)
 
 
-class Linear:
-    """Linear with an fp32 or quantized weight (linear.py:10-108).
+class Linear(Layer):
+    """Linear with an fp32 or quantized weight (linear.py:10-118).
 
-    weight (out_features, in_features); bias (1, out_features) zeros.  The
-    forward input is cached for ``backward`` (linear.py:81-82)."""
+    weight (out_features, in_features); bias (1, out_features) zeros.
+    ``reset_parameters`` draws the weight with ``initializer``, else ``init``,
+    else DEFAULT_NORMAL_INIT_MAP["default"] (``random_init_``, linear.py:47-68),
+    from numpy's global generator; ``weight_dtype`` ('e4m3' | 'e5m2' | 'e2m1')
+    then stores it quantized (per-tensor amax scale, fp32 master kept for the
+    optimizer).  The forward input, coerced to float32 as linear.py:81 does,
+    is cached for ``backward``."""
 
-    def __init__(self, in_features: int, out_features: int, bias: bool = True,
-                 weight_dtype: Optional[str] = None, init=None) -> None:
+    def __init__(self, in_features: int, out_features: int, bias: bool = True, init=None,
+                 weight_dtype: Optional[str] = None) -> None:
+        super().__init__()
         self.in_features, self.out_features = in_features, out_features
-        w = (init or kaiming_normal_)((out_features, in_features))
+        self.use_bias = bias
+        self.init_fn = init
+        self.weight_dtype = weight_dtype
+        self.weight = None
+        self.bias = None
+        self._cache_input = None
+        self.reset_parameters()
+
+    def reset_parameters(self, initializer=None) -> None:
+        init = initializer or self.init_fn or DEFAULT_NORMAL_INIT_MAP["default"]
+        w = init((self.out_features, self.in_features))
         self.weight = Parameters(np.asarray(w, dtype=np.float32))
         self.weight.name = "linear weight"
-        if weight_dtype is not None:
-            self.weight = QuantizedParameters.from_float(self.weight, weight_dtype,
+        if self.weight_dtype is not None:
+            self.weight = QuantizedParameters.from_float(self.weight, self.weight_dtype,
                                                          keep_master=True)
             self.weight.name = "linear weight"
         self.bias = None
-        if bias:
-            self.bias = Parameters(np.zeros((1, out_features), dtype=np.float32))
+        if self.use_bias:
+            self.bias = Parameters(np.zeros((1, self.out_features), dtype=np.float32))
             self.bias.name = "linear bias"
-        self._cache_input = None
-
-    def __call__(self, x):
-        return self.forward(x)
 
     def forward(self, x):
         from . import functional as F
+        x = _as_f32(x)
         self._cache_input = x
         return F.linear(x, self.weight, self.bias)
 
@@ -154,7 +238,7 @@ class Linear:
         """Sets weight.grad = grad.T @ x and bias.grad = grad summed over the
         batch, returns grad @ W (linear.py:85-108)."""
         from . import functional as F
-        gi, gw, gb = F.linear_backward(grad, self._cache_input, self.weight,
+        gi, gw, gb = F.linear_backward(_as_f32(grad), self._cache_input, self.weight,
                                        self.bias is not None)
         self.weight.grad = gw
         if self.bias is not None:
@@ -164,41 +248,57 @@ class Linear:
     def parameters(self):
         return [self.weight] + ([self.bias] if self.bias is not None else [])
 
+    def __repr__(self) -> str:
+        return (f"Linear(in_features={self.in_features}, out_features={self.out_features}, "
+                f"bias={self.use_bias})")
 
-class Conv2d:
-    """Conv2d with an fp32 or quantized weight (conv2d.py:9-207); the forward
-    input is cached for ``backward`` (the reference caches its im2col matrix,
-    conv2d.py:173-175; here the input itself, the matrix is never built).
+
+class Conv2d(Layer):
+    """Conv2d with an fp32 or quantized weight (conv2d.py:9-217).
 
     weight (out_channels, in_channels, KH, KW); bias (out_channels, 1) zeros;
-    stride defaults to 1 (a None stride means kernel_size, conv2d.py:41)."""
+    stride defaults to 1 (a None stride means kernel_size, conv2d.py:41).
+    ``reset_parameters`` draws the weight with ``initializer``, else ``init``,
+    else DEFAULT_UNIFORM_INIT_MAP["relu"] (Kaiming-uniform for ReLU,
+    conv2d.py:55-72), from numpy's global generator; ``weight_dtype`` stores it
+    quantized as in Linear.  The forward input, coerced to float32 as
+    conv2d.py:159 does, is cached for ``backward`` (the reference caches its
+    im2col matrix, conv2d.py:173-175; this path never builds one)."""
 
     def __init__(self, in_channels: int, out_channels: int, kernel_size, stride=1,
-                 padding=0, bias: bool = True, padding_mode: str = "zeros",
-                 weight_dtype: Optional[str] = None, init=None) -> None:
+                 padding=0, bias: bool = True, padding_mode: str = "zeros", init=None,
+                 weight_dtype: Optional[str] = None) -> None:
+        super().__init__()
         self.in_channels, self.out_channels = in_channels, out_channels
         self.KH, self.KW = _pair(kernel_size)
         self.sh, self.sw = _pair(stride if stride is not None else kernel_size)
         self.ph, self.pw = _pair(padding)
         self.pm = padding_mode
-        w = (init or kaiming_normal_)((out_channels, in_channels, self.KH, self.KW))
+        self.init_fn = init
+        self.use_bias = bias
+        self.weight_dtype = weight_dtype
+        self.weight = None
+        self.bias = None
+        self._cache_input = None
+        self.reset_parameters()
+
+    def reset_parameters(self, initializer=None) -> None:
+        init = initializer or self.init_fn or DEFAULT_UNIFORM_INIT_MAP["relu"]
+        w = init((self.out_channels, self.in_channels, self.KH, self.KW))
         self.weight = Parameters(np.asarray(w, dtype=np.float32))
         self.weight.name = "conv2d weight"
-        if weight_dtype is not None:
-            self.weight = QuantizedParameters.from_float(self.weight, weight_dtype,
+        if self.weight_dtype is not None:
+            self.weight = QuantizedParameters.from_float(self.weight, self.weight_dtype,
                                                          keep_master=True)
             self.weight.name = "conv2d weight"
         self.bias = None
-        if bias:
-            self.bias = Parameters(np.zeros((out_channels, 1), dtype=np.float32))
+        if self.use_bias:
+            self.bias = Parameters(np.zeros((self.out_channels, 1), dtype=np.float32))
             self.bias.name = "conv2d bias"
-        self._cache_input = None
-
-    def __call__(self, x):
-        return self.forward(x)
 
     def forward(self, x):
         from . import functional as F
+        x = _as_f32(x)
         self._cache_input = x
         return F.conv2d(x, self.weight, (self.KH, self.KW), (self.sh, self.sw),
                         (self.ph, self.pw), bias=self.bias, padding_mode=self.pm)
@@ -207,7 +307,7 @@ class Conv2d:
         """Sets weight.grad and bias.grad, returns the input gradient
         (conv2d.py:179-207)."""
         from . import functional as F
-        gi, gw, gb = F.conv2d_backward(grad, self._cache_input, self.weight,
+        gi, gw, gb = F.conv2d_backward(_as_f32(grad), self._cache_input, self.weight,
                                        (self.KH, self.KW), (self.sh, self.sw),
                                        (self.ph, self.pw), bias=self.bias is not None,
                                        padding_mode=self.pm)
@@ -220,13 +320,14 @@ class Conv2d:
         return [self.weight] + ([self.bias] if self.bias is not None else [])
 
 
-class _BatchNorm:
+class _BatchNorm(Module):
     """Parameters and running statistics of novann's BatchNorm layers, used
     as an eval-mode epilogue of the product before them."""
 
     _shape_tail: tuple = ()
 
     def __init__(self, num_features: int, momentum: float = 0.1, eps: float = 1e-5) -> None:
+        super().__init__()
         self.num_features = int(num_features)
         self.momentum, self.eps = float(momentum), float(eps)
         shape = (1, self.num_features) + self._shape_tail
@@ -257,12 +358,12 @@ class BatchNorm1d(_BatchNorm):
     _shape_tail = ()
 
 
-class ReLU:
+class ReLU(Module):
     """novann's ReLU layer (relu.py:8-48): x * (x > 0), fused into the
     product before it."""
 
 
-class Fused:
+class Fused(Module):
     """A Linear or Conv2d followed by an eval-mode BatchNorm and / or a ReLU,
     run as one product whose epilogue applies them (the layers that follow a
     product on novann's main path, main.py:24-46).  ``out_dtype`` 'bf16',
@@ -276,8 +377,12 @@ class Fused:
         want = BatchNorm2d if isinstance(layer, Conv2d) else BatchNorm1d
         if bn is not None and not isinstance(bn, want):
             raise TypeError(f"fuse: {type(layer).__name__} is followed by {want.__name__}")
+        super().__init__()
         self.layer, self.bn, self.relu = layer, bn, relu
         self.out_dtype, self.out_scale = out_dtype, out_scale
+
+    def parameters(self):
+        return self.layer.parameters() + (self.bn.parameters() if self.bn is not None else [])
 
     def __call__(self, x, out_amax=None):
         return self.forward(x, out_amax)
@@ -309,11 +414,12 @@ def fuse(*layers, out_dtype: str = "f32", out_scale=None) -> Fused:
     return Fused(head, bn, relu, out_dtype, out_scale)
 
 
-class MaxPool2d:
+class MaxPool2d(Module):
     """novann MaxPool2d (layers/pooling/maxpool/maxpool2d.py:8-79): kernel,
     stride (None = kernel size), padding, padding_mode; forward on the GPU."""
 
     def __init__(self, kernel_size, stride=None, padding=0, padding_mode: str = "zeros") -> None:
+        super().__init__()
         self.KH, self.KW = _pair(kernel_size)
         self.sh, self.sw = _pair(stride if stride is not None else kernel_size)
         self.ph, self.pw = _pair(padding)
@@ -328,7 +434,7 @@ class MaxPool2d:
                             padding_mode=self.pm)
 
 
-class GlobalAvgPool2d:
+class GlobalAvgPool2d(Module):
     """novann GlobalAvgPool2d (layers/pooling/gap/global_avg_pool2d.py:7-32):
     (N, C, H, W) -> (N, C, 1, 1) means, on the GPU."""
 

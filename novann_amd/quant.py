@@ -40,6 +40,18 @@ def storage_numel(dtype: str, n: int) -> int:
     return (n + 1) // 2 if dtype == "e2m1" else n
 
 
+_BITS = {"f32": 32, "f16": 16, "bf16": 16, "e4m3": 8, "e5m2": 8, "e2m1": 4}
+
+
+def _require_holds(t: torch.Tensor, dtype: str, n: int, what: str) -> None:
+    """ValueError unless t's storage holds n logical elements of dtype (the
+    kernels would otherwise read or write past the end of the buffer)."""
+    need = (n * _BITS[dtype] + 7) // 8
+    have = t.numel() * t.element_size()
+    if have < need:
+        raise ValueError(f"{what} holds {have} bytes, {n} {dtype} elements need {need}")
+
+
 def _stream(t: torch.Tensor) -> int:
     return torch.cuda.current_stream(t.device).cuda_stream
 
@@ -49,6 +61,13 @@ def _require_device(t: torch.Tensor, what: str) -> None:
         raise ValueError(f"{what} must be a CUDA (HIP) device tensor")
     if not t.is_contiguous():
         raise ValueError(f"{what} must be contiguous")
+
+
+def _aligned16(t: torch.Tensor) -> torch.Tensor:
+    """t itself when its data starts on a 16-byte boundary (what the kernels'
+    vector accesses need), else an aligned copy: a view into a larger tensor
+    works, at the cost of the copy."""
+    return t if t.data_ptr() % 16 == 0 else t.clone()
 
 
 def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
@@ -75,11 +94,24 @@ def cast(src: torch.Tensor, dst_dtype: str, *, src_dtype: Optional[str] = None,
     st, dt = _dtype_code(src_dtype), _dtype_code(dst_dtype)
     if n is None:
         n = src.numel() * 2 if src_dtype == "e2m1" else src.numel()
+    n = int(n)
+    if n < 0:
+        raise ValueError(f"cast: negative element count {n}")
+    _require_holds(src, src_dtype, n, "src")
+    src = _aligned16(src)
+    target = None
     if out is None:
         out = torch.empty(storage_numel(dst_dtype, n), dtype=STORAGE[dst_dtype],
                           device=src.device)
     else:
         _require_device(out, "out")
+        if out.dtype != STORAGE[dst_dtype]:
+            raise TypeError(f"out must be {STORAGE[dst_dtype]} for {dst_dtype}, got {out.dtype}")
+        _require_holds(out, dst_dtype, n, "out")
+        if out.data_ptr() % 16:
+            # write into an aligned buffer, then copy into the caller's view
+            target, out = out, torch.empty(storage_numel(dst_dtype, n),
+                                           dtype=STORAGE[dst_dtype], device=src.device)
     if scale is not None:
         _require_device(scale, "scale")
         if scale.dtype != torch.float32:
@@ -87,12 +119,16 @@ def cast(src: torch.Tensor, dst_dtype: str, *, src_dtype: Optional[str] = None,
     lib = _lib.load()
     check(lib.novaq_cast(src.data_ptr(), st, out.data_ptr(), dt, n, _ptr(scale),
                          _stream(src)), f"cast {src_dtype}->{dst_dtype}")
+    if target is not None:
+        target.reshape(-1)[:out.numel()].copy_(out)
+        return target
     return out
 
 
 def amax(x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """NaN-ignoring max |x| as a one-element fp32 device tensor."""
     _require_device(x, "x")
+    x = _aligned16(x)
     if out is None:
         out = torch.empty(1, dtype=torch.float32, device=x.device)
     check(_lib.load().novaq_amax(x.data_ptr(), _dtype_code(dtype_of(x)), x.numel(),
@@ -126,12 +162,20 @@ class Quantized:
             n *= int(d)
         return n
 
+    def check(self, what: str = "quantized tensor") -> None:
+        """ValueError unless ``data`` holds the codes of prod(shape) elements."""
+        if self.dtype not in QUANTIZED:
+            raise TypeError(f"{what}: dtype must be one of {QUANTIZED}, got {self.dtype}")
+        _require_device(self.data, f"{what} data")
+        _require_holds(self.data, self.dtype, self.numel, f"{what} data")
+
 
 def quantize(x: torch.Tensor, dst_dtype: str) -> Quantized:
     """amax -> s = amax / fmt_max -> encode(x * (1/s)), all on the device."""
     _require_device(x, "x")
     if dst_dtype not in QUANTIZED:
         raise TypeError(f"quantize target must be one of {QUANTIZED}")
+    x = _aligned16(x)
     n = x.numel()
     data = torch.empty(storage_numel(dst_dtype, n), dtype=STORAGE[dst_dtype], device=x.device)
     st = torch.empty(2, dtype=torch.float32, device=x.device)
@@ -144,6 +188,7 @@ def quantize(x: torch.Tensor, dst_dtype: str) -> Quantized:
 
 def dequantize(q: Quantized, dst_dtype: str = "f32") -> torch.Tensor:
     """decode(q) * s in the requested float type, reshaped to q.shape."""
+    q.check()
     y = cast(q.data, dst_dtype, src_dtype=q.dtype, n=q.numel, scale=q.scale)
     return y.view(q.shape)
 

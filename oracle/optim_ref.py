@@ -37,3 +37,23 @@ def adamw_step(w, g, m, v, t: int, lr: float, b1: float = 0.9, b2: float = 0.999
         w -= lr * wd * w
     assert w.dtype == m.dtype == v.dtype == np.float32
     return w, m, v
+
+
+def adamw_step_f64(w, g, m, v, t: int, lr: float, b1: float = 0.9, b2: float = 0.999,
+                   eps: float = 1e-8, wd: float = 0.0, decay: bool = True):
+    """The same statements on a float64 parameter with float64 moments (the
+    reference's BatchNorm gamma / beta are float64 arrays, batchnorm2d.py:
+    33-55, and ``np.zeros_like`` gives their moments that dtype).  ``g`` keeps
+    its own dtype: numpy forms ``(1 - b1) * g`` and ``g ** 2`` in float32 for a
+    float32 gradient (a Python float does not widen an array) and widens only
+    when adding them to the float64 moments.  Returns new (w, m, v)."""
+    w = np.array(w, dtype=np.float64)
+    m = b1 * np.asarray(m, np.float64) + (1 - b1) * g
+    v = b2 * np.asarray(v, np.float64) + (1 - b2) * (g ** 2)
+    m_hat = m / (1 - b1 ** t)
+    v_hat = v / (1 - b2 ** t)
+    w -= lr * m_hat / (np.sqrt(v_hat) + eps)
+    if wd > 0 and decay:
+        w -= lr * wd * w
+    assert w.dtype == m.dtype == v.dtype == np.float64
+    return w, m, v

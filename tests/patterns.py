@@ -40,7 +40,7 @@ def config1_tensor(seed: int = 1, shape=(4096, 4096)) -> np.ndarray:
     k = int(special.sum())
     kind = rng.integers(0, 6, size=k)
     vals = np.empty(k, dtype=np.float32)
-    sgn = np.where(rng.random(k) < 0.5, -1.0, 1.0).astype(np.float32)
+    neg = rng.random(k) < 0.5
     # 0: signed zeros
     vals[kind == 0] = 0.0
     # 1: infinities
@@ -67,7 +67,10 @@ def config1_tensor(seed: int = 1, shape=(4096, 4096)) -> np.ndarray:
     # 5: fp32 subnormals and tiny values
     m5 = kind == 5
     vals[m5] = rng.integers(1, 1 << 23, size=int(m5.sum()), dtype=np.uint32).view(np.float32)
-    x[special] = vals * sgn
+    # the sign goes in as a bit: a float multiply would quiet the signalling
+    # NaNs and, on x86, keep a NaN operand's own sign
+    bits = vals.view(np.uint32) | np.where(neg, np.uint32(0x80000000), np.uint32(0))
+    x[special] = bits.astype(np.uint32).view(np.float32)
     return x.reshape(shape)
 
 

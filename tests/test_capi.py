@@ -66,10 +66,11 @@ def test_other_entry_points_validation():
     assert lib.novaq_quantize(FAKE, 0, FAKE, 1, 16, FAKE, None) == _lib.EDTYPE
     assert lib.novaq_quantize(FAKE, 3, FAKE, 4, 16, FAKE, None) == _lib.EDTYPE
     assert lib.novaq_quantize(FAKE, 0, FAKE, 3, 16, None, None) == _lib.EINVAL
-    # linear: bad dtype, negative size, odd packed rows, misaligned
+    # linear: bad dtype, negative size, misaligned (odd E2M1 rows are valid:
+    # each row is padded to whole bytes)
     assert lib.novaq_linear_forward(FAKE, 4, 8, FAKE, 7, None, None, 4, FAKE, None) == _lib.EDTYPE
     assert lib.novaq_linear_forward(FAKE, -1, 8, FAKE, 3, None, None, 4, FAKE, None) == _lib.EINVAL
-    assert lib.novaq_linear_forward(FAKE, 4, 7, FAKE, 5, None, None, 4, FAKE, None) == _lib.ESHAPE
+    assert lib.novaq_linear_forward(FAKE, 4, 7, FAKE, 5, None, None, 4, FAKE + 8, None) == _lib.EALIGN
     assert lib.novaq_linear_forward(FAKE, 4, 8, FAKE + 1, 3, None, None, 4, FAKE, None) == _lib.EALIGN
     assert lib.novaq_linear_forward(None, 0, 8, None, 3, None, None, 4, None, None) == _lib.OK
     # conv2d: pad mode, geometry, kernel larger than padded input
@@ -158,7 +159,7 @@ def test_fused_forward_validation():
     assert lcall(a6=9) == _lib.EDTYPE                      # weight dtype
     assert lcall(a10=ctypes.byref(bad_out)) == _lib.EDTYPE  # FP4 output
     assert lcall(a3=-1) == _lib.EINVAL
-    assert lcall(a6=_lib.E2M1, a4=7) == _lib.ESHAPE        # odd D_in for E2M1 rows
+    assert lcall(a6=_lib.E2M1, a4=7, a11=FAKE + 8) == _lib.EALIGN  # odd E2M1 rows pass the shape checks
     assert lcall(a0=FAKE + 4) == _lib.EALIGN
     assert lcall(a10=ctypes.byref(odd)) == _lib.EALIGN      # epilogue pointer
     assert lcall(a3=0, a10=ctypes.byref(ep)) == _lib.OK     # empty batch
@@ -206,6 +207,9 @@ def test_optimizer_and_pool_validation():
     assert mcall(a6=11) == _lib.ESHAPE
     assert mcall(a8=0) == _lib.EINVAL
     assert mcall(a2=0) == _lib.OK
+    # views need element alignment only; a pointer inside an element is refused
+    assert mcall(a0=FAKE + 2) == _lib.EALIGN
+    assert mcall(a13=FAKE + 1, a1=_lib.BF16) == _lib.EALIGN
     gap = lib.novaq_global_avg_pool2d
     assert gap(FAKE, _lib.E2M1, None, 2, 3, 4, 4, FAKE, None) == _lib.EDTYPE
     assert gap(FAKE, _lib.F32, None, 2, 0, 4, 4, FAKE, None) == _lib.EINVAL

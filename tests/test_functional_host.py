@@ -5,7 +5,7 @@ import numpy as np
 import pytest
 
 from novann_amd import functional as F
-from novann_amd.module import Parameters, _pair, kaiming_normal_
+from novann_amd.module import Parameters, _pair
 
 
 def test_pair_rules():
@@ -40,16 +40,6 @@ def test_conv2d_extras_not_available():
         F.conv2d(x, w, 3, extras=True)
 
 
-def test_kaiming_normal_statistics():
-    """std = sqrt(2 / fan_in), fan_in = C*KH*KW (novann/core/init.py:55-90,155-179)."""
-    rng = np.random.RandomState(0)
-    w = kaiming_normal_((64, 32, 3, 3), rng=rng)
-    assert w.dtype == np.float32 and w.shape == (64, 32, 3, 3)
-    assert abs(w.std() - np.sqrt(2.0 / 288)) < 0.01 * np.sqrt(2.0 / 288) * 5
-    w = kaiming_normal_((4096, 4096), rng=rng)
-    assert abs(w.std() - np.sqrt(2.0 / 4096)) < 1e-3
-
-
 def test_fuse_validates_the_layer_sequence():
     """fuse() takes [Linear|Conv2d] [BatchNorm] [ReLU], in that order (host logic)."""
     from novann_amd import module as M
@@ -65,3 +55,20 @@ def test_fuse_validates_the_layer_sequence():
     bn = M.BatchNorm2d(3)
     assert bn.gamma.data.shape == (1, 3, 1, 1) and bn.running_var.shape == (1, 3, 1, 1)
     assert M.BatchNorm1d(5).running_mean.shape == (1, 5)
+
+
+def test_storage_size_checks():
+    """The host layer refuses buffers too small for the element count before
+    any launch (a kernel would read or write past their end)."""
+    import torch
+
+    from novann_amd import quant
+    quant._require_holds(torch.empty(4, dtype=torch.float32), "f32", 4, "x")
+    quant._require_holds(torch.empty(3, dtype=torch.uint8), "e2m1", 5, "x")   # ceil(5/2) bytes
+    quant._require_holds(torch.empty(2, dtype=torch.float32), "e4m3", 8, "x")  # bytes count
+    with pytest.raises(ValueError, match="need"):
+        quant._require_holds(torch.empty(3, dtype=torch.float32), "f32", 4, "x")
+    with pytest.raises(ValueError, match="need"):
+        quant._require_holds(torch.empty(2, dtype=torch.uint8), "e2m1", 5, "x")
+    with pytest.raises(ValueError, match="need"):
+        quant._require_holds(torch.empty(7, dtype=torch.int16), "f16", 8, "x")

@@ -191,3 +191,57 @@ def test_quantize_empty_tensor():
     q = quant.quantize(x, "e5m2")
     torch.cuda.synchronize()
     assert q.amax.item() == 0.0 and q.scale.item() == 1.0
+
+
+def test_host_layer_refuses_short_buffers():
+    """quant.cast / dequantize / the products check element counts against
+    the buffers before launching (ValueError, as numpy raises for a size
+    mismatch)."""
+    from novann_amd import functional as F
+    from novann_amd import quant
+    from novann_amd.module import Parameters
+    x = torch.ones(100, device="cuda")
+    with pytest.raises(ValueError):
+        quant.cast(x, "e4m3", n=101)
+    with pytest.raises(ValueError):
+        quant.cast(x, "f16", out=torch.empty(99, dtype=torch.float16, device="cuda"))
+    with pytest.raises(TypeError):
+        quant.cast(x, "f16", out=torch.empty(100, dtype=torch.bfloat16, device="cuda"))
+    q = quant.quantize(x, "e4m3")
+    bad = quant.Quantized(q.data[:50], (100,), "e4m3", q.scale)
+    with pytest.raises(ValueError):
+        quant.dequantize(bad)
+    xq = quant.quantize(torch.ones((4, 8), device="cuda"), "e4m3")
+    short = quant.Quantized(xq.data[:16], (4, 8), "e4m3", xq.scale)
+    with pytest.raises(ValueError):
+        F.linear(short, Parameters(np.ones((2, 8), np.float32)), None)
+    assert quant.cast(x, "f16", n=100).numel() == 100
+
+
+@pytest.mark.parametrize("st", [O.F16, O.BF16], ids=lambda d: NAME[d])
+@pytest.mark.parametrize("dt", QUANT, ids=lambda d: NAME[d])
+@pytest.mark.parametrize("n", [1, 4097, (1 << 20) + 5])
+def test_scaled_quantize_from_16bit_sources(st, dt, n):
+    """novaq_quantize from fp16 / bf16 sources (amax of the 16-bit values,
+    s = amax / fmt_max, enc(x * (1/s))) and novaq_cast with explicit scales,
+    bit-exact against the oracle; the input carries NaNs (ignored by the
+    amax), signed zeros and exact E2M1 / FP8 ties after scaling."""
+    print(f"scaled quantize {NAME[st]} -> {NAME[dt]} n={n}", flush=True)
+    rng = np.random.default_rng(n + 31 * st + dt)
+    f = (rng.standard_normal(n) * np.exp2(rng.uniform(-10, 10, n))).astype(np.float32)
+    if n > 10:
+        f[rng.integers(0, n, 7)] = np.nan
+        f[rng.integers(0, n, 7)] = -0.0
+        f[rng.integers(0, n, 7)] = np.float32(2.5) * np.float32(np.abs(f[0]) + 1)
+    src = O.cast(f, O.F32, st)
+    q = quant.quantize(to_dev(src, st), NAME[dt])
+    torch.cuda.synchronize()
+    a = O.amax(src, st)
+    s = O.scale_from_amax(a, dt)
+    assert q.amax.item() == a and q.scale.item() == s
+    want = O.cast(src, st, dt, n=n, scale=s)
+    assert (m := first_mismatch(to_host(q.data), want)) is None, m
+    for scale in (0.0123, -0.75, 7e30, 0.0):
+        got = gpu_cast(src, st, dt, n=n, scale=scale)
+        want = O.cast(src, st, dt, n=n, scale=scale)
+        assert (m := first_mismatch(got, want)) is None, (scale, m)

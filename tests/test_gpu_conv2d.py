@@ -147,3 +147,46 @@ def test_layer_shape_contracts_like_reference():
         layer = Conv2d(1, 2, kernel_size=3, padding=2, padding_mode=mode, bias=False)
         out = layer(np.ones((1, 1, 8, 8), dtype=np.float32))
         assert out.shape[:2] == (1, 2)
+
+
+@pytest.mark.parametrize("wdt,mode,xs,ws,stride,pad", [
+    ("e2m1", "zeros", (1, 64, 3, 4096), (8, 64, 3, 3), (1, 1), (1, 1)),
+    ("e4m3", "reflect", (2, 3, 4, 3000), (5, 3, 3, 5), (1, 2), (1, 2)),
+    ("f32", "circular", (1, 80, 2, 2500), (3, 80, 2, 3), (1, 1), (0, 1)),
+])
+def test_rows_too_wide_for_lds(wdt, mode, xs, ws, stride, pad):
+    """Images whose padded rows do not fit in LDS take the direct-gather
+    kernel (no NOVAQ_ENOTSUP), within the same tolerance, with an epilogue."""
+    print(f"conv2d wide rows {wdt} {mode} {xs} {ws}", flush=True)
+    rng = np.random.default_rng(xs[3])
+    x = rng.uniform(-1, 1, xs).astype(np.float32)
+    w = (rng.standard_normal(ws) * np.sqrt(2.0 / np.prod(ws[1:]))).astype(np.float32)
+    codes, s, wdeq = quantize_weights(w, wdt)
+    b = rng.standard_normal(ws[0]).astype(np.float32)
+    y = run_conv(x, codes, wdt, ws, s, b, stride, pad, mode)
+    r = O.conv2d_f64(x, wdeq, stride, pad, mode, b)
+    assert y.shape == r.shape and normwise(y, r) <= TOL
+    # the same launch through the layer path with a ReLU epilogue
+    wq = Parameters(wdeq) if wdt == "f32" else QuantizedParameters(
+        to_dev(codes, QCODE[wdt]), ws, wdt, torch.tensor([s], device="cuda"))
+    yr = F.conv2d(x, wq, ws[2:], stride, pad, bias=Parameters(b.reshape(-1, 1)),
+                  padding_mode=mode, epilogue=F.Epilogue(relu=True))
+    assert normwise(yr, np.maximum(r, 0.0)) <= TOL
+
+
+def test_backward_rows_too_wide_for_lds():
+    """Conv2d.backward on a wide image: grad_input's flipped-weight convolution
+    falls back to the direct gather; all gradients within tolerance."""
+    N, C, H, W, Co = 1, 64, 3, 4096, 8
+    rng = np.random.default_rng(5)
+    x = rng.uniform(-1, 1, (N, C, H, W)).astype(np.float32)
+    w = (rng.standard_normal((Co, C, 3, 3)) * np.sqrt(2.0 / (C * 9))).astype(np.float32)
+    codes, s, wdeq = quantize_weights(w, "e2m1")
+    wq = QuantizedParameters(to_dev(codes, O.E2M1), w.shape, "e2m1",
+                             torch.tensor([s], device="cuda"))
+    g = rng.standard_normal((N, Co, H, W)).astype(np.float32)
+    gi, gw, gb = F.conv2d_backward(g, x, wq, 3, 1, 1, bias=True)
+    ri, rw, rb = R.conv2d_backward(g.astype(np.float64), x.astype(np.float64),
+                                   wdeq.astype(np.float64), (1, 1), (1, 1))
+    assert normwise(gi, ri) <= TOL and normwise(gw, rw) <= TOL
+    assert normwise(gb.reshape(-1), rb.reshape(-1)) <= TOL

@@ -93,20 +93,24 @@ def test_golden_fixture(golden):
 
 @pytest.mark.parametrize("wdt", ["e4m3", "e5m2", "e2m1"])
 @pytest.mark.parametrize("M,N,K", [(1, 5, 10), (7, 300, 64), (130, 257, 130), (256, 512, 96),
-                                   (33, 31, 4098), (2, 3, 2)])
+                                   (33, 31, 4098), (2, 3, 2), (1, 5, 11), (33, 31, 4097),
+                                   (130, 257, 129), (3, 4, 1)])
 @pytest.mark.parametrize("with_bias", [True, False])
 def test_ragged_shapes_vs_oracle(wdt, M, N, K, with_bias):
-    if wdt == "e2m1" and K % 2:
-        pytest.skip("E2M1 rows are whole bytes")
+    """Any shape; E2M1 rows of odd length are stored as whole bytes (a +0
+    pad nibble ends each row)."""
+    print(f"linear ragged {wdt} {M}x{N}x{K} bias={with_bias}", flush=True)
     rng = np.random.default_rng(M * 7 + N * 3 + K)
     x = rng.standard_normal((M, K)).astype(np.float32)
     w = (rng.standard_normal((N, K)) * np.sqrt(2.0 / K)).astype(np.float32)
     c = QCODE[wdt]
     s = O.scale_from_amax(O.amax(w), c)
-    codes = O.cast(w.reshape(-1), O.F32, c, scale=s)
+    kp = K + (K % 2 if wdt == "e2m1" else 0)
+    wp = np.pad(w, ((0, 0), (0, kp - K)))
+    codes = O.cast(wp.reshape(-1), O.F32, c, scale=s)
     b = rng.standard_normal(N).astype(np.float32) if with_bias else None
     y = run_linear(x, codes, wdt, s, b, N, K)
-    r = O.linear_f64(x, dequant(codes, wdt, N * K, s).reshape(N, K), b)
+    r = O.linear_f64(x, dequant(codes, wdt, N * kp, s).reshape(N, kp)[:, :K], b)
     assert normwise(y, r.astype(np.float64)) <= TOL
 
 
@@ -306,3 +310,61 @@ def test_fp8_x_vs_oracle(xdt, wdt):
     xd = dequant(xc, xdt, M * K, sx).reshape(M, K).astype(np.float64)
     wd = dequant(wc, wdt, N * K, sw).reshape(N, K).astype(np.float64)
     assert normwise(y, xd @ wd.T) <= 1e-4
+
+
+def test_odd_width_e2m1_layer_forward_backward_step():
+    """A Linear(11 -> 6) with E2M1 weights: rows stored as whole bytes, the
+    forward and all three gradients against the oracle, and an AdamW step that
+    keeps the pad column at zero and the re-quantized codes consistent."""
+    from oracle import functional_ref as R
+    from novann_amd.optim import AdamW
+    rng = np.random.RandomState(3)
+    layer = Linear(11, 6, bias=True, weight_dtype="e2m1")
+    assert layer.weight.stored_shape == (6, 12) and layer.weight.codes.numel() == 36
+    x = rng.randn(9, 11).astype(np.float32)
+    wdeq = layer.weight.dequantize().cpu().numpy()
+    assert wdeq.shape == (6, 11)
+    y = layer(x)
+    r = O.linear_f64(x, wdeq, layer.bias.data)
+    assert normwise(y, r) <= TOL
+    G = rng.randn(9, 6).astype(np.float32)
+    gi = layer.backward(G)
+    ri, rw, rb = R.linear_backward(G.astype(np.float64), x.astype(np.float64),
+                                   wdeq.astype(np.float64))
+    assert normwise(gi, ri) <= TOL and normwise(layer.weight.grad, rw) <= TOL
+    assert normwise(layer.bias.grad, rb) <= TOL
+    opt = AdamW(layer.parameters(), lr=1e-2)
+    opt.step()
+    torch.cuda.synchronize()
+    m = layer.weight.master.cpu().numpy()
+    assert m.shape == (6, 12) and not m[:, 11].any()
+    codes = to_host(layer.weight.codes)
+    s = float(layer.weight.scale.cpu()[0])
+    assert np.array_equal(codes, O.cast(m.reshape(-1), O.F32, O.E2M1, scale=s))
+    assert codes.reshape(6, 6)[:, 5].max() >> 4 == 0   # pad nibbles are +0
+
+
+def test_misaligned_device_views_are_copied_not_refused():
+    """Views starting inside a 16-byte group (slices of a larger tensor) work
+    through the host layer: products, casts (input and output views) and
+    quantize give the results of the aligned tensors."""
+    rng = np.random.default_rng(12)
+    M, K, N = 8, 64, 32
+    big = torch.from_numpy(rng.standard_normal(M * K + 1).astype(np.float32)).cuda()
+    x = big[1:].view(M, K)
+    assert x.data_ptr() % 16 != 0
+    w = (rng.standard_normal((N, K)) * 0.1).astype(np.float32)
+    wq = QuantizedParameters.from_float(w, "e4m3")
+    y = F.linear(x, wq, None)
+    y_ref = F.linear(x.clone(), wq, None)
+    torch.cuda.synchronize()
+    assert torch.equal(y.cpu(), y_ref.cpu())
+    out = torch.empty(M * K + 3, dtype=torch.float16, device="cuda")
+    got = quant.cast(big[1:], "f16", out=out[3:])
+    torch.cuda.synchronize()
+    assert got.data_ptr() == out[3:].data_ptr()
+    assert torch.equal(out[3:].cpu(), quant.cast(big[1:].clone(), "f16").cpu())
+    q1, q2 = quant.quantize(big[1:], "e4m3"), quant.quantize(big[1:].clone(), "e4m3")
+    torch.cuda.synchronize()
+    assert torch.equal(q1.data.view(torch.uint8).cpu(), q2.data.view(torch.uint8).cpu())
+    assert q1.scale.item() == q2.scale.item()

@@ -131,3 +131,56 @@ def test_training_steps_reduce_the_loss():
         opt.step()
         opt.zero_grad()
     assert losses[-1] < 0.5 * losses[0], losses
+
+
+@pytest.mark.parametrize("gdt", [np.float32, np.float64])
+@pytest.mark.parametrize("n", [1, 37, 4096 + 5])
+def test_float64_entry_point_bit_exact(gdt, n):
+    """novaq_adamw_step_f64 against the oracle's float64 statements (numpy's
+    promotion of a float32 gradient included), 4 steps, with and without
+    decay."""
+    print(f"adamw f64 n={n} grad {np.dtype(gdt).name}", flush=True)
+    rng = np.random.default_rng(n)
+    lib = _lib.load()
+    for decay in (1, 0):
+        w = rng.standard_normal(n)
+        m, v = np.zeros(n), np.zeros(n)
+        wd_, md, vd = (torch.from_numpy(a.copy()).cuda() for a in (w, m, v))
+        for t in range(1, 5):
+            g = rng.standard_normal(n).astype(gdt)
+            gd = torch.from_numpy(g).cuda()
+            hp = _lib.AdamW(3e-2, 0.9, 0.999, 1e-8, 0.1, t, decay)
+            assert lib.novaq_adamw_step_f64(wd_.data_ptr(), gd.data_ptr(), int(gdt == np.float32),
+                                            md.data_ptr(), vd.data_ptr(), n, ctypes.byref(hp),
+                                            stream()) == _lib.OK
+            w, m, v = OR.adamw_step_f64(w, g, m, v, t, 3e-2, wd=0.1, decay=bool(decay))
+        torch.cuda.synchronize()
+        for got, want in ((wd_, w), (md, m), (vd, v)):
+            assert np.array_equal(got.cpu().numpy().view(np.uint64), want.view(np.uint64))
+
+
+def test_batchnorm_parameters_as_constructed():
+    """BatchNorm2d's gamma / beta are float64 (as in the reference) and step in
+    float64 with float64 moments; a float32 gradient is promoted as numpy
+    does.  Changing .data between steps counts, as with the reference."""
+    from novann_amd.module import BatchNorm2d
+    bn = BatchNorm2d(16)
+    assert bn.gamma.data.dtype == np.float64
+    opt = AdamW(bn.parameters(), lr=1e-2, weight_decay=0.1)
+    rng = np.random.default_rng(8)
+    ref = {k: [p.data.copy(), np.zeros_like(p.data), np.zeros_like(p.data)]
+           for k, p in (("g", bn.gamma), ("b", bn.beta))}
+    for t in range(1, 4):
+        gg = rng.standard_normal(bn.gamma.data.shape).astype(np.float32)
+        gb = rng.standard_normal(bn.beta.data.shape)
+        bn.gamma.grad, bn.beta.grad = gg, gb
+        opt.step()
+        for k, g in (("g", gg), ("b", gb)):
+            ref[k] = list(OR.adamw_step_f64(*ref[k][:1], g, *ref[k][1:], t, 1e-2, wd=0.1,
+                                            decay=False))
+        if t == 2:  # the caller rewrites a parameter between steps
+            bn.beta.data[...] = 0.25
+            ref["b"][0] = np.full_like(ref["b"][0], 0.25)
+    assert bn.gamma.data.dtype == bn.beta.data.dtype == np.float64
+    assert np.array_equal(bn.gamma.data.view(np.uint64), ref["g"][0].view(np.uint64))
+    assert np.array_equal(bn.beta.data.view(np.uint64), ref["b"][0].view(np.uint64))

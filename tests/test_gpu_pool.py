@@ -62,6 +62,29 @@ def test_max_pool2d_f32_bit_exact(xs, k, s, p, mode):
     same_bits_or_nan(got, R.max_pool2d(x, k, s, p, mode))
 
 
+@pytest.mark.parametrize("xt,off_x,off_y", [("f32", 1, 0), ("f32", 2, 1), ("bf16", 1, 1),
+                                             ("e4m3", 3, 1)])
+def test_max_pool2d_element_offset_views(xt, off_x, off_y):
+    """x and y as views starting some elements into larger buffers (W % 4 == 0,
+    OW even: the shape that reads 4 elements and stores pairs at once)."""
+    print(f"max_pool2d views {xt} +{off_x} +{off_y}", flush=True)
+    rng = np.random.default_rng(off_x * 10 + off_y)
+    shape, oshape = (2, 3, 8, 12), (2, 3, 4, 6)
+    n, no = int(np.prod(shape)), int(np.prod(oshape))
+    v = relu_like(rng, (n + off_x,))
+    codes = v.view(np.uint32) if xt == "f32" else O.cast(v, O.F32, CODE[xt])
+    xbuf = to_dev(codes, CODE[xt])
+    ybuf = torch.empty(no + off_y, dtype=xbuf.dtype, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    rc = _lib.load().novaq_max_pool2d(xbuf[off_x:].data_ptr(), CODE[xt], *shape, 2, 2, 2, 2,
+                                      0, 0, 0, ybuf[off_y:].data_ptr(), stream)
+    assert rc == _lib.OK
+    torch.cuda.synchronize()
+    got = O.cast(to_host(ybuf[off_y:]), CODE[xt], O.F32).reshape(oshape)
+    dec = O.cast(codes[off_x:], CODE[xt], O.F32, n=n).reshape(shape)
+    same_bits_or_nan(got, R.max_pool2d(dec, 2, 2, 0, "zeros"))
+
+
 @pytest.mark.parametrize("ksp", [(3, 2, 1), (2, 2, 0)])
 @pytest.mark.parametrize("xt", ["bf16", "f16", "e4m3", "e5m2"])
 def test_max_pool2d_narrow_codes(xt, ksp):
@@ -88,8 +111,12 @@ def test_max_pool2d_narrow_codes(xt, ksp):
         assert y.shape == want.shape and float(y.scale.cpu()[0]) == np.float32(scale)
 
 
+# (2, 3, 89, 89), (1, 2, 90, 90), (1, 3, 1, 8191), (1, 1, 87, 89): planes whose
+# numpy pairwise tree has 65 leaves; (2, 2, 64, 128): one whole 8192 block
 @pytest.mark.parametrize("xs", [(2, 3, 4, 5), (4, 3, 10, 12), (128, 64, 7, 7), (3, 2, 1, 7),
-                                (2, 2, 14, 14), (1, 3, 28, 28), (2, 2, 37, 41), (1, 1, 128, 129)])
+                                (2, 2, 14, 14), (1, 3, 28, 28), (2, 2, 37, 41), (1, 1, 128, 129),
+                                (2, 3, 89, 89), (1, 2, 90, 90), (1, 3, 1, 8191), (1, 1, 87, 89),
+                                (2, 2, 64, 128)])
 def test_avg_pool2d_bit_exact(xs):
     print(f"avg_pool2d {xs}", flush=True)
     rng = np.random.default_rng(sum(xs))

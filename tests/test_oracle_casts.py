@@ -188,3 +188,39 @@ def test_amax_and_scale():
 def test_cast_rejects_quantized_to_quantized():
     with pytest.raises(ValueError):
         O.cast(np.zeros(4, np.uint8), O.E4M3, O.E5M2)
+
+
+def test_config1_tensor_holds_every_special():
+    """BASELINE config [1]'s specials really occur: signed zeros, both
+    infinities, quiet and signalling NaNs of both signs, values past +-448
+    (464 and 480 exactly), E4M3-subnormal neighbours and fp32 subnormals."""
+    from tests.patterns import config1_tensor
+    x = config1_tensor().reshape(-1)
+    b = x.view(np.uint32)
+    mag, neg = b & 0x7FFFFFFF, (b >> 31) == 1
+    nan = mag > 0x7F800000
+    quiet = (b & 0x00400000) != 0
+    for sel in (nan & quiet & neg, nan & quiet & ~neg, nan & ~quiet & neg, nan & ~quiet & ~neg):
+        assert sel.sum() > 1000
+    assert ((mag == 0x7F800000) & neg).any() and ((mag == 0x7F800000) & ~neg).any()
+    assert ((mag == 0) & neg).any() and ((mag == 0) & ~neg).any()
+    assert (np.abs(x) == 464).any() and (np.abs(x) == 480).any()
+    assert ((np.abs(x) > 448) & np.isfinite(x) & neg).any()
+    assert ((mag > 0) & (mag < 0x00800000)).sum() > 1000
+
+
+@pytest.mark.parametrize("st", [O.F16, O.BF16])
+@pytest.mark.parametrize("dt", [O.E4M3, O.E5M2, O.E2M1])
+def test_scaled_cast_from_16bit_sources_is_the_widened_cast(st, dt):
+    """Widening fp16 / bf16 to fp32 is exact, so a scaled cast from a 16-bit
+    source must equal the (pinned) scaled fp32 cast of the widened values --
+    for every 16-bit code, with a positive, a negative and a zero scale; the
+    amax of a 16-bit tensor is the amax of its widening."""
+    codes = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    wide = O.cast(codes, st, O.F32)
+    for s in (0.0123, -3.5, 0.0):
+        got = O.cast(codes, st, dt, scale=s)
+        want = O.cast(wide, O.F32, dt, scale=s)
+        assert np.array_equal(got, want)
+    finite = codes[np.isfinite(wide)]
+    assert O.amax(finite, st) == O.amax(O.cast(finite, st, O.F32))

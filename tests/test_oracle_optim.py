@@ -83,3 +83,42 @@ def test_float32_evaluation():
     w64 -= 1e-3 * 0.01 * w64
     assert not np.array_equal(w32, w64.astype(np.float32))
     np.testing.assert_allclose(w32, w64, rtol=1e-6, atol=1e-7)
+
+
+def run_oracle64(w0, grads, **hp):
+    w, m, v = w0.copy(), np.zeros_like(w0), np.zeros_like(w0)
+    for t, g in enumerate(grads, 1):
+        w, m, v = OR.adamw_step_f64(w, g, m, v, t, **hp)
+    return w, m, v
+
+
+@pytest.mark.parametrize("gdt", [np.float64, np.float32])
+def test_float64_parameters_match_torch_adam(gdt):
+    """float64 parameters (BatchNorm's gamma / beta) step in float64: torch's
+    Adam in float64 agrees to float64 rounding for a float64 gradient; a
+    float32 gradient's products are float32 roundings (relative 2^-24) in
+    numpy, which stays well within float32 distance of torch."""
+    rng = np.random.default_rng(4)
+    w0 = rng.standard_normal(400)
+    grads = [rng.standard_normal(400).astype(gdt) for _ in range(15)]
+    got, m, v = run_oracle64(w0, grads, lr=1e-2, b1=0.9, b2=0.999, eps=1e-8, wd=0.0)
+    assert got.dtype == m.dtype == v.dtype == np.float64
+    want = run_torch(w0, grads, torch.optim.Adam, lr=1e-2, betas=(0.9, 0.999), eps=1e-8)
+    tol = 1e-12 if gdt == np.float64 else 1e-6
+    np.testing.assert_allclose(got, want, rtol=0, atol=tol)
+
+
+def test_float64_parameter_with_float32_gradient_rounds_the_products():
+    """With a float32 gradient numpy rounds (1 - b1) * g and (1 - b2) * g**2 to
+    float32 (a Python scalar keeps a float32 array float32) before the float64
+    sums: the moments then differ from those of the widened gradient."""
+    rng = np.random.default_rng(5)
+    w0 = rng.standard_normal(2000)
+    g32 = rng.standard_normal(2000).astype(np.float32)
+    _, m32, v32 = OR.adamw_step_f64(w0, g32, np.zeros(2000), np.zeros(2000), 1, 1e-3)
+    _, m64, v64 = OR.adamw_step_f64(w0, g32.astype(np.float64), np.zeros(2000), np.zeros(2000),
+                                    1, 1e-3)
+    assert not np.array_equal(m32, m64) and not np.array_equal(v32, v64)
+    np.testing.assert_allclose(m32, m64, rtol=2 ** -23)
+    # m = b1 * 0 + f32(0.1 * g): each moment is a float32 value
+    assert np.array_equal(m32, m32.astype(np.float32).astype(np.float64))
