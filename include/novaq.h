@@ -74,7 +74,9 @@ enum novaq_status {
   NOVAQ_EPADMODE = -4, /* padding mode unknown (NovaNN raises ValueError) */
   NOVAQ_EALIGN = -5,   /* a buffer is not 16-byte aligned */
   NOVAQ_EHIP = -6,     /* the HIP runtime reported an error */
-  NOVAQ_ENOTSUP = -7   /* valid request this build does not implement */
+  NOVAQ_ENOTSUP = -7,  /* valid request this build does not implement */
+  NOVAQ_ESCRATCH = -8  /* request needs more than an allocation-free entry point's
+                          static scratch holds */
 };
 
 /* Library version as MAJOR*10000 + MINOR*100 + PATCH. */
@@ -330,6 +332,23 @@ int novaq_conv2d_backward(const float *grad, const float *x, int64_t N, int64_t 
                           int pad_mode, float *grad_input, float *grad_weight,
                           float *grad_bias, void *workspace, size_t workspace_bytes,
                           void *stream);
+
+/* novaq_conv2d_backward without a workspace argument and without allocating:
+ * no counterpart in the reference; it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving or training
+ * loops, harnesses that forbid hipMalloc).  Same arguments (less the
+ * workspace), same kernels and the same results as novaq_conv2d_backward.
+ * The workspace is a static device array in the library of 32 MiB per GPU
+ * (held from the library's load until the process ends); a call whose
+ * novaq_conv2d_backward_workspace() exceeds it returns NOVAQ_ESCRATCH (config
+ * [5]'s conv2 at batch 256 needs 30.8 MB).  Every call on one GPU shares that
+ * GPU's array: calls that overlap on one GPU (different streams, or threads)
+ * race; calls ordered on one stream do not. */
+int novaq_conv2d_backward_noalloc(const float *grad, const float *x, int64_t N, int64_t C,
+                                  int64_t H, int64_t W, const void *w_q, int w_dtype,
+                                  const float *w_scale, int64_t C_out, int KH, int KW, int sh,
+                                  int sw, int ph, int pw, int pad_mode, float *grad_input,
+                                  float *grad_weight, float *grad_bias, void *stream);
 
 #ifdef __cplusplus
 }

@@ -16,7 +16,8 @@ DTYPES = {"f32": F32, "f16": F16, "bf16": BF16, "e4m3": E4M3, "e5m2": E5M2, "e2m
 DTYPE_NAMES = {v: k for k, v in DTYPES.items()}
 PAD_MODES = {"zeros": 0, "reflect": 1, "replicate": 2, "circular": 3}
 
-OK, EINVAL, EDTYPE, ESHAPE, EPADMODE, EALIGN, EHIP, ENOTSUP = 0, -1, -2, -3, -4, -5, -6, -7
+OK, EINVAL, EDTYPE, ESHAPE, EPADMODE, EALIGN, EHIP, ENOTSUP, ESCRATCH = (
+    0, -1, -2, -3, -4, -5, -6, -7, -8)
 
 
 
@@ -75,6 +76,9 @@ SIGNATURES = {
     "novaq_conv2d_backward": (_i32, [_f32p, _f32p, _i64, _i64, _i64, _i64, _vp, _i32, _f32p,
                                      _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _f32p,
                                      _f32p, _f32p, _vp, ctypes.c_size_t, _vp]),
+    "novaq_conv2d_backward_noalloc": (_i32, [_f32p, _f32p, _i64, _i64, _i64, _i64, _vp, _i32,
+                                             _f32p, _i64, _i32, _i32, _i32, _i32, _i32, _i32,
+                                             _i32, _f32p, _f32p, _f32p, _vp]),
 }
 
 _lib = None

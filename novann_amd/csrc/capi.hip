@@ -66,6 +66,7 @@ const char* novaq_status_string(int status) {
     case NOVAQ_EALIGN: return "buffer not 16-byte aligned";
     case NOVAQ_EHIP: return "HIP runtime error";
     case NOVAQ_ENOTSUP: return "not supported";
+    case NOVAQ_ESCRATCH: return "request exceeds the static scratch of an allocation-free entry point";
     default: return "unknown status";
   }
 }
@@ -154,6 +155,33 @@ int novaq_conv2d_forward(const float* x, int64_t N, int64_t C, int64_t H, int64_
 }  // extern "C"
 
 namespace {
+
+// Argument checks shared by the two Conv2d backward entry points; *need gets
+// the workspace bytes the call uses (0: nothing to compute).
+int conv_bwd_check(const float* grad, const float* x, int64_t N, int64_t C, int64_t H,
+                   int64_t W, const void* w_q, int w_dtype, int64_t C_out, int KH, int KW,
+                   int sh, int sw, int ph, int pw, int pad_mode, const float* grad_input,
+                   const float* grad_weight, const float* grad_bias, size_t* need) {
+  *need = 0;
+  if (!valid_dtype(w_dtype)) return NOVAQ_EDTYPE;
+  if (pad_mode < NOVAQ_PAD_ZEROS || pad_mode > NOVAQ_PAD_CIRCULAR) return NOVAQ_EPADMODE;
+  if (N < 0 || C <= 0 || H <= 0 || W <= 0 || C_out <= 0 || KH <= 0 || KW <= 0 || sh <= 0 ||
+      sw <= 0 || ph < 0 || pw < 0)
+    return NOVAQ_EINVAL;
+  if (H + 2 * (int64_t)ph < KH || W + 2 * (int64_t)pw < KW) return NOVAQ_ESHAPE;
+  if (N > 0x7FFFFFFF || C * H * W > 0x7FFFFFFF || C_out * C * KH * KW > 0x7FFFFFFF ||
+      C_out > 0x7FFFFFFF)
+    return NOVAQ_EINVAL;
+  if (!grad_input && !grad_weight && !grad_bias) return NOVAQ_OK;
+  if (N > 0 && !grad) return NOVAQ_EINVAL;
+  if (grad_input && N > 0 && !w_q) return NOVAQ_EINVAL;
+  if (grad_weight && N > 0 && !x) return NOVAQ_EINVAL;
+  for (const void* p : {(const void*)grad, (const void*)x, w_q, (const void*)grad_input,
+                        (const void*)grad_weight, (const void*)grad_bias})
+    if (p && !aligned16(p)) return NOVAQ_EALIGN;
+  *need = conv2d_bwd_workspace(N, C, C_out, KH, KW, w_dtype, device_cu_count()).total;
+  return NOVAQ_OK;
+}
 
 // Device-side epilogue from the C struct (NULL: bias only, fp32 output);
 // zeroes the amax output first.  Returns a status.
@@ -372,27 +400,33 @@ int novaq_conv2d_backward(const float* grad, const float* x, int64_t N, int64_t 
                           int pad_mode, float* grad_input, float* grad_weight,
                           float* grad_bias, void* workspace, size_t workspace_bytes,
                           void* stream) {
-  if (!valid_dtype(w_dtype)) return NOVAQ_EDTYPE;
-  if (pad_mode < NOVAQ_PAD_ZEROS || pad_mode > NOVAQ_PAD_CIRCULAR) return NOVAQ_EPADMODE;
-  if (N < 0 || C <= 0 || H <= 0 || W <= 0 || C_out <= 0 || KH <= 0 || KW <= 0 || sh <= 0 ||
-      sw <= 0 || ph < 0 || pw < 0)
-    return NOVAQ_EINVAL;
-  if (H + 2 * (int64_t)ph < KH || W + 2 * (int64_t)pw < KW) return NOVAQ_ESHAPE;
-  if (N > 0x7FFFFFFF || C * H * W > 0x7FFFFFFF || C_out * C * KH * KW > 0x7FFFFFFF ||
-      C_out > 0x7FFFFFFF)
-    return NOVAQ_EINVAL;
-  if (!grad_input && !grad_weight && !grad_bias) return NOVAQ_OK;
-  const size_t need = conv2d_bwd_workspace(N, C, C_out, KH, KW, w_dtype, device_cu_count()).total;
+  size_t need = 0;
+  int rc = conv_bwd_check(grad, x, N, C, H, W, w_q, w_dtype, C_out, KH, KW, sh, sw, ph, pw,
+                          pad_mode, grad_input, grad_weight, grad_bias, &need);
+  if (rc != NOVAQ_OK || need == 0) return rc;
   if (!workspace || workspace_bytes < need) return NOVAQ_EINVAL;
-  if (N > 0 && !grad) return NOVAQ_EINVAL;
-  if (grad_input && N > 0 && !w_q) return NOVAQ_EINVAL;
-  if (grad_weight && N > 0 && !x) return NOVAQ_EINVAL;
-  for (const void* p : {(const void*)grad, (const void*)x, w_q, (const void*)grad_input,
-                        (const void*)grad_weight, (const void*)grad_bias, (const void*)workspace})
-    if (p && !aligned16(p)) return NOVAQ_EALIGN;
+  if (!aligned16(workspace)) return NOVAQ_EALIGN;
   return conv2d_backward_launch(grad, x, N, C, H, W, w_q, w_dtype, w_scale, C_out, KH, KW, sh,
                                 sw, ph, pw, pad_mode, grad_input, grad_weight, grad_bias,
                                 workspace, static_cast<hipStream_t>(stream));
+}
+
+int novaq_conv2d_backward_noalloc(const float* grad, const float* x, int64_t N, int64_t C,
+                                  int64_t H, int64_t W, const void* w_q, int w_dtype,
+                                  const float* w_scale, int64_t C_out, int KH, int KW, int sh,
+                                  int sw, int ph, int pw, int pad_mode, float* grad_input,
+                                  float* grad_weight, float* grad_bias, void* stream) {
+  size_t need = 0;
+  int rc = conv_bwd_check(grad, x, N, C, H, W, w_q, w_dtype, C_out, KH, KW, sh, sw, ph, pw,
+                          pad_mode, grad_input, grad_weight, grad_bias, &need);
+  if (rc != NOVAQ_OK || need == 0) return rc;
+  if (need > CONV_BWD_SCRATCH_BYTES) return NOVAQ_ESCRATCH;
+  void* work = nullptr;
+  rc = conv2d_bwd_scratch(&work);
+  if (rc != NOVAQ_OK) return rc;
+  return conv2d_backward_launch(grad, x, N, C, H, W, w_q, w_dtype, w_scale, C_out, KH, KW, sh,
+                                sw, ph, pw, pad_mode, grad_input, grad_weight, grad_bias, work,
+                                static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

@@ -34,6 +34,7 @@
 #include <stdint.h>
 
 #include <algorithm>
+#include <mutex>
 
 #include "novaq_colsum.h"
 #include "novaq_convert.h"
@@ -823,6 +824,37 @@ int conv2d_backward_launch(const float* grad, const float* x, int64_t N, int64_t
     case F16: return launch_dinput<F16>(grad, w_q, wf, w_scale, grad_input, g, stream);
     default: return launch_dinput<F32>(grad, w_q, wf, w_scale, grad_input, g, stream);
   }
+}
+
+// ---------------------------------------------------------------------------
+// Scratch of the allocation-free backward (novaq_conv2d_backward_noalloc): a
+// file-scope device array, so every GPU the library runs on holds its own
+// copy from module load until the process ends.  In host code `scratch` only
+// names the symbol; its device address is looked up once per device with
+// hipGetSymbolAddress (with that device current) and used from then on.  Every
+// call on a GPU shares that GPU's array: calls that overlap on one GPU (on
+// different streams) race; calls in one stream's order do not.  Nothing in it
+// must start at zero: the weight-gradient kernels write every partial the
+// finishing launch reads, and the flip writes every flipped weight.
+static __device__ __align__(256) uint8_t scratch[CONV_BWD_SCRATCH_BYTES];
+
+int conv2d_bwd_scratch(void** ptr) {
+  static std::mutex lock;
+  static void* per_device[64] = {};
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e);
+  if (dev < 0 || dev >= 64) return NOVAQ_EINVAL;
+  std::lock_guard<std::mutex> guard(lock);
+  if (!per_device[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e);
+    if (!p) return NOVAQ_EHIP;
+    per_device[dev] = p;
+  }
+  *ptr = per_device[dev];
+  return NOVAQ_OK;
 }
 
 }  // namespace novaq

@@ -81,6 +81,11 @@ struct ConvBwdWs {
 };
 ConvBwdWs conv2d_bwd_workspace(int64_t N, int64_t C, int64_t C_out, int KH, int KW, int w_dtype,
                                int cus);
+// Capacity of the static scratch the allocation-free Conv2d backward uses
+// (novaq_conv2d_backward_noalloc): config [5] conv2 needs 30.8 MB.
+constexpr size_t CONV_BWD_SCRATCH_BYTES = (size_t)32 << 20;
+// The current device's address of that scratch (looked up on first use).
+int conv2d_bwd_scratch(void** ptr);
 int conv2d_backward_launch(const float* grad, const float* x, int64_t N, int64_t C, int64_t H,
                            int64_t W, const void* w_q, int w_dtype, const float* w_scale,
                            int64_t C_out, int KH, int KW, int sh, int sw, int ph, int pw,
