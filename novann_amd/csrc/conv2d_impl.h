@@ -911,9 +911,231 @@ __global__ __launch_bounds__(256) void conv2d_direct_kernel(
   epi_amax_commit(ep, am);
 }
 
+// Few input channels (C <= 4, stride 1, windows up to 7 x 7): the GEMM's K is
+// only C*KH*KW, so padding it to whole 8-channel MFMA groups would multiply
+// the work (11x for MNIST's 1-channel 3 x 3 conv).  Instead a workgroup owns
+// one image and SC_CO output channels: it stages the image's padded planes in
+// LDS once (padding mode resolved, values rounded to bf16 as the MFMA paths
+// round x) and the channels' weights decoded (exact bf16 values, laid out
+// [c][kh][kw][8 channels] so one tap's 8 weights are two 16-byte reads), then
+// each lane takes a chunk of 4 consecutive outputs of one row and makes them
+// for all SC_CO channels with VALU FMAs from one input window in registers --
+// every product exact in fp32, summed in (c, kh, kw) order -- and writes each
+// channel's 4 values with one 16- (8-, 4-) byte store.  Consecutive lanes take
+// consecutive chunks of a plane, so a wave's stores are one contiguous span.
+// HBM-bound on the output.
+constexpr int SC_CO = 8;          // output channels per workgroup
+constexpr int SC_MAX_C = 4, SC_MAX_K = 7;
+constexpr size_t SC_LDS = 64 * 1024;
+
+struct SmallGeom {
+  int N, C, H, W, C_out, KH, KW, ph, pw, pad_mode, OH, OW;
+  int HP, WP;   // staged plane: HP padded rows of WP floats (rows 16-byte aligned)
+  int WV;       // columns of the padded image (W + 2 pw); staged columns past it are 0
+  int cpr;      // 4-pixel chunks per output row
+  int vec;      // OW % 4 == 0: whole chunks, vector stores
+};
+
+template <int WT, int XT>
+__global__ __launch_bounds__(256) void conv2d_smallc_kernel(
+    const uint8_t* __restrict__ x, const float* __restrict__ x_scale,
+    const uint8_t* __restrict__ w, const float* __restrict__ w_scale, Epilogue ep,
+    void* __restrict__ y, SmallGeom g) {
+  extern __shared__ __attribute__((aligned(16))) float sc_lds[];
+  const int n = blockIdx.x;
+  const int co0 = blockIdx.y * SC_CO;
+  const int nco = min(SC_CO, g.C_out - co0);
+  const int plane = g.HP * g.WP;
+  const int taps = g.KH * g.KW;
+  float* xs = sc_lds;                          // C planes of HP x WP
+  float* ws = sc_lds + g.C * plane;            // C*KH*KW taps x SC_CO channels
+  // stage the weights and the padded planes: every load of a round is issued
+  // before the first LDS write, so the round pays one memory latency, not one
+  // per element.  A lane covers rows (lane / 32) + 8 i and columns
+  // (lane % 32) + 32 j of the C*HP staged rows, SC_SR x SC_SC slots a round.
+  constexpr int SC_SR = 4, SC_SC = 2;
+  const int64_t wb = (int64_t)co0 * g.C * taps;
+  const int nwt = g.C * taps * SC_CO;
+  float wv0[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int i = threadIdx.x + 256 * k;
+    const int t = i / SC_CO, cl = i - t * SC_CO;
+    wv0[k] = (i < nwt && cl < nco)
+                 ? u2f((uint32_t)weight_bf16<WT>(w, wb + (int64_t)cl * g.C * taps + t) << 16)
+                 : 0.0f;
+  }
+  const int64_t xb = (int64_t)n * g.C * g.H * g.W;
+  const int rows = g.C * g.HP;
+  for (int r0 = 0; r0 < rows; r0 += 8 * SC_SR) {
+    for (int c0 = 0; c0 < g.WP; c0 += 32 * SC_SC) {
+      float v[SC_SR][SC_SC];
+#pragma unroll
+      for (int i = 0; i < SC_SR; ++i) {
+        const int r = r0 + (threadIdx.x >> 5) + 8 * i;
+        const int c = r / g.HP, hp = r - c * g.HP;
+        const int hi = r < rows ? pad_index(hp - g.ph, g.H, g.pad_mode) : -1;
+        const int64_t rb = xb + ((int64_t)c * g.H + hi) * g.W;
+#pragma unroll
+        for (int j = 0; j < SC_SC; ++j) {
+          const int col = c0 + (threadIdx.x & 31) + 32 * j;
+          const int wi = col < g.WV ? pad_index(col - g.pw, g.W, g.pad_mode) : -1;
+          v[i][j] = (hi >= 0 && wi >= 0) ? x_val<XT>(x, rb + wi) : 0.0f;
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < SC_SR; ++i) {
+        const int r = r0 + (threadIdx.x >> 5) + 8 * i;
+#pragma unroll
+        for (int j = 0; j < SC_SC; ++j) {
+          const int col = c0 + (threadIdx.x & 31) + 32 * j;
+          if (r < rows && col < g.WP) xs[r * g.WP + col] = u2f(enc_bf16(f2u(v[i][j])) << 16);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < 2; ++k)
+    if (threadIdx.x + 256 * k < nwt) ws[threadIdx.x + 256 * k] = wv0[k];
+  for (int i = threadIdx.x + 512; i < nwt; i += 256) {  // windows past 8 x 8 x C
+    const int t = i / SC_CO, cl = i - t * SC_CO;
+    ws[i] = cl < nco ? u2f((uint32_t)weight_bf16<WT>(w, wb + (int64_t)cl * g.C * taps + t) << 16)
+                     : 0.0f;
+  }
+  __syncthreads();
+
+  const float s = product_scale(w_scale, x_scale);
+  const float inv_o = epi_inv_scale(ep);
+  const float z = epi_relu_factor(ep);
+  const bool plain = !ep.mul && !ep.add && !ep.relu && !ep.amax && ep.out_dtype == F32;
+  const int per_plane = g.OH * g.cpr;
+  uint32_t am = 0;
+  for (int p = threadIdx.x; p < per_plane; p += 256) {
+    const int oh = p / g.cpr, ow0 = (p - oh * g.cpr) * 4;
+    float acc[SC_CO][4];
+#pragma unroll
+    for (int cl = 0; cl < SC_CO; ++cl)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc[cl][q] = 0.0f;
+    for (int c = 0; c < g.C; ++c) {
+      for (int kh = 0; kh < g.KH; ++kh) {
+        const float4* row =
+            reinterpret_cast<const float4*>(xs + (c * g.HP + oh + kh) * g.WP + ow0);
+        float v[12];
+#pragma unroll
+        for (int q = 0; q < 3; ++q) {
+          const float4 f = row[q];
+          v[4 * q] = f.x; v[4 * q + 1] = f.y; v[4 * q + 2] = f.z; v[4 * q + 3] = f.w;
+        }
+        const float4* wk = reinterpret_cast<const float4*>(ws + (c * g.KH + kh) * g.KW * SC_CO);
+#pragma unroll
+        for (int kw = 0; kw < SC_MAX_K; ++kw) {
+          if (kw < g.KW) {
+            const float4 wa = wk[2 * kw], wbv = wk[2 * kw + 1];
+            const float wv[SC_CO] = {wa.x, wa.y, wa.z, wa.w, wbv.x, wbv.y, wbv.z, wbv.w};
+            // a bf16 x bf16 product is exact in fp32, so the fused
+            // multiply-add rounds exactly as the separate add would
+#pragma unroll
+            for (int cl = 0; cl < SC_CO; ++cl)
+#pragma unroll
+              for (int q = 0; q < 4; ++q) acc[cl][q] = __builtin_fmaf(v[q + kw], wv[cl], acc[cl][q]);
+          }
+        }
+      }
+    }
+    const int64_t e0 = (((int64_t)n * g.C_out + co0) * g.OH + oh) * g.OW + ow0;
+    const int64_t cstep = (int64_t)g.OH * g.OW;
+    if (plain) {
+      // bias only, fp32 output: acc * s + bias, one 16-byte store per channel
+#pragma unroll
+      for (int cl = 0; cl < SC_CO; ++cl) {
+        if (cl >= nco) break;
+        const float b = ep.bias ? ep.bias[co0 + cl] : 0.0f;
+        float o[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) o[q] = acc[cl][q] * s + b;
+        float* dst = reinterpret_cast<float*>(y) + e0 + cl * cstep;
+        if (g.vec) {
+          *reinterpret_cast<float4*>(dst) = make_float4(o[0], o[1], o[2], o[3]);
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            if (ow0 + q < g.OW) dst[q] = o[q];
+        }
+      }
+      continue;
+    }
+    // the epilogue, one copy of the store loop per output dtype, no branch on
+    // the epilogue's fields per element
+    auto store_all = [&](auto od) {
+      constexpr int OD = decltype(od)::value;
+#pragma unroll
+      for (int cl = 0; cl < SC_CO; ++cl) {
+        if (cl >= nco) break;
+        const EpiChan k = epi_chan(ep, co0 + cl);
+        float o[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          o[q] = epi_value_nb(k, acc[cl][q], s, z);
+          if (ow0 + q < g.OW) am = epi_track(am, o[q]);
+        }
+        const int64_t e = e0 + cl * cstep;
+        if (g.vec) {
+          epi_store4_t<OD>(y, e, o, inv_o);
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            if (ow0 + q < g.OW) epi_store_t<OD>(y, e + q, o[q], inv_o);
+        }
+      }
+    };
+    switch (ep.out_dtype) {
+      case F16: store_all(OutDtype<F16>{}); break;
+      case BF16: store_all(OutDtype<BF16>{}); break;
+      case E4M3: store_all(OutDtype<E4M3>{}); break;
+      case E5M2: store_all(OutDtype<E5M2>{}); break;
+      default: store_all(OutDtype<F32>{}); break;
+    }
+  }
+  epi_amax_commit(ep, am);
+}
+
+// The small-channel path when the shape fits it; returns false otherwise.
+template <int WT, int XT>
+bool launch_smallc(const uint8_t* x, const float* x_scale, const void* w, const float* w_scale,
+                   const Epilogue& ep, void* y, const ConvGeom& cg, hipStream_t stream,
+                   int* rc) {
+  if (cg.C > SC_MAX_C || cg.sh != 1 || cg.sw != 1 || cg.KH > SC_MAX_K || cg.KW > SC_MAX_K)
+    return false;
+  SmallGeom g{};
+  g.N = cg.N; g.C = cg.C; g.H = cg.H; g.W = cg.W; g.C_out = cg.C_out; g.KH = cg.KH;
+  g.KW = cg.KW; g.ph = cg.ph; g.pw = cg.pw; g.pad_mode = cg.pad_mode; g.OH = cg.OH;
+  g.OW = cg.OW;
+  g.HP = cg.OH + cg.KH - 1;
+  g.cpr = (cg.OW + 3) / 4;
+  g.WV = cg.OW + cg.KW - 1;
+  g.WP = 4 * g.cpr + 8;  // a chunk reads 12 floats (3 x 16 bytes) from its start
+  g.vec = cg.OW % 4 == 0 && (reinterpret_cast<uintptr_t>(y) % 16) == 0;
+  const size_t lds =
+      ((size_t)g.C * g.HP * g.WP + (size_t)SC_CO * g.C * g.KH * g.KW) * sizeof(float);
+  // (within the default 64 KB of dynamic LDS: no attribute to raise)
+  if (lds > SC_LDS || (int64_t)g.OH * g.cpr * SC_CO > 0x7FFFFFFF) return false;
+  const int64_t co_groups = (cg.C_out + SC_CO - 1) / SC_CO;
+  if (co_groups > 65535) return false;
+  hipLaunchKernelGGL((conv2d_smallc_kernel<WT, XT>), dim3((unsigned)cg.N, (unsigned)co_groups),
+                     dim3(256), lds, stream, x, x_scale, static_cast<const uint8_t*>(w), w_scale,
+                     ep, y, g);
+  *rc = check_launch();
+  return true;
+}
+
 template <int WT, int XT>
 int launch(const uint8_t* x, const float* x_scale, const void* w, const float* w_scale,
            const Epilogue& ep, void* y, ConvGeom g, hipStream_t stream) {
+  {
+    int rc = NOVAQ_OK;
+    if (launch_smallc<WT, XT>(x, x_scale, w, w_scale, ep, y, g, stream, &rc)) return rc;
+  }
   {
     BandGeom b;
     size_t lds = 0;

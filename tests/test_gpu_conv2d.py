@@ -85,6 +85,13 @@ def test_golden_fixture_all_padding_modes(golden):
     # partial output-channel block
     (2, 16, 12, 12, 40, 3, 3, 1, 1, 1, 1),
     (1, 8, 9, 16, 70, 3, 3, 2, 2, 1, 1),
+    # few input channels, stride 1 (the VALU small-channel kernel): config
+    # [5]'s conv1 shape at batch 3, widths that are no multiple of 4, 5 x 5 /
+    # 7 x 7 / non-square windows, more than 8 output channels
+    (3, 1, 28, 28, 32, 3, 3, 1, 1, 1, 1),
+    (2, 4, 13, 10, 9, 5, 5, 1, 1, 2, 2),
+    (1, 2, 9, 7, 3, 7, 7, 1, 1, 3, 3),
+    (2, 3, 6, 6, 12, 2, 4, 1, 1, 0, 3),
 ])
 def test_shapes_and_modes_vs_oracle(wdt, mode, case):
     N, C, H, W, C_out, KH, KW, sh, sw, ph, pw = case

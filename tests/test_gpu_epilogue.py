@@ -148,10 +148,12 @@ def test_linear_epilogue_bit_exact(wdt, N, D_in, D_out):
 CONV_CASES = [
     # wdt, (N, C, H, W), C_out, (KH, KW), stride, pad, mode
     ("e2m1", (3, 8, 12, 12), 16, (3, 3), (1, 1), (1, 1), "zeros"),     # band, K9
-    ("e4m3", (2, 3, 10, 11), 20, (5, 5), (1, 1), (2, 2), "reflect"),   # band, generic regroup
+    ("e4m3", (2, 5, 10, 11), 20, (5, 5), (1, 1), (2, 2), "reflect"),   # band, generic regroup
     ("bf16", (2, 4, 9, 9), 70, (3, 3), (2, 2), (1, 1), "replicate"),  # band, 2 co blocks
     ("e5m2", (2, 65, 7, 7), 24, (3, 3), (1, 1), (1, 1), "circular"),  # conv2d_kernel (C > 64)
-    ("f32", (1, 2, 6, 301), 5, (1, 3), (1, 1), (0, 1), "zeros"),      # conv2d_kernel (OW > 256)
+    ("f32", (1, 5, 6, 301), 5, (1, 3), (1, 1), (0, 1), "zeros"),      # conv2d_kernel (OW > 256)
+    ("e2m1", (3, 1, 28, 28), 32, (3, 3), (1, 1), (1, 1), "zeros"),    # small-C, vector stores
+    ("e4m3", (2, 3, 7, 10), 9, (3, 5), (1, 1), (1, 2), "reflect"),    # small-C, OW % 4 != 0
 ]
 
 
