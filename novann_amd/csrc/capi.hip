@@ -33,8 +33,9 @@ int device_cu_count() {
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
-// Workspace of novaq_linear_backward: W^T in W's format, grad^T (bf16) and
-// x^T (bf16), each 256-byte aligned.
+// Workspace of novaq_linear_backward: W^T in W's format, then grad in bf16
+// (at gyt) where the in-place weight-gradient product takes the shape, else
+// grad^T (bf16, at gyt) and x^T (bf16, at xt); each part 256-byte aligned.
 struct LinearBwdWs {
   size_t wt, gyt, xt, total;
 };
@@ -43,7 +44,8 @@ static LinearBwdWs linear_bwd_ws(int64_t N, int64_t D_in, int64_t D_out, int w_d
   w.wt = 0;
   w.gyt = align256(((size_t)D_in * (size_t)D_out * dtype_bits(w_dtype) + 7) / 8);
   w.xt = w.gyt + align256((size_t)D_out * (size_t)N * 2);
-  w.total = w.xt + align256((size_t)D_in * (size_t)N * 2);
+  const bool tn = linear_tn_supported(D_out, D_in, N);
+  w.total = w.xt + (tn ? 0 : align256((size_t)D_in * (size_t)N * 2));
   return w;
 }
 static bool valid_dtype(int dt) { return dt >= F32 && dt <= E2M1; }
@@ -360,18 +362,35 @@ int novaq_linear_backward(const float* grad, const float* x, int64_t N, int64_t 
   hipStream_t s = static_cast<hipStream_t>(stream);
   uint8_t* base = static_cast<uint8_t*>(workspace);
   int rc = NOVAQ_OK;
+  // grad_weight = grad^T @ x: where the shape allows, the product that reads
+  // grad and x in place; it runs first, as it also leaves grad rounded to
+  // bf16 for grad_input's product (the rounding that product's staging would
+  // apply) and sums grad's columns into grad_bias
+  const bool tn = grad_weight && D_out > 0 && D_in > 0 && linear_tn_supported(D_out, D_in, N);
+  uint16_t* g16 = tn && grad_input ? reinterpret_cast<uint16_t*>(base + ws.gyt) : nullptr;
+  bool bias_done = false;
+  if (tn) {
+    rc = linear_tn_launch(grad, x, D_out, D_in, N, grad_weight, grad_bias, g16, s);
+    if (rc != NOVAQ_OK) return rc;
+    bias_done = true;
+  }
   // grad_input = grad @ (s * dec(W)): the forward product on W^T (codes permuted)
   if (grad_input && N > 0 && D_in > 0) {
     void* wt = base + ws.wt;
     rc = transpose_launch(w_q, w_dtype, D_out, D_in, wt, w_dtype, s);
     if (rc != NOVAQ_OK) return rc;
-    rc = linear_launch(grad, N, D_out, wt, w_dtype, w_scale, nullptr, D_in, grad_input, s);
+    Epilogue ep{};
+    ep.out_dtype = F32;
+    if (g16)
+      rc = linear_launch(g16, BF16, nullptr, N, D_out, wt, w_dtype, w_scale, ep, D_in,
+                         grad_input, s);
+    else
+      rc = linear_launch(grad, N, D_out, wt, w_dtype, w_scale, nullptr, D_in, grad_input, s);
     if (rc != NOVAQ_OK) return rc;
   }
-  // grad_weight = grad^T @ x: the forward product of grad^T and x^T, both
-  // transposed straight to bf16 (the fp32 operand would be rounded to bf16 with
-  // the same round-to-nearest-even while staged)
-  if (grad_weight && D_out > 0 && D_in > 0) {
+  // otherwise the forward product of grad^T and x^T, both transposed straight
+  // to bf16 (the same round-to-nearest-even)
+  if (grad_weight && D_out > 0 && D_in > 0 && !tn) {
     void* gyt = base + ws.gyt;
     void* xt = base + ws.xt;
     rc = transpose_launch(grad, F32, N, D_out, gyt, BF16, s);
@@ -384,7 +403,7 @@ int novaq_linear_backward(const float* grad, const float* x, int64_t N, int64_t 
     if (rc != NOVAQ_OK) return rc;
   }
   // grad_bias = grad summed over the batch
-  if (grad_bias && D_out > 0) rc = colsum_launch(grad, N, D_out, grad_bias, s);
+  if (grad_bias && D_out > 0 && !bias_done) rc = colsum_launch(grad, N, D_out, grad_bias, s);
   return rc;
 }
 

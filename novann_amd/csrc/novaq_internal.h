@@ -72,6 +72,15 @@ int fill_u32_launch(uint32_t* p, uint32_t v, int count, hipStream_t stream);
 int transpose_launch(const void* src, int st, int64_t rows, int64_t cols, void* dst, int dt,
                      hipStream_t stream);
 
+// c[M, N] = sum over k of a[k, m] * b[k, n] (a: K x M, b: K x N, row-major
+// fp32), both rounded to bf16, fp32 sums: the Linear weight gradient without
+// transposed copies.  Shapes: M % 128, N % 256, K % 64, K * M and K * N
+// fp32 bytes under 2 GiB.  colsum (optional): colsum[m] = sum over k of
+// a[k, m] in fp32, in a fixed order.  a16 (optional): a rounded to bf16.
+bool linear_tn_supported(int64_t M, int64_t N, int64_t K);
+int linear_tn_launch(const float* a, const float* b, int64_t M, int64_t N, int64_t K, float* c,
+                     float* colsum, uint16_t* a16, hipStream_t stream);
+
 // Workspace parts of conv2d_backward_launch (byte offsets, 256-byte aligned):
 // the flipped weights, the grad_weight partials (chunks x C_out x C*KH*KW
 // fp32) and the grad_bias partials (chunks x C_out fp32).

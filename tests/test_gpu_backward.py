@@ -137,6 +137,38 @@ def test_linear_backward_vs_oracle(wdt, N, D_in, D_out):
     assert normwise(gb.cpu().numpy(), rb) <= TOL
 
 
+def bf16_round(a):
+    """fp32 -> bf16 (nearest even) -> fp32, by the oracle's cast."""
+    flat = np.ascontiguousarray(a, np.float32).reshape(-1)
+    return O.cast(O.cast(flat, O.F32, O.BF16), O.BF16, O.F32).reshape(a.shape)
+
+
+# D_out % 128, D_in % 256, N % 64: the weight gradient reads grad and x in
+# place (transposing LDS reads); tile counts 1, 9 (not a multiple of 8) and 16
+@pytest.mark.parametrize("N,D_in,D_out", [(64, 256, 128), (128, 768, 384), (192, 1024, 512)])
+def test_weight_gradient_in_place_product(N, D_in, D_out):
+    """grad_weight = grad^T x equals the fp64 product of the bf16-rounded
+    operands up to fp32 summation error (1e-5 normwise): an index or layout
+    slip in the transposing reads is far outside that; likewise grad_input on
+    the bf16 copy of grad that product stores, and the fused bias sum."""
+    print(f"grad_weight in place N={N} D_in={D_in} D_out={D_out}", flush=True)
+    rng = np.random.default_rng(N * 7 + D_in)
+    x = rng.standard_normal((N, D_in)).astype(np.float32)
+    g = rng.standard_normal((N, D_out)).astype(np.float32)
+    w, wdeq = weight_of((rng.standard_normal((D_out, D_in)) * 0.05).astype(np.float32), "e4m3")
+    gi, gw, gb = F.linear_backward(torch.from_numpy(g).cuda(), torch.from_numpy(x).cuda(), w,
+                                   True)
+    torch.cuda.synchronize()
+    g16 = bf16_round(g).astype(np.float64)
+    assert normwise(gw.cpu().numpy(), g16.T @ bf16_round(x).astype(np.float64)) <= 1e-5
+    assert normwise(gb.cpu().numpy(), g.astype(np.float64).sum(0, keepdims=True)) <= 1e-5
+    # grad_input multiplies the bf16 grad the weight-gradient product left behind
+    assert normwise(gi.cpu().numpy(), g16 @ wdeq) <= 1e-5
+    lib = _lib.load()
+    assert lib.novaq_linear_backward_workspace(N, D_in, D_out, 3) < \
+        lib.novaq_linear_backward_workspace(N + 1, D_in, D_out, 3)
+
+
 def test_linear_backward_skips_null_outputs_and_empty_batch():
     rng = np.random.default_rng(3)
     w = QuantizedParameters.from_float(rng.standard_normal((64, 128)).astype(np.float32), "e4m3")
