@@ -92,6 +92,9 @@ def test_golden_fixture_all_padding_modes(golden):
     (2, 4, 13, 10, 9, 5, 5, 1, 1, 2, 2),
     (1, 2, 9, 7, 3, 7, 7, 1, 1, 3, 3),
     (2, 3, 6, 6, 12, 2, 4, 1, 1, 0, 3),
+    # batch x channel groups large enough for two 8-channel groups per
+    # workgroup, the last group partial (37 = 4 x 8 + 5)
+    (208, 2, 6, 6, 37, 3, 3, 1, 1, 1, 1),
 ])
 def test_shapes_and_modes_vs_oracle(wdt, mode, case):
     N, C, H, W, C_out, KH, KW, sh, sw, ph, pw = case

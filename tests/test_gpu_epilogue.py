@@ -154,6 +154,8 @@ CONV_CASES = [
     ("f32", (1, 5, 6, 301), 5, (1, 3), (1, 1), (0, 1), "zeros"),      # conv2d_kernel (OW > 256)
     ("e2m1", (3, 1, 28, 28), 32, (3, 3), (1, 1), (1, 1), "zeros"),    # small-C, vector stores
     ("e4m3", (2, 3, 7, 10), 9, (3, 5), (1, 1), (1, 2), "reflect"),    # small-C, OW % 4 != 0
+    # small-C with two 8-channel groups per workgroup and a partial last group
+    ("e2m1", (208, 2, 6, 6), 37, (3, 3), (1, 1), (1, 1), "zeros"),
 ]
 
 
