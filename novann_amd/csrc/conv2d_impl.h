@@ -480,27 +480,44 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
         v[j] = x4_f32<XT>(x, xn + c * HW + (int64_t)hi * g.W + cg * 4);
     }
   };
-  // the band's 16-byte loads go out first
-  BandRegs<IPT> r0;
-  if constexpr (IPT > 0) {
-    if (tid < g.vitems) vload(band, tid, r0.v[0]);
-  }
-
   // --- weights: (co, c, kh, kw) -> [co][K group] ---------------------------
   const int row_elems = g.C * g.taps;
   const uint8_t* src = w;
   int cofs = 0;
+  // packed codes of rows co0 .. co0+63 (the first element is even, so the
+  // E2M1 byte boundary matches), coalesced dwords then bytes, into the
+  // staged-input region.  The first RAW_REGS dwords per lane are loaded into
+  // registers before the band's loads are issued, so writing them to LDS
+  // waits for those few loads only, not for the band behind them.
+  constexpr int RAW_REGS = 12;
+  uint32_t rw[RAW_REGS];
+  int nbytes = 0, nwords = 0;
+  const uint8_t* gsrc = w;
   if (g.raw_ok) {
-    // packed codes of rows co0 .. co0+63 (the first element is even, so the
-    // E2M1 byte boundary matches), coalesced dwords then bytes, into the
-    // staged-input region
     const int rows = min(CO_TILE, g.C_out - co0);
     const int64_t first = (int64_t)co0 * row_elems;
-    const int nbytes = (int)(((int64_t)rows * row_elems * dtype_bits(WT) + 7) / 8);
-    const uint8_t* gsrc = w + first * dtype_bits(WT) / 8;
+    nbytes = (int)(((int64_t)rows * row_elems * dtype_bits(WT) + 7) / 8);
+    gsrc = w + first * dtype_bits(WT) / 8;
+    nwords = (reinterpret_cast<uintptr_t>(gsrc) & 3) ? 0 : nbytes >> 2;
+#pragma unroll
+    for (int k = 0; k < RAW_REGS; ++k) {
+      const int i = tid + k * THREADS;
+      rw[k] = i < nwords ? reinterpret_cast<const uint32_t*>(gsrc)[i] : 0u;
+    }
+  }
+  // then the band's 16-byte loads
+  BandRegs<IPT> r0;
+  if constexpr (IPT > 0) {
+    if (tid < g.vitems) vload(band, tid, r0.v[0]);
+  }
+  if (g.raw_ok) {
     uint8_t* raw = lds + g.x_off;
-    const int nwords = (reinterpret_cast<uintptr_t>(gsrc) & 3) ? 0 : nbytes >> 2;
-    for (int i = tid; i < nwords; i += THREADS)
+#pragma unroll
+    for (int k = 0; k < RAW_REGS; ++k) {
+      const int i = tid + k * THREADS;
+      if (i < nwords) reinterpret_cast<uint32_t*>(raw)[i] = rw[k];
+    }
+    for (int i = tid + RAW_REGS * THREADS; i < nwords; i += THREADS)
       reinterpret_cast<uint32_t*>(raw)[i] = reinterpret_cast<const uint32_t*>(gsrc)[i];
     for (int i = (nwords << 2) + tid; i < nbytes; i += THREADS) raw[i] = gsrc[i];
     __syncthreads();
