@@ -434,6 +434,7 @@ struct BandGeom {
   int raw_ok;    // packed weights copied to LDS before regrouping
   int x_off;     // LDS byte offset of the staged input
   int x_bytes;   // bytes of the staged input
+  int ostage;    // narrow output stored through LDS (whole store units per channel row)
 };
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -799,6 +800,68 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
         }
       }
     };
+    // A narrow output goes through LDS when its channel rows pack into whole
+    // store units: the codes are written [channel][pixel] over the staged
+    // input (every wave's MFMAs are done with it), then consecutive lanes
+    // store each channel's run of P pixels in 8-byte (16-bit codes) or
+    // 4-byte (8-bit) pieces -- contiguous spans, where the lanes' own stores
+    // would be 32- or 16-byte pieces of 16 channel rows.
+    auto stage_out = [&](auto od) {
+      constexpr int OD = decltype(od)::value;
+      constexpr int ES = dtype_bits(OD) / 8;
+      constexpr int SU = ES == 2 ? 8 : 4;
+      uint8_t* ol = lds + g.x_off;
+      const int rowb = P * ES;
+      __syncthreads();
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        if (m >= my_mt) break;
+        const int p = (wave + 4 * m) * 16 + 4 * lg;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int co = co0 + t * 16 + lr;
+          if (t >= nt_live || co >= g.C_out || p >= P) continue;
+          // P is a multiple of 4 here, so all four pixels are in the band
+          float v[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            v[i] = epi_value_nb(kc[t], acc[m][t][i], s, z);
+            am = epi_track(am, v[i]);  // committed only with ep.amax
+          }
+          uint8_t* d = ol + (t * 16 + lr) * rowb + p * ES;
+          if constexpr (ES == 2) {
+            *reinterpret_cast<u32x2v*>(d) =
+                u32x2v{epi_encode2_t<OD>(v[0], v[1], inv_o), epi_encode2_t<OD>(v[2], v[3], inv_o)};
+          } else {
+            uint32_t w = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) w |= epi_encode_t<OD>(v[i], inv_o) << (8 * i);
+            *reinterpret_cast<uint32_t*>(d) = w;
+          }
+        }
+      }
+      __syncthreads();
+      const int live = min(CO_TILE, g.C_out - co0);
+      const int per_row = rowb / SU;
+      uint8_t* yb = reinterpret_cast<uint8_t*>(y) +
+                    (((int64_t)n * g.C_out + co0) * npix + (int64_t)oh0 * g.OW) * ES;
+      for (int u = tid; u < live * per_row; u += THREADS) {
+        const int cl = u / per_row, o = (u - cl * per_row) * SU;
+        const uint8_t* sp = ol + cl * rowb + o;
+        uint8_t* dp = yb + (int64_t)cl * npix * ES + o;
+        if constexpr (SU == 8) *reinterpret_cast<u32x2v*>(dp) = *reinterpret_cast<const u32x2v*>(sp);
+        else *reinterpret_cast<uint32_t*>(dp) = *reinterpret_cast<const uint32_t*>(sp);
+      }
+    };
+    if (g.ostage) {
+      switch (ep.out_dtype) {
+        case F16: stage_out(OutDtype<F16>{}); return;
+        case BF16: stage_out(OutDtype<BF16>{}); return;
+        case E4M3: stage_out(OutDtype<E4M3>{}); return;
+        case E5M2: stage_out(OutDtype<E5M2>{}); return;
+        default: break;
+      }
+    }
     switch (ep.out_dtype) {
       case F16: store_all(OutDtype<F16>{}); break;
       case BF16: store_all(OutDtype<BF16>{}); break;
@@ -820,7 +883,7 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
 // number of 16-byte-load items per thread held in registers (0: loaded while
 // staging).
 template <int WT>
-bool band_geometry(const ConvGeom& cg, BandGeom& b, size_t& lds, int* ipt) {
+bool band_geometry(const ConvGeom& cg, BandGeom& b, size_t& lds, int* ipt, int out_dtype) {
   if (cg.C > MAX_CB || cg.OW > 256) return false;
   b = BandGeom{};
   b.N = cg.N; b.C = cg.C; b.H = cg.H; b.W = cg.W; b.C_out = cg.C_out; b.KH = cg.KH;
@@ -859,7 +922,20 @@ bool band_geometry(const ConvGeom& cg, BandGeom& b, size_t& lds, int* ipt) {
   b.x_bytes = (int)(((size_t)b.rows_in * b.wp * b.cstride * 2 + 15) / 16 * 16);
   const size_t raw_bytes = ((size_t)b.co_rows * cg.C * b.taps * dtype_bits(WT) + 7) / 8;
   b.raw_ok = dtype_bits(WT) <= 8 && raw_bytes <= (size_t)b.x_bytes;
-  lds = b.x_off + (size_t)b.x_bytes;
+  // a narrow output through LDS: every channel row of every band (and a
+  // plane) a whole number of store units, P a multiple of 4
+  size_t region = (size_t)b.x_bytes;
+  const int ob = dtype_bits(out_dtype) / 8, su = ob == 2 ? 8 : 4;
+  b.ostage = 0;
+  if (ob < 4 && ((int64_t)b.R * cg.OW) % 4 == 0 && ((int64_t)b.R * cg.OW * ob) % su == 0 &&
+      (npix * ob) % su == 0) {
+    const size_t out_bytes = ((size_t)b.co_rows * b.R * cg.OW * ob + 15) / 16 * 16;
+    if (b.x_off + std::max(region, out_bytes) <= 80 * 1024) {
+      region = std::max(region, out_bytes);
+      b.ostage = 1;
+    }
+  }
+  lds = b.x_off + region;
   return lds <= 80 * 1024;
 }
 
@@ -1157,7 +1233,7 @@ int launch(const uint8_t* x, const float* x_scale, const void* w, const float* w
     BandGeom b;
     size_t lds = 0;
     int ipt = 0;
-    if (band_geometry<WT>(g, b, lds, &ipt)) {
+    if (band_geometry<WT>(g, b, lds, &ipt, ep.out_dtype)) {
       const int64_t co_blocks = (g.C_out + CO_TILE - 1) / CO_TILE;
       if constexpr (group_bytes<WT>() < 16) {
         if (b.taps == 9 && g.C % 8 == 0 && b.raw_ok) {

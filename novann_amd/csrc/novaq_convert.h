@@ -55,6 +55,18 @@ __device__ __forceinline__ uint32_t enc_bf16(uint32_t x) {
   return (x & 0x7FFFFFFFu) > 0x7F800000u ? ((x >> 16) | 0x0040u) : r;
 }
 
+// Two fp32 values (bits a, b) to two bf16 codes in one word, a in the low
+// half, with one gfx950 v_cvt_pk_bf16_f32: round to nearest even, a NaN
+// quieted with its sign and payload kept -- the codes of enc_bf16 for every
+// input.  The fp32 -> bf16 cast kernel goes through it, so that cast's parity
+// test over all 2^32 fp32 patterns pins the equality.
+typedef float cv_f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 cv_bf16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16x2(uint32_t a, uint32_t b) {
+  const cv_f32x2 f = {u2f(a), u2f(b)};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, cv_bf16x2));
+}
+
 __device__ __forceinline__ uint32_t enc_f16(uint32_t x) {
   uint32_t a = x & 0x7FFFFFFFu;
   uint32_t c = min(round_mag<10, 15>(a), 0x7C00u);  // overflow -> Inf

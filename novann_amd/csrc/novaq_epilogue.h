@@ -145,6 +145,13 @@ __device__ __forceinline__ uint32_t epi_encode_t(float v, float inv_s) {
   else return f2u(v);
 }
 
+// Two 16-bit codes in one word (v0 in the low half).
+template <int OD>
+__device__ __forceinline__ uint32_t epi_encode2_t(float v0, float v1, float inv_s) {
+  if constexpr (OD == BF16) return pack_bf16x2(f2u(v0), f2u(v1));
+  else return epi_encode_t<OD>(v0, inv_s) | (epi_encode_t<OD>(v1, inv_s) << 16);
+}
+
 template <int OD>
 __device__ __forceinline__ void epi_store_t(void* y, int64_t i, float v, float inv_s) {
   if constexpr (OD == F32) reinterpret_cast<float*>(y)[i] = v;
@@ -158,10 +165,8 @@ __device__ __forceinline__ void epi_store4_t(void* y, int64_t i, const float* v,
   if constexpr (OD == F32) {
     *reinterpret_cast<float4*>(reinterpret_cast<float*>(y) + i) = make_float4(v[0], v[1], v[2], v[3]);
   } else if constexpr (OD == F16 || OD == BF16) {
-    const uint32_t c0 = epi_encode_t<OD>(v[0], inv_s), c1 = epi_encode_t<OD>(v[1], inv_s);
-    const uint32_t c2 = epi_encode_t<OD>(v[2], inv_s), c3 = epi_encode_t<OD>(v[3], inv_s);
     *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(y) + i) =
-        make_uint2(c0 | (c1 << 16), c2 | (c3 << 16));
+        make_uint2(epi_encode2_t<OD>(v[0], v[1], inv_s), epi_encode2_t<OD>(v[2], v[3], inv_s));
   } else {
     uint32_t w = 0;
 #pragma unroll
