@@ -3,10 +3,12 @@
 
 One step = BASELINE config [2]: a cast sweep over 2^28 fp32 elements held in
 HBM: fp32 -> fp16 -> fp32, fp32 -> bf16 -> fp32, and for E4M3 and E5M2 the
-per-tensor amax, the scale, the scaled cast and the scaled dequantization
-back to fp32.  `value` is the algorithmic bytes of the step (52 B/element)
-over its wall time, in GB/s.  Each kernel is also bracketed by HIP events on
-the stream it runs on, which gives the per-kernel roofline figures.  Further
+per-tensor quantization (the amax pass, then the scaled cast, which derives
+the scale from the amax itself) and the scaled dequantization back to fp32.
+`value` is the algorithmic bytes of the step (52 B/element) over its wall
+time, in GB/s, timed with nothing but the ops on the stream.  A second pass of
+the same steps brackets each op with HIP events on its stream, which gives
+the per-kernel roofline figures.  Further
 legs, each with its own roofline: the FP8-weight Linear of config [4]
 (x 2048x4096, W 4096x4096 E4M3) and its backward in TFLOP/s, the FP4 pack / unpack of config
 [3] and the two FP4-weight convolutions of config [5] in GB/s.  The CPU
@@ -34,8 +36,10 @@ METRIC = "cast GB/s (% HBM peak) at 256M elems; FP8-weight Linear TFLOP/s at 409
 # (op name, algorithmic bytes per element); the sequence of one step
 SWEEP = [
     ("f32->f16", 6), ("f16->f32", 6), ("f32->bf16", 6), ("bf16->f32", 6),
-    ("amax e4m3", 4), ("scale e4m3", 0), ("f32->e4m3 scaled", 5), ("e4m3->f32 scaled", 5),
-    ("amax e5m2", 4), ("scale e5m2", 0), ("f32->e5m2 scaled", 5), ("e5m2->f32 scaled", 5),
+    # novaq_quantize: the amax pass (4 B/element), then the scaled cast (5 B)
+    # deriving s = amax / 448 (57344) itself and writing it out
+    ("quantize f32->e4m3 (amax + scaled cast)", 9), ("e4m3->f32 scaled", 5),
+    ("quantize f32->e5m2 (amax + scaled cast)", 9), ("e5m2->f32 scaled", 5),
 ]
 BYTES_PER_ELEM = sum(b for _, b in SWEEP)
 # kernel behind each single-kernel op (rocprofv3 names), for the measured traffic
@@ -46,7 +50,7 @@ KERNEL_OF = {
     "f32->e5m2 scaled": "cast_kernel<0, 4, 1>", "e5m2->f32 scaled": "cast_kernel<4, 0, 1>",
 }
 FP4_KERNEL = {"pack f32->e2m1": "cast_kernel<0, 5, 1>", "unpack e2m1->f32": "cast_kernel<5, 0, 1>"}
-CONV_KERNEL = {1: "conv2d_band_kernel<5, 0, 1, false>", 32: "conv2d_band_kernel<5, 0, 1, true>"}
+CONV_KERNEL = {1: "conv2d_smallc_kernel<5, 0>", 32: "conv2d_band_kernel<5, 0, 1, true>"}
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 
 
@@ -81,8 +85,7 @@ def make_sweep(n: int, dev):
     y = torch.empty_like(x)
     h = torch.empty(n, dtype=torch.int16, device=dev)
     q = torch.empty(n, dtype=torch.uint8, device=dev)
-    amax = torch.zeros(2, dtype=torch.float32, device=dev)
-    scale = torch.ones(2, dtype=torch.float32, device=dev)
+    amax_scale = torch.zeros(4, dtype=torch.float32, device=dev)  # (amax, s) per FP8 format
     stream = torch.cuda.current_stream(dev).cuda_stream
     P = lambda t: t.data_ptr()  # noqa: E731
 
@@ -93,14 +96,13 @@ def make_sweep(n: int, dev):
         cast(x, 0, h, 1), cast(h, 1, y, 0), cast(x, 0, h, 2), cast(h, 2, y, 0),
     ]
     for k, dt in enumerate((3, 4)):
-        a_ptr, s_ptr = P(amax) + 4 * k, P(scale) + 4 * k
+        as_ptr = P(amax_scale) + 8 * k
         ops += [
-            lambda a_ptr=a_ptr: _lib.check(lib.novaq_amax(P(x), 0, n, a_ptr, stream), "amax"),
-            lambda a_ptr=a_ptr, s_ptr=s_ptr, dt=dt: _lib.check(
-                lib.novaq_scale_from_amax(a_ptr, dt, s_ptr, stream), "scale"),
-            cast(x, 0, q, dt, s_ptr), cast(q, dt, y, 0, s_ptr),
+            lambda as_ptr=as_ptr, dt=dt: _lib.check(
+                lib.novaq_quantize(P(x), 0, P(q), dt, n, as_ptr, stream), "quantize"),
+            cast(q, dt, y, 0, as_ptr + 4),
         ]
-    return [(name, b, fn) for (name, b), fn in zip(SWEEP, ops)], (x, y, h, q, amax, scale)
+    return [(name, b, fn) for (name, b), fn in zip(SWEEP, ops)], (x, y, h, q, amax_scale)
 
 
 def bench_sweep(n: int, steps: int, warmup: int, dev):
@@ -110,17 +112,22 @@ def bench_sweep(n: int, steps: int, warmup: int, dev):
         for _, _, fn in ops:
             fn()
     torch.cuda.synchronize(dev)
+    # the timed steps: the ops back to back, nothing else on the stream
+    t0 = time.perf_counter()
+    for s in range(steps):
+        for _, _, fn in ops:
+            fn()
+    torch.cuda.synchronize(dev)
+    t1 = time.perf_counter()
+    # then, as diagnostics, the same number of steps with events around each op
     events = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
                for _ in ops] for _ in range(steps)]
-    torch.cuda.synchronize(dev)
-    t0 = time.perf_counter()
     for s in range(steps):
         for (_, _, fn), (e0, e1) in zip(ops, events[s]):
             e0.record()
             fn()
             e1.record()
     torch.cuda.synchronize(dev)
-    t1 = time.perf_counter()
     per_op = []
     for i, (name, b, _) in enumerate(ops):
         t = [events[s][i][0].elapsed_time(events[s][i][1]) for s in range(steps)]
