@@ -806,6 +806,7 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
     // store each channel's run of P pixels in 8-byte (16-bit codes) or
     // 4-byte (8-bit) pieces -- contiguous spans, where the lanes' own stores
     // would be 32- or 16-byte pieces of 16 channel rows.
+    const bool track = ep.amax != nullptr;  // uniform: the amax is asked for
     auto stage_out = [&](auto od) {
       constexpr int OD = decltype(od)::value;
       constexpr int ES = dtype_bits(OD) / 8;
@@ -824,9 +825,10 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
           // P is a multiple of 4 here, so all four pixels are in the band
           float v[4];
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            v[i] = epi_value_nb(kc[t], acc[m][t][i], s, z);
-            am = epi_track(am, v[i]);  // committed only with ep.amax
+          for (int i = 0; i < 4; ++i) v[i] = epi_value_nb(kc[t], acc[m][t][i], s, z);
+          if (track) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) am = epi_track(am, v[i]);
           }
           uint8_t* d = ol + (t * 16 + lr) * rowb + p * ES;
           if constexpr (ES == 2) {
