@@ -181,17 +181,10 @@ __global__ __launch_bounds__(kCastThreads) void cast_kernel(
       int64_t u = base + (int64_t)j * kCastThreads;
       if (u < units) {
         Words<Sh::dst_words> out;
-        if constexpr (ST == F32 && DT == BF16) {
-          // two codes per packed convert (the rounding of enc_bf16)
 #pragma unroll
-          for (int i = 0; i < EPL; i += 2)
-            out.w[i / 2] = pack_bf16x2(get_elem<32>(in[j], i), get_elem<32>(in[j], i + 1));
-        } else {
-#pragma unroll
-          for (int i = 0; i < EPL; ++i) {
-            uint32_t c = get_elem<dtype_bits(ST)>(in[j], i);
-            put_elem<dtype_bits(DT)>(out, i, convert<ST, DT, SCALED>(c, s, inv_s));
-          }
+        for (int i = 0; i < EPL; ++i) {
+          uint32_t c = get_elem<dtype_bits(ST)>(in[j], i);
+          put_elem<dtype_bits(DT)>(out, i, convert<ST, DT, SCALED>(c, s, inv_s));
         }
         store_words<Sh::dst_bits>(dst + u * (Sh::dst_bits / 8), out);
       }

@@ -58,8 +58,10 @@ __device__ __forceinline__ uint32_t enc_bf16(uint32_t x) {
 // Two fp32 values (bits a, b) to two bf16 codes in one word, a in the low
 // half, with one gfx950 v_cvt_pk_bf16_f32: round to nearest even, a NaN
 // quieted with its sign and payload kept -- the codes of enc_bf16 for every
-// input.  The fp32 -> bf16 cast kernel goes through it, so that cast's parity
-// test over all 2^32 fp32 patterns pins the equality.
+// fp32 input (compared over all 2^32 patterns on the device).  The product
+// epilogues' bf16 stores use it; their parity tests check it against the
+// oracle's cast on every rounding class.  (The cast kernels keep enc_bf16:
+// the packed convert made the fp32 -> bf16 cast 2% slower.)
 typedef float cv_f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 cv_bf16x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack_bf16x2(uint32_t a, uint32_t b) {

@@ -123,6 +123,47 @@ def check_all_outputs(run, y0_bits, C, rng, axis=1):
         assert np.array_equal(got, O.cast(flat, O.F32, OUT[out], scale=s)), out
 
 
+def rounding_classes(rng):
+    """fp32 values covering every bf16 rounding case: random bf16 values of
+    every exponent (subnormal to the largest finite) plus 0, 1, just below /
+    at / just above the tie and the largest offset below the next value,
+    with both parities of the kept bit; and the specials (signed zeros and
+    infinities, NaNs with high / low / full payloads, subnormals at and
+    around the tie, the largest finite that rounds to infinity)."""
+    hi = rng.integers(0, 1 << 16, 400, dtype=np.uint32)
+    base = hi << 16
+    offs = np.array([0, 1, 0x7FFF, 0x8000, 0x8001, 0xFFFF], np.uint32)
+    vals = (base[:, None] + offs[None, :]).reshape(-1)
+    specials = np.array([0x00000000, 0x80000000, 0x7F800000, 0xFF800000, 0x7F800001,
+                         0x7FC00000, 0x7FFFFFFF, 0xFF800001, 0xFFC00001, 0x7F80FFFF,
+                         0x7FBFFFFF, 0x00000001, 0x00007FFF, 0x00008000, 0x00008001,
+                         0x00018000, 0x007FFFFF, 0x807FFFFF, 0x7F7FFFFF, 0x7F7F7FFF,
+                         0x7F7F8000, 0xFF7F8000], np.uint32)
+    v = np.concatenate([vals, specials])
+    v = np.concatenate([v, np.zeros((-v.size) % 64, np.uint32)])
+    return v.view(np.float32)
+
+
+@pytest.mark.parametrize("hw", [4, 3])
+def test_bf16_stores_round_every_class(hw):
+    """bf16 stores of the convolution's epilogue (staged through LDS when
+    rows pack into 8-byte pieces, hw = 4; the lanes' own stores otherwise)
+    equal the oracle's cast for every rounding class: with x = 0 each output
+    channel is its bias, so the bias vector feeds the encoder chosen values."""
+    print(f"bf16 store rounding hw={hw}", flush=True)
+    rng = np.random.default_rng(17)
+    bias = rounding_classes(rng)
+    C_out, C = bias.size, 8
+    x = np.zeros((2, C, hw, hw), np.float32)
+    w = rng.standard_normal((C_out, C, 1, 1)).astype(np.float32)
+    wd, ws, _ = quantized_codes(w, "e4m3", rng)
+    y0 = conv_ex(x, wd, "e4m3", ws, w.shape, (1, 1), (0, 0), "zeros", None, bias)
+    want = R.epilogue_f32(y0.view(np.float32), None, None, False, axis=1)
+    ep = Epi(C_out, rng, relu=False, out="bf16", amax=False, mul=False, add=False)
+    got = conv_ex(x, wd, "e4m3", ws, w.shape, (1, 1), (0, 0), "zeros", ep, bias).reshape(-1)
+    assert np.array_equal(got, O.cast(want.reshape(-1), O.F32, O.BF16))
+
+
 LINEAR_CASES = [
     ("e4m3", 256, 512, 256),   # linear_wide_kernel
     ("e2m1", 128, 256, 512),   # linear_wide_kernel, FP4
