@@ -33,19 +33,22 @@ int device_cu_count() {
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
-// Workspace of novaq_linear_backward: W^T in W's format, then grad in bf16
-// (at gyt) where the in-place weight-gradient product takes the shape, else
-// grad^T (bf16, at gyt) and x^T (bf16, at xt); each part 256-byte aligned.
+// Workspace of novaq_linear_backward: W^T in W's format (none when grad_input
+// reads W's codes in place), then grad in bf16 (at gyt) where the in-place
+// weight-gradient product takes the shape, else grad^T (bf16, at gyt) and x^T
+// (bf16, at xt); each part 256-byte aligned.
 struct LinearBwdWs {
   size_t wt, gyt, xt, total;
+  bool tn, wn;
 };
 static LinearBwdWs linear_bwd_ws(int64_t N, int64_t D_in, int64_t D_out, int w_dtype) {
   LinearBwdWs w;
+  w.tn = linear_tn_supported(D_out, D_in, N);
+  w.wn = w.tn && linear_wn_supported(N, D_out, D_in, w_dtype);
   w.wt = 0;
-  w.gyt = align256(((size_t)D_in * (size_t)D_out * dtype_bits(w_dtype) + 7) / 8);
+  w.gyt = w.wn ? 0 : align256(((size_t)D_in * (size_t)D_out * dtype_bits(w_dtype) + 7) / 8);
   w.xt = w.gyt + align256((size_t)D_out * (size_t)N * 2);
-  const bool tn = linear_tn_supported(D_out, D_in, N);
-  w.total = w.xt + (tn ? 0 : align256((size_t)D_in * (size_t)N * 2));
+  w.total = w.xt + (w.tn ? 0 : align256((size_t)D_in * (size_t)N * 2));
   return w;
 }
 static bool valid_dtype(int dt) { return dt >= F32 && dt <= E2M1; }
@@ -366,7 +369,7 @@ int novaq_linear_backward(const float* grad, const float* x, int64_t N, int64_t 
   // grad and x in place; it runs first, as it also leaves grad rounded to
   // bf16 for grad_input's product (the rounding that product's staging would
   // apply) and sums grad's columns into grad_bias
-  const bool tn = grad_weight && D_out > 0 && D_in > 0 && linear_tn_supported(D_out, D_in, N);
+  const bool tn = grad_weight && D_out > 0 && D_in > 0 && ws.tn;
   uint16_t* g16 = tn && grad_input ? reinterpret_cast<uint16_t*>(base + ws.gyt) : nullptr;
   bool bias_done = false;
   if (tn) {
@@ -374,18 +377,29 @@ int novaq_linear_backward(const float* grad, const float* x, int64_t N, int64_t 
     if (rc != NOVAQ_OK) return rc;
     bias_done = true;
   }
-  // grad_input = grad @ (s * dec(W)): the forward product on W^T (codes permuted)
+  // grad_input = grad @ (s * dec(W)): on the bf16 grad with W's FP8 codes read
+  // in place where the shape allows (transposing LDS reads), else the forward
+  // product on W^T (codes permuted)
   if (grad_input && N > 0 && D_in > 0) {
-    void* wt = base + ws.wt;
-    rc = transpose_launch(w_q, w_dtype, D_out, D_in, wt, w_dtype, s);
-    if (rc != NOVAQ_OK) return rc;
     Epilogue ep{};
     ep.out_dtype = F32;
-    if (g16)
-      rc = linear_launch(g16, BF16, nullptr, N, D_out, wt, w_dtype, w_scale, ep, D_in,
-                         grad_input, s);
-    else
-      rc = linear_launch(grad, N, D_out, wt, w_dtype, w_scale, nullptr, D_in, grad_input, s);
+    if (ws.wn) {
+      if (!g16) {  // no weight-gradient product to leave grad in bf16: round it here
+        g16 = reinterpret_cast<uint16_t*>(base + ws.gyt);
+        rc = cast_launch(grad, F32, g16, BF16, N * D_out, 0, nullptr, nullptr, s);
+        if (rc != NOVAQ_OK) return rc;
+      }
+      rc = linear_wn_launch(g16, BF16, N, D_out, w_q, w_dtype, w_scale, ep, D_in, grad_input, s);
+    } else {
+      void* wt = base + ws.wt;
+      rc = transpose_launch(w_q, w_dtype, D_out, D_in, wt, w_dtype, s);
+      if (rc != NOVAQ_OK) return rc;
+      if (g16)
+        rc = linear_launch(g16, BF16, nullptr, N, D_out, wt, w_dtype, w_scale, ep, D_in,
+                           grad_input, s);
+      else
+        rc = linear_launch(grad, N, D_out, wt, w_dtype, w_scale, nullptr, D_in, grad_input, s);
+    }
     if (rc != NOVAQ_OK) return rc;
   }
   // otherwise the forward product of grad^T and x^T, both transposed straight

@@ -361,6 +361,34 @@ __device__ __forceinline__ bf16x8 frag_to_bf16(const uint8_t* p) {
   return __builtin_bit_cast(bf16x8, r);
 }
 
+// The same 8 FP8 codes read from W kept in its own [K][N] layout in LDS with
+// gfx950's transposing read (ds_read_b64_tr_b8): within each group of 16
+// lanes, lane p names 8 bytes (row 2 j + h of the group's 8 rows, with
+// j = (p % 16) / 2 and h = p % 2 picking the half of a 16-byte column run),
+// and lane i receives byte i % 8 of the runs named by lanes 2 j + i / 8:
+// 8 consecutive K of one N index.
+typedef int i32x2_lds __attribute__((ext_vector_type(2)));
+template <int WT>
+__device__ __forceinline__ bf16x8 frag_to_bf16_tr(const uint8_t* p) {
+  static_assert(WT == E4M3 || WT == E5M2, "8-bit codes");
+  typedef __attribute__((address_space(3))) i32x2_lds lds_i32x2;
+  const i32x2_lds r = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2*)p);
+  const u32x2 v = {(uint32_t)r[0], (uint32_t)r[1]};
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    if constexpr (WT == E4M3) {
+      o[2 * i] = bf16_pair(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v[i], 1.0f, false));
+      o[2 * i + 1] = bf16_pair(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v[i], 1.0f, true));
+    } else {
+      o[2 * i] = bf16_pair(__builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(v[i], 1.0f, false));
+      o[2 * i + 1] = bf16_pair(__builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(v[i], 1.0f, true));
+    }
+  }
+  u32x4 rr = {o[0], o[1], o[2], o[3]};
+  return __builtin_bit_cast(bf16x8, rr);
+}
+
 constexpr int B_PITCH = BK + 8;  // bf16 per W row in LDS (144 B, conflict-free fragment reads)
 
 // ---------------------------------------------------------------------------
@@ -542,7 +570,12 @@ struct Wide {
   static constexpr int cpr = row_bytes / 16;            // W 16-byte chunks per row
 };
 
-template <int WT, int XT>
+// WN: W arrives in its natural [K][N] layout (the Linear backward's
+// grad_input = grad @ W reads the forward's W without a transposed copy; FP8
+// codes only): K blocks of W rows are staged as they are, 288-byte LDS rows
+// (8 mod 64 banks, so a transposing read's 8 rows x 32 bytes meet no
+// conflict), and B fragments come from frag_to_bf16_tr.
+template <int WT, int XT, bool WN = false>
 __global__ __launch_bounds__(512, 1) void linear_wide_kernel(
     const uint8_t* __restrict__ x, const float* __restrict__ x_scale, const uint8_t* __restrict__ w,
     const float* __restrict__ w_scale,
@@ -552,8 +585,11 @@ __global__ __launch_bounds__(512, 1) void linear_wide_kernel(
   constexpr int KB = F::KB;
   constexpr int FBN = 256, NTH = 512;
   constexpr int FWN = 64, FNT = 2;
+  static_assert(!WN || WT == E4M3 || WT == E5M2, "W in [K][N] layout: FP8 codes only");
+  constexpr int WNP = 288;                              // [K][N] layout: bytes per K row
   constexpr int A_ST = BM * F::a_pitch * 2;
-  constexpr int STAGE = A_ST + FBN * F::pitch;
+  constexpr int B_ST = WN ? KB * WNP : FBN * F::pitch;
+  constexpr int STAGE = A_ST + B_ST;
   constexpr int XC = BM * KB / 4 / NTH;                 // 8 x chunks per thread
   constexpr int WC = FBN * F::row_bytes / 16 / NTH;     // 4 (FP8) or 2 (E2M1) W chunks
   constexpr int UNITS = XC + WC;
@@ -584,31 +620,50 @@ __global__ __launch_bounds__(512, 1) void linear_wide_kernel(
       const_cast<uint8_t*>(x + (size_t)m0 * K * XB), (short)0, BM * K * XB, 0x00020000);
   const uint32_t xlane = (uint32_t)((tid >> 5) * K + (tid & 31) * 4) * (uint32_t)XB;
   const uint32_t xstep = 16u * (uint32_t)K * (uint32_t)XB;
+  // W rows are N (the forward's layout) or, with WN, K: then a K block is
+  // 128 rows of N bytes, of which the tile's 256 columns are 16 chunks
   const uint32_t w_row_bytes = (uint32_t)K * F::bits / 8;
-  const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint8_t*>(w + (size_t)n0 * w_row_bytes), (short)0, (int)(FBN * w_row_bytes),
-      0x00020000);
-  const uint32_t wlane = (uint32_t)(tid / F::cpr) * w_row_bytes + (uint32_t)(tid % F::cpr) * 16u;
-  const uint32_t wstep = (uint32_t)(NTH / F::cpr) * w_row_bytes;
+  const __amdgpu_buffer_rsrc_t wrs =
+      WN ? __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(w + n0), (short)0,
+                                             (int)((size_t)K * N - n0), 0x00020000)
+         : __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(w + (size_t)n0 * w_row_bytes),
+                                             (short)0, (int)(FBN * w_row_bytes), 0x00020000);
+  const uint32_t wlane = WN ? (uint32_t)(tid >> 4) * (uint32_t)N + (uint32_t)(tid & 15) * 16u
+                            : (uint32_t)(tid / F::cpr) * w_row_bytes + (uint32_t)(tid % F::cpr) * 16u;
+  const uint32_t wstep = WN ? 32u * (uint32_t)N : (uint32_t)(NTH / F::cpr) * w_row_bytes;
 
   // LDS: [A0 | A1 | B0 | B1].  Per-lane bases below; every other offset is a
   // compile-time constant that fits a ds instruction's 16-bit offset field.
-  constexpr int B_ST = FBN * F::pitch;
   constexpr int XDST_STEP = 16 * F::a_pitch * 2;
-  constexpr int WDST_STEP = (NTH / F::cpr) * F::pitch;
+  constexpr int WDST_STEP = WN ? 32 * WNP : (NTH / F::cpr) * F::pitch;
   constexpr int A_ROWS32 = 32 * F::a_pitch * 2;
-  constexpr int B_ROWS32 = 32 * F::pitch;
   const int xw = ((tid >> 5) * F::a_pitch + (tid & 31) * 4) * 2;
-  const int ww0 = 2 * A_ST + (tid / F::cpr) * F::pitch + (tid % F::cpr) * 16, ww1 = ww0 + B_ST;
+  const int ww0 = WN ? 2 * A_ST + (tid >> 4) * WNP + (tid & 15) * 16
+                     : 2 * A_ST + (tid / F::cpr) * F::pitch + (tid % F::cpr) * 16;
+  const int ww1 = ww0 + B_ST;
   const int ar = ((wm + (lane & 31)) * F::a_pitch + half * 8) * 2;
-  const int br0 = 2 * A_ST + (wn + (lane & 31)) * F::pitch + half * F::frag_bytes, br1 = br0 + B_ST;
+  // WN: the lane's role in the transposing read (row 8 (lane / 32) +
+  // (lane % 16) / 2 of the step's 16, columns 16 ((lane / 16) % 2) +
+  // 8 (lane % 2) .. +7 of the sub-tile's 32)
+  const int br0 = WN ? 2 * A_ST + (8 * (lane >> 5) + ((lane & 15) >> 1)) * WNP + wn +
+                           16 * ((lane >> 4) & 1) + 8 * (lane & 1)
+                     : 2 * A_ST + (wn + (lane & 31)) * F::pitch + half * F::frag_bytes;
+  const int br1 = br0 + B_ST;
+  // B fragment offsets: per 32-column sub-tile and per 16-K step
+  constexpr int BJ = WN ? 32 : 32 * F::pitch;
+  constexpr int BSTEP = WN ? 16 * WNP : 2 * F::frag_bytes;
+  auto bfrag = [](const uint8_t* p) {
+    if constexpr (WN) return frag_to_bf16_tr<WT>(p);
+    else return frag_to_bf16<WT>(p);
+  };
 
   struct Regs {
     u32x4 x[XC];
     u32x4 w[WC];
   };
   auto fetch = [&](Regs& r, int kb) {
-    const uint32_t xk = (uint32_t)kb * (KB * XB), wk = (uint32_t)kb * F::row_bytes;
+    const uint32_t xk = (uint32_t)kb * (KB * XB);
+    const uint32_t wk = WN ? (uint32_t)kb * KB * (uint32_t)N : (uint32_t)kb * F::row_bytes;
 #pragma unroll
     for (int i = 0; i < XC; ++i) {
       if constexpr (XB == 4) {
@@ -666,7 +721,7 @@ __global__ __launch_bounds__(512, 1) void linear_wide_kernel(
 #pragma unroll
     for (int i = 0; i < MT; ++i) a[0][i] = *reinterpret_cast<const bf16x8*>(SA + i * A_ROWS32);
 #pragma unroll
-    for (int j = 0; j < FNT; ++j) b[0][j] = frag_to_bf16<WT>(SB + j * B_ROWS32);
+    for (int j = 0; j < FNT; ++j) b[0][j] = bfrag(SB + j * BJ);
 #pragma unroll
     for (int s = 0; s < STEPS; ++s) {
       const int cur = s & 1, nxt = cur ^ 1;
@@ -676,7 +731,7 @@ __global__ __launch_bounds__(512, 1) void linear_wide_kernel(
           a[nxt][i] = *reinterpret_cast<const bf16x8*>(SA + i * A_ROWS32 + (s + 1) * 32);
 #pragma unroll
         for (int j = 0; j < FNT; ++j)
-          b[nxt][j] = frag_to_bf16<WT>(SB + j * B_ROWS32 + (s + 1) * 2 * F::frag_bytes);
+          b[nxt][j] = bfrag(SB + j * BJ + (s + 1) * BSTEP);
       }
 #pragma unroll
       for (int i = 0; i < MT; ++i)
@@ -983,6 +1038,28 @@ int launch(const uint8_t* x, const float* x_scale, int64_t M, int64_t K, const v
 }
 
 }  // namespace
+
+// y[M, N] = x[M, K] @ (s * dec(W[K, N])) with W in its natural [K][N] layout
+// (the Linear backward's grad_input = grad @ W on the forward's weight codes),
+// FP8 codes only, M % 128, N % 256, K % 128; NOVAQ_ENOTSUP for anything else
+// (the caller transposes W and uses the forward product instead).
+template <int XT>
+int linear_wn_launch_xt(const uint8_t* x, int64_t M, int64_t K, const void* w_q, int w_dtype,
+                        const float* w_scale, const Epilogue& ep, int64_t N, void* y,
+                        hipStream_t stream) {
+  if (!linear_wn_supported(M, K, N, w_dtype)) return NOVAQ_ENOTSUP;
+  const int64_t tiles_m = M / BM, tiles_n = N / 256;
+  const auto* wq = static_cast<const uint8_t*>(w_q);
+  if (w_dtype == E4M3)
+    hipLaunchKernelGGL((linear_wide_kernel<E4M3, XT, true>), dim3((unsigned)(tiles_m * tiles_n)),
+                       dim3(512), 0, stream, x, nullptr, wq, w_scale, ep, y, (int)M, (int)N,
+                       (int)K, (int)tiles_m, (int)tiles_n);
+  else
+    hipLaunchKernelGGL((linear_wide_kernel<E5M2, XT, true>), dim3((unsigned)(tiles_m * tiles_n)),
+                       dim3(512), 0, stream, x, nullptr, wq, w_scale, ep, y, (int)M, (int)N,
+                       (int)K, (int)tiles_m, (int)tiles_n);
+  return check_launch();
+}
 
 // The product for x stored as XT (one translation unit per XT instantiates it).
 template <int XT>

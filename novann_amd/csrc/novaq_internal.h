@@ -37,6 +37,17 @@ int linear_launch(const float* x, int64_t N, int64_t D_in, const void* w_q, int 
 int linear_launch(const void* x, int x_dtype, const float* x_scale, int64_t N, int64_t D_in,
                   const void* w_q, int w_dtype, const float* w_scale, const Epilogue& ep,
                   int64_t D_out, void* y, hipStream_t stream);
+// y[M, N] = x[M, K] @ (s * dec(W[K, N])) with W's codes in their natural
+// [K][N] layout (no transposed copy): bf16 x, FP8 W, M % 128, N % 256,
+// K % 128; NOVAQ_ENOTSUP otherwise.
+inline bool linear_wn_supported(int64_t M, int64_t K, int64_t N, int w_dtype) {
+  return (w_dtype == 3 || w_dtype == 4) && M > 0 && M % 128 == 0 && M <= 0x7FFFFFFF &&
+         N > 0 && N % 256 == 0 && K > 0 && K % 128 == 0 && K <= (1 << 21) &&
+         K * N < ((int64_t)1 << 31);
+}
+int linear_wn_launch(const void* x, int x_dtype, int64_t M, int64_t K, const void* w_q,
+                     int w_dtype, const float* w_scale, const Epilogue& ep, int64_t N, void* y,
+                     hipStream_t stream);
 int conv2d_launch(const float* x, int64_t N, int64_t C, int64_t H, int64_t W, const void* w_q,
                   int w_dtype, const float* w_scale, int64_t C_out, int KH, int KW, int sh,
                   int sw, int ph, int pw, int pad_mode, const float* bias, float* y,

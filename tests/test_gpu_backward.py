@@ -169,6 +169,43 @@ def test_weight_gradient_in_place_product(N, D_in, D_out):
         lib.novaq_linear_backward_workspace(N + 1, D_in, D_out, 3)
 
 
+@pytest.mark.parametrize("N,D_in,D_out,dt", [(128, 256, 128, "e4m3"), (256, 512, 384, "e5m2"),
+                                          (384, 768, 1024, "e4m3"), (128, 512, 256, "e2m1")])
+def test_input_gradient_on_weight_codes_in_place(N, D_in, D_out, dt):
+    """grad_input = bf16(grad) @ (s * dec(W)) with W's FP8 codes read in their
+    stored (D_out, D_in) layout through transposing LDS reads: within 1e-5
+    normwise of the fp64 product, with and without grad_weight asked for (the
+    bf16 grad then comes from a cast of its own); E2M1 takes the transposed
+    copy.  The in-place shapes need no W^T in the workspace."""
+    print(f"grad_input in place N={N} D_in={D_in} D_out={D_out} {dt}", flush=True)
+    rng = np.random.default_rng(N + D_in * 3 + D_out)
+    x = rng.standard_normal((N, D_in)).astype(np.float32)
+    g = rng.standard_normal((N, D_out)).astype(np.float32)
+    w, wdeq = weight_of((rng.standard_normal((D_out, D_in)) * 0.05).astype(np.float32), dt)
+    ref = bf16_round(g).astype(np.float64) @ wdeq
+    gi, gw, _ = F.linear_backward(torch.from_numpy(g).cuda(), torch.from_numpy(x).cuda(), w,
+                                  False)
+    torch.cuda.synchronize()
+    assert normwise(gi.cpu().numpy(), ref) <= 1e-5
+    assert normwise(gw.cpu().numpy(), bf16_round(g).astype(np.float64).T @
+                    bf16_round(x).astype(np.float64)) <= 1e-5
+    lib = _lib.load()
+    wdt = {"e4m3": O.E4M3, "e5m2": O.E5M2, "e2m1": O.E2M1}[dt]
+    nbytes = lib.novaq_linear_backward_workspace(N, D_in, D_out, wdt)
+    work = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    gd = torch.from_numpy(g).cuda()
+    gi2 = torch.full((N, D_in), float("nan"), device="cuda")
+    st = torch.cuda.current_stream().cuda_stream
+    _lib.check(lib.novaq_linear_backward(gd.data_ptr(), None, N, D_in, w.codes.data_ptr(), wdt,
+                                         w.scale.data_ptr(), D_out, gi2.data_ptr(), None, None,
+                                         work.data_ptr(), nbytes, st), "bwd")
+    torch.cuda.synchronize()
+    assert normwise(gi2.cpu().numpy(), ref) <= 1e-5
+    grad_bytes = -(-N * D_out * 2 // 256) * 256
+    wt_bytes = -(-D_in * D_out * (4 if dt == "e2m1" else 8) // 8 // 256) * 256
+    assert nbytes == grad_bytes + (wt_bytes if dt == "e2m1" else 0)
+
+
 def test_linear_backward_skips_null_outputs_and_empty_batch():
     rng = np.random.default_rng(3)
     w = QuantizedParameters.from_float(rng.standard_normal((64, 128)).astype(np.float32), "e4m3")
