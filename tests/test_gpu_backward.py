@@ -144,8 +144,10 @@ def bf16_round(a):
 
 
 # D_out % 128, D_in % 256, N % 64: the weight gradient reads grad and x in
-# place (transposing LDS reads); tile counts 1, 9 (not a multiple of 8) and 16
-@pytest.mark.parametrize("N,D_in,D_out", [(64, 256, 128), (128, 768, 384), (192, 1024, 512)])
+# place (transposing LDS reads); tile counts 1, 9 (not a multiple of 8) and 16,
+# and config [4]'s weight (256 x 256 tiles, one per CU)
+@pytest.mark.parametrize("N,D_in,D_out", [(64, 256, 128), (128, 768, 384), (192, 1024, 512),
+                                          (1024, 4096, 4096)])
 def test_weight_gradient_in_place_product(N, D_in, D_out):
     """grad_weight = grad^T x equals the fp64 product of the bf16-rounded
     operands up to fp32 summation error (1e-5 normwise): an index or layout
