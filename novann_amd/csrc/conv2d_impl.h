@@ -644,10 +644,15 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
           if (it < g.vitems) vstore(xl, it, rg.v[k]);
         }
       } else {
-        for (int it = tid; it < g.vitems; it += THREADS) {
-          f32x4 v[8];
-          vload(b, it, v);
-          vstore(xl, it, v);
+        // two items a pass, both items' loads issued before either is
+        // stored: one memory latency per pass
+        for (int it = tid; it < g.vitems; it += 2 * THREADS) {
+          f32x4 v[2][8];
+          const bool two = it + THREADS < g.vitems;
+          vload(b, it, v[0]);
+          if (two) vload(b, it + THREADS, v[1]);
+          vstore(xl, it, v[0]);
+          if (two) vstore(xl, it + THREADS, v[1]);
         }
       }
     }
