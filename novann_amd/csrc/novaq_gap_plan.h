@@ -26,8 +26,11 @@ struct GapLeaf {
 
 // The leaves in order and the combining tree as a postfix program: bit k of
 // prog is 1 for "push the next leaf's sum", 0 for "add the two top values".
+// balanced: the tree is complete (L = 2^d <= 8 leaves, all at depth d), so
+// adding neighbouring leaf sums pairwise, then neighbouring pairs, and so on,
+// associates exactly as the program does.
 struct GapPlan {
-  int L, nops;
+  int L, nops, balanced;
   uint32_t prog[GAP_PROG_WORDS];
   GapLeaf leaf[GAP_MAX_LEAVES];
 };
@@ -52,6 +55,17 @@ inline bool plan_rec(int n, int off, int depth, GapPlan& p) {
   ++p.nops;  // bit 0: add
   return true;
 }
+inline void depth_range(int n, int depth, int& lo, int& hi) {
+  if (n <= 128) {
+    lo = depth < lo ? depth : lo;
+    hi = depth > hi ? depth : hi;
+    return;
+  }
+  int n2 = n / 2;
+  n2 -= n2 % 8;
+  depth_range(n2, depth + 1, lo, hi);
+  depth_range(n - n2, depth + 1, lo, hi);
+}
 }  // namespace gap_detail
 
 // Fills p for a plane of n elements (1 <= n).  Returns false, leaving p
@@ -60,7 +74,11 @@ inline bool plan_rec(int n, int off, int depth, GapPlan& p) {
 inline bool gap_plan(int n, GapPlan& p) {
   p = GapPlan{};
   if (n < 1) return false;
-  return gap_detail::plan_rec(n, 0, 0, p);
+  if (!gap_detail::plan_rec(n, 0, 0, p)) return false;
+  int lo = 1 << 30, hi = -1;
+  gap_detail::depth_range(n, 0, lo, hi);
+  p.balanced = (lo == hi && p.L == (1 << lo) && p.L <= 8) ? 1 : 0;
+  return true;
 }
 
 }  // namespace novaq

@@ -339,7 +339,7 @@ __global__ __launch_bounds__(256) void global_avg_pool2d_kernel(const uint8_t* _
 // --- global average, wave-parallel (planes of at most 8192 elements) -------
 //
 // numpy's pairwise recursion on a plane of n <= 8192 elements (one buffer
-// block) splits it into leaves of <= 128 elements (at most 64) combined by a
+// block) splits it into leaves of <= 128 elements (at most 65) combined by a
 // fixed binary tree; the host works both out once per launch (every plane
 // has the same n) into a GapPlan: the leaves in order and the tree as a
 // postfix program (bit 1: push the next leaf's sum, bit 0: add the two top
@@ -348,7 +348,10 @@ __global__ __launch_bounds__(256) void global_avg_pool2d_kernel(const uint8_t* _
 // combine them as ((r0+r1)+(r2+r3))+((r4+r5)+(r6+r7)), lane 0 of the 8 adds
 // the leaf's remainder in order; the plane's first lane then runs the program
 // over the leaf sums with an 8-deep register stack (the tree is at most 7
-// levels deep).  Same operations in the same association as numpy.
+// levels deep).  Same operations in the same association as numpy.  When the
+// tree is complete (L = 2^d <= 8 leaves at one depth: 28 x 28, 14 x 14 and
+// 7 x 7 planes among them) the leaf sums are added by shuffles instead,
+// neighbours first, which is the same association.
 constexpr int GAP_STAGE = 2048;  // at most this many elements of a wave's planes staged in LDS
 
 // STAGED (a wave's planes hold at most GAP_STAGE elements): the wave first
@@ -402,6 +405,8 @@ __global__ __launch_bounds__(256) void global_avg_pool2d_wave_kernel(
     if constexpr (STAGED) return gap_stage[(wave * ppw + pi) * hw + lt.off + i];
     else return elem<XT>(x, base + lt.off + i, s, scaled);
   };
+  const bool bal = plan.balanced != 0;  // uniform: one pass (L <= 8), sums in registers
+  float leafsum = 0.0f;
   for (int p0 = 0; p0 < L; p0 += G) {
     const int leaf = p0 + li;
     const bool on = live && leaf < L;
@@ -436,8 +441,18 @@ __global__ __launch_bounds__(256) void global_avg_pool2d_wave_kernel(
 #pragma unroll
       for (int q = 0; q < 7; ++q)
         if (e0 + q < lt.len) res += t[q];
-      sums[wave][pi * L + leaf] = res;
+      if (bal) leafsum = res;
+      else sums[wave][pi * L + leaf] = res;
     }
+  }
+  if (bal) {
+    // a complete tree: leaf sums sit in lanes 8 li of the plane's 8 L lanes;
+    // adding neighbours, then pairs of neighbours, ... associates as the
+    // plan's program does
+    float v = leafsum;
+    for (int d = 8; d < 8 * L; d <<= 1) v = v + __shfl_down(v, d, 8 * L);
+    if (live && rem == 0) y[plane] = (0.0f + v) / (float)hw;
+    return;
   }
   __syncthreads();
   if (live && rem == 0) {

@@ -45,15 +45,15 @@ def plans(tmp_path_factory):
     res = {}
     for line in out.splitlines():
         f = line.split()
-        n, ok, L, nops = map(int, f[:4])
+        n, ok, L, nops, bal = map(int, f[:5])
         if not ok:
             res[n] = None
             continue
-        words = len(f) - 4 - L
-        prog_words = [int(v) for v in f[4:4 + words]]
-        leaves = [tuple(map(int, v.split(","))) for v in f[4 + words:]]
+        words = len(f) - 5 - L
+        prog_words = [int(v) for v in f[5:5 + words]]
+        leaves = [tuple(map(int, v.split(","))) for v in f[5 + words:]]
         prog = [(prog_words[k >> 5] >> (k & 31)) & 1 for k in range(nops)]
-        res[n] = (L, nops, leaves, prog)
+        res[n] = (L, nops, leaves, prog, bal)
     return res
 
 
@@ -61,10 +61,35 @@ def test_plan_matches_numpy_split_for_every_plane_size(plans):
     assert len(plans) == 9000
     for n in range(1, 8193):
         assert plans[n] is not None, n
-        L, nops, leaves, prog = plans[n]
+        L, nops, leaves, prog = plans[n][:4]
         want_leaves, want_prog = numpy_split(n)
         assert leaves == want_leaves and prog == want_prog, n
         assert L == len(leaves) and nops == 2 * L - 1, n
+
+
+def complete_tree_prog(L):
+    """Postfix program of the complete binary tree over L = 2^d leaves."""
+    if L == 1:
+        return [1]
+    half = complete_tree_prog(L // 2)
+    return half + half + [0]
+
+
+def test_balanced_flag_marks_exactly_the_complete_trees(plans):
+    # the kernel adds such plans' leaf sums by pairwise shuffles (neighbours,
+    # then pairs of pairs): that is the program's association exactly when the
+    # program is the complete tree's; plane sizes up to 1024 (32 x 32) cover
+    # every L in {1, 2, 4, 8}
+    seen = set()
+    for n in range(1, 8193):
+        L, nops, leaves, prog, bal = plans[n]
+        complete = L in (1, 2, 4, 8) and prog == complete_tree_prog(L)
+        assert bool(bal) == complete, n
+        if bal:
+            seen.add(L)
+    assert seen == {1, 2, 4, 8}
+    assert plans[784][4] == 1 and plans[49][4] == 1 and plans[196][4] == 1
+    assert plans[7921][4] == 0
 
 
 def test_capacity_covers_65_leaves():
@@ -109,7 +134,7 @@ def _leaf_sum(a):
 def test_plan_evaluates_to_np_mean(plans, n):
     rng = np.random.default_rng(n)
     a = (rng.standard_normal(n) * np.exp2(rng.integers(-6, 6, n))).astype(np.float32)
-    L, nops, leaves, prog = plans[n]
+    L, nops, leaves, prog = plans[n][:4]
     sums = [_leaf_sum(a[o:o + ln]) for o, ln in leaves]
     st, k = [], 0
     for op in prog:

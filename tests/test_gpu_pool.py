@@ -112,9 +112,12 @@ def test_max_pool2d_narrow_codes(xt, ksp):
 
 
 # (2, 3, 89, 89), (1, 2, 90, 90), (1, 3, 1, 8191), (1, 1, 87, 89): planes whose
-# numpy pairwise tree has 65 leaves; (2, 2, 64, 128): one whole 8192 block
+# numpy pairwise tree has 65 leaves; (2, 2, 64, 128): one whole 8192 block;
+# 7 x 7, 14 x 14, 20 x 20 and 28 x 28: complete trees of 1, 2, 4 and 8 leaves
+# (leaf sums added by shuffles)
 @pytest.mark.parametrize("xs", [(2, 3, 4, 5), (4, 3, 10, 12), (128, 64, 7, 7), (3, 2, 1, 7),
-                                (2, 2, 14, 14), (1, 3, 28, 28), (2, 2, 37, 41), (1, 1, 128, 129),
+                                (2, 2, 14, 14), (1, 3, 28, 28), (8, 64, 28, 28), (3, 5, 20, 20),
+                                (2, 2, 37, 41), (1, 1, 128, 129),
                                 (2, 3, 89, 89), (1, 2, 90, 90), (1, 3, 1, 8191), (1, 1, 87, 89),
                                 (2, 2, 64, 128)])
 def test_avg_pool2d_bit_exact(xs):
