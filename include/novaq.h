@@ -298,13 +298,14 @@ size_t novaq_linear_backward_workspace(int64_t N, int64_t D_in, int64_t D_out, i
  * Replaces: Linear.backward (novann/layers/linear/linear.py:85-108).  Any of
  * the three outputs may be NULL (not computed).  The products run on bf16
  * MFMA with fp32 accumulation on grad and x rounded to bf16: grad_input on
- * w_q's FP8 codes read in place when D_out % 128, D_in % 256 and N % 128 are
- * 0, else on the Linear forward kernels with w_q's codes transposed (exact);
- * grad_weight with grad and x read in place when D_out % 128, D_in % 256 and
- * N % 64 are 0, else through bf16 transposed copies.  workspace: device memory of
- * novaq_linear_backward_workspace() bytes
- * (16-byte aligned) the call may overwrite; it is not used after the call's
- * kernels complete. */
+ * w_q's FP8 codes and the fp32 grad, both read in place, when D_out % 128,
+ * D_in % 256 and N % 128 are 0, else on the Linear forward kernels with
+ * w_q's codes transposed (exact); grad_weight with grad and x read in place
+ * when D_out % 128, D_in % 256 and N % 64 are 0, else through bf16
+ * transposed copies.  workspace: device memory of
+ * novaq_linear_backward_workspace() bytes (16-byte aligned; may be NULL when
+ * that is 0) the call may overwrite; it is not used after the call's kernels
+ * complete. */
 int novaq_linear_backward(const float *grad, const float *x, int64_t N, int64_t D_in,
                           const void *w_q, int w_dtype, const float *w_scale, int64_t D_out,
                           float *grad_input, float *grad_weight, float *grad_bias,

@@ -33,10 +33,11 @@ int device_cu_count() {
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
-// Workspace of novaq_linear_backward: W^T in W's format (none when grad_input
-// reads W's codes in place), then grad in bf16 (at gyt) where the in-place
-// weight-gradient product takes the shape, else grad^T (bf16, at gyt) and x^T
-// (bf16, at xt); each part 256-byte aligned.
+// Workspace of novaq_linear_backward: none when grad_input reads W's codes in
+// place (and the fp32 grad, rounding it while staging); otherwise W^T in W's
+// format, then grad in bf16 (at gyt) where the in-place weight-gradient
+// product takes the shape, else grad^T (bf16, at gyt) and x^T (bf16, at xt);
+// each part 256-byte aligned.
 struct LinearBwdWs {
   size_t wt, gyt, xt, total;
   bool tn, wn;
@@ -46,9 +47,9 @@ static LinearBwdWs linear_bwd_ws(int64_t N, int64_t D_in, int64_t D_out, int w_d
   w.tn = linear_tn_supported(D_out, D_in, N);
   w.wn = w.tn && linear_wn_supported(N, D_out, D_in, w_dtype);
   w.wt = 0;
-  w.gyt = w.wn ? 0 : align256(((size_t)D_in * (size_t)D_out * dtype_bits(w_dtype) + 7) / 8);
+  w.gyt = align256(((size_t)D_in * (size_t)D_out * dtype_bits(w_dtype) + 7) / 8);
   w.xt = w.gyt + align256((size_t)D_out * (size_t)N * 2);
-  w.total = w.xt + (w.tn ? 0 : align256((size_t)D_in * (size_t)N * 2));
+  w.total = w.wn ? 0 : w.xt + (w.tn ? 0 : align256((size_t)D_in * (size_t)N * 2));
   return w;
 }
 static bool valid_dtype(int dt) { return dt >= F32 && dt <= E2M1; }
@@ -354,7 +355,7 @@ int novaq_linear_backward(const float* grad, const float* x, int64_t N, int64_t 
   if (N < 0 || D_in < 0 || D_out < 0) return NOVAQ_EINVAL;
   if (w_dtype == E2M1 && ((D_in | D_out) & 1)) return NOVAQ_ESHAPE;  // whole bytes both ways
   const LinearBwdWs ws = linear_bwd_ws(N, D_in, D_out, w_dtype);
-  if ((grad_input || grad_weight) && (!workspace || workspace_bytes < ws.total))
+  if ((grad_input || grad_weight) && ws.total > 0 && (!workspace || workspace_bytes < ws.total))
     return NOVAQ_EINVAL;
   if (N > 0 && D_out > 0 && !grad) return NOVAQ_EINVAL;
   if (grad_input && N > 0 && D_in > 0 && D_out > 0 && !w_q) return NOVAQ_EINVAL;
@@ -370,26 +371,23 @@ int novaq_linear_backward(const float* grad, const float* x, int64_t N, int64_t 
   // bf16 for grad_input's product (the rounding that product's staging would
   // apply) and sums grad's columns into grad_bias
   const bool tn = grad_weight && D_out > 0 && D_in > 0 && ws.tn;
-  uint16_t* g16 = tn && grad_input ? reinterpret_cast<uint16_t*>(base + ws.gyt) : nullptr;
+  uint16_t* g16 =
+      tn && grad_input && !ws.wn ? reinterpret_cast<uint16_t*>(base + ws.gyt) : nullptr;
   bool bias_done = false;
   if (tn) {
     rc = linear_tn_launch(grad, x, D_out, D_in, N, grad_weight, grad_bias, g16, s);
     if (rc != NOVAQ_OK) return rc;
     bias_done = true;
   }
-  // grad_input = grad @ (s * dec(W)): on the bf16 grad with W's FP8 codes read
-  // in place where the shape allows (transposing LDS reads), else the forward
-  // product on W^T (codes permuted)
+  // grad_input = grad @ (s * dec(W)): where the shape allows, on W's FP8 codes
+  // read in place (transposing LDS reads) and the fp32 grad, rounded to bf16
+  // while staged; else the forward product on W^T (codes permuted) and the
+  // bf16 grad the weight-gradient product left
   if (grad_input && N > 0 && D_in > 0) {
     Epilogue ep{};
     ep.out_dtype = F32;
     if (ws.wn) {
-      if (!g16) {  // no weight-gradient product to leave grad in bf16: round it here
-        g16 = reinterpret_cast<uint16_t*>(base + ws.gyt);
-        rc = cast_launch(grad, F32, g16, BF16, N * D_out, 0, nullptr, nullptr, s);
-        if (rc != NOVAQ_OK) return rc;
-      }
-      rc = linear_wn_launch(g16, BF16, N, D_out, w_q, w_dtype, w_scale, ep, D_in, grad_input, s);
+      rc = linear_wn_launch(grad, F32, N, D_out, w_q, w_dtype, w_scale, ep, D_in, grad_input, s);
     } else {
       void* wt = base + ws.wt;
       rc = transpose_launch(w_q, w_dtype, D_out, D_in, wt, w_dtype, s);

@@ -19,6 +19,8 @@ extern template int linear_launch_xt<E4M3>(const uint8_t*, const float*, int64_t
 extern template int linear_launch_xt<E5M2>(const uint8_t*, const float*, int64_t, int64_t,
                                            const void*, int, const float*, const Epilogue&,
                                            int64_t, void*, hipStream_t);
+template int linear_wn_launch_xt<F32>(const uint8_t*, int64_t, int64_t, const void*, int,
+                                      const float*, const Epilogue&, int64_t, void*, hipStream_t);
 extern template int linear_wn_launch_xt<BF16>(const uint8_t*, int64_t, int64_t, const void*, int,
                                               const float*, const Epilogue&, int64_t, void*,
                                               hipStream_t);
@@ -26,9 +28,12 @@ extern template int linear_wn_launch_xt<BF16>(const uint8_t*, int64_t, int64_t, 
 int linear_wn_launch(const void* x, int x_dtype, int64_t M, int64_t K, const void* w_q,
                      int w_dtype, const float* w_scale, const Epilogue& ep, int64_t N, void* y,
                      hipStream_t stream) {
-  if (x_dtype != BF16) return NOVAQ_ENOTSUP;
-  return linear_wn_launch_xt<BF16>(static_cast<const uint8_t*>(x), M, K, w_q, w_dtype, w_scale, ep,
-                                   N, y, stream);
+  const auto* xb = static_cast<const uint8_t*>(x);
+  switch (x_dtype) {
+    case F32: return linear_wn_launch_xt<F32>(xb, M, K, w_q, w_dtype, w_scale, ep, N, y, stream);
+    case BF16: return linear_wn_launch_xt<BF16>(xb, M, K, w_q, w_dtype, w_scale, ep, N, y, stream);
+    default: return NOVAQ_ENOTSUP;
+  }
 }
 
 int linear_launch(const void* x, int x_dtype, const float* x_scale, int64_t N, int64_t D_in,
