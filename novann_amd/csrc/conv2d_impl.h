@@ -408,9 +408,10 @@ __global__ __launch_bounds__(THREADS, CONV_OCC) void conv2d_kernel(
 //     FP8 / FP4 codes kept packed and decoded per MFMA fragment (exact);
 //   - the band's input rows are staged in LDS channel-last in bf16 (RNE);
 //     whole 4-column groups of the interior come in as 16-byte loads of 8
-//     channels, issued into registers before the weights are regrouped (when
-//     there is at most one such item per thread) so their latency overlaps
-//     that work, and are transposed in registers; padding columns are
+//     channels (bf16 x: its codes as they are), issued into registers before
+//     the weights are regrouped (when there is at most one such item per
+//     thread) so their latency overlaps that work, and are transposed in
+//     registers; padding columns are
 //     resolved element-wise with numpy.pad's index rules;
 //   - many small workgroups per CU: one's loads overlap another's MFMAs and
 //     stores.
@@ -439,11 +440,22 @@ struct BandGeom {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-// 16-byte-load items of one band held in registers: IPT items per thread,
-// each 8 channels x 4 columns.
-template <int IPT>
+// A staging item's registers: 8 channels x 4 columns as fp32 values, or for
+// bf16 x the raw codes (two words a channel): the staged layout is bf16, so
+// bf16 codes move as they are, never widened and narrowed again.
+template <int XT>
+struct BandItem {
+  f32x4 v[8];
+};
+template <>
+struct BandItem<BF16> {
+  uint32_t w[8][2];
+};
+
+// 16-byte-load items of one band held in registers: IPT items per thread.
+template <int IPT, int XT>
 struct BandRegs {
-  f32x4 v[IPT > 0 ? IPT : 1][8];
+  BandItem<XT> v[IPT > 0 ? IPT : 1];
 };
 
 // K9: 3x3 window, C a multiple of 8 and packed FP8 / FP4 codes copied to LDS:
@@ -468,7 +480,7 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
   const int W4 = g.W >> 2;
 
   // 16-byte-load item `it` of band b: (row r, column group cg, channel group q)
-  auto vload = [&](int b, int it, f32x4* v) {
+  auto vload = [&](int b, int it, BandItem<XT>& v) {
     const int q = it % g.c8, rest = it / g.c8;
     const int cg = rest % W4, r = rest / W4;
     const int hi = pad_index(b * g.R * g.sh - g.ph + r, g.H, g.pad_mode);
@@ -476,9 +488,20 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int c = q * 8 + j;
-      v[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-      if (used && hi >= 0 && c < g.C)
-        v[j] = x4_f32<XT>(x, xn + c * HW + (int64_t)hi * g.W + cg * 4);
+      const bool live = used && hi >= 0 && c < g.C;
+      const int64_t e = xn + c * HW + (int64_t)hi * g.W + cg * 4;
+      if constexpr (XT == BF16) {
+        v.w[j][0] = v.w[j][1] = 0u;
+        if (live) {
+          const xl_u32x4 raw = x4_raw<BF16>(x, e);
+          const uint32_t w0 = raw[0], w1 = raw[1];
+          v.w[j][0] = w0;
+          v.w[j][1] = w1;
+        }
+      } else {
+        v.v[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        if (live) v.v[j] = x4_f32<XT>(x, e);
+      }
     }
   };
   // --- weights: (co, c, kh, kw) -> [co][K group] ---------------------------
@@ -507,7 +530,7 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
     }
   }
   // then the band's 16-byte loads
-  BandRegs<IPT> r0;
+  BandRegs<IPT, XT> r0;
   if constexpr (IPT > 0) {
     if (tid < g.vitems) vload(band, tid, r0.v[0]);
   }
@@ -616,7 +639,7 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
   }
   __syncthreads();  // weights regrouped; the raw copy region is free
 
-  auto vstore = [&](uint16_t* xl, int it, const f32x4* v) {
+  auto vstore = [&](uint16_t* xl, int it, const BandItem<XT>& v) {
     const int q = it % g.c8, rest = it / g.c8;
     const int cg = rest % W4, r = rest / W4;
     const int col0 = cg * 4 + g.pw;  // staged column of input column 4*cg
@@ -627,15 +650,21 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
       uint32_t pk[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        f32x2 f = {v[2 * j][i], v[2 * j + 1][i]};
-        pk[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));
+        if constexpr (XT == BF16) {
+          // column i's codes of channels 2j and 2j + 1
+          const uint32_t a = v.w[2 * j][i >> 1], b2 = v.w[2 * j + 1][i >> 1];
+          pk[j] = (i & 1) ? ((a >> 16) | (b2 & 0xFFFF0000u)) : ((a & 0xFFFFu) | (b2 << 16));
+        } else {
+          f32x2 f = {v.v[2 * j][i], v.v[2 * j + 1][i]};
+          pk[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));
+        }
       }
       *reinterpret_cast<uint4*>(&xl[(r * g.wp + col) * g.cstride + q * 8]) =
           make_uint4(pk[0], pk[1], pk[2], pk[3]);
     }
   };
   // stage band b into buffer xl (from the registers when IPT > 0)
-  auto stage = [&](const BandRegs<IPT>& rg, int b, uint16_t* xl) {
+  auto stage = [&](const BandRegs<IPT, XT>& rg, int b, uint16_t* xl) {
     if (g.vec) {
       if constexpr (IPT > 0) {
 #pragma unroll
@@ -647,7 +676,7 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
         // two items a pass, both items' loads issued before either is
         // stored: one memory latency per pass
         for (int it = tid; it < g.vitems; it += 2 * THREADS) {
-          f32x4 v[2][8];
+          BandItem<XT> v[2];
           const bool two = it + THREADS < g.vitems;
           vload(b, it, v[0]);
           if (two) vload(b, it + THREADS, v[1]);
