@@ -4,7 +4,8 @@
 whole-tile shapes), MaxPool2d and GlobalAvgPool2d.  Each case is drawn from a
 seeded generator and printed before it runs; the bars are the suites' own
 (normwise 1e-2 against fp64 for the products and gradients, bit-exact for the
-pools)."""
+pools; the fused epilogues bit-exact on the unfused output, every narrow store
+equal to the oracle's cast)."""
 import numpy as np
 import pytest
 import torch
@@ -15,6 +16,7 @@ from novann_amd import functional as F
 from tests import test_gpu_backward as TLB
 from tests import test_gpu_conv2d as TC
 from tests import test_gpu_conv2d_backward as TB
+from tests import test_gpu_epilogue as TE
 from tests import test_gpu_linear as TL
 
 pytestmark = pytest.mark.gpu
@@ -148,3 +150,35 @@ def test_pools_random_shapes_bit_exact(seed):
         got = np.asarray(F.max_pool2d(x, k, st, pd, "zeros"))
         want = R.max_pool2d(x, k, st, pd, "zeros")
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("seed", SEEDS)
+def test_fused_epilogues_random_geometries(seed):
+    """BN-style per-channel affine + ReLU + amax, and bf16 / f16 / E4M3 /
+    E5M2 stores, on random convolutions and Linear shapes."""
+    rng = np.random.default_rng(seed + 500)
+    for i in range(8):
+        N, C, H, W, C_out, KH, KW, sh, sw, ph, pw, mode, wdt = conv_case(rng)
+        print(f"conv epilogue seed {seed} case {i}: "
+              f"{(N, C, H, W, C_out, KH, KW, sh, sw, ph, pw, mode, wdt)}", flush=True)
+        x = rng.standard_normal((N, C, H, W)).astype(np.float32)
+        wshape = (C_out, C, KH, KW)
+        w = (rng.standard_normal(wshape) * np.sqrt(2.0 / (C * KH * KW))).astype(np.float32)
+        bias = rng.standard_normal(C_out).astype(np.float32)
+        wd, ws, _ = TE.quantized_codes(w, wdt, rng)
+        run = lambda ep: TE.conv_ex(x, wd, wdt, ws, wshape, (sh, sw), (ph, pw), mode, ep,  # noqa: E731
+                                    bias)
+        TE.check_all_outputs(run, run(None), C_out, rng)
+    for i in range(6):
+        M, D_in, D_out = int(rng.integers(1, 300)), int(rng.integers(1, 600)), int(rng.integers(1, 500))
+        if rng.random() < 0.5:
+            M, D_in, D_out = (128 * int(rng.integers(1, 3)), 64 * int(rng.integers(1, 5)),
+                              256 * int(rng.integers(1, 3)))
+        wdt = str(rng.choice(["e4m3", "e5m2", "bf16"]))
+        print(f"linear epilogue seed {seed} case {i}: {(M, D_in, D_out, wdt)}", flush=True)
+        x = rng.standard_normal((M, D_in)).astype(np.float32)
+        w = (rng.standard_normal((D_out, D_in)) * np.sqrt(2.0 / D_in)).astype(np.float32)
+        bias = rng.standard_normal(D_out).astype(np.float32)
+        wd, ws, _ = TE.quantized_codes(w, wdt, rng)
+        run = lambda ep: TE.linear_ex(x, wd, wdt, ws, D_out, ep, bias)  # noqa: E731
+        TE.check_all_outputs(run, run(None), D_out, rng)
