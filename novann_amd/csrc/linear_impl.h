@@ -13,14 +13,18 @@
 // run on v_mfma_f32_32x32x16_bf16 with fp32 accumulation; the per-tensor scale
 // s and the bias are applied in fp32 after accumulation.
 //
-// Four kernels, chosen by shape and the operands' formats:
+// Five kernels, chosen by shape and the operands' formats:
 //   - linear_f8_kernel (x stored as E4M3 / E5M2 and FP8 / FP4 weights, M % 128,
 //     N % 256, K % 128): both operands' codes on the FP8 MFMA
 //     (v_mfma_f32_32x32x64_f8f6f4), loaded straight into LDS;
-//   - linear_wide_kernel (FP8 / FP4 weights, M % 128, N % 256, K % 128): one
-//     128 x 256 tile per workgroup of 8 waves, K blocks of 128 (one 128-byte
-//     line of an FP8 W row), W raw in LDS and decoded per MFMA fragment,
-//     buffer loads with SGPR offsets;
+//   - linear_pingpong_kernel (FP8 weights, x in fp32 / bf16 / f16, M % 128,
+//     N % 256, K % 128): the 128 x 256 tile on two wave groups that take
+//     turns at the matrix cores and at the operand traffic;
+//   - linear_wide_kernel (E2M1 weights, and FP8 weights in their [K][N]
+//     layout for the backward; M % 128, N % 256, K % 128): one 128 x 256 tile
+//     per workgroup of 8 waves, K blocks of 128 (one 128-byte line of an FP8
+//     W row), W raw in LDS and decoded per MFMA fragment, buffer loads with
+//     SGPR offsets;
 //   - linear_pipe_kernel (whole 128-row tiles, K % 64): W decoded once per
 //     workgroup into bf16 LDS tiles, loads kept up to 3 K blocks ahead;
 //   - linear_kernel: any shape (guarded edge tiles) and fp32 weights.
@@ -757,6 +761,236 @@ __global__ __launch_bounds__(512, 1) void linear_wide_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Ping-pong kernel (E4M3 / E5M2 weights, x in fp32 / bf16 / f16, M % 128,
+// N % 256, K % 128): the wide kernel's 128 x 256 tile and 64 x 64 wave tiles,
+// scheduled so that the matrix cores are not idle while operands move.  The
+// 8 waves form two groups of 4 (rows 0-63 and 64-127 of the tile); waves w
+// and w + 4 share a SIMD.  Every wave runs the same program of phases
+// separated by workgroup barriers -- per K block of 128: M0 (read the
+// fragments of K 0-63, stage half of the next block), C0 (16 MFMAs), M1 (the
+// fragments of K 64-127, the other half), C1 -- and group 1 passes one extra
+// barrier first, so it runs one phase behind group 0: while one wave of a
+// SIMD multiplies, the other reads LDS and issues loads.
+//
+// x: each group loads its own 64 rows into registers (two register sets, so a
+// block's loads are issued two blocks before it is staged) and rounds them to
+// bf16 into padded LDS rows.  W: group 0 copies each block straight into LDS
+// with buffer_load ... lds, in two K halves of 256 rows x 64 bytes whose
+// 16-byte chunks are XOR-swizzled by row (chunk c of row r at slot
+// c ^ ((r / 4) % 4): the 16 rows one fragment read serves per LDS cycle hit
+// distinct banks).  A lane's B fragment for two consecutive 16-K MFMA steps
+// is one 16-byte read: lane half h holds K [16 h, 16 h + 16) of a 32-K pair,
+// and the x fragments follow the same K order (MFMA step u of the pair takes
+// K 16 h + 8 u .. + 7 in both operands).  Synchronisation: s_waitcnt
+// lgkmcnt(0) then s_barrier at every phase end; after each multiply phase
+// s_waitcnt vmcnt(12) -- group 0's copy of the previous memory phase has
+// landed (the x loads issued after it may still be in flight).
+
+template <int WT, int XT>
+__global__ __launch_bounds__(512, 1) void linear_pingpong_kernel(
+    const uint8_t* __restrict__ x, const float* __restrict__ x_scale, const uint8_t* __restrict__ w,
+    const float* __restrict__ w_scale, Epilogue ep, void* __restrict__ y, int M, int N, int K,
+    int tiles_m, int tiles_n) {
+  static_assert(WT == E4M3 || WT == E5M2, "FP8 weights");
+  constexpr int KB = 128, FBN = 256, FNT = 2;
+  constexpr int XB = XL<XT>::bytes;
+  static_assert(XB == 4 || XB == 2, "x in fp32 or a 16-bit format");
+  constexpr int XP = 2 * KB + 16;     // bytes per bf16 x row in LDS
+  constexpr int XS = BM * XP;         // x stage
+  constexpr int WS = FBN * KB;        // W stage: two K halves of 256 rows x 64 bytes
+  constexpr int WH = WS / 2;
+  constexpr int WOFF = 2 * XS;
+  constexpr int XC = 8;               // x chunks (4 elements) per lane per block
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * XS + 2 * WS];
+
+  const int T = tiles_m * tiles_n;
+  int t = blockIdx.x;
+  if ((T & 7) == 0) t = (t & 7) * (T >> 3) + (t >> 3);
+  constexpr int GM = 4;
+  const int grp = t / (GM * tiles_n);
+  const int first_m = grp * GM;
+  const int gm = min(tiles_m - first_m, GM);
+  const int rem = t - grp * GM * tiles_n;
+  const int m0 = (first_m + rem % gm) * BM;
+  const int n0 = (rem / gm) * FBN;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = wave >> 2, q = wave & 3;
+  const int wm = g * 64, wn = q * 64;
+  const int gt = tid & 255;
+  const int la = lane & 31, h = lane >> 5;
+
+  // x: the group's 64 rows, 8 rows of 4-element chunks per pass of its lanes
+  const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(x + (size_t)(m0 + wm) * K * XB), (short)0, 64 * K * XB, 0x00020000);
+  const uint32_t xlane = (uint32_t)((gt >> 5) * K + (gt & 31) * 4) * (uint32_t)XB;
+  const uint32_t xstep = 8u * (uint32_t)K * (uint32_t)XB;
+  const int xw = (wm + (gt >> 5)) * XP + (gt & 31) * 8;
+
+  // W: instruction j (= 4 i + q for wave q) of a K half fills LDS slots
+  // 64 j + lane: row 16 j + lane / 4, slot lane % 4, holding that row's chunk
+  // (lane % 4) ^ ((lane / 16) % 4) of the half
+  const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(w + (size_t)n0 * K), (short)0, FBN * K, 0x00020000);
+  const uint32_t wlane = (uint32_t)((lane >> 2) * K + (((lane & 3) ^ (lane >> 4)) << 4));
+
+  // fragment bases: A row wm + la (+ 32 i), bytes 32 h (+ 64 t + 16 u) of
+  // the row; B row wn + la (+ 32 j), chunk 2 t + h of the K half at slot
+  // (2 t + h) ^ ((la / 4) % 4), so step t only flips address bit 5
+  const int abase = (wm + la) * XP + 32 * h;
+  const int bbase = WOFF + (wn + la) * 64 + ((h ^ ((la >> 2) & 3)) << 4);
+
+  const int nb = K / KB;
+  u32x4 xr[2][XC];
+  bf16x8 fa[2][2][MT];  // [32-K pair][step][M tile]
+  u32x4 fb[2][FNT];     // [32-K pair][N tile]: 16 codes
+  f32x16 acc[MT][FNT];
+#pragma unroll
+  for (int a = 0; a < MT; ++a)
+#pragma unroll
+    for (int b = 0; b < FNT; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.0f;
+
+  auto fetch_x = [&](u32x4 (&xs)[XC], int kb, const int i0, const int i1) {
+    const uint32_t xk = (uint32_t)kb * (KB * XB);
+#pragma unroll
+    for (int i = i0; i < i1; ++i) {
+      if constexpr (XB == 4) {
+        xs[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xlane, xk + i * xstep, 0);
+      } else {
+        const xl_u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(xrs, xlane, xk + i * xstep, 0);
+        xs[i] = u32x4{v[0], v[1], 0u, 0u};
+      }
+    }
+  };
+  auto stage_x = [&](const u32x4 (&xs)[XC], int slot, const int i0, const int i1) {
+    uint8_t* d = lds + slot * XS + xw;
+#pragma unroll
+    for (int i = i0; i < i1; ++i) {
+      const xl_u32x2 pr = x4_bf16<XT>(xs[i]);
+      *reinterpret_cast<u32x2*>(d + i * 8 * XP) = u32x2{pr[0], pr[1]};
+    }
+  };
+  auto copy_w = [&](int kb, int slot, const int hf) {
+    typedef __attribute__((address_space(3))) void lds_void;
+    uint8_t* d = lds + WOFF + slot * WS + hf * WH;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int j = 4 * i + q;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          wrs, (lds_void*)(d + j * 64 * 16), 16, wlane,
+          (uint32_t)(16 * j) * (uint32_t)K + (uint32_t)kb * KB + 64u * hf, 0, 0);
+    }
+  };
+  auto read_frags = [&](int kb, const int hf) {
+    const uint8_t* sa = lds + (kb & 1) * XS + abase;
+    const int sb = bbase + (kb & 1) * WS + hf * WH;
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+      const int t4 = 2 * hf + tt;
+#pragma unroll
+      for (int j = 0; j < FNT; ++j)
+        fb[tt][j] = *reinterpret_cast<const u32x4*>(lds + ((sb + j * 32 * 64) ^ (tt << 5)));
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+          fa[tt][u][i] = *reinterpret_cast<const bf16x8*>(sa + i * 32 * XP + 64 * t4 + 16 * u);
+    }
+  };
+  auto dec = [](uint32_t w0, uint32_t w1) {
+    uint32_t o[4];
+    if constexpr (WT == E4M3) {
+      o[0] = bf16_pair(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, false));
+      o[1] = bf16_pair(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, true));
+      o[2] = bf16_pair(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, false));
+      o[3] = bf16_pair(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, true));
+    } else {
+      o[0] = bf16_pair(__builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(w0, 1.0f, false));
+      o[1] = bf16_pair(__builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(w0, 1.0f, true));
+      o[2] = bf16_pair(__builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(w1, 1.0f, false));
+      o[3] = bf16_pair(__builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(w1, 1.0f, true));
+    }
+    return __builtin_bit_cast(bf16x8, u32x4{o[0], o[1], o[2], o[3]});
+  };
+  auto multiply = [&]() {
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        bf16x8 bb[FNT];
+#pragma unroll
+        for (int j = 0; j < FNT; ++j) bb[j] = dec(fb[tt][j][2 * u], fb[tt][j][2 * u + 1]);
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+          for (int j = 0; j < FNT; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[tt][u][i], bb[j], acc[i][j], 0, 0, 0);
+      }
+  };
+  auto bar = [&]() {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // Memory phase hf of block kb: its fragments of K half hf; group 0 copies
+  // K half hf of block kb+1's W; half the x chunks of block kb+1 are staged
+  // from register set (kb+1) % 2 and that set's loads for block kb+3 issued.
+  // Past the last block the last one is copied and staged again into the
+  // idle slot, so the loop has no tail.
+  auto mem = [&](u32x4 (&xs)[XC], int kb, const int hf) {
+    read_frags(kb, hf);
+    if (g == 0) copy_w(min(kb + 1, nb - 1), (kb + 1) & 1, hf);
+    stage_x(xs, (kb + 1) & 1, 4 * hf, 4 * hf + 4);
+    fetch_x(xs, min(kb + 3, nb - 1), 4 * hf, 4 * hf + 4);
+  };
+  // after a multiply phase: group 0's W copy of the memory phase before it
+  // has landed (4 copies and 4 x loads per memory phase, in that order)
+  auto wait_copy = [&]() {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
+  };
+  auto block = [&](u32x4 (&xs)[XC], int b) {
+    mem(xs, b, 0);
+    bar();
+    multiply();  // C0(b)
+    wait_copy();
+    bar();
+    mem(xs, b, 1);
+    bar();
+    multiply();  // C1(b)
+    wait_copy();
+    bar();
+  };
+
+  // Prologue: block 0 staged and its W copied, blocks 1 and 2 loaded.
+  fetch_x(xr[0], 0, 0, XC);
+  if (g == 0) {
+    copy_w(0, 0, 0);
+    copy_w(0, 0, 1);
+  }
+  stage_x(xr[0], 0, 0, XC);
+  fetch_x(xr[1], min(1, nb - 1), 0, XC);
+  fetch_x(xr[0], min(2, nb - 1), 0, XC);
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+  bar();
+  if (g == 1) bar();  // group 1 runs one phase behind
+  int b = 0;
+  for (; b + 1 < nb; b += 2) {
+    block(xr[1], b);
+    block(xr[0], b + 1);
+  }
+  if (b < nb) block(xr[1], b);
+  if (g == 0) bar();  // both groups pass the same number of barriers
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+  tile_epilogue(ep, acc, product_scale(w_scale, x_scale), y, N, m0 + wm, n0 + wn, lane);
+}
+
+// ---------------------------------------------------------------------------
 // FP8 product for x stored as E4M3 / E5M2 (the narrow activations a fused
 // epilogue writes) with E4M3 / E5M2 / E2M1 weights; M % 128, N % 256,
 // K % 128.  gfx950's v_mfma_f32_32x32x64_f8f6f4 takes both operands' codes
@@ -1006,7 +1240,16 @@ int launch(const uint8_t* x, const float* x_scale, int64_t M, int64_t K, const v
     if (rows_whole && N % 256 == 0 && K % F8<WT, XT>::KS == 0)
       return launch_f8<WT, XT>(x, x_scale, M, K, wq, w_scale, ep, N, y, stream);
   }
-  if constexpr (dtype_bits(WT) <= 8) {
+  if constexpr ((WT == E4M3 || WT == E5M2) && XL<XT>::bytes >= 2) {
+    // W tile (256 rows x K bytes) and x tile bytes must fit the buffer range
+    if (rows_whole && N % 256 == 0 && K % 128 == 0 && K <= (1 << 21)) {
+      hipLaunchKernelGGL((linear_pingpong_kernel<WT, XT>), dim3((unsigned)(tiles_m * (N / 256))),
+                         dim3(512), 0, stream, x, x_scale, wq, w_scale, ep, y, (int)M, (int)N,
+                         (int)K, (int)tiles_m, (int)(N / 256));
+      return check_launch();
+    }
+  }
+  if constexpr (WT == E2M1) {
     // tile byte sizes (BM * K * bytes(x) for x) must fit the 31-bit buffer range
     if (rows_whole && N % 256 == 0 && K % 128 == 0 && K <= (1 << 21)) {
       hipLaunchKernelGGL((linear_wide_kernel<WT, XT>), dim3((unsigned)(tiles_m * (N / 256))),

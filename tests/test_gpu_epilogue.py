@@ -165,7 +165,7 @@ def test_bf16_stores_round_every_class(hw):
 
 
 LINEAR_CASES = [
-    ("e4m3", 256, 512, 256),   # linear_wide_kernel
+    ("e4m3", 256, 512, 256),   # linear_pingpong_kernel
     ("e2m1", 128, 256, 512),   # linear_wide_kernel, FP4
     ("bf16", 128, 128, 256),   # linear_pipe_kernel
     ("f16", 128, 64, 128),     # linear_pipe_kernel, 128-wide tiles

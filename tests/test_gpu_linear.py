@@ -61,9 +61,10 @@ def valid_codes(wdt):
                          ids=["edge-tiles", "wide-k", "staged-256", "staged-128"])
 def test_identity_input_reproduces_dequantized_weights_exactly(wdt, scale, K, N):
     """x = I: y[i, j] = s * dec(W[j, i]) exactly, for every finite code.  The
-    shapes reach each kernel: guarded edge tiles (N % 128 != 0), the wide-K
-    kernel (N % 256 == 0, K % 128 == 0) and the staged-decode kernel at both
-    tile widths (K % 128 != 0; N % 256 != 0)."""
+    shapes reach each kernel: guarded edge tiles (N % 128 != 0), the K-block
+    kernels for N % 256 == 0, K % 128 == 0 (ping-pong for FP8, wide for FP4)
+    and the staged-decode kernel at both tile widths (K % 128 != 0;
+    N % 256 != 0)."""
     rng = np.random.default_rng(1)
     vals = valid_codes(wdt)
     nib = vals[rng.integers(0, vals.size, size=N * K)]
@@ -119,8 +120,8 @@ def test_ragged_shapes_vs_oracle(wdt, M, N, K, with_bias):
                                    (256, 384, 192), (128, 256, 1024)])
 def test_whole_tile_shapes_vs_oracle(wdt, M, N, K):
     """Shapes that take the guard-free kernels (M % 128, N % 128, K % 64 == 0):
-    wide-K for FP8/FP4 when N % 256 and K % 128 are 0, staged-decode at tile
-    width 256 or 128 otherwise and for 16-bit weights."""
+    ping-pong (FP8) / wide-K (FP4) when N % 256 and K % 128 are 0,
+    staged-decode at tile width 256 or 128 otherwise and for 16-bit weights."""
     rng = np.random.default_rng(M + N + K)
     x = rng.standard_normal((M, K)).astype(np.float32)
     w = (rng.standard_normal((N, K)) * np.sqrt(2.0 / K)).astype(np.float32)
