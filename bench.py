@@ -206,7 +206,7 @@ def bench_linear(dev, iters: int = 20, warmup: int = 5):
             "roofline": {"bound": "mfma", "achieved": round(tflops, 1),
                          "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
-                         "traffic": measured_traffic("linear_pingpong_kernel<3, 0>")}}
+                         "traffic": measured_traffic("linear_pingpong_kernel<3, 0, false>")}}
 
 
 def bench_linear_backward(dev, iters: int = 10, warmup: int = 3):

@@ -365,33 +365,12 @@ __device__ __forceinline__ bf16x8 frag_to_bf16(const uint8_t* p) {
   return __builtin_bit_cast(bf16x8, r);
 }
 
-// The same 8 FP8 codes read from W kept in its own [K][N] layout in LDS with
-// gfx950's transposing read (ds_read_b64_tr_b8): within each group of 16
-// lanes, lane p names 8 bytes (row 2 j + h of the group's 8 rows, with
-// j = (p % 16) / 2 and h = p % 2 picking the half of a 16-byte column run),
-// and lane i receives byte i % 8 of the runs named by lanes 2 j + i / 8:
-// 8 consecutive K of one N index.
+// gfx950's transposing LDS read (ds_read_b64_tr_b8), for W kept in its own
+// [K][N] layout: within each group of 16 lanes, lane p names 8 bytes (row
+// 2 j + h of the group's 8 rows, with j = (p % 16) / 2 and h = p % 2 picking
+// the half of a 16-byte column run), and lane i receives byte i % 8 of the
+// runs named by lanes 2 j + i / 8: 8 consecutive K of one N index.
 typedef int i32x2_lds __attribute__((ext_vector_type(2)));
-template <int WT>
-__device__ __forceinline__ bf16x8 frag_to_bf16_tr(const uint8_t* p) {
-  static_assert(WT == E4M3 || WT == E5M2, "8-bit codes");
-  typedef __attribute__((address_space(3))) i32x2_lds lds_i32x2;
-  const i32x2_lds r = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_i32x2*)p);
-  const u32x2 v = {(uint32_t)r[0], (uint32_t)r[1]};
-  uint32_t o[4];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    if constexpr (WT == E4M3) {
-      o[2 * i] = bf16_pair(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v[i], 1.0f, false));
-      o[2 * i + 1] = bf16_pair(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(v[i], 1.0f, true));
-    } else {
-      o[2 * i] = bf16_pair(__builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(v[i], 1.0f, false));
-      o[2 * i + 1] = bf16_pair(__builtin_amdgcn_cvt_scalef32_pk_bf16_bf8(v[i], 1.0f, true));
-    }
-  }
-  u32x4 rr = {o[0], o[1], o[2], o[3]};
-  return __builtin_bit_cast(bf16x8, rr);
-}
 
 constexpr int B_PITCH = BK + 8;  // bf16 per W row in LDS (144 B, conflict-free fragment reads)
 
@@ -556,9 +535,10 @@ __global__ __launch_bounds__(NW * 64, OCC) void linear_pipe_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Wide-K kernel (E4M3 / E5M2 / E2M1 weights, K % 128 == 0): K blocks of 128,
-// so one K block of a W row is a whole 128-byte line for FP8 (64 bytes for
-// E2M1) and each W load fetches no line it uses only half of; barriers are
+// Wide-K kernel (dispatched for E2M1 weights; it also handles FP8, which the
+// ping-pong kernel below takes; K % 128 == 0): K blocks of 128, so one K
+// block of a W row is a whole 128-byte line for FP8 (64 bytes for E2M1) and
+// each W load fetches no line it uses only half of; barriers are
 // half as many.  W stays in its stored format in LDS (decoded per fragment),
 // x is rounded to bf16 on the way in; two LDS stages, two register sets
 // (block kb+2 is loaded while block kb+1 is staged).
@@ -574,12 +554,7 @@ struct Wide {
   static constexpr int cpr = row_bytes / 16;            // W 16-byte chunks per row
 };
 
-// WN: W arrives in its natural [K][N] layout (the Linear backward's
-// grad_input = grad @ W reads the forward's W without a transposed copy; FP8
-// codes only): K blocks of W rows are staged as they are, 288-byte LDS rows
-// (8 mod 64 banks, so a transposing read's 8 rows x 32 bytes meet no
-// conflict), and B fragments come from frag_to_bf16_tr.
-template <int WT, int XT, bool WN = false>
+template <int WT, int XT>
 __global__ __launch_bounds__(512, 1) void linear_wide_kernel(
     const uint8_t* __restrict__ x, const float* __restrict__ x_scale, const uint8_t* __restrict__ w,
     const float* __restrict__ w_scale,
@@ -589,10 +564,8 @@ __global__ __launch_bounds__(512, 1) void linear_wide_kernel(
   constexpr int KB = F::KB;
   constexpr int FBN = 256, NTH = 512;
   constexpr int FWN = 64, FNT = 2;
-  static_assert(!WN || WT == E4M3 || WT == E5M2, "W in [K][N] layout: FP8 codes only");
-  constexpr int WNP = 288;                              // [K][N] layout: bytes per K row
   constexpr int A_ST = BM * F::a_pitch * 2;
-  constexpr int B_ST = WN ? KB * WNP : FBN * F::pitch;
+  constexpr int B_ST = FBN * F::pitch;
   constexpr int STAGE = A_ST + B_ST;
   constexpr int XC = BM * KB / 4 / NTH;                 // 8 x chunks per thread
   constexpr int WC = FBN * F::row_bytes / 16 / NTH;     // 4 (FP8) or 2 (E2M1) W chunks
@@ -624,42 +597,28 @@ __global__ __launch_bounds__(512, 1) void linear_wide_kernel(
       const_cast<uint8_t*>(x + (size_t)m0 * K * XB), (short)0, BM * K * XB, 0x00020000);
   const uint32_t xlane = (uint32_t)((tid >> 5) * K + (tid & 31) * 4) * (uint32_t)XB;
   const uint32_t xstep = 16u * (uint32_t)K * (uint32_t)XB;
-  // W rows are N (the forward's layout) or, with WN, K: then a K block is
-  // 128 rows of N bytes, of which the tile's 256 columns are 16 chunks
   const uint32_t w_row_bytes = (uint32_t)K * F::bits / 8;
-  const __amdgpu_buffer_rsrc_t wrs =
-      WN ? __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(w + n0), (short)0,
-                                             (int)((size_t)K * N - n0), 0x00020000)
-         : __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(w + (size_t)n0 * w_row_bytes),
-                                             (short)0, (int)(FBN * w_row_bytes), 0x00020000);
-  const uint32_t wlane = WN ? (uint32_t)(tid >> 4) * (uint32_t)N + (uint32_t)(tid & 15) * 16u
-                            : (uint32_t)(tid / F::cpr) * w_row_bytes + (uint32_t)(tid % F::cpr) * 16u;
-  const uint32_t wstep = WN ? 32u * (uint32_t)N : (uint32_t)(NTH / F::cpr) * w_row_bytes;
+  const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(w + (size_t)n0 * w_row_bytes), (short)0, (int)(FBN * w_row_bytes),
+      0x00020000);
+  const uint32_t wlane = (uint32_t)(tid / F::cpr) * w_row_bytes + (uint32_t)(tid % F::cpr) * 16u;
+  const uint32_t wstep = (uint32_t)(NTH / F::cpr) * w_row_bytes;
 
   // LDS: [A0 | A1 | B0 | B1].  Per-lane bases below; every other offset is a
   // compile-time constant that fits a ds instruction's 16-bit offset field.
   constexpr int XDST_STEP = 16 * F::a_pitch * 2;
-  constexpr int WDST_STEP = WN ? 32 * WNP : (NTH / F::cpr) * F::pitch;
+  constexpr int WDST_STEP = (NTH / F::cpr) * F::pitch;
   constexpr int A_ROWS32 = 32 * F::a_pitch * 2;
   const int xw = ((tid >> 5) * F::a_pitch + (tid & 31) * 4) * 2;
-  const int ww0 = WN ? 2 * A_ST + (tid >> 4) * WNP + (tid & 15) * 16
-                     : 2 * A_ST + (tid / F::cpr) * F::pitch + (tid % F::cpr) * 16;
+  const int ww0 = 2 * A_ST + (tid / F::cpr) * F::pitch + (tid % F::cpr) * 16;
   const int ww1 = ww0 + B_ST;
   const int ar = ((wm + (lane & 31)) * F::a_pitch + half * 8) * 2;
-  // WN: the lane's role in the transposing read (row 8 (lane / 32) +
-  // (lane % 16) / 2 of the step's 16, columns 16 ((lane / 16) % 2) +
-  // 8 (lane % 2) .. +7 of the sub-tile's 32)
-  const int br0 = WN ? 2 * A_ST + (8 * (lane >> 5) + ((lane & 15) >> 1)) * WNP + wn +
-                           16 * ((lane >> 4) & 1) + 8 * (lane & 1)
-                     : 2 * A_ST + (wn + (lane & 31)) * F::pitch + half * F::frag_bytes;
+  const int br0 = 2 * A_ST + (wn + (lane & 31)) * F::pitch + half * F::frag_bytes;
   const int br1 = br0 + B_ST;
   // B fragment offsets: per 32-column sub-tile and per 16-K step
-  constexpr int BJ = WN ? 32 : 32 * F::pitch;
-  constexpr int BSTEP = WN ? 16 * WNP : 2 * F::frag_bytes;
-  auto bfrag = [](const uint8_t* p) {
-    if constexpr (WN) return frag_to_bf16_tr<WT>(p);
-    else return frag_to_bf16<WT>(p);
-  };
+  constexpr int BJ = 32 * F::pitch;
+  constexpr int BSTEP = 2 * F::frag_bytes;
+  auto bfrag = [](const uint8_t* p) { return frag_to_bf16<WT>(p); };
 
   struct Regs {
     u32x4 x[XC];
@@ -667,7 +626,7 @@ __global__ __launch_bounds__(512, 1) void linear_wide_kernel(
   };
   auto fetch = [&](Regs& r, int kb) {
     const uint32_t xk = (uint32_t)kb * (KB * XB);
-    const uint32_t wk = WN ? (uint32_t)kb * KB * (uint32_t)N : (uint32_t)kb * F::row_bytes;
+    const uint32_t wk = (uint32_t)kb * F::row_bytes;
 #pragma unroll
     for (int i = 0; i < XC; ++i) {
       if constexpr (XB == 4) {
@@ -785,8 +744,15 @@ __global__ __launch_bounds__(512, 1) void linear_wide_kernel(
 // lgkmcnt(0) then s_barrier at every phase end; after each multiply phase
 // s_waitcnt vmcnt(12) -- group 0's copy of the previous memory phase has
 // landed (the x loads issued after it may still be in flight).
+//
+// WN: W in its natural [K][N] layout (the Linear backward's grad_input =
+// grad @ W on the forward's codes): a K half is 64 rows of the tile's 256
+// columns, chunk c of row r at slot c ^ (2 (r % 8)), and B fragments come
+// from gfx950's transposing read (8 consecutive K of one column per lane; the
+// 32 lanes of a half-wave read 8 rows x 32 bytes, all in distinct banks) in
+// the MFMA's own K order, which the x fragments then follow.
 
-template <int WT, int XT>
+template <int WT, int XT, bool WN = false>
 __global__ __launch_bounds__(512, 1) void linear_pingpong_kernel(
     const uint8_t* __restrict__ x, const float* __restrict__ x_scale, const uint8_t* __restrict__ w,
     const float* __restrict__ w_scale, Epilogue ep, void* __restrict__ y, int M, int N, int K,
@@ -830,21 +796,34 @@ __global__ __launch_bounds__(512, 1) void linear_pingpong_kernel(
 
   // W: instruction j (= 4 i + q for wave q) of a K half fills LDS slots
   // 64 j + lane: row 16 j + lane / 4, slot lane % 4, holding that row's chunk
-  // (lane % 4) ^ ((lane / 16) % 4) of the half
-  const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint8_t*>(w + (size_t)n0 * K), (short)0, FBN * K, 0x00020000);
-  const uint32_t wlane = (uint32_t)((lane >> 2) * K + (((lane & 3) ^ (lane >> 4)) << 4));
+  // (lane % 4) ^ ((lane / 16) % 4) of the half.  WN: row 4 j + lane / 16 of
+  // the half's 64, slot lane % 16, holding column chunk
+  // (lane % 16) ^ (2 (row % 8)), row % 8 = 4 (q % 2) + lane / 16.
+  const __amdgpu_buffer_rsrc_t wrs =
+      WN ? __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(w + n0), (short)0,
+                                             (int)((size_t)K * N - n0), 0x00020000)
+         : __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(w + (size_t)n0 * K), (short)0,
+                                             FBN * K, 0x00020000);
+  const uint32_t wlane =
+      WN ? (uint32_t)((lane >> 4) * N + (((lane & 15) ^ (2 * (4 * (q & 1) + (lane >> 4)))) << 4))
+         : (uint32_t)((lane >> 2) * K + (((lane & 3) ^ (lane >> 4)) << 4));
 
   // fragment bases: A row wm + la (+ 32 i), bytes 32 h (+ 64 t + 16 u) of
   // the row; B row wn + la (+ 32 j), chunk 2 t + h of the K half at slot
-  // (2 t + h) ^ ((la / 4) % 4), so step t only flips address bit 5
-  const int abase = (wm + la) * XP + 32 * h;
-  const int bbase = WOFF + (wn + la) * 64 + ((h ^ ((la >> 2) & 3)) << 4);
+  // (2 t + h) ^ ((la / 4) % 4), so step t only flips address bit 5.  WN: A
+  // bytes 16 h (+ 64 t + 32 u); B rows 8 h + (lane % 16) / 2 (+ 16 (2 t + u))
+  // of the half, column chunk 4 q + (lane / 16) % 2 (+ 2 j), 8 (lane % 2)
+  // bytes in, so sub-tile j only flips address bit 5.
+  const int abase = (wm + la) * XP + (WN ? 16 : 32) * h;
+  const int bx = (lane & 15) >> 1;
+  const int bbase =
+      WN ? WOFF + (8 * h + bx) * 256 + (((4 * q + ((lane >> 4) & 1)) ^ (2 * bx)) << 4) + 8 * (lane & 1)
+         : WOFF + (wn + la) * 64 + ((h ^ ((la >> 2) & 3)) << 4);
 
   const int nb = K / KB;
   u32x4 xr[2][XC];
   bf16x8 fa[2][2][MT];  // [32-K pair][step][M tile]
-  u32x4 fb[2][FNT];     // [32-K pair][N tile]: 16 codes
+  u32x4 fb[2][FNT];     // [32-K pair][N tile]: 16 codes (WN: 8 per 16-K step)
   f32x16 acc[MT][FNT];
 #pragma unroll
   for (int a = 0; a < MT; ++a)
@@ -879,9 +858,10 @@ __global__ __launch_bounds__(512, 1) void linear_pingpong_kernel(
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int j = 4 * i + q;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          wrs, (lds_void*)(d + j * 64 * 16), 16, wlane,
-          (uint32_t)(16 * j) * (uint32_t)K + (uint32_t)kb * KB + 64u * hf, 0, 0);
+      const uint32_t so = WN ? (uint32_t)(kb * KB + 64 * hf + 4 * j) * (uint32_t)N
+                             : (uint32_t)(16 * j) * (uint32_t)K + (uint32_t)kb * KB + 64u * hf;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(wrs, (lds_void*)(d + j * 64 * 16), 16, wlane, so,
+                                               0, 0);
     }
   };
   auto read_frags = [&](int kb, const int hf) {
@@ -891,13 +871,24 @@ __global__ __launch_bounds__(512, 1) void linear_pingpong_kernel(
     for (int tt = 0; tt < 2; ++tt) {
       const int t4 = 2 * hf + tt;
 #pragma unroll
-      for (int j = 0; j < FNT; ++j)
-        fb[tt][j] = *reinterpret_cast<const u32x4*>(lds + ((sb + j * 32 * 64) ^ (tt << 5)));
+      for (int j = 0; j < FNT; ++j) {
+        if constexpr (WN) {
+          typedef __attribute__((address_space(3))) i32x2_lds lds_i32x2;
+          const i32x2_lds r0 = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+              (lds_i32x2*)(lds + ((sb + 16 * (2 * tt) * 256) ^ (j << 5))));
+          const i32x2_lds r1 = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+              (lds_i32x2*)(lds + ((sb + 16 * (2 * tt + 1) * 256) ^ (j << 5))));
+          fb[tt][j] = u32x4{(uint32_t)r0[0], (uint32_t)r0[1], (uint32_t)r1[0], (uint32_t)r1[1]};
+        } else {
+          fb[tt][j] = *reinterpret_cast<const u32x4*>(lds + ((sb + j * 32 * 64) ^ (tt << 5)));
+        }
+      }
 #pragma unroll
       for (int u = 0; u < 2; ++u)
 #pragma unroll
         for (int i = 0; i < MT; ++i)
-          fa[tt][u][i] = *reinterpret_cast<const bf16x8*>(sa + i * 32 * XP + 64 * t4 + 16 * u);
+          fa[tt][u][i] = *reinterpret_cast<const bf16x8*>(sa + i * 32 * XP + 64 * t4 +
+                                                          (WN ? 32 : 16) * u);
     }
   };
   auto dec = [](uint32_t w0, uint32_t w1) {
@@ -1294,13 +1285,13 @@ int linear_wn_launch_xt(const uint8_t* x, int64_t M, int64_t K, const void* w_q,
   const int64_t tiles_m = M / BM, tiles_n = N / 256;
   const auto* wq = static_cast<const uint8_t*>(w_q);
   if (w_dtype == E4M3)
-    hipLaunchKernelGGL((linear_wide_kernel<E4M3, XT, true>), dim3((unsigned)(tiles_m * tiles_n)),
-                       dim3(512), 0, stream, x, nullptr, wq, w_scale, ep, y, (int)M, (int)N,
-                       (int)K, (int)tiles_m, (int)tiles_n);
+    hipLaunchKernelGGL((linear_pingpong_kernel<E4M3, XT, true>),
+                       dim3((unsigned)(tiles_m * tiles_n)), dim3(512), 0, stream, x, nullptr, wq,
+                       w_scale, ep, y, (int)M, (int)N, (int)K, (int)tiles_m, (int)tiles_n);
   else
-    hipLaunchKernelGGL((linear_wide_kernel<E5M2, XT, true>), dim3((unsigned)(tiles_m * tiles_n)),
-                       dim3(512), 0, stream, x, nullptr, wq, w_scale, ep, y, (int)M, (int)N,
-                       (int)K, (int)tiles_m, (int)tiles_n);
+    hipLaunchKernelGGL((linear_pingpong_kernel<E5M2, XT, true>),
+                       dim3((unsigned)(tiles_m * tiles_n)), dim3(512), 0, stream, x, nullptr, wq,
+                       w_scale, ep, y, (int)M, (int)N, (int)K, (int)tiles_m, (int)tiles_n);
   return check_launch();
 }
 
