@@ -117,7 +117,8 @@ def test_ragged_shapes_vs_oracle(wdt, M, N, K, with_bias):
 
 @pytest.mark.parametrize("wdt", ["e4m3", "e5m2", "e2m1", "bf16", "f16"])
 @pytest.mark.parametrize("M,N,K", [(128, 256, 64), (256, 512, 128), (384, 768, 320),
-                                   (256, 384, 192), (128, 256, 1024)])
+                                   (256, 384, 192), (128, 256, 1024), (128, 256, 384),
+                                   (256, 768, 640)])
 def test_whole_tile_shapes_vs_oracle(wdt, M, N, K):
     """Shapes that take the guard-free kernels (M % 128, N % 128, K % 64 == 0):
     ping-pong (FP8) / wide-K (FP4) when N % 256 and K % 128 are 0,
