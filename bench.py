@@ -145,8 +145,20 @@ def bench_sweep(n: int, steps: int, warmup: int, dev):
         mean, med = _time_launches(dev, fn, max(steps, 5), 0, flush)
         p["evicted_median_ms"] = round(med, 4)
         p["evicted_GB/s"] = round(b * n / (med * 1e-3) / 1e9, 1)
-    del bufs, flush
-    return (t1 - t0) * 1e3 / steps, per_op
+    # context for the HBM roofline: the vendor's own conversion kernels (torch
+    # copy_ between dtypes) on the same buffers, timed the same way
+    x, y = bufs[0], bufs[1]
+    h16 = {torch.float16: bufs[2].view(torch.float16), torch.bfloat16: bufs[2].view(torch.bfloat16)}
+    vendor = {}
+    for name, dt in (("f16", torch.float16), ("bf16", torch.bfloat16)):
+        for label, fn in ((f"f32->{name}", lambda dt=dt: h16[dt].copy_(x)),
+                          (f"{name}->f32", lambda dt=dt: y.copy_(h16[dt]))):
+            med = _time_launches(dev, fn, max(steps, 5), 1, flush)[1]
+            gbs = 6 * n / (med * 1e-3) / 1e9
+            vendor[label] = {"evicted_median_ms": round(med, 4), "GB/s": round(gbs, 1),
+                             "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    del bufs, flush, x, y, h16
+    return (t1 - t0) * 1e3 / steps, per_op, vendor
 
 
 def bench_linear(dev, iters: int = 20, warmup: int = 5):
@@ -813,10 +825,10 @@ def main() -> int:
         torch.cuda.synchronize(dev)
         del src, dst
     ms = value = None
-    per_op, roof = None, None
+    per_op, roof, vendor_casts = None, None, None
     if "sweep" in legs:
         log(f"sweep: {args.elems} elements, {args.steps} steps, {args.warmup} warmup")
-        ms, per_op = bench_sweep(args.elems, args.steps, args.warmup, dev)
+        ms, per_op, vendor_casts = bench_sweep(args.elems, args.steps, args.warmup, dev)
         value = BYTES_PER_ELEM * args.elems / (ms * 1e-3) / 1e9
         # dominant single-kernel op (the amax op also launches a 1-thread fill kernel)
         kernels = [p for p in per_op if p["op"] in KERNEL_OF]
@@ -856,6 +868,7 @@ def main() -> int:
                    "elements": args.elems, "bytes_per_element": BYTES_PER_ELEM},
         "roofline": roof,
         "kernels": per_op,
+        "vendor_casts": vendor_casts,
         "linear": run["linear"],
         "linear_backward": run["linear_backward"],
         "conv2d": run["conv"],
