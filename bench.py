@@ -186,6 +186,11 @@ def bench_linear(dev, iters: int = 20, warmup: int = 5):
     except NotImplementedError:
         return None
     ms, med = _time_launches(dev, run, iters, warmup)
+    # the same launches with the MALL evicted before each (x and W, 48 MB, are
+    # otherwise still cached from the launch before)
+    flush = torch.zeros(1 << 27, dtype=torch.float32, device=dev)
+    _, emed = _time_launches(dev, run, iters, 0, flush)
+    del flush
     flops = 2.0 * M * N * K
     tflops = flops / (ms * 1e-3) / 1e12
     # context: the vendor bf16 GEMM (torch -> hipBLASLt) on the same shape with
@@ -204,6 +209,7 @@ def bench_linear(dev, iters: int = 20, warmup: int = 5):
     tf8 = flops / (ms8 * 1e-3) / 1e12
     return {"metric": "FP8-weight Linear TFLOP/s at 4096^2", "value": round(tflops, 1),
             "unit": "TFLOP/s", "ms": round(ms, 4), "median_ms": round(med, 4),
+            "evicted_median_ms": round(emed, 4),
             "vendor_bf16_gemm": {"what": "torch.nn.functional.linear, bf16 x and W in HBM",
                                  "ms": round(vms, 4),
                                  "TFLOP/s": round(flops / (vms * 1e-3) / 1e12, 1)},
@@ -258,10 +264,14 @@ def bench_linear_backward(dev, iters: int = 10, warmup: int = 3):
     e1.record()
     torch.cuda.synchronize(dev)
     ms = e0.elapsed_time(e1) / iters
+    flush = torch.zeros(1 << 27, dtype=torch.float32, device=dev)
+    _, emed = _time_launches(dev, run, iters, 0, flush)  # MALL evicted before each call
+    del flush
     flops = 2 * 2.0 * M * N * K
     tflops = flops / (ms * 1e-3) / 1e12
     return {"metric": "Linear backward TFLOP/s (grad_input + grad_weight) at config [4]",
             "value": round(tflops, 1), "unit": "TFLOP/s", "ms": round(ms, 4),
+            "evicted_median_ms": round(emed, 4),
             "workspace_bytes": nbytes,
             "roofline": {"bound": "mfma", "achieved": round(tflops, 1),
                          "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
