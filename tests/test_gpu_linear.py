@@ -370,3 +370,57 @@ def test_misaligned_device_views_are_copied_not_refused():
     torch.cuda.synchronize()
     assert torch.equal(q1.data.view(torch.uint8).cpu(), q2.data.view(torch.uint8).cpu())
     assert q1.scale.item() == q2.scale.item()
+
+
+@pytest.mark.parametrize("wdt", ["e4m3", "e5m2"])
+def test_longest_k_one_hot_rows(wdt):
+    """K = 2^21, the longest K the K-block kernels take, forward (W rows of 2
+    MiB) and backward grad_input (W read in its [K][N] layout): every row of x
+    (of grad) is one-hot at a K index spread over the whole range, the first
+    and the last included, so y[i, :] = s * dec(W[:, k_i]) (grad_input[i, :]
+    = s * dec(W[k_i, :])) exactly -- the offsets of the last K blocks, near
+    the top of the 31-bit buffer ranges, are exercised."""
+    M, N, K = 128, 256, 1 << 21
+    print(f"longest K one-hot {wdt}", flush=True)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(21)
+    codes = torch.randint(0, 256, (N, K), generator=g, device="cuda", dtype=torch.int32)
+    if wdt == "e4m3":  # no NaN codes (0x7F / 0xFF)
+        codes = torch.where((codes & 0x7F) == 0x7F, codes - 1, codes)
+    else:  # no Inf / NaN codes (exponent all ones): clear the exponent's low bit
+        codes = torch.where((codes & 0x7C) == 0x7C, codes & 0xFB, codes)
+    codes = codes.to(torch.uint8).contiguous()
+    s = 0.0123
+    sd = torch.tensor([s], dtype=torch.float32, device="cuda")
+    rng = np.random.default_rng(21)
+    ks = rng.integers(0, K, size=M)
+    ks[0], ks[1], ks[2] = 0, K - 1, K - 128
+    kd = torch.from_numpy(ks).cuda()
+    rows = torch.arange(M, device="cuda")
+    lib, stream = _lib.load(), torch.cuda.current_stream().cuda_stream
+    code = _lib.DTYPES[wdt]
+
+    x = torch.zeros((M, K), dtype=torch.float32, device="cuda")
+    x[rows, kd] = 1.0
+    y = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    _lib.check(lib.novaq_linear_forward(x.data_ptr(), M, K, codes.data_ptr(), code, sd.data_ptr(),
+                                        None, N, y.data_ptr(), stream), "linear")
+    cols = codes[:, kd].t().contiguous().cpu().numpy()  # (M, N): W[:, k_i]
+    want = O.cast(cols.reshape(-1), QCODE[wdt], O.F32, scale=s).view(np.float32).reshape(M, N)
+    torch.cuda.synchronize()
+    assert np.array_equal(y.cpu().numpy(), want)
+    del x, y
+
+    # backward: W (D_out = K, D_in = N) is the same bytes read as [K][N]
+    wkn = codes.view(K, N)
+    assert lib.novaq_linear_backward_workspace(M, N, K, code) == 0
+    grad = torch.zeros((M, K), dtype=torch.float32, device="cuda")
+    grad[rows, kd] = 1.0
+    gi = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    _lib.check(lib.novaq_linear_backward(grad.data_ptr(), None, M, N, wkn.data_ptr(), code,
+                                         sd.data_ptr(), K, gi.data_ptr(), None, None, None, 0,
+                                         stream), "linear backward")
+    rows_w = wkn[kd].contiguous().cpu().numpy()  # (M, N): W[k_i, :]
+    want_b = O.cast(rows_w.reshape(-1), QCODE[wdt], O.F32, scale=s).view(np.float32).reshape(M, N)
+    torch.cuda.synchronize()
+    assert np.array_equal(gi.cpu().numpy(), want_b)
