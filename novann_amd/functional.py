@@ -254,12 +254,13 @@ def linear_backward(grad, input, weight, bias: bool = True):
     gw = torch.empty((D_out, D_in), dtype=torch.float32, device=x.device)
     gb = torch.empty((1, D_out), dtype=torch.float32, device=x.device) if bias else None
     nbytes = lib.novaq_linear_backward_workspace(N, D_in, D_out, wdt)
-    work = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=x.device)
+    # FP8 weights at whole-tile shapes need no workspace (the query returns 0)
+    work = torch.empty(nbytes, dtype=torch.uint8, device=x.device) if nbytes else None
     check(lib.novaq_linear_backward(
         g.data_ptr(), x.data_ptr(), N, D_in, w.data_ptr(), wdt,
         None if ws is None else ws.data_ptr(), D_out, gi.data_ptr(), gw.data_ptr(),
-        None if gb is None else gb.data_ptr(), work.data_ptr(), nbytes,
-        _stream(x.device)), "linear backward")
+        None if gb is None else gb.data_ptr(), None if work is None else work.data_ptr(),
+        nbytes, _stream(x.device)), "linear backward")
     if was_numpy:
         return (gi.cpu().numpy(), gw.cpu().numpy(), None if gb is None else gb.cpu().numpy())
     return gi, gw, gb
