@@ -27,11 +27,11 @@ struct CastShape {
   static constexpr int dst_bits = epl * dtype_bits(DT);
   static constexpr int src_words = (src_bits + 31) / 32;  // 32-bit words holding a unit
   static constexpr int dst_words = (dst_bits + 31) / 32;
-  // units per thread: 2 for 16 -> 32-bit widening (twice the workgroups:
-  // bf16 -> fp32 on 2^28 elements 271 -> 255 us; 4 and 8 units and the 8 / 4
-  // -> 32-bit casts at 2 units measured slower)
+  // units per thread: 1 for 16 -> 32-bit widening (four times the
+  // workgroups: bf16 -> fp32 on 2^28 elements 271 us at 4 units, 255 at 2,
+  // 252 at 1; 8 units and the 8 / 4 -> 32-bit casts at 2 units measured slower)
   static constexpr int upt =
-      dtype_bits(ST) == 16 && dtype_bits(DT) == 32 ? kUnitsPerThread / 2 : kUnitsPerThread;
+      dtype_bits(ST) == 16 && dtype_bits(DT) == 32 ? kUnitsPerThread / 4 : kUnitsPerThread;
 };
 
 template <int N>
