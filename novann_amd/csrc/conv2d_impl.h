@@ -1059,7 +1059,8 @@ constexpr size_t SC_LDS = 64 * 1024;
 
 struct SmallGeom {
   int N, C, H, W, C_out, KH, KW, ph, pw, pad_mode, OH, OW;
-  int HP, WP;   // staged plane: HP padded rows of WP floats (rows 16-byte aligned)
+  int HP, WP;   // staged plane: HP padded rows, WP floats apart (16-byte aligned)
+  int WS;       // staged columns of a row (WS <= WP; the pitch's extra floats are never read)
   int WV;       // columns of the padded image (W + 2 pw); staged columns past it are 0
   int cpr;      // 4-pixel chunks per output row
   int vec;      // OW % 4 == 0: whole chunks, vector stores
@@ -1097,7 +1098,7 @@ __global__ __launch_bounds__(256) void conv2d_smallc_kernel(
   const int64_t xb = (int64_t)n * g.C * g.H * g.W;
   const int rows = g.C * g.HP;
   for (int r0 = 0; r0 < rows; r0 += 8 * SC_SR) {
-    for (int c0 = 0; c0 < g.WP; c0 += 32 * SC_SC) {
+    for (int c0 = 0; c0 < g.WS; c0 += 32 * SC_SC) {
       float v[SC_SR][SC_SC];
 #pragma unroll
       for (int i = 0; i < SC_SR; ++i) {
@@ -1118,7 +1119,7 @@ __global__ __launch_bounds__(256) void conv2d_smallc_kernel(
 #pragma unroll
         for (int j = 0; j < SC_SC; ++j) {
           const int col = c0 + (threadIdx.x & 31) + 32 * j;
-          if (r < rows && col < g.WP) xs[r * g.WP + col] = u2f(enc_bf16(f2u(v[i][j])) << 16);
+          if (r < rows && col < g.WS) xs[r * g.WP + col] = u2f(enc_bf16(f2u(v[i][j])) << 16);
         }
       }
     }
@@ -1243,10 +1244,15 @@ bool launch_smallc(const uint8_t* x, const float* x_scale, const void* w, const 
   g.HP = cg.OH + cg.KH - 1;
   g.cpr = (cg.OW + 3) / 4;
   g.WV = cg.OW + cg.KW - 1;
-  g.WP = 4 * g.cpr + 8;  // a chunk reads 12 floats (3 x 16 bytes) from its start
+  g.WS = 4 * g.cpr + 8;  // a chunk reads 12 floats (3 x 16 bytes) from its start
   g.vec = cg.OW % 4 == 0 && (reinterpret_cast<uintptr_t>(y) % 16) == 0;
-  const size_t lds =
-      ((size_t)g.C * g.HP * g.WP + (size_t)SC_CO * g.C * g.KH * g.KW) * sizeof(float);
+  // row pitch 4 * cpr + 64 floats when it fits: the chunks' 16-byte reads then
+  // fall on the banks of a contiguous run (pitch = one row of chunks mod 64
+  // banks), with no conflicts where a group of lanes crosses a row
+  const size_t wts = (size_t)SC_CO * g.C * g.KH * g.KW;
+  g.WP = 4 * g.cpr + 64;
+  if (((size_t)g.C * g.HP * g.WP + wts) * sizeof(float) > SC_LDS) g.WP = g.WS;
+  const size_t lds = ((size_t)g.C * g.HP * g.WP + wts) * sizeof(float);
   // (within the default 64 KB of dynamic LDS: no attribute to raise)
   if (lds > SC_LDS || (int64_t)g.OH * g.cpr * SC_CO > 0x7FFFFFFF) return false;
   const int64_t co_groups = (cg.C_out + SC_CO - 1) / SC_CO;
