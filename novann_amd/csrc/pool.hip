@@ -363,7 +363,7 @@ __global__ __launch_bounds__(256) void global_avg_pool2d_wave_kernel(
     const uint8_t* __restrict__ x, const float* __restrict__ x_scale, float* __restrict__ y,
     int64_t planes, int hw, GapPlan plan) {
   __shared__ float sums[4][GAP_MAX_LEAVES];
-  extern __shared__ float gap_stage[];  // STAGED: 4 waves x ppw * hw elements
+  extern __shared__ __attribute__((aligned(16))) float gap_stage[];  // STAGED: 4 waves x ppw * hw elements
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int L = plan.L;
   const int G = L < 8 ? L : 8;         // leaves per pass
@@ -383,16 +383,29 @@ __global__ __launch_bounds__(256) void global_avg_pool2d_wave_kernel(
     const int64_t e0 = plane0 * hw;
     float* st = gap_stage + wave * ppw * hw;
     if ((e0 & 3) == 0) {
+      // one 16-byte LDS store per lane where the wave's region is 16-byte
+      // aligned: consecutive lanes then write consecutive banks (four 4-byte
+      // stores 16 bytes apart would fall 4 lanes to a bank)
+      const bool st16 = (reinterpret_cast<uintptr_t>(st) & 15) == 0;
       for (int g4 = lane; 4 * g4 < n; g4 += 64) {
         const int64_t e = e0 + 4 * g4;
-        const xl_u32x4 r = 4 * g4 + 3 < n ? x4_raw<XT>(x, e) : x4_raw_guarded<XT>(x, e, e0 + n);
+        const bool whole = 4 * g4 + 3 < n;
+        const xl_u32x4 r = whole ? x4_raw<XT>(x, e) : x4_raw_guarded<XT>(x, e, e0 + n);
         constexpr int B = XL<XT>::bits;
+        float f[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const uint32_t c =
               B == 32 ? r[q] : (r[(q * B) / 32] >> ((q * B) % 32)) & ((1u << (B & 31)) - 1u);
           const float v = u2f(decode<XT>(c));
-          if (4 * g4 + q < n) st[4 * g4 + q] = scaled ? v * s : v;
+          f[q] = scaled ? v * s : v;
+        }
+        if (st16 && whole) {
+          *reinterpret_cast<float4*>(st + 4 * g4) = make_float4(f[0], f[1], f[2], f[3]);
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            if (4 * g4 + q < n) st[4 * g4 + q] = f[q];
         }
       }
     } else {
