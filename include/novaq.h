@@ -226,6 +226,34 @@ int novaq_max_pool2d(const void *x, int x_dtype, int64_t N, int64_t C, int64_t H
 int novaq_global_avg_pool2d(const void *x, int x_dtype, const float *x_scale, int64_t N,
                             int64_t C, int64_t H, int64_t W, float *y, void *stream);
 
+/* col (C*KH*KW, N*OH*OW) fp32, row-major = the column matrix of NovaNN's
+ * conv2d: col[(c*KH + kh)*KW + kw][(n*OH + oh)*OW + ow] = x padded (ph, pw) in
+ * pad_mode with numpy.pad's rules, at [n][c][oh*sh + kh][ow*sw + kw]; rows
+ * ordered (c, kh, kw) and columns (n, oh, ow) as the reference's
+ * windows.transpose(1, 4, 5, 0, 2, 3).reshape(C*KH*KW, -1).  x (N, C, H, W)
+ * is in x_dtype (F32, F16, BF16, E4M3, E5M2), decoded exactly; FP8 values are
+ * multiplied by *x_scale when x_scale is given (one fp32 multiply, as
+ * novaq_cast's dequantize).  x needs element alignment only; col 16 bytes.
+ * Replaces: conv2d's _im2col (novann/functional.py:346-368), the `col` that
+ * conv2d(..., extras=True) returns (:383-384) and Conv2d.forward caches for
+ * its backward (novann/layers/convolutional/conv2d.py:162-175).  The forward
+ * products never materialise it. */
+int novaq_im2col(const void *x, int x_dtype, const float *x_scale, int64_t N, int64_t C,
+                 int64_t H, int64_t W, int KH, int KW, int sh, int sw, int ph, int pw,
+                 int pad_mode, float *col, void *stream);
+
+/* y (N, C, H + 2ph, W + 2pw) = x (N, C, H, W) padded in pad_mode with
+ * numpy.pad's rules (zeros pads +0; reflect, edge, wrap with any width), in
+ * x's own storage (x_dtype F32, F16, BF16, E4M3 or E5M2; codes copied as
+ * stored, so FP8 keeps its scale).  x needs element alignment only; y 16
+ * bytes.  Replaces: max_pool2d's _add_padding (novann/functional.py:495-514),
+ * the padded array behind the window view that max_pool2d(..., extras=True)
+ * returns with its padded shape (:516-534) and MaxPool2d.forward caches
+ * (novann/layers/pooling/maxpool/maxpool2d.py:63-75); the caller takes the
+ * (N, C, OH, OW, KH, KW) window view of y with strides. */
+int novaq_pad2d(const void *x, int x_dtype, int64_t N, int64_t C, int64_t H, int64_t W, int ph,
+                int pw, int pad_mode, void *y, void *stream);
+
 /* Hyper-parameters of one AdamW step (novann AdamW, adamw.py:17-38): Python
  * floats there, doubles here; step is the 1-based step count t; decay = 0
  * marks a parameter the reference never decays (BatchNorm gamma / beta,
@@ -297,15 +325,19 @@ size_t novaq_linear_backward_workspace(int64_t N, int64_t D_in, int64_t D_out, i
  *   grad_bias   (D_out)       = grad summed over the N rows
  * Replaces: Linear.backward (novann/layers/linear/linear.py:85-108).  Any of
  * the three outputs may be NULL (not computed).  The products run on bf16
- * MFMA with fp32 accumulation on grad and x rounded to bf16: grad_input on
- * w_q's FP8 codes and the fp32 grad, both read in place, when D_out % 128,
- * D_in % 256 and N % 128 are 0, else on the Linear forward kernels with
- * w_q's codes transposed (exact); grad_weight with grad and x read in place
- * when D_out % 128, D_in % 256 and N % 64 are 0, else through bf16
- * transposed copies.  workspace: device memory of
- * novaq_linear_backward_workspace() bytes (16-byte aligned; may be NULL when
- * that is 0) the call may overwrite; it is not used after the call's kernels
- * complete. */
+ * MFMA with fp32 accumulation on grad and x rounded to bf16.  For FP8 w_q at
+ * whole-tile shapes (among other limits D_out % 128, D_in % 256 and N % 128
+ * are 0) grad_input reads w_q's codes and the fp32 grad in place and
+ * grad_weight reads grad and x in place; other shapes go through transposed
+ * copies in the workspace (w_q's codes, exact; grad and x in bf16).  The
+ * whole condition is the one novaq_linear_backward_workspace() evaluates:
+ * when it returns 0, no workspace is needed, whichever gradients are asked
+ * for.  grad_bias sums in a fixed order that depends on the shape and on the
+ * device's CU count (the tile size the weight-gradient product picks), so it
+ * is bit-reproducible per device and shape, not across them.  workspace:
+ * device memory of novaq_linear_backward_workspace() bytes (16-byte aligned;
+ * may be NULL when that is 0) the call may overwrite; it is not used after
+ * the call's kernels complete. */
 int novaq_linear_backward(const float *grad, const float *x, int64_t N, int64_t D_in,
                           const void *w_q, int w_dtype, const float *w_scale, int64_t D_out,
                           float *grad_input, float *grad_weight, float *grad_bias,

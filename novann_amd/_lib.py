@@ -62,6 +62,9 @@ SIGNATURES = {
     "novaq_max_pool2d": (_i32, [_vp, _i32, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32,
                                 _i32, _i32, _vp, _vp]),
     "novaq_global_avg_pool2d": (_i32, [_vp, _i32, _f32p, _i64, _i64, _i64, _i64, _f32p, _vp]),
+    "novaq_im2col": (_i32, [_vp, _i32, _f32p, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _i32,
+                            _i32, _i32, _i32, _f32p, _vp]),
+    "novaq_pad2d": (_i32, [_vp, _i32, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _vp, _vp]),
     "novaq_adamw_step": (_i32, [_f32p, _f32p, _f32p, _f32p, _i64, ctypes.POINTER(AdamW), _f32p,
                                 _vp]),
     "novaq_adamw_step_f64": (_i32, [_vp, _vp, _i32, _vp, _vp, _i64, ctypes.POINTER(AdamW), _vp]),

@@ -282,8 +282,47 @@ int novaq_global_avg_pool2d(const void* x, int x_dtype, const float* x_scale, in
   if (N < 0 || C <= 0 || H <= 0 || W <= 0) return NOVAQ_EINVAL;
   if (N == 0) return NOVAQ_OK;
   if (!x || !y) return NOVAQ_EINVAL;
+  // the plane loads are 4-element vectors wherever the plane offset allows
+  if (!aligned16(x) || (reinterpret_cast<uintptr_t>(y) & 3) ||
+      (x_scale && (reinterpret_cast<uintptr_t>(x_scale) & 3)))
+    return NOVAQ_EALIGN;
   return global_avg_pool2d_launch(x, x_dtype, x_scale, N * C, H * W, y,
                                   static_cast<hipStream_t>(stream));
+}
+
+int novaq_im2col(const void* x, int x_dtype, const float* x_scale, int64_t N, int64_t C,
+                 int64_t H, int64_t W, int KH, int KW, int sh, int sw, int ph, int pw,
+                 int pad_mode, float* col, void* stream) {
+  if (!valid_dtype(x_dtype) || x_dtype == E2M1) return NOVAQ_EDTYPE;
+  if (x_scale && !is_quant(x_dtype)) return NOVAQ_EDTYPE;
+  if (pad_mode < NOVAQ_PAD_ZEROS || pad_mode > NOVAQ_PAD_CIRCULAR) return NOVAQ_EPADMODE;
+  if (N < 0 || C <= 0 || H <= 0 || W <= 0 || KH <= 0 || KW <= 0 || sh <= 0 || sw <= 0 ||
+      ph < 0 || pw < 0)
+    return NOVAQ_EINVAL;
+  if (H + 2 * (int64_t)ph < KH || W + 2 * (int64_t)pw < KW) return NOVAQ_ESHAPE;
+  if (H > 0x7FFFFFFF || W > 0x7FFFFFFF || C > 0x7FFFFFFF || N > 0x7FFFFFFF) return NOVAQ_EINVAL;
+  if (N == 0) return NOVAQ_OK;
+  if (!x || !col) return NOVAQ_EINVAL;
+  const uintptr_t eb = (uintptr_t)dtype_bits(x_dtype) / 8;  // element-aligned x views work
+  if (reinterpret_cast<uintptr_t>(x) % eb || !aligned16(col) ||
+      (x_scale && (reinterpret_cast<uintptr_t>(x_scale) & 3)))
+    return NOVAQ_EALIGN;
+  return im2col_launch(x, x_dtype, x_scale, N, C, H, W, KH, KW, sh, sw, ph, pw, pad_mode, col,
+                       static_cast<hipStream_t>(stream));
+}
+
+int novaq_pad2d(const void* x, int x_dtype, int64_t N, int64_t C, int64_t H, int64_t W, int ph,
+                int pw, int pad_mode, void* y, void* stream) {
+  if (!valid_dtype(x_dtype) || x_dtype == E2M1) return NOVAQ_EDTYPE;
+  if (pad_mode < NOVAQ_PAD_ZEROS || pad_mode > NOVAQ_PAD_CIRCULAR) return NOVAQ_EPADMODE;
+  if (N < 0 || C <= 0 || H <= 0 || W <= 0 || ph < 0 || pw < 0) return NOVAQ_EINVAL;
+  if (H > 0x7FFFFFFF || W > 0x7FFFFFFF || ph > 0x3FFFFFFF || pw > 0x3FFFFFFF) return NOVAQ_EINVAL;
+  if (N == 0) return NOVAQ_OK;
+  if (!x || !y) return NOVAQ_EINVAL;
+  const uintptr_t eb = (uintptr_t)dtype_bits(x_dtype) / 8;
+  if (reinterpret_cast<uintptr_t>(x) % eb || !aligned16(y)) return NOVAQ_EALIGN;
+  return pad2d_launch(x, x_dtype, N, C, H, W, ph, pw, pad_mode, y,
+                      static_cast<hipStream_t>(stream));
 }
 
 int novaq_adamw_step(float* w, const float* grad, float* m, float* v, int64_t n,

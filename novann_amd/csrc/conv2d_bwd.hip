@@ -48,21 +48,6 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-__device__ __forceinline__ int pad_idx(int i, int n, int mode) {
-  if (i >= 0 && i < n) return i;
-  if (mode == NOVAQ_PAD_ZEROS) return -1;
-  if (mode == NOVAQ_PAD_REPLICATE) return i < 0 ? 0 : n - 1;
-  if (mode == NOVAQ_PAD_CIRCULAR) {
-    int r = i % n;
-    return r < 0 ? r + n : r;
-  }
-  if (n == 1) return 0;  // reflect, period 2(n-1)
-  const int p = 2 * (n - 1);
-  int r = i % p;
-  if (r < 0) r += p;
-  return r >= n ? p - r : r;
-}
-
 template <int WT>
 __device__ __forceinline__ uint32_t code_at(const uint8_t* __restrict__ w, int64_t e) {
   if constexpr (WT == E2M1) return (w[e >> 1] >> ((e & 1) * 4)) & 0xFu;
@@ -292,8 +277,8 @@ __global__ __launch_bounds__(DW_THREADS, 2) void dweight_kernel(
             if ((unsigned)hi < (unsigned)g.H && (unsigned)wi < (unsigned)g.W)
               bv[i][q] = xn[t.x + hb[q] * g.W + wb[q]];
           } else {
-            hi = pad_idx(hi, g.H, g.pad_mode);
-            wi = pad_idx(wi, g.W, g.pad_mode);
+            hi = pad_index(hi, g.H, g.pad_mode);
+            wi = pad_index(wi, g.W, g.pad_mode);
             if (hi >= 0 && wi >= 0) bv[i][q] = xn[t.x - t.y * g.W - t.z + hi * g.W + wi];
           }
         }
@@ -457,7 +442,7 @@ __global__ __launch_bounds__(768) void dweight_rows_kernel(
     const int e = lane + 64 * j;
     xr[j] = e / rg.XW;
     const int col = e - xr[j] * rg.XW;
-    xw[j] = (e < xslots && col < g.OW + g.KW - 1) ? pad_idx(col - g.pw, g.W, g.pad_mode) : -1;
+    xw[j] = (e < xslots && col < g.OW + g.KW - 1) ? pad_index(col - g.pw, g.W, g.pad_mode) : -1;
     xk[j] = e < xslots ? e : xslots;
   }
   const bool odd = kw & 1;
@@ -482,7 +467,7 @@ __global__ __launch_bounds__(768) void dweight_rows_kernel(
       goff[j] = (gk[j] < DR_K && gr[j] < rows_left)
                     ? (uint32_t)(oh0 * g.OW + lane + 64 * j) * 4u : DR_OOB;
     // input row of staged row rr (lane rr holds it; -1: a zero row)
-    const int hi_l = lane < rows_read ? pad_idx(oh0 + lane - g.ph, g.H, g.pad_mode) : -1;
+    const int hi_l = lane < rows_read ? pad_index(oh0 + lane - g.ph, g.H, g.pad_mode) : -1;
 #pragma unroll
     for (int j = 0; j < XJ; ++j) {
       const int hi = __shfl(hi_l, xr[j] < 63 ? xr[j] : 63);

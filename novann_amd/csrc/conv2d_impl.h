@@ -80,21 +80,6 @@ struct ConvGeom {
   int64_t tiles;
 };
 
-__device__ __forceinline__ int pad_index(int i, int n, int mode) {
-  if (i >= 0 && i < n) return i;
-  if (mode == NOVAQ_PAD_ZEROS) return -1;
-  if (mode == NOVAQ_PAD_REPLICATE) return i < 0 ? 0 : n - 1;
-  if (mode == NOVAQ_PAD_CIRCULAR) {
-    int r = i % n;
-    return r < 0 ? r + n : r;
-  }
-  if (n == 1) return 0;  // reflect, period 2(n-1)
-  int p = 2 * (n - 1);
-  int r = i % p;
-  if (r < 0) r += p;
-  return r >= n ? p - r : r;
-}
-
 __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
   return (uint16_t)enc_bf16(__float_as_uint(f));
 }

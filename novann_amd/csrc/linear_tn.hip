@@ -27,7 +27,10 @@
 // linear.py:103-104) from the values they stage: each thread adds its 4
 // columns over the rows it loads (one residue class of rows modulo the rows
 // per staging pass), in row order, and a column's partial sums are added in
-// order of that residue at the end.
+// order of that residue at the end.  The rows per pass depend on the tile
+// size the launch picks (256 x 256 tiles when they fill the device's CUs,
+// else 128 x 256), so the sums are reproducible bit for bit per device and
+// shape, not across devices with other CU counts or across shapes.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 

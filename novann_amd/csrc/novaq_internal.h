@@ -8,6 +8,26 @@
 
 namespace novaq {
 
+// Source index of padded position i (-1 .. n + pad) along an axis of length n
+// under numpy.pad's index rules for NovaNN's padding modes
+// (novann/functional.py:325-344): -1 where zeros mode pads a 0; edge
+// (replicate) repeats the end element; wrap (circular) is i mod n; reflect
+// mirrors without repeating the end element, period 2(n - 1), any width.
+__device__ __forceinline__ int pad_index(int i, int n, int mode) {
+  if (i >= 0 && i < n) return i;
+  if (mode == NOVAQ_PAD_ZEROS) return -1;
+  if (mode == NOVAQ_PAD_REPLICATE) return i < 0 ? 0 : n - 1;
+  if (mode == NOVAQ_PAD_CIRCULAR) {
+    const int r = i % n;
+    return r < 0 ? r + n : r;
+  }
+  if (n == 1) return 0;  // reflect, period 2(n-1)
+  const int p = 2 * (n - 1);
+  int r = i % p;
+  if (r < 0) r += p;
+  return r >= n ? p - r : r;
+}
+
 // Records a failed HIP call for novaq_last_hip_error() and maps it to a status.
 int hip_fail(hipError_t e);
 
@@ -76,6 +96,15 @@ int max_pool2d_launch(const void* x, int x_dtype, int64_t N, int64_t C, int64_t 
                       hipStream_t stream);
 int global_avg_pool2d_launch(const void* x, int x_dtype, const float* x_scale, int64_t planes,
                              int64_t hw, float* y, hipStream_t stream);
+
+// col (C*KH*KW, N*OH*OW) fp32 = the conv2d column matrix of x in x_dtype
+// (FP8 times *x_scale when given); pad modes resolved as pad_index does.
+int im2col_launch(const void* x, int x_dtype, const float* x_scale, int64_t N, int64_t C,
+                  int64_t H, int64_t W, int KH, int KW, int sh, int sw, int ph, int pw,
+                  int pad_mode, float* col, hipStream_t stream);
+// y (N, C, H + 2 ph, W + 2 pw) = x padded in pad_mode, codes copied as stored.
+int pad2d_launch(const void* x, int x_dtype, int64_t N, int64_t C, int64_t H, int64_t W, int ph,
+                 int pw, int pad_mode, void* y, hipStream_t stream);
 
 // Sets count 32-bit words at p to v (a kernel, so it may be captured in graphs).
 int fill_u32_launch(uint32_t* p, uint32_t v, int count, hipStream_t stream);

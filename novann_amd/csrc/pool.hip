@@ -42,21 +42,6 @@ struct PoolGeom {
   int H, W, KH, KW, sh, sw, ph, pw, pad_mode, OH, OW;
 };
 
-__device__ __forceinline__ int pool_pad_index(int i, int n, int mode) {
-  if (i >= 0 && i < n) return i;
-  if (mode == NOVAQ_PAD_ZEROS) return -1;
-  if (mode == NOVAQ_PAD_REPLICATE) return i < 0 ? 0 : n - 1;
-  if (mode == NOVAQ_PAD_CIRCULAR) {
-    int r = i % n;
-    return r < 0 ? r + n : r;
-  }
-  if (n == 1) return 0;  // reflect, period 2(n-1)
-  const int p = 2 * (n - 1);
-  int r = i % p;
-  if (r < 0) r += p;
-  return r >= n ? p - r : r;
-}
-
 template <int XT>
 __device__ __forceinline__ void store_code(uint8_t* __restrict__ y, int64_t i, uint32_t c) {
   if constexpr (XL<XT>::bits == 32) reinterpret_cast<uint32_t*>(y)[i] = c;
@@ -80,9 +65,9 @@ __global__ __launch_bounds__(256) void max_pool2d_kernel(const uint8_t* __restri
   float bv = 0.0f;
   bool first = true;
   for (int kh = 0; kh < g.KH; ++kh) {
-    const int hi = pool_pad_index(oh * g.sh + kh - g.ph, g.H, g.pad_mode);
+    const int hi = pad_index(oh * g.sh + kh - g.ph, g.H, g.pad_mode);
     for (int kw = 0; kw < g.KW; ++kw) {
-      const int wi = pool_pad_index(ow * g.sw + kw - g.pw, g.W, g.pad_mode);
+      const int wi = pad_index(ow * g.sw + kw - g.pw, g.W, g.pad_mode);
       uint32_t c = 0;  // the zero padding's +0
       if (hi >= 0 && wi >= 0) c = x_code<XT>(x, base + (int64_t)hi * g.W + wi);
       const float v = u2f(decode<XT>(c));
@@ -168,7 +153,7 @@ __global__ __launch_bounds__(256) void max_pool2d_w2_kernel(const uint8_t* __res
   auto load = [&](const Item& it, int kh, uint32_t* c) {
     c[0] = c[1] = c[2] = c[3] = 0u;  // the zero padding's +0
     if (!it.live) return;
-    const int hi = pool_pad_index(it.oh * g.sh + kh - g.ph, g.H, g.pad_mode);
+    const int hi = pad_index(it.oh * g.sh + kh - g.ph, g.H, g.pad_mode);
     if (hi < 0) return;
     const int64_t e = it.base + (int64_t)hi * g.W + 4 * it.u;
     if (vec) {

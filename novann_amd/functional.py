@@ -286,20 +286,23 @@ def conv2d(input, weight, kernel_size: IntPair, stride: IntPair = 1, padding: In
     """2-D cross-correlation (novann/functional.py:275-385).
 
     input (N, C, H, W); weight (C_out, C, KH, KW); returns (N, C_out, OH, OW)
-    fp32 with OH = (H + 2ph - KH)//sh + 1.  The reference materialises the
-    im2col matrix; this computes the same values with implicit im2col, so
-    ``extras=True`` (which asks for that matrix, a training-time cache) is not
-    available.  ``epilogue`` (not in the reference) fuses eval BatchNorm2d,
-    ReLU and a cast of y into the convolution; see Epilogue."""
+    fp32 with OH = (H + 2ph - KH)//sh + 1.  The product uses implicit im2col
+    (no column matrix).  ``extras=True`` returns ``(out, col, w_col)`` as the
+    reference does (:383-384) for callers that cache them (Conv2d.forward,
+    novann/layers/convolutional/conv2d.py:162-175): ``col`` is the
+    (C*KH*KW, N*OH*OW) fp32 column matrix (rows (c, kh, kw), columns
+    (n, oh, ow), the padding mode resolved), written by its own gather kernel;
+    ``w_col`` is the weight as a (C_out, C*KH*KW) fp32 matrix -- a view of an
+    fp32 weight's data, as ``weight.data.reshape(C_out, -1)`` is in the
+    reference, or s * decode(codes) for a quantized weight.  numpy in -> numpy
+    out.  ``epilogue`` (not in the reference) fuses eval BatchNorm2d, ReLU and a
+    cast of y into the convolution; see Epilogue."""
     KH, KW = _pair(kernel_size)
     ph, pw = _pair(padding)
     sh, sw = _pair(stride)
     modes = tuple(PAD_MODES)
     if padding_mode not in PAD_MODES:
         raise ValueError(f"padding_mode Only accept {modes} not '{padding_mode}'")
-    if extras:
-        raise NotImplementedError("conv2d(extras=True): the im2col matrix is never "
-                                  "materialised on this path")
     x, xdt, xs, xshape, was_numpy = _x_arg(input, "input")
     if len(xshape) != 4:
         raise ValueError(f"conv2d expects (N, C, H, W), got {xshape}")
@@ -327,13 +330,61 @@ def conv2d(input, weight, kernel_size: IntPair, stride: IntPair = 1, padding: In
             pw, PAD_MODES[padding_mode], None if b is None else b.data_ptr(),
             None if st is None else ctypes.byref(st), y.data_ptr(), _stream(x.device)),
             "conv2d")
-        return _finish(y, epilogue, was_numpy)
-    y = torch.empty((N, C_out, OH, OW), dtype=torch.float32, device=x.device)
-    check(_lib.load().novaq_conv2d_forward(
-        x.data_ptr(), N, C, H, W, w.data_ptr(), wdt, None if ws is None else ws.data_ptr(),
-        C_out, KH, KW, sh, sw, ph, pw, PAD_MODES[padding_mode],
-        None if b is None else b.data_ptr(), y.data_ptr(), _stream(x.device)), "conv2d")
-    return y.cpu().numpy() if was_numpy else y
+        out = _finish(y, epilogue, was_numpy)
+    else:
+        y = torch.empty((N, C_out, OH, OW), dtype=torch.float32, device=x.device)
+        check(_lib.load().novaq_conv2d_forward(
+            x.data_ptr(), N, C, H, W, w.data_ptr(), wdt, None if ws is None else ws.data_ptr(),
+            C_out, KH, KW, sh, sw, ph, pw, PAD_MODES[padding_mode],
+            None if b is None else b.data_ptr(), y.data_ptr(), _stream(x.device)), "conv2d")
+        out = y.cpu().numpy() if was_numpy else y
+    if not extras:
+        return out
+    col = im2col(x, (KH, KW), (sh, sw), (ph, pw), padding_mode, _xdtype=xdt, _xscale=xs,
+                 _shape=xshape)
+    return out, (col.cpu().numpy() if was_numpy else col), _w_col(weight, C_out, was_numpy)
+
+
+def _w_col(weight, C_out: int, was_numpy: bool):
+    """conv2d's (C_out, C*KH*KW) weight matrix (functional.py:374): a view of
+    an fp32 weight's data, the dequantized weight for quantized codes."""
+    if isinstance(weight, QuantizedParameters):
+        w = weight.dequantize().reshape(C_out, -1)
+        return w.cpu().numpy() if was_numpy else w
+    data = weight.data if isinstance(weight, Parameters) else weight
+    if isinstance(data, torch.Tensor):
+        w = data.reshape(C_out, -1)
+        return w.detach().cpu().numpy() if was_numpy else w
+    return np.asarray(data).reshape(C_out, -1)
+
+
+def im2col(input, kernel_size: IntPair, stride: IntPair = 1, padding: IntPair = 0,
+           padding_mode: str = "zeros", *, _xdtype=None, _xscale=None, _shape=None):
+    """The column matrix of conv2d (novann/functional.py:346-368) as a
+    (C*KH*KW, N*OH*OW) fp32 device tensor: col[(c, kh, kw), (n, oh, ow)] =
+    the input padded with numpy.pad's rules at [n, c, oh*sh + kh, ow*sw + kw].
+    Narrow inputs are decoded (FP8 times its scale)."""
+    KH, KW = _pair(kernel_size)
+    ph, pw = _pair(padding)
+    sh, sw = _pair(stride)
+    if padding_mode not in PAD_MODES:
+        raise ValueError(f"padding_mode Only accept {tuple(PAD_MODES)} not '{padding_mode}'")
+    if _xdtype is None:
+        x, xdt, xs, xshape, _ = _x_arg(input, "input")
+    else:
+        x, xdt, xs, xshape = input, _xdtype, _xscale, _shape
+    if len(xshape) != 4:
+        raise ValueError(f"im2col expects (N, C, H, W), got {xshape}")
+    N, C, H, W = xshape
+    OH = (H + 2 * ph - KH) // sh + 1
+    OW = (W + 2 * pw - KW) // sw + 1
+    if OH <= 0 or OW <= 0:
+        raise ValueError(f"output size {(OH, OW)} is empty")
+    col = torch.empty((C * KH * KW, N * OH * OW), dtype=torch.float32, device=x.device)
+    check(_lib.load().novaq_im2col(x.data_ptr(), DTYPES[xdt], None if xs is None else xs.data_ptr(),
+                                   N, C, H, W, KH, KW, sh, sw, ph, pw, PAD_MODES[padding_mode],
+                                   col.data_ptr(), _stream(x.device)), "im2col")
+    return col
 
 
 def conv2d_backward(grad, input, weight, kernel_size: IntPair, stride: IntPair = 1,
@@ -399,16 +450,17 @@ def max_pool2d(input, kernel_size: IntPair, stride: IntPair, padding: IntPair = 
     numpy.pad's rules (zeros pads 0), the max of each window.  Returns
     (N, C, OH, OW) in the input's storage (fp32 ndarray for numpy input; bf16
     / f16 tensors and FP8 Quantized activations pool without decoding: the
-    result is one of the input values).  ``extras=True`` (the window view,
-    a training cache of the reference) is not available."""
+    result is one of the input values).  ``extras=True`` returns
+    ``(out, windows, OH, OW, padded_shape)`` as the reference does (:533-534)
+    for MaxPool2d.forward's cache (layers/pooling/maxpool/maxpool2d.py:63-75):
+    ``windows`` is the (N, C, OH, OW, KH, KW) strided view of the padded input
+    (padded on the device in the input's storage, FP8 as codes), an ndarray
+    for numpy input."""
     KH, KW = _pair(kernel_size)
     ph, pw = _pair(padding)
     sh, sw = _pair(stride)
     if padding_mode not in PAD_MODES:
         raise ValueError(f"padding_mode Only accept {tuple(PAD_MODES)} not '{padding_mode}'")
-    if extras:
-        raise NotImplementedError("max_pool2d(extras=True): the window view is never "
-                                  "materialised on this path")
     x, xdt, xs, xshape, was_numpy = _x_arg(input, "input")
     if len(xshape) != 4:
         raise ValueError(f"max_pool2d expects (N, C, H, W), got {xshape}")
@@ -421,7 +473,24 @@ def max_pool2d(input, kernel_size: IntPair, stride: IntPair, padding: IntPair = 
     check(_lib.load().novaq_max_pool2d(x.data_ptr(), DTYPES[xdt], N, C, H, W, KH, KW, sh, sw,
                                        ph, pw, PAD_MODES[padding_mode], y.data_ptr(),
                                        _stream(x.device)), "max_pool2d")
-    return _narrow_out(y.view(N, C, OH, OW), xdt, xs, was_numpy, (N, C, OH, OW))
+    out = _narrow_out(y.view(N, C, OH, OW), xdt, xs, was_numpy, (N, C, OH, OW))
+    if not extras:
+        return out
+    Hp, Wp = H + 2 * ph, W + 2 * pw
+    xp = torch.empty((N, C, Hp, Wp), dtype=x.dtype, device=x.device)
+    check(_lib.load().novaq_pad2d(x.data_ptr(), DTYPES[xdt], N, C, H, W, ph, pw,
+                                  PAD_MODES[padding_mode], xp.data_ptr(), _stream(x.device)),
+          "max_pool2d padding")
+    shape = (N, C, OH, OW, KH, KW)
+    if was_numpy:
+        from numpy.lib.stride_tricks import as_strided
+        xp_h = xp.cpu().numpy()
+        s0, s1, s2, s3 = xp_h.strides
+        windows = as_strided(xp_h, shape=shape, strides=(s0, s1, s2 * sh, s3 * sw, s2, s3))
+    else:
+        s0, s1, s2, s3 = xp.stride()
+        windows = xp.as_strided(shape, (s0, s1, s2 * sh, s3 * sw, s2, s3))
+    return out, windows, OH, OW, (N, C, Hp, Wp)
 
 
 def avg_pool2d(input):

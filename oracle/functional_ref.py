@@ -12,8 +12,9 @@ Restates, with this build's own code, the arithmetic of
     grad scattered with np.add.at into a zero-padded (N, C, H_p, W_p) buffer
     whose border is then cropped;
   - ``novann.functional.relu`` (novann/functional.py:8-22): ``x * (x > 0)``;
-  - ``novann.functional.max_pool2d`` (:450-532): np.pad, an as_strided
-    (N, C, OH, OW, KH, KW) window view, ``max(axis=(4, 5))``; and
+  - ``novann.functional.max_pool2d`` (:450-534): np.pad, an as_strided
+    (N, C, OH, OW, KH, KW) window view (returned with extras=True),
+    ``max(axis=(4, 5))``; and
     ``avg_pool2d`` (:548-559): ``np.mean(x, axis=(2, 3), keepdims=True)``;
   - eval-mode ``BatchNorm2d`` / ``BatchNorm1d`` (batchnorm2d.py:98-102,
     batchnorm1d.py:138-149): ``gamma * (x - mean) / sqrt(var + eps) + beta``
@@ -159,9 +160,11 @@ def epilogue_f32(y: np.ndarray, mul=None, add=None, do_relu: bool = False,
     return v
 
 
-def max_pool2d(x: np.ndarray, kernel_size, stride, padding=(0, 0),
-               padding_mode: str = "zeros") -> np.ndarray:
-    """The reference's window view and max (functional.py:493-532)."""
+def pool_windows(x: np.ndarray, kernel_size, stride, padding=(0, 0),
+                 padding_mode: str = "zeros"):
+    """(windows, OH, OW, padded_shape): the (N, C, OH, OW, KH, KW) strided view
+    of the padded input that max_pool2d(..., extras=True) returns
+    (functional.py:516-534)."""
     KH, KW = _pair(kernel_size)
     sh, sw = _pair(stride)
     ph, pw = _pair(padding)
@@ -172,7 +175,13 @@ def max_pool2d(x: np.ndarray, kernel_size, stride, padding=(0, 0),
     s0, s1, s2, s3 = xp.strides
     win = as_strided(xp, shape=(N, C, OH, OW, KH, KW),
                      strides=(s0, s1, s2 * sh, s3 * sw, s2, s3))
-    return win.max(axis=(4, 5))
+    return win, OH, OW, xp.shape
+
+
+def max_pool2d(x: np.ndarray, kernel_size, stride, padding=(0, 0),
+               padding_mode: str = "zeros") -> np.ndarray:
+    """The reference's window view and max (functional.py:493-532)."""
+    return pool_windows(x, kernel_size, stride, padding, padding_mode)[0].max(axis=(4, 5))
 
 
 def avg_pool2d(x: np.ndarray) -> np.ndarray:

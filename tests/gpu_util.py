@@ -37,3 +37,23 @@ def first_mismatch(got: np.ndarray, want: np.ndarray, inputs: np.ndarray | None 
     i = bad[0]
     inp = "" if inputs is None else f" input=0x{int(inputs[i]):08x}"
     return f"{bad.size} mismatches; first at {i}:{inp} got=0x{int(got[i]):x} want=0x{int(want[i]):x}"
+
+
+def bf16_round(a: np.ndarray) -> np.ndarray:
+    """fp32 -> bf16 (nearest even) -> fp32, by the oracle's cast: the operand
+    values the bf16 MFMA products multiply."""
+    flat = np.ascontiguousarray(a, np.float32).reshape(-1)
+    return O.cast(O.cast(flat, O.F32, O.BF16), O.BF16, O.F32).reshape(a.shape)
+
+
+def error_report(y: np.ndarray, r: np.ndarray) -> dict:
+    """Normwise max|y - r| / max|r| (the gate) and the elementwise relative
+    error with a floor, max |y - r| / max(|r|, f * max|r|), for floors f of
+    1e-3 and 1e-2, plus the share of elements within 1e-2 relative error."""
+    d = np.abs(y.astype(np.float64) - r)
+    m = max(float(np.abs(r).max()), 1e-30)
+    a = np.abs(r)
+    return {"normwise": float(d.max() / m),
+            "elem_floor1e-3": float((d / np.maximum(a, 1e-3 * m)).max()),
+            "elem_floor1e-2": float((d / np.maximum(a, 1e-2 * m)).max()),
+            "share_within_1e-2": float(np.mean(d <= 1e-2 * a))}

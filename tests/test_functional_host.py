@@ -33,11 +33,17 @@ def test_conv2d_same_padding_raises_value_error():
         F.conv2d(x, w, 3, padding="same")
 
 
-def test_conv2d_extras_not_available():
+def test_extras_requests_are_validated_first():
+    """extras=True (the reference's training caches) is accepted; bad
+    arguments still raise the reference's ValueError before any device work."""
     x = np.ones((1, 1, 8, 8), np.float32)
     w = Parameters(np.ones((2, 1, 3, 3), np.float32))
-    with pytest.raises(NotImplementedError):
-        F.conv2d(x, w, 3, extras=True)
+    with pytest.raises(ValueError, match="padding_mode"):
+        F.conv2d(x, w, 3, padding=1, padding_mode="mirror", extras=True)
+    with pytest.raises(ValueError, match="padding_mode"):
+        F.max_pool2d(x, 2, 2, padding_mode="mirror", extras=True)
+    with pytest.raises(ValueError):
+        F.im2col(x, 3, padding="same")
 
 
 def test_fuse_validates_the_layer_sequence():

@@ -1,0 +1,175 @@
+"""extras=True of conv2d and max_pool2d (novann/functional.py:383-384,
+533-534): the column matrix, the weight matrix and the pooling window view the
+reference's Conv2d and MaxPool2d layers cache for their backward
+(layers/convolutional/conv2d.py:162-175, layers/pooling/maxpool/
+maxpool2d.py:63-75).  Pure data movement, so every element is compared bit for
+bit with the oracle's restatement (oracle/functional_ref.py: im2col,
+pool_windows), itself pinned against index loops on the CPU."""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from oracle import functional_ref as R
+from novann_amd import functional as F
+from novann_amd import quant
+from novann_amd.module import Parameters, QuantizedParameters
+from tests.gpu_util import to_dev, to_host
+
+pytestmark = pytest.mark.gpu
+
+MODES = ["zeros", "reflect", "replicate", "circular"]
+
+
+def bits(a):
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+GEOS = [  # N, C, H, W, KH, KW, sh, sw, ph, pw
+    (2, 3, 9, 7, 3, 3, 1, 1, 1, 1),
+    (1, 2, 12, 10, 3, 5, 2, 1, 2, 1),
+    (3, 1, 6, 6, 2, 2, 2, 2, 0, 0),
+    (2, 4, 5, 11, 1, 3, 1, 2, 0, 3),    # padding wider than the row in reflect / wrap
+    (1, 5, 13, 13, 5, 5, 2, 2, 4, 4),
+]
+
+
+@pytest.mark.parametrize("mode", MODES)
+@pytest.mark.parametrize("geo", GEOS)
+def test_im2col_bit_exact(geo, mode):
+    N, C, H, W, KH, KW, sh, sw, ph, pw = geo
+    print(f"im2col {geo} {mode}", flush=True)
+    rng = np.random.default_rng(sum(geo))
+    x = rng.standard_normal((N, C, H, W)).astype(np.float32)
+    x.reshape(-1)[::7] = -0.0
+    col = F.im2col(torch.from_numpy(x).cuda(), (KH, KW), (sh, sw), (ph, pw), mode)
+    want, OH, OW = R.im2col(x, KH, KW, (sh, sw), (ph, pw), mode)
+    assert tuple(col.shape) == want.shape == (C * KH * KW, N * OH * OW)
+    assert np.array_equal(bits(col.cpu().numpy()), bits(want))
+
+
+@pytest.mark.parametrize("xt", ["bf16", "f16", "e4m3", "e5m2"])
+def test_im2col_of_narrow_inputs_is_the_decoded_matrix(xt):
+    """A bf16 / f16 device tensor or an FP8 Quantized activation: the column
+    matrix of the values the products read (FP8: dequantized with the scale)."""
+    N, C, H, W, KH, KW = 2, 3, 7, 9, 3, 3
+    rng = np.random.default_rng(5)
+    x = torch.from_numpy(rng.standard_normal((N, C, H, W)).astype(np.float32)).cuda()
+    if xt in ("e4m3", "e5m2"):
+        q = quant.quantize(x, xt)
+        xin, dec = q, quant.dequantize(q).cpu().numpy()
+    else:
+        xin = x.to(torch.bfloat16 if xt == "bf16" else torch.float16)
+        dec = xin.float().cpu().numpy()
+    for mode in MODES:
+        col = F.im2col(xin, (KH, KW), 1, 1, mode)
+        want, _, _ = R.im2col(dec, KH, KW, (1, 1), (1, 1), mode)
+        assert np.array_equal(bits(col.cpu().numpy()), bits(want)), (xt, mode)
+
+
+@pytest.mark.parametrize("wdt", [None, "e4m3", "e2m1"])
+def test_conv2d_extras_numpy_caller(wdt):
+    """numpy in -> (out, col, w_col) as ndarrays, the reference's triple: out
+    equals the extras=False result, col the oracle's column matrix, w_col the
+    weight matrix (a view of fp32 data; s * decode(codes) when quantized)."""
+    N, C, H, W, Co, K = 2, 3, 10, 8, 5, 3
+    rng = np.random.default_rng(11)
+    x = rng.uniform(0, 1, (N, C, H, W)).astype(np.float32)
+    w = (rng.standard_normal((Co, C, K, K)) * 0.3).astype(np.float32)
+    b = Parameters(rng.standard_normal((Co, 1)).astype(np.float32))
+    weight = Parameters(w) if wdt is None else QuantizedParameters.from_float(w, wdt)
+    for mode in MODES:
+        out, col, w_col = F.conv2d(x, weight, K, 1, 1, bias=b, padding_mode=mode, extras=True)
+        assert all(isinstance(a, np.ndarray) for a in (out, col, w_col))
+        plain = F.conv2d(x, weight, K, 1, 1, bias=b, padding_mode=mode)
+        assert np.array_equal(bits(out), bits(plain))
+        want, OH, OW = R.im2col(x, K, K, (1, 1), (1, 1), mode)
+        assert np.array_equal(bits(col), bits(want))
+        assert w_col.shape == (Co, C * K * K)
+        if wdt is None:
+            assert np.shares_memory(w_col, w) and np.array_equal(w_col, w.reshape(Co, -1))
+        else:
+            deq = weight.dequantize().cpu().numpy().reshape(Co, -1)
+            assert np.array_equal(bits(w_col), bits(deq))
+
+
+def test_reference_conv2d_layer_flow_on_the_extras():
+    """Conv2d.forward/backward as the reference writes them
+    (layers/convolutional/conv2d.py:150-207), restated here on the arrays
+    conv2d(extras=True) returned: the cached col and w_col give the weight,
+    bias and input gradients of the oracle's own backward bit for bit (the
+    same numpy operations on bit-equal arrays)."""
+    N, C, H, W, Co, K = 3, 4, 9, 9, 6, 3
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal((N, C, H, W)).astype(np.float32)
+    w = (rng.standard_normal((Co, C, K, K)) * 0.2).astype(np.float32)
+    weight = Parameters(w)
+    for mode, st, pd in [("zeros", 1, 1), ("reflect", 2, 1), ("circular", 1, 2)]:
+        out, col, w_col = F.conv2d(x, weight, K, st, pd, padding_mode=mode, extras=True)
+        grad = rng.standard_normal(out.shape).astype(np.float32)
+        g = grad.transpose(1, 0, 2, 3).reshape(Co, -1)
+        gw = (g @ col.T).reshape(w.shape)
+        gb = np.sum(g, axis=1).reshape(-1, 1)
+        gi = R.col2im(w_col.T @ g, x.shape, K, K, (st, st), (pd, pd))
+        rgi, rgw, rgb = R.conv2d_backward(grad, x, w, (st, st), (pd, pd), mode)
+        assert np.array_equal(bits(gw), bits(rgw))
+        assert np.array_equal(bits(gb), bits(rgb))
+        assert np.array_equal(bits(gi), bits(rgi))
+
+
+def test_config5_conv2_column_matrix_full_size():
+    """config [5]'s conv2 input (256, 32, 28, 28): the 288 x 200704 column
+    matrix (231 MB) the reference materialises, bit for bit."""
+    print("im2col config [5] conv2 (231 MB)", flush=True)
+    rng = np.random.default_rng(55)
+    x = rng.standard_normal((256, 32, 28, 28)).astype(np.float32)
+    col = F.im2col(torch.from_numpy(x).cuda(), 3, 1, 1, "zeros")
+    torch.cuda.synchronize()
+    want, OH, OW = R.im2col(x, 3, 3, (1, 1), (1, 1), "zeros")
+    assert tuple(col.shape) == (288, 256 * 28 * 28)
+    got = to_host(col)
+    assert np.array_equal(got, bits(want))
+
+
+@pytest.mark.parametrize("mode", MODES)
+@pytest.mark.parametrize("kspd", [((2, 2), (2, 2), (0, 0)), ((3, 3), (1, 1), (1, 1)),
+                                  ((3, 2), (2, 1), (2, 1)), ((2, 3), (1, 2), (3, 0))])
+def test_max_pool2d_extras_numpy_caller(kspd, mode):
+    """(out, windows, OH, OW, padded_shape) as the reference returns them; the
+    windows equal the oracle's strided view element for element and the
+    reference's backward mask (windows == windows.max) comes out the same."""
+    k, s, p = kspd
+    rng = np.random.default_rng(sum(k) + sum(s) + sum(p))
+    x = rng.standard_normal((2, 3, 9, 8)).astype(np.float32)
+    x[0, 0, :2, :2] = 0.5          # ties inside a window
+    out, win, OH, OW, pshape = F.max_pool2d(x, k, s, p, padding_mode=mode, extras=True)
+    want, rOH, rOW, rshape = R.pool_windows(x, k, s, p, mode)
+    assert (OH, OW, tuple(pshape)) == (rOH, rOW, tuple(rshape))
+    assert isinstance(win, np.ndarray) and win.shape == want.shape
+    assert np.array_equal(bits(win), bits(want))
+    assert np.array_equal(bits(out), bits(R.max_pool2d(x, k, s, p, mode)))
+    mask = (win == win.max(axis=(4, 5), keepdims=True))
+    assert np.array_equal(mask, want == want.max(axis=(4, 5), keepdims=True))
+
+
+@pytest.mark.parametrize("xt", ["f32", "bf16", "e4m3"])
+def test_max_pool2d_extras_device_caller(xt):
+    """Device input -> a device window view of the padded copy in the input's
+    storage (FP8 Quantized: the codes), equal to the oracle's view of the
+    padded codes."""
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((2, 4, 7, 10)).astype(np.float32)
+    code = {"f32": O.F32, "bf16": O.BF16, "e4m3": O.E4M3}[xt]
+    raw = x.view(np.uint32) if xt == "f32" else O.cast(x.reshape(-1), O.F32, code)
+    dev = to_dev(raw, code).view(x.shape)
+    arg = quant.Quantized(dev.reshape(-1), x.shape, "e4m3",
+                          torch.ones(1, device="cuda")) if xt == "e4m3" else dev
+    for mode in MODES:
+        _, win, OH, OW, pshape = F.max_pool2d(arg, 3, 2, 1, padding_mode=mode, extras=True)
+        assert isinstance(win, torch.Tensor) and win.is_cuda
+        host = np.asarray(raw).reshape(x.shape)
+        want, _, _, rshape = R.pool_windows(host, 3, 2, 1, mode)
+        assert tuple(pshape) == tuple(rshape)
+        ints = {4: torch.int32, 2: torch.int16, 1: torch.uint8}[win.element_size()]
+        got = to_host(win.view(ints).contiguous()).reshape(win.shape)
+        assert np.array_equal(got, want), (xt, mode)

@@ -74,3 +74,29 @@ def test_pad_index_matches_numpy_pad_any_width():
 def test_conv2d_rejects_bad_mode():
     with pytest.raises(ValueError):
         R.im2col(np.zeros((1, 1, 4, 4)), 3, 3, padding_mode="mirror")
+
+
+@pytest.mark.parametrize("mode", ["zeros", "reflect", "replicate", "circular"])
+@pytest.mark.parametrize("case", [(2, 3, 5, 4, 3, 2, 1, 1, 1, 1), (1, 2, 7, 6, 2, 3, 2, 1, 2, 0),
+                                  (3, 1, 4, 4, 1, 1, 1, 2, 0, 0)])
+def test_im2col_and_windows_match_index_loops(mode, case):
+    """The column matrix conv2d(extras=True) returns and max_pool2d's window
+    view, against their definitions written as index loops over np.pad:
+    col[(c, kh, kw), (n, oh, ow)] = xp[n, c, oh*sh + kh, ow*sw + kw] with rows
+    and columns numbered row-major (a transposed or mis-strided view fails)."""
+    N, C, H, W, KH, KW, sh, sw, ph, pw = case
+    x = np.arange(N * C * H * W, dtype=np.float32).reshape(N, C, H, W) * 0.5 - 3.0
+    xp = np.pad(x, ((0, 0), (0, 0), (ph, ph), (pw, pw)), mode=R.NP_PAD[mode])
+    col, OH, OW = R.im2col(x, KH, KW, (sh, sw), (ph, pw), mode)
+    win, OH2, OW2, pshape = R.pool_windows(x, (KH, KW), (sh, sw), (ph, pw), mode)
+    assert (OH2, OW2) == (OH, OW) and pshape == xp.shape
+    assert col.shape == (C * KH * KW, N * OH * OW) and win.shape == (N, C, OH, OW, KH, KW)
+    for c in range(C):
+        for kh in range(KH):
+            for kw in range(KW):
+                for n in range(N):
+                    for oh in range(OH):
+                        for ow in range(OW):
+                            v = xp[n, c, oh * sh + kh, ow * sw + kw]
+                            assert col[(c * KH + kh) * KW + kw, (n * OH + oh) * OW + ow] == v
+                            assert win[n, c, oh, ow, kh, kw] == v

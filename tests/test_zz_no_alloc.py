@@ -75,10 +75,22 @@ def test_noalloc_matches_workspace_entry_point_twice():
 def test_noalloc_refuses_requests_beyond_the_scratch():
     lib = _lib.load()
     # C_out x C*KH*KW fp32 partials per chunk: 512 x 512 x 9 x 4 B x chunks > 32 MiB
-    N, C, Co, K = 64, 512, 512, 3
+    N, C, H, W, Co, K = 64, 512, 8, 8, 512, 3
     assert lib.novaq_conv2d_backward_workspace(N, C, Co, K, K, _lib.E2M1) > 32 << 20
-    fake = 0x10000  # never dereferenced: the call is refused before any launch
-    rc = lib.novaq_conv2d_backward_noalloc(fake, fake, N, C, 8, 8, fake, _lib.E2M1, None, Co, K,
-                                           K, 1, 1, 1, 1, 0, fake, fake, fake, None)
+    # real buffers of the call's sizes (zeros), so that a regression that
+    # launched before the size check would compute garbage, not fault
+    x = torch.zeros((N, C, H, W), device="cuda")
+    g = torch.zeros((N, Co, H, W), device="cuda")
+    wq = torch.zeros(Co * C * K * K // 2, dtype=torch.uint8, device="cuda")
+    gi = torch.full((N, C, H, W), np.nan, device="cuda")
+    gw = torch.full((Co, C, K, K), np.nan, device="cuda")
+    gb = torch.full((Co,), np.nan, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    rc = lib.novaq_conv2d_backward_noalloc(g.data_ptr(), x.data_ptr(), N, C, H, W, wq.data_ptr(),
+                                           _lib.E2M1, None, Co, K, K, 1, 1, 1, 1, 0,
+                                           gi.data_ptr(), gw.data_ptr(), gb.data_ptr(), stream)
+    torch.cuda.synchronize()
     assert rc == _lib.ESCRATCH
     assert b"scratch" in lib.novaq_status_string(_lib.ESCRATCH)
+    # refused before any launch: the outputs are untouched
+    assert torch.isnan(gw).all() and torch.isnan(gb).all() and torch.isnan(gi).all()
