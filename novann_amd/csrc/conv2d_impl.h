@@ -1051,7 +1051,7 @@ struct SmallGeom {
   int vec;      // OW % 4 == 0: whole chunks, vector stores
 };
 
-template <int WT, int XT>
+template <int WT, int XT, bool VEC>
 __global__ __launch_bounds__(256) void conv2d_smallc_kernel(
     const uint8_t* __restrict__ x, const float* __restrict__ x_scale,
     const uint8_t* __restrict__ w, const float* __restrict__ w_scale, Epilogue ep,
@@ -1080,34 +1080,46 @@ __global__ __launch_bounds__(256) void conv2d_smallc_kernel(
                  ? u2f((uint32_t)weight_bf16<WT>(w, wb + (int64_t)cl * g.C * taps + t) << 16)
                  : 0.0f;
   }
-  const int64_t xb = (int64_t)n * g.C * g.H * g.W;
+  // the scale and the bias of the plain store path, loaded before the
+  // barrier so their latency hides behind the staging
+  const bool plain = !ep.mul && !ep.add && !ep.relu && !ep.amax && ep.out_dtype == F32;
+  const float s = product_scale(w_scale, x_scale);
+  float bias[SC_CO];
+#pragma unroll
+  for (int cl = 0; cl < SC_CO; ++cl)
+    bias[cl] = (plain && ep.bias && cl < nco) ? ep.bias[co0 + cl] : 0.0f;
+  const uint8_t* xn = x + (int64_t)n * g.C * g.H * g.W * XL<XT>::bytes;
   const int rows = g.C * g.HP;
-  for (int r0 = 0; r0 < rows; r0 += 8 * SC_SR) {
-    for (int c0 = 0; c0 < g.WS; c0 += 32 * SC_SC) {
-      float v[SC_SR][SC_SC];
+  auto stage_round = [&](int r0, int c0) {
+    float v[SC_SR][SC_SC];
 #pragma unroll
-      for (int i = 0; i < SC_SR; ++i) {
-        const int r = r0 + (threadIdx.x >> 5) + 8 * i;
-        const int c = r / g.HP, hp = r - c * g.HP;
-        const int hi = r < rows ? pad_index(hp - g.ph, g.H, g.pad_mode) : -1;
-        const int64_t rb = xb + ((int64_t)c * g.H + hi) * g.W;
+    for (int i = 0; i < SC_SR; ++i) {
+      const int r = r0 + (threadIdx.x >> 5) + 8 * i;
+      const int c = r / g.HP, hp = r - c * g.HP;
+      const int hi = r < rows ? pad_index(hp - g.ph, g.H, g.pad_mode) : -1;
+      const int rb = (c * g.H + hi) * g.W;
 #pragma unroll
-        for (int j = 0; j < SC_SC; ++j) {
-          const int col = c0 + (threadIdx.x & 31) + 32 * j;
-          const int wi = col < g.WV ? pad_index(col - g.pw, g.W, g.pad_mode) : -1;
-          v[i][j] = (hi >= 0 && wi >= 0) ? x_val<XT>(x, rb + wi) : 0.0f;
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < SC_SR; ++i) {
-        const int r = r0 + (threadIdx.x >> 5) + 8 * i;
-#pragma unroll
-        for (int j = 0; j < SC_SC; ++j) {
-          const int col = c0 + (threadIdx.x & 31) + 32 * j;
-          if (r < rows && col < g.WS) xs[r * g.WP + col] = u2f(enc_bf16(f2u(v[i][j])) << 16);
-        }
+      for (int j = 0; j < SC_SC; ++j) {
+        const int col = c0 + (threadIdx.x & 31) + 32 * j;
+        const int wi = col < g.WV ? pad_index(col - g.pw, g.W, g.pad_mode) : -1;
+        v[i][j] = (hi >= 0 && wi >= 0) ? x_val<XT>(xn, rb + wi) : 0.0f;
       }
     }
+#pragma unroll
+    for (int i = 0; i < SC_SR; ++i) {
+      const int r = r0 + (threadIdx.x >> 5) + 8 * i;
+#pragma unroll
+      for (int j = 0; j < SC_SC; ++j) {
+        const int col = c0 + (threadIdx.x & 31) + 32 * j;
+        if (r < rows && col < g.WS) xs[r * g.WP + col] = u2f(enc_bf16(f2u(v[i][j])) << 16);
+      }
+    }
+  };
+  if (rows <= 8 * SC_SR && g.WS <= 32 * SC_SC) {
+    stage_round(0, 0);  // one round covers the image: straight-line code
+  } else {
+    for (int r0 = 0; r0 < rows; r0 += 8 * SC_SR)
+      for (int c0 = 0; c0 < g.WS; c0 += 32 * SC_SC) stage_round(r0, c0);
   }
 #pragma unroll
   for (int k = 0; k < 2; ++k)
@@ -1119,11 +1131,10 @@ __global__ __launch_bounds__(256) void conv2d_smallc_kernel(
   }
   __syncthreads();
 
-  const float s = product_scale(w_scale, x_scale);
   const float inv_o = epi_inv_scale(ep);
   const float z = epi_relu_factor(ep);
-  const bool plain = !ep.mul && !ep.add && !ep.relu && !ep.amax && ep.out_dtype == F32;
   const int per_plane = g.OH * g.cpr;
+  const int cstep = g.OH * g.OW;  // one output plane (elements)
   uint32_t am = 0;
   for (int p = threadIdx.x; p < per_plane; p += 256) {
     const int oh = p / g.cpr, ow0 = (p - oh * g.cpr) * 4;
@@ -1159,24 +1170,24 @@ __global__ __launch_bounds__(256) void conv2d_smallc_kernel(
       }
     }
     const int64_t e0 = (((int64_t)n * g.C_out + co0) * g.OH + oh) * g.OW + ow0;
-    const int64_t cstep = (int64_t)g.OH * g.OW;
     if (plain) {
       // bias only, fp32 output: acc * s + bias, one 16-byte store per channel
+      // (one lane pointer stepped by a plane)
+      float* dst = reinterpret_cast<float*>(y) + e0;
 #pragma unroll
       for (int cl = 0; cl < SC_CO; ++cl) {
         if (cl >= nco) break;
-        const float b = ep.bias ? ep.bias[co0 + cl] : 0.0f;
         float o[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) o[q] = acc[cl][q] * s + b;
-        float* dst = reinterpret_cast<float*>(y) + e0 + cl * cstep;
-        if (g.vec) {
+        for (int q = 0; q < 4; ++q) o[q] = acc[cl][q] * s + bias[cl];
+        if constexpr (VEC) {
           *reinterpret_cast<float4*>(dst) = make_float4(o[0], o[1], o[2], o[3]);
         } else {
 #pragma unroll
           for (int q = 0; q < 4; ++q)
             if (ow0 + q < g.OW) dst[q] = o[q];
         }
+        dst += cstep;
       }
       continue;
     }
@@ -1194,8 +1205,8 @@ __global__ __launch_bounds__(256) void conv2d_smallc_kernel(
           o[q] = epi_value_nb(k, acc[cl][q], s, z);
           if (ow0 + q < g.OW) am = epi_track(am, o[q]);
         }
-        const int64_t e = e0 + cl * cstep;
-        if (g.vec) {
+        const int64_t e = e0 + (int64_t)cl * cstep;
+        if constexpr (VEC) {
           epi_store4_t<OD>(y, e, o, inv_o);
         } else {
 #pragma unroll
@@ -1238,13 +1249,21 @@ bool launch_smallc(const uint8_t* x, const float* x_scale, const void* w, const 
   g.WP = 4 * g.cpr + 64;
   if (((size_t)g.C * g.HP * g.WP + wts) * sizeof(float) > SC_LDS) g.WP = g.WS;
   const size_t lds = ((size_t)g.C * g.HP * g.WP + wts) * sizeof(float);
-  // (within the default 64 KB of dynamic LDS: no attribute to raise)
-  if (lds > SC_LDS || (int64_t)g.OH * g.cpr * SC_CO > 0x7FFFFFFF) return false;
+  // (within the default 64 KB of dynamic LDS: no attribute to raise); the
+  // image's input offsets and one output plane fit 32-bit indices
+  if (lds > SC_LDS || (int64_t)g.OH * g.cpr * SC_CO > 0x7FFFFFFF ||
+      (int64_t)g.C * g.H * g.W > 0x7FFFFFFF || (int64_t)g.OH * g.OW > 0x7FFFFFFF)
+    return false;
   const int64_t co_groups = (cg.C_out + SC_CO - 1) / SC_CO;
   if (co_groups > 65535) return false;
-  hipLaunchKernelGGL((conv2d_smallc_kernel<WT, XT>), dim3((unsigned)cg.N, (unsigned)co_groups),
-                     dim3(256), lds, stream, x, x_scale, static_cast<const uint8_t*>(w), w_scale,
-                     ep, y, g);
+  if (g.vec)
+    hipLaunchKernelGGL((conv2d_smallc_kernel<WT, XT, true>), dim3((unsigned)cg.N, (unsigned)co_groups),
+                       dim3(256), lds, stream, x, x_scale, static_cast<const uint8_t*>(w), w_scale,
+                       ep, y, g);
+  else
+    hipLaunchKernelGGL((conv2d_smallc_kernel<WT, XT, false>), dim3((unsigned)cg.N, (unsigned)co_groups),
+                       dim3(256), lds, stream, x, x_scale, static_cast<const uint8_t*>(w), w_scale,
+                       ep, y, g);
   *rc = check_launch();
   return true;
 }

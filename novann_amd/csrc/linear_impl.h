@@ -766,7 +766,15 @@ __global__ __launch_bounds__(512, 1) void linear_pingpong_kernel(
   constexpr int WS = FBN * KB;        // W stage: two K halves of 256 rows x 64 bytes
   constexpr int WH = WS / 2;
   constexpr int WOFF = 2 * XS;
-  constexpr int XC = 8;               // x chunks (4 elements) per lane per block
+  // x moves in 16-byte chunks (4 fp32 or 8 16-bit elements): RL lanes cover
+  // a row's 128 K, a pass of the group's 256 lanes 256 / RL rows, and each
+  // lane holds XC chunks of a block (fp32: 32 lanes a row, 8 chunks; 16-bit:
+  // 16 lanes a row, 4 chunks, so half the load and LDS-write instructions)
+  constexpr int EPC = 16 / XB;        // elements per chunk
+  constexpr int RL = KB / EPC;        // lanes per row
+  constexpr int RP = 256 / RL;        // rows per pass
+  constexpr int XC = 64 / RP;         // x chunks per lane per block
+  static_assert(XC % 2 == 0, "x chunks split over the two memory phases");
   __shared__ __attribute__((aligned(16))) uint8_t lds[2 * XS + 2 * WS];
 
   const int T = tiles_m * tiles_n;
@@ -787,12 +795,12 @@ __global__ __launch_bounds__(512, 1) void linear_pingpong_kernel(
   const int gt = tid & 255;
   const int la = lane & 31, h = lane >> 5;
 
-  // x: the group's 64 rows, 8 rows of 4-element chunks per pass of its lanes
+  // x: the group's 64 rows, RP rows of 16-byte chunks per pass of its lanes
   const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint8_t*>(x + (size_t)(m0 + wm) * K * XB), (short)0, 64 * K * XB, 0x00020000);
-  const uint32_t xlane = (uint32_t)((gt >> 5) * K + (gt & 31) * 4) * (uint32_t)XB;
-  const uint32_t xstep = 8u * (uint32_t)K * (uint32_t)XB;
-  const int xw = (wm + (gt >> 5)) * XP + (gt & 31) * 8;
+  const uint32_t xlane = (uint32_t)((gt / RL) * K + (gt % RL) * EPC) * (uint32_t)XB;
+  const uint32_t xstep = (uint32_t)RP * (uint32_t)K * (uint32_t)XB;
+  const int xw = (wm + gt / RL) * XP + (gt % RL) * EPC * 2;
 
   // W: instruction j (= 4 i + q for wave q) of a K half fills LDS slots
   // 64 j + lane: row 16 j + lane / 4, slot lane % 4, holding that row's chunk
@@ -835,21 +843,21 @@ __global__ __launch_bounds__(512, 1) void linear_pingpong_kernel(
   auto fetch_x = [&](u32x4 (&xs)[XC], int kb, const int i0, const int i1) {
     const uint32_t xk = (uint32_t)kb * (KB * XB);
 #pragma unroll
-    for (int i = i0; i < i1; ++i) {
-      if constexpr (XB == 4) {
-        xs[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xlane, xk + i * xstep, 0);
-      } else {
-        const xl_u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(xrs, xlane, xk + i * xstep, 0);
-        xs[i] = u32x4{v[0], v[1], 0u, 0u};
-      }
-    }
+    for (int i = i0; i < i1; ++i)
+      xs[i] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xlane, xk + i * xstep, 0);
   };
   auto stage_x = [&](const u32x4 (&xs)[XC], int slot, const int i0, const int i1) {
     uint8_t* d = lds + slot * XS + xw;
 #pragma unroll
     for (int i = i0; i < i1; ++i) {
-      const xl_u32x2 pr = x4_bf16<XT>(xs[i]);
-      *reinterpret_cast<u32x2*>(d + i * 8 * XP) = u32x2{pr[0], pr[1]};
+      if constexpr (XB == 4) {
+        const xl_u32x2 pr = x4_bf16<XT>(xs[i]);
+        *reinterpret_cast<u32x2*>(d + i * RP * XP) = u32x2{pr[0], pr[1]};
+      } else {
+        const xl_u32x2 lo = x4_bf16<XT>(xs[i]);
+        const xl_u32x2 hi = x4_bf16<XT>(u32x4{xs[i][2], xs[i][3], 0u, 0u});
+        *reinterpret_cast<u32x4*>(d + i * RP * XP) = u32x4{lo[0], lo[1], hi[0], hi[1]};
+      }
     }
   };
   auto copy_w = [&](int kb, int slot, const int hf) {
@@ -931,17 +939,20 @@ __global__ __launch_bounds__(512, 1) void linear_pingpong_kernel(
   // from register set (kb+1) % 2 and that set's loads for block kb+3 issued.
   // Past the last block the last one is copied and staged again into the
   // idle slot, so the loop has no tail.
+  constexpr int XH = XC / 2;  // x chunks staged and loaded per memory phase
   auto mem = [&](u32x4 (&xs)[XC], int kb, const int hf) {
     read_frags(kb, hf);
     if (g == 0) copy_w(min(kb + 1, nb - 1), (kb + 1) & 1, hf);
-    stage_x(xs, (kb + 1) & 1, 4 * hf, 4 * hf + 4);
-    fetch_x(xs, min(kb + 3, nb - 1), 4 * hf, 4 * hf + 4);
+    stage_x(xs, (kb + 1) & 1, XH * hf, XH * hf + XH);
+    fetch_x(xs, min(kb + 3, nb - 1), XH * hf, XH * hf + XH);
   };
   // after a multiply phase: group 0's W copy of the memory phase before it
-  // has landed (4 copies and 4 x loads per memory phase, in that order)
+  // has landed (4 copies and XH x loads per memory phase, in that order: the
+  // last phase's loads and copies and the phase before's x loads may still
+  // be in flight)
   auto wait_copy = [&]() {
     __builtin_amdgcn_sched_barrier(0);
-    asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 + 2 * XH) : "memory");
   };
   auto block = [&](u32x4 (&xs)[XC], int b) {
     mem(xs, b, 0);
@@ -966,7 +977,7 @@ __global__ __launch_bounds__(512, 1) void linear_pingpong_kernel(
   fetch_x(xr[1], min(1, nb - 1), 0, XC);
   fetch_x(xr[0], min(2, nb - 1), 0, XC);
   __builtin_amdgcn_sched_barrier(0);
-  asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * XC) : "memory");  // block 0's W copies
   bar();
   if (g == 1) bar();  // group 1 runs one phase behind
   int b = 0;
