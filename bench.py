@@ -50,7 +50,7 @@ KERNEL_OF = {
     "f32->e5m2 scaled": "cast_kernel<0, 4, 1>", "e5m2->f32 scaled": "cast_kernel<4, 0, 1>",
 }
 FP4_KERNEL = {"pack f32->e2m1": "cast_kernel<0, 5, 1>", "unpack e2m1->f32": "cast_kernel<5, 0, 1>"}
-CONV_KERNEL = {1: "conv2d_smallc_kernel<5, 0>", 32: "conv2d_band_kernel<5, 0, 1, true>"}
+CONV_KERNEL = {1: "conv2d_smallc_kernel<5, 0, true>", 32: "conv2d_band_kernel<5, 0, 1, true>"}
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 
 
@@ -207,6 +207,21 @@ def bench_linear(dev, iters: int = 20, warmup: int = 5):
             wq.scale.data_ptr(), b.data_ptr(), N, None, y.data_ptr(), stream), "linear fp8 x")
     ms8, _ = _time_launches(dev, run8, iters, warmup)
     tf8 = flops / (ms8 * 1e-3) / 1e12
+    # x stored as bf16 (as a fused epilogue writes activations), and config
+    # [4]'s fp32 x cast to bf16 by a separate launch first (both timed)
+    x16 = torch.empty((M, K), dtype=torch.bfloat16, device=dev)
+
+    def cast16():
+        _lib.check(lib.novaq_cast(x.data_ptr(), _lib.F32, x16.data_ptr(), _lib.BF16, M * K, None,
+                                  stream), "cast")
+
+    def run16():
+        _lib.check(lib.novaq_linear_forward_ex(
+            x16.data_ptr(), _lib.BF16, None, M, K, wq.data.data_ptr(), 3, wq.scale.data_ptr(),
+            b.data_ptr(), N, None, y.data_ptr(), stream), "linear bf16 x")
+    cast16()
+    ms16, _ = _time_launches(dev, run16, iters, warmup)
+    mscast, _ = _time_launches(dev, lambda: (cast16(), run16()), iters, warmup)
     return {"metric": "FP8-weight Linear TFLOP/s at 4096^2", "value": round(tflops, 1),
             "unit": "TFLOP/s", "ms": round(ms, 4), "median_ms": round(med, 4),
             "evicted_median_ms": round(emed, 4),
@@ -219,6 +234,13 @@ def bench_linear(dev, iters: int = 20, warmup: int = 5):
                        "frac_bf16_peak": round(tf8 / BF16_PEAK_TFLOPS, 4),
                        "frac_fp8_peak": round(tf8 / FP8_PEAK_TFLOPS, 4),
                        "traffic": measured_traffic("linear_f8_kernel<3, 3>")},
+            "bf16_x": {"what": "x stored as bf16 (a fused epilogue's output): "
+                               "linear_pingpong_kernel<3, 2>, 16-byte x loads",
+                       "ms": round(ms16, 4), "TFLOP/s": round(flops / (ms16 * 1e-3) / 1e12, 1)},
+            "cast_then_bf16_x": {"what": "config [4]'s fp32 x cast to bf16 by novaq_cast, then "
+                                         "the bf16-x product (both launches timed)",
+                                 "ms": round(mscast, 4),
+                                 "TFLOP/s": round(flops / (mscast * 1e-3) / 1e12, 1)},
             "config": {"workload": "BASELINE config [4]", "M": M, "K": K, "N": N,
                        "w_dtype": "e4m3", "mfma": "bf16"},
             "roofline": {"bound": "mfma", "achieved": round(tflops, 1),
@@ -657,6 +679,44 @@ def bench_pool(dev, iters: int = 20, warmup: int = 3):
     return {"workload": "pools on config [5]-sized and main.py activations", "kernels": out}
 
 
+def bench_extras(dev, iters: int = 20, warmup: int = 3):
+    """The arrays conv2d / max_pool2d return with extras=True, materialised on
+    the device: the column matrix of config [5]'s conv2 (x (256, 32, 28, 28)
+    fp32, col 288 x 200704 fp32 = 231 MB) and the padded copy behind the
+    pooling window view of a (256, 64, 28, 28) activation padded by 1.
+    Algorithmic bytes: read x once, write the output once; the MALL is evicted
+    before each launch."""
+    import torch
+
+    from novann_amd import _lib
+    lib = _lib.load()
+    g = torch.Generator(device=dev)
+    g.manual_seed(12)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    out = []
+    x = torch.randn((256, 32, 28, 28), generator=g, device=dev)
+    col = torch.empty((288, 256 * 28 * 28), device=dev)
+    fn = lambda: _lib.check(lib.novaq_im2col(  # noqa: E731
+        x.data_ptr(), _lib.F32, None, 256, 32, 28, 28, 3, 3, 1, 1, 1, 1, 0, col.data_ptr(),
+        stream), "im2col")
+    ms = _timed_flush(dev, fn, iters, warmup)
+    nb = (x.numel() + col.numel()) * 4
+    out.append({"op": "im2col config [5] conv2 (col 288 x 200704 fp32)", "ms": round(ms, 4),
+                "GB/s": round(nb / (ms * 1e-3) / 1e9, 1),
+                "frac": round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "bytes": nb})
+    del col
+    x = torch.randn((256, 64, 28, 28), generator=g, device=dev)
+    xp = torch.empty((256, 64, 30, 30), device=dev)
+    fn = lambda: _lib.check(lib.novaq_pad2d(  # noqa: E731
+        x.data_ptr(), _lib.F32, 256, 64, 28, 28, 1, 1, 0, xp.data_ptr(), stream), "pad2d")
+    ms = _timed_flush(dev, fn, iters, warmup)
+    nb = (x.numel() + xp.numel()) * 4
+    out.append({"op": "pad2d (256,64,28,28) -> (256,64,30,30) f32", "ms": round(ms, 4),
+                "GB/s": round(nb / (ms * 1e-3) / 1e9, 1),
+                "frac": round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "bytes": nb})
+    return {"workload": "extras=True arrays of conv2d / max_pool2d", "kernels": out}
+
+
 def cpu_baseline(sample: int, min_seconds: float = 10.0):
     """The C oracle running the same sweep on a bounded sample (all host cores)."""
     import numpy as np
@@ -784,7 +844,7 @@ def cpu_conv_baseline():
 
 
 LEGS = ("sweep", "linear", "linear_backward", "conv", "conv_backward", "epilogue", "adamw",
-        "pool", "fp4", "cpu")
+        "pool", "extras", "fp4", "cpu")
 
 
 def main() -> int:
@@ -818,7 +878,7 @@ def main() -> int:
     if args.no_linear:
         legs -= {"linear", "linear_backward"}
     if args.no_conv:
-        legs -= {"conv", "conv_backward", "epilogue", "adamw", "pool"}
+        legs -= {"conv", "conv_backward", "epilogue", "adamw", "pool", "extras"}
     if args.no_fp4:
         legs.discard("fp4")
     if args.no_cpu:
@@ -855,7 +915,7 @@ def main() -> int:
     for leg, fn in (("linear", bench_linear), ("linear_backward", bench_linear_backward),
                     ("conv", bench_conv), ("conv_backward", bench_conv_backward),
                     ("epilogue", bench_epilogue), ("adamw", bench_optim),
-                    ("pool", bench_pool), ("fp4", bench_fp4)):
+                    ("pool", bench_pool), ("extras", bench_extras), ("fp4", bench_fp4)):
         run[leg] = fn(dev) if leg in legs else None
         log(f"{leg}: {run[leg]}")
     cpu = None
@@ -886,6 +946,7 @@ def main() -> int:
         "epilogue": run["epilogue"],
         "adamw": run["adamw"],
         "pool": run["pool"],
+        "extras": run["extras"],
         "fp4": run["fp4"],
         "cpu_baseline": cpu,
     }

@@ -763,6 +763,28 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
       const int co = co0 + t * 16 + lr;
       kc[t] = (t < nt_live && co < g.C_out) ? epi_chan(ep, co) : EpiChan{0.0f, 1.0f, -0.0f};
     }
+    if (plain && (npix & 3) == 0 && ((oh0 * g.OW) & 3) == 0 && (P & 3) == 0) {
+      // bias only, fp32 output, every lane's four pixels one aligned 16-byte
+      // run (uniform per band): one lane base pointer, constant steps
+      // (plain stores: the 64-byte pieces of a line written by neighbouring
+      // lanes and waves merge in L2 before they reach HBM)
+      float* ybase = reinterpret_cast<float*>(y) +
+                     (((int64_t)n * g.C_out + co0 + lr) * npix + (int64_t)oh0 * g.OW);
+      const int64_t tstep = 16 * npix;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        if (m >= my_mt) break;
+        const int p = (wave + 4 * m) * 16 + 4 * lg;
+        if (p >= P) continue;
+        float* dm = ybase + p;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          if (t >= nt_live || co0 + t * 16 + lr >= g.C_out) continue;
+          *reinterpret_cast<f32x4*>(dm + t * tstep) = acc[m][t] * s + kc[t].bias;
+        }
+      }
+      return;
+    }
     if (plain) {
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
@@ -773,8 +795,6 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
           const int co = co0 + t * 16 + lr;
           if (t >= nt_live || co >= g.C_out) continue;
           // bias only, fp32 output: one 16-byte store of the four pixels
-          // (plain stores: the 64-byte pieces of a line written by
-          // neighbouring lanes and waves merge in L2 before they reach HBM)
           const int64_t di = ((int64_t)n * g.C_out + co) * npix + (int64_t)oh0 * g.OW + p;
           float* dst = reinterpret_cast<float*>(y) + di;
           const f32x4 v = acc[m][t] * s + kc[t].bias;

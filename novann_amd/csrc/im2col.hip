@@ -21,10 +21,14 @@
 // KH * KW times the input (config [5] conv2: 231 MB written), each input
 // element read KH * KW times from L2.  Each lane makes 4 consecutive outputs
 // and stores them with one vector store; consecutive lanes continue along the
-// output row, so a wave's stores are one contiguous span.
+// output row, so a wave's stores are one contiguous span.  A workgroup covers
+// a span of 1024 columns (elements) and walks a block of consecutive rows
+// (im2col) or a strided set of planes (pad), about 16 workgroups per CU in
+// all.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
 #include <type_traits>
 
 #include "novaq_convert.h"
@@ -38,6 +42,7 @@ constexpr int THREADS = 256;
 constexpr int PER_LANE = 4;
 constexpr int SPAN = THREADS * PER_LANE;  // outputs per workgroup and row
 constexpr int MAX_GRID_Y = 65535;
+constexpr int WG_PER_CU = 16;  // launch size: workgroups per CU (each loops over rows / planes)
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
@@ -48,8 +53,12 @@ struct ColGeom {
   int segs;    // workgroups along a row
 };
 
-// Workgroup (seg, y) writes columns [seg * SPAN, +SPAN) of rows y, y + gridDim.y, ...
-template <int XT>
+// Workgroup (seg, y) writes columns [seg * SPAN, +SPAN) of the y-th block of
+// ceil(rows / gridDim.y) consecutive rows.  A lane's 4 columns fix their
+// (n, oh, ow) for every row, so the window origin and the image offset are
+// worked out once; a row only adds its uniform (c, kh, kw).  ZEROS: the zeros
+// padding mode (an out-of-range tap reads 0), no index folding.
+template <int XT, bool ZEROS>
 __global__ __launch_bounds__(THREADS) void im2col_kernel(const uint8_t* __restrict__ x,
                                                          const float* __restrict__ scale,
                                                          float* __restrict__ col, ColGeom g) {
@@ -59,33 +68,21 @@ __global__ __launch_bounds__(THREADS) void im2col_kernel(const uint8_t* __restri
   if constexpr (is_quant(XT)) {
     if (scale) s = *scale;
   }
-  // column j0 -> (n, oh, ow), the next three by carrying
-  const int q = j0 / g.OW;
-  const int ow0 = j0 - q * g.OW;
-  const int n0 = q / g.OH;
-  const int oh0 = q - n0 * g.OH;
-  const int plane_hw = g.H * g.W;
-  const bool whole = (g.L & 3) == 0 && j0 + PER_LANE <= g.L;
-  for (int r = blockIdx.y; r < g.rows; r += gridDim.y) {
-    const int c = r / (g.KH * g.KW);
-    const int kk = r - c * (g.KH * g.KW);
-    const int kh = kk / g.KW, kw = kk - (kk / g.KW) * g.KW;
-    int n = n0, oh = oh0, ow = ow0;
-    float v[PER_LANE];
+  // columns j0 .. j0 + 3 -> image offset, window origin (row, column)
+  int64_t xoff[PER_LANE];
+  int hb[PER_LANE], wb[PER_LANE];
+  bool live[PER_LANE];
+  {
+    const int q = j0 / g.OW;
+    int ow = j0 - q * g.OW;
+    int n = q / g.OH;
+    int oh = q - n * g.OH;
 #pragma unroll
     for (int e = 0; e < PER_LANE; ++e) {
-      float val = 0.0f;
-      if (j0 + e < g.L) {
-        const int hi = pad_index(oh * g.sh + kh - g.ph, g.H, g.pad_mode);
-        const int wi = pad_index(ow * g.sw + kw - g.pw, g.W, g.pad_mode);
-        if (hi >= 0 && wi >= 0) {
-          const int64_t idx = ((int64_t)n * g.C + c) * plane_hw + (int64_t)hi * g.W + wi;
-          uint32_t bits = decode<XT>(x_code<XT>(x, idx));
-          if constexpr (is_quant(XT)) bits = scale_mul(bits, s);
-          val = u2f(bits);
-        }
-      }
-      v[e] = val;
+      live[e] = j0 + e < g.L;
+      xoff[e] = (int64_t)n * g.C * g.H * g.W;
+      hb[e] = oh * g.sh - g.ph;
+      wb[e] = ow * g.sw - g.pw;
       if (++ow == g.OW) {
         ow = 0;
         if (++oh == g.OH) {
@@ -94,13 +91,46 @@ __global__ __launch_bounds__(THREADS) void im2col_kernel(const uint8_t* __restri
         }
       }
     }
+  }
+  const int plane_hw = g.H * g.W;
+  const int taps = g.KH * g.KW;
+  const bool whole = (g.L & 3) == 0 && j0 + PER_LANE <= g.L;
+  // a contiguous block of rows per workgroup: the KH * KW rows of one input
+  // channel re-read the same input lines, from this CU's L1 / its XCD's L2
+  const int rpw = (g.rows + gridDim.y - 1) / gridDim.y;
+  const int r_end = min(g.rows, (int)(blockIdx.y + 1) * rpw);
+  for (int r = blockIdx.y * rpw; r < r_end; ++r) {
+    const int c = r / taps;
+    const int kk = r - c * taps;
+    const int kh = kk / g.KW, kw = kk - kh * g.KW;
+    const int cbase = c * plane_hw;
+    float v[PER_LANE];
+#pragma unroll
+    for (int e = 0; e < PER_LANE; ++e) {
+      int hi = hb[e] + kh, wi = wb[e] + kw;
+      bool in;
+      if constexpr (ZEROS) {
+        in = (unsigned)hi < (unsigned)g.H && (unsigned)wi < (unsigned)g.W;
+      } else {
+        hi = pad_index(hi, g.H, g.pad_mode);
+        wi = pad_index(wi, g.W, g.pad_mode);
+        in = hi >= 0 && wi >= 0;
+      }
+      float val = 0.0f;
+      if (live[e] && in) {
+        uint32_t bits = decode<XT>(x_code<XT>(x, xoff[e] + (cbase + hi * g.W + wi)));
+        if constexpr (is_quant(XT)) bits = scale_mul(bits, s);
+        val = u2f(bits);
+      }
+      v[e] = val;
+    }
     float* dst = col + (int64_t)r * g.L + j0;
     if (whole) {
       __builtin_nontemporal_store(f32x4{v[0], v[1], v[2], v[3]}, reinterpret_cast<f32x4*>(dst));
     } else {
 #pragma unroll
       for (int e = 0; e < PER_LANE; ++e)
-        if (j0 + e < g.L) dst[e] = v[e];
+        if (live[e]) dst[e] = v[e];
     }
   }
 }
@@ -121,28 +151,30 @@ __global__ __launch_bounds__(THREADS) void pad2d_kernel(const uint8_t* __restric
   const int hw = g.Hp * g.Wp;
   const int i0 = blockIdx.x * SPAN + threadIdx.x * PER_LANE;
   if (i0 >= hw) return;
-  const int hp0 = i0 / g.Wp, wp0 = i0 - hp0 * g.Wp;
-  const T* src = reinterpret_cast<const T*>(x);
-  T* dst = reinterpret_cast<T*>(y);
-  const bool whole = (hw & 3) == 0 && i0 + PER_LANE <= hw;
-  for (int64_t p = blockIdx.y; p < g.planes; p += gridDim.y) {
-    const T* plane = src + p * g.H * g.W;
-    int hp = hp0, wp = wp0;
-    T v[PER_LANE];
+  // the lane's 4 padded positions are the same in every plane: their source
+  // offsets in a plane (-1: the zero pad) are worked out once
+  int soff[PER_LANE];
+  {
+    int hp = i0 / g.Wp, wp = i0 - (i0 / g.Wp) * g.Wp;
 #pragma unroll
     for (int e = 0; e < PER_LANE; ++e) {
-      T val = 0;
-      if (i0 + e < hw) {
-        const int hi = pad_index(hp - g.ph, g.H, g.pad_mode);
-        const int wi = pad_index(wp - g.pw, g.W, g.pad_mode);
-        if (hi >= 0 && wi >= 0) val = plane[hi * g.W + wi];
-      }
-      v[e] = val;
+      const int hi = pad_index(hp - g.ph, g.H, g.pad_mode);
+      const int wi = pad_index(wp - g.pw, g.W, g.pad_mode);
+      soff[e] = (i0 + e < hw && hi >= 0 && wi >= 0) ? hi * g.W + wi : -1;
       if (++wp == g.Wp) {
         wp = 0;
         ++hp;
       }
     }
+  }
+  const T* src = reinterpret_cast<const T*>(x);
+  T* dst = reinterpret_cast<T*>(y);
+  const bool whole = (hw & 3) == 0 && i0 + PER_LANE <= hw;
+  for (int64_t p = blockIdx.y; p < g.planes; p += gridDim.y) {
+    const T* plane = src + p * g.H * g.W;
+    T v[PER_LANE];
+#pragma unroll
+    for (int e = 0; e < PER_LANE; ++e) v[e] = soff[e] >= 0 ? plane[soff[e]] : (T)0;
     T* out = dst + p * hw + i0;
     if (whole) {
       if constexpr (EB == 4) {
@@ -173,23 +205,33 @@ int im2col_launch(const void* x, int x_dtype, const float* x_scale, int64_t N, i
   const int64_t OW = (W + 2 * (int64_t)pw - KW) / sw + 1;
   const int64_t L = N * OH * OW, rows = C * KH * KW;
   // 32-bit column and plane indices; the padded window positions fit int
-  if (L > 0x7FFFFFFF - SPAN || rows > 0x7FFFFFFF || H * W > 0x7FFFFFFF || OH * sh + KH > 0x3FFFFFFF ||
+  if (L > 0x7FFFFFFF - SPAN || rows > 0x7FFFFFFF || C * H * W > 0x7FFFFFFF || OH * sh + KH > 0x3FFFFFFF ||
       OW * sw + KW > 0x3FFFFFFF)
     return NOVAQ_EINVAL;
   if (L == 0) return NOVAQ_OK;
   ColGeom g{(int)C, (int)H, (int)W, KH, KW, sh, sw, ph, pw, pad_mode, (int)OH, (int)OW, (int)L,
             (int)rows, (int)((L + SPAN - 1) / SPAN)};
-  const dim3 grid((unsigned)g.segs, (unsigned)(rows < MAX_GRID_Y ? rows : MAX_GRID_Y));
+  // about WG_PER_CU workgroups per CU, each walking rows (one output row of
+  // SPAN columns is a single 4 KB store per workgroup: too little per launch)
+  const int64_t ry = std::max<int64_t>(1, (int64_t)device_cu_count() * WG_PER_CU / g.segs);
+  const dim3 grid((unsigned)g.segs, (unsigned)std::min<int64_t>(std::min<int64_t>(rows, ry), MAX_GRID_Y));
   const auto* xb = static_cast<const uint8_t*>(x);
+  auto go = [&](auto xt) {
+    constexpr int XT = decltype(xt)::value;
+    if (pad_mode == NOVAQ_PAD_ZEROS)
+      hipLaunchKernelGGL((im2col_kernel<XT, true>), grid, dim3(THREADS), 0, stream, xb, x_scale, col, g);
+    else
+      hipLaunchKernelGGL((im2col_kernel<XT, false>), grid, dim3(THREADS), 0, stream, xb, x_scale, col, g);
+    return check_launch();
+  };
   switch (x_dtype) {
-    case F32: hipLaunchKernelGGL(im2col_kernel<F32>, grid, dim3(THREADS), 0, stream, xb, nullptr, col, g); break;
-    case F16: hipLaunchKernelGGL(im2col_kernel<F16>, grid, dim3(THREADS), 0, stream, xb, nullptr, col, g); break;
-    case BF16: hipLaunchKernelGGL(im2col_kernel<BF16>, grid, dim3(THREADS), 0, stream, xb, nullptr, col, g); break;
-    case E4M3: hipLaunchKernelGGL(im2col_kernel<E4M3>, grid, dim3(THREADS), 0, stream, xb, x_scale, col, g); break;
-    case E5M2: hipLaunchKernelGGL(im2col_kernel<E5M2>, grid, dim3(THREADS), 0, stream, xb, x_scale, col, g); break;
+    case F32: return go(std::integral_constant<int, F32>{});
+    case F16: return go(std::integral_constant<int, F16>{});
+    case BF16: return go(std::integral_constant<int, BF16>{});
+    case E4M3: return go(std::integral_constant<int, E4M3>{});
+    case E5M2: return go(std::integral_constant<int, E5M2>{});
     default: return NOVAQ_EDTYPE;
   }
-  return check_launch();
 }
 
 int pad2d_launch(const void* x, int x_dtype, int64_t N, int64_t C, int64_t H, int64_t W, int ph,
@@ -199,8 +241,10 @@ int pad2d_launch(const void* x, int x_dtype, int64_t N, int64_t C, int64_t H, in
   const int64_t planes = N * C;
   if (planes == 0) return NOVAQ_OK;
   PadGeom g{(int)H, (int)W, ph, pw, pad_mode, (int)Hp, (int)Wp, planes};
-  const dim3 grid((unsigned)((Hp * Wp + SPAN - 1) / SPAN),
-                  (unsigned)(planes < MAX_GRID_Y ? planes : MAX_GRID_Y));
+  const int64_t segs = (Hp * Wp + SPAN - 1) / SPAN;
+  const int64_t py = std::max<int64_t>(1, (int64_t)device_cu_count() * WG_PER_CU / segs);
+  const dim3 grid((unsigned)segs,
+                  (unsigned)std::min<int64_t>(std::min<int64_t>(planes, py), MAX_GRID_Y));
   const auto* xb = static_cast<const uint8_t*>(x);
   auto* yb = static_cast<uint8_t*>(y);
   switch (dtype_bits(x_dtype)) {

@@ -37,6 +37,10 @@
 namespace novaq {
 namespace {
 
+#ifndef POOL_WG_PER_CU
+#define POOL_WG_PER_CU 64
+#endif
+
 struct PoolGeom {
   int64_t N, C;
   int H, W, KH, KW, sh, sw, ph, pw, pad_mode, OH, OW;
@@ -396,7 +400,12 @@ __global__ __launch_bounds__(256) void global_avg_pool2d_wave_kernel(
     } else {
       for (int i = lane; i < n; i += 64) st[i] = elem<XT>(x, e0 + i, s, scaled);
     }
-    __syncthreads();
+    // each wave reads back only the region it staged: a wave-level fence
+    // (its LDS writes complete and visible to its own lanes), no workgroup
+    // barrier, so waves do not wait for one another
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
   // element i of leaf lt of this lane's plane
   auto val = [&](const GapLeaf& lt, int i) {
@@ -452,7 +461,10 @@ __global__ __launch_bounds__(256) void global_avg_pool2d_wave_kernel(
     if (live && rem == 0) y[plane] = (0.0f + v) / (float)hw;
     return;
   }
-  __syncthreads();
+  // the leaf sums of this wave's planes, written by its own lanes
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   if (live && rem == 0) {
     const float* ls = &sums[wave][pi * L];
     float st[GAP_MAX_STACK] = {};  // the plan's tree never needs more
@@ -487,9 +499,9 @@ int launch_max(const void* x, void* y, const PoolGeom& g, hipStream_t stream) {
     const int64_t per = (int64_t)g.OH * ((g.OW + 1) / 2);
     const int64_t items = g.N * g.C * per;
     if (items < ((int64_t)1 << 31)) {
-      // two items per lane per step, about 8 workgroups per CU
+      // two items per lane per step, at most POOL_WG_PER_CU workgroups per CU
       int64_t blocks = (items + 511) / 512;
-      const int64_t cap = (int64_t)device_cu_count() * 8;
+      const int64_t cap = (int64_t)device_cu_count() * POOL_WG_PER_CU;
       if (blocks > cap) blocks = cap;
       if (blocks < 1) blocks = 1;
       const FastDiv dper = fast_div((uint32_t)per), dou = fast_div((uint32_t)((g.OW + 1) / 2));
