@@ -50,7 +50,7 @@ KERNEL_OF = {
     "f32->e5m2 scaled": "cast_kernel<0, 4, 1>", "e5m2->f32 scaled": "cast_kernel<4, 0, 1>",
 }
 FP4_KERNEL = {"pack f32->e2m1": "cast_kernel<0, 5, 1>", "unpack e2m1->f32": "cast_kernel<5, 0, 1>"}
-CONV_KERNEL = {1: "conv2d_smallc_kernel<5, 0, true>", 32: "conv2d_band_kernel<5, 0, 1, true>"}
+CONV_KERNEL = {1: "conv2d_smallc_kernel<5, 0, true, true>", 32: "conv2d_band_kernel<5, 0, 1, true>"}
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 
 

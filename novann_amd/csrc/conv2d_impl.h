@@ -1071,7 +1071,9 @@ struct SmallGeom {
   int vec;      // OW % 4 == 0: whole chunks, vector stores
 };
 
-template <int WT, int XT, bool VEC>
+// F3: a 3 x 3 window with zeros padding (config [5]'s conv1), its loops and
+// padding tests fixed at compile time; other windows and modes take F3 = false.
+template <int WT, int XT, bool VEC, bool F3>
 __global__ __launch_bounds__(256) void conv2d_smallc_kernel(
     const uint8_t* __restrict__ x, const float* __restrict__ x_scale,
     const uint8_t* __restrict__ w, const float* __restrict__ w_scale, Epilogue ep,
@@ -1081,7 +1083,8 @@ __global__ __launch_bounds__(256) void conv2d_smallc_kernel(
   const int co0 = blockIdx.y * SC_CO;
   const int nco = min(SC_CO, g.C_out - co0);
   const int plane = g.HP * g.WP;
-  const int taps = g.KH * g.KW;
+  const int KH = F3 ? 3 : g.KH, KW = F3 ? 3 : g.KW;
+  const int taps = KH * KW;
   float* xs = sc_lds;                          // C planes of HP x WP
   float* ws = sc_lds + g.C * plane;            // C*KH*KW taps x SC_CO channels
   // stage the weights and the padded planes: every load of a round is issued
@@ -1116,12 +1119,20 @@ __global__ __launch_bounds__(256) void conv2d_smallc_kernel(
     for (int i = 0; i < SC_SR; ++i) {
       const int r = r0 + (threadIdx.x >> 5) + 8 * i;
       const int c = r / g.HP, hp = r - c * g.HP;
-      const int hi = r < rows ? pad_index(hp - g.ph, g.H, g.pad_mode) : -1;
+      int hi = -1;
+      if (r < rows) {
+        if constexpr (F3) hi = (unsigned)(hp - g.ph) < (unsigned)g.H ? hp - g.ph : -1;
+        else hi = pad_index(hp - g.ph, g.H, g.pad_mode);
+      }
       const int rb = (c * g.H + hi) * g.W;
 #pragma unroll
       for (int j = 0; j < SC_SC; ++j) {
         const int col = c0 + (threadIdx.x & 31) + 32 * j;
-        const int wi = col < g.WV ? pad_index(col - g.pw, g.W, g.pad_mode) : -1;
+        int wi = -1;
+        if (col < g.WV) {
+          if constexpr (F3) wi = (unsigned)(col - g.pw) < (unsigned)g.W ? col - g.pw : -1;
+          else wi = pad_index(col - g.pw, g.W, g.pad_mode);
+        }
         v[i][j] = (hi >= 0 && wi >= 0) ? x_val<XT>(xn, rb + wi) : 0.0f;
       }
     }
@@ -1164,7 +1175,7 @@ __global__ __launch_bounds__(256) void conv2d_smallc_kernel(
 #pragma unroll
       for (int q = 0; q < 4; ++q) acc[cl][q] = 0.0f;
     for (int c = 0; c < g.C; ++c) {
-      for (int kh = 0; kh < g.KH; ++kh) {
+      for (int kh = 0; kh < KH; ++kh) {
         const float4* row =
             reinterpret_cast<const float4*>(xs + (c * g.HP + oh + kh) * g.WP + ow0);
         float v[12];
@@ -1173,10 +1184,10 @@ __global__ __launch_bounds__(256) void conv2d_smallc_kernel(
           const float4 f = row[q];
           v[4 * q] = f.x; v[4 * q + 1] = f.y; v[4 * q + 2] = f.z; v[4 * q + 3] = f.w;
         }
-        const float4* wk = reinterpret_cast<const float4*>(ws + (c * g.KH + kh) * g.KW * SC_CO);
+        const float4* wk = reinterpret_cast<const float4*>(ws + (c * KH + kh) * KW * SC_CO);
 #pragma unroll
         for (int kw = 0; kw < SC_MAX_K; ++kw) {
-          if (kw < g.KW) {
+          if (kw < KW) {
             const float4 wa = wk[2 * kw], wbv = wk[2 * kw + 1];
             const float wv[SC_CO] = {wa.x, wa.y, wa.z, wa.w, wbv.x, wbv.y, wbv.z, wbv.w};
             // a bf16 x bf16 product is exact in fp32, so the fused
@@ -1276,14 +1287,18 @@ bool launch_smallc(const uint8_t* x, const float* x_scale, const void* w, const 
     return false;
   const int64_t co_groups = (cg.C_out + SC_CO - 1) / SC_CO;
   if (co_groups > 65535) return false;
-  if (g.vec)
-    hipLaunchKernelGGL((conv2d_smallc_kernel<WT, XT, true>), dim3((unsigned)cg.N, (unsigned)co_groups),
-                       dim3(256), lds, stream, x, x_scale, static_cast<const uint8_t*>(w), w_scale,
-                       ep, y, g);
+  const dim3 grid((unsigned)cg.N, (unsigned)co_groups);
+  const auto* wq = static_cast<const uint8_t*>(w);
+  const bool f3 = cg.KH == 3 && cg.KW == 3 && cg.pad_mode == NOVAQ_PAD_ZEROS;
+  if (g.vec && f3)
+    hipLaunchKernelGGL((conv2d_smallc_kernel<WT, XT, true, true>), grid, dim3(256), lds, stream, x,
+                       x_scale, wq, w_scale, ep, y, g);
+  else if (g.vec)
+    hipLaunchKernelGGL((conv2d_smallc_kernel<WT, XT, true, false>), grid, dim3(256), lds, stream, x,
+                       x_scale, wq, w_scale, ep, y, g);
   else
-    hipLaunchKernelGGL((conv2d_smallc_kernel<WT, XT, false>), dim3((unsigned)cg.N, (unsigned)co_groups),
-                       dim3(256), lds, stream, x, x_scale, static_cast<const uint8_t*>(w), w_scale,
-                       ep, y, g);
+    hipLaunchKernelGGL((conv2d_smallc_kernel<WT, XT, false, false>), grid, dim3(256), lds, stream, x,
+                       x_scale, wq, w_scale, ep, y, g);
   *rc = check_launch();
   return true;
 }
