@@ -882,16 +882,21 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
         }
       }
       __syncthreads();
+      // wave w copies channel rows w, w + 4, ...: its lanes take consecutive
+      // store units of the row, the row pointer steps by four planes
       const int live = min(CO_TILE, g.C_out - co0);
       const int per_row = rowb / SU;
-      uint8_t* yb = reinterpret_cast<uint8_t*>(y) +
-                    (((int64_t)n * g.C_out + co0) * npix + (int64_t)oh0 * g.OW) * ES;
-      for (int u = tid; u < live * per_row; u += THREADS) {
-        const int cl = u / per_row, o = (u - cl * per_row) * SU;
-        const uint8_t* sp = ol + cl * rowb + o;
-        uint8_t* dp = yb + (int64_t)cl * npix * ES + o;
-        if constexpr (SU == 8) *reinterpret_cast<u32x2v*>(dp) = *reinterpret_cast<const u32x2v*>(sp);
-        else *reinterpret_cast<uint32_t*>(dp) = *reinterpret_cast<const uint32_t*>(sp);
+      const int64_t cstep = 4 * npix * ES;
+      uint8_t* dr = reinterpret_cast<uint8_t*>(y) +
+                    (((int64_t)n * g.C_out + co0 + wave) * npix + (int64_t)oh0 * g.OW) * ES;
+      for (int cl = wave; cl < live; cl += 4, dr += cstep) {
+        const uint8_t* sr = ol + cl * rowb;
+        for (int o = lane; o < per_row; o += 64) {
+          if constexpr (SU == 8)
+            *reinterpret_cast<u32x2v*>(dr + o * SU) = *reinterpret_cast<const u32x2v*>(sr + o * SU);
+          else
+            *reinterpret_cast<uint32_t*>(dr + o * SU) = *reinterpret_cast<const uint32_t*>(sr + o * SU);
+        }
       }
     };
     if (g.ostage) {
