@@ -214,3 +214,21 @@ def test_optimizer_and_pool_validation():
     assert gap(FAKE, _lib.E2M1, None, 2, 3, 4, 4, FAKE, None) == _lib.EDTYPE
     assert gap(FAKE, _lib.F32, None, 2, 0, 4, 4, FAKE, None) == _lib.EINVAL
     assert gap(FAKE, _lib.F32, None, 0, 3, 4, 4, FAKE, None) == _lib.OK
+    # the plane loads are 4-element vectors: x must be 16-byte aligned
+    assert gap(FAKE + 4, _lib.F32, None, 2, 3, 4, 4, FAKE, None) == _lib.EALIGN
+    assert gap(FAKE, _lib.F32, None, 2, 3, 4, 4, FAKE + 2, None) == _lib.EALIGN
+    # extras: element-aligned x, 16-byte aligned outputs; bad dtype / mode / scale
+    im = lib.novaq_im2col
+    assert im(FAKE, _lib.E2M1, None, 1, 1, 4, 4, 3, 3, 1, 1, 1, 1, 0, FAKE, None) == _lib.EDTYPE
+    assert im(FAKE, _lib.F32, FAKE, 1, 1, 4, 4, 3, 3, 1, 1, 1, 1, 0, FAKE, None) == _lib.EDTYPE
+    assert im(FAKE, _lib.F32, None, 1, 1, 4, 4, 3, 3, 1, 1, 1, 1, 7, FAKE, None) == _lib.EPADMODE
+    assert im(FAKE, _lib.F32, None, 1, 1, 2, 2, 5, 5, 1, 1, 0, 0, 0, FAKE, None) == _lib.ESHAPE
+    assert im(FAKE + 2, _lib.F32, None, 1, 1, 4, 4, 3, 3, 1, 1, 1, 1, 0, FAKE, None) == _lib.EALIGN
+    assert im(FAKE, _lib.F32, None, 1, 1, 4, 4, 3, 3, 1, 1, 1, 1, 0, FAKE + 4, None) == _lib.EALIGN
+    assert im(None, _lib.F32, None, 0, 1, 4, 4, 3, 3, 1, 1, 1, 1, 0, None, None) == _lib.OK
+    pad = lib.novaq_pad2d
+    assert pad(FAKE, _lib.E2M1, 1, 1, 4, 4, 1, 1, 0, FAKE, None) == _lib.EDTYPE
+    assert pad(FAKE, _lib.F32, 1, 1, 4, 4, 1, 1, 9, FAKE, None) == _lib.EPADMODE
+    assert pad(FAKE, _lib.F32, 1, 1, 4, 4, -1, 1, 0, FAKE, None) == _lib.EINVAL
+    assert pad(FAKE + 1, _lib.BF16, 1, 1, 4, 4, 1, 1, 0, FAKE, None) == _lib.EALIGN
+    assert pad(FAKE, _lib.F32, 1, 1, 4, 4, 1, 1, 0, FAKE + 8, None) == _lib.EALIGN

@@ -150,6 +150,31 @@ def test_avg_pool2d_known_answer_and_narrow_input():
     assert np.array_equal(got.cpu().numpy().view(np.uint32), R.avg_pool2d(deq).view(np.uint32))
 
 
+@pytest.mark.parametrize("xt,off", [("f32", 1), ("f32", 3), ("bf16", 2), ("e4m3", 5)])
+def test_avg_pool2d_offset_views(xt, off):
+    """x as a view some elements into a larger buffer: the C ABI refuses it
+    (NOVAQ_EALIGN: the plane loads are 4-element vectors), the host layer
+    copies it to an aligned buffer and returns the same bits as the aligned
+    call."""
+    print(f"avg_pool2d view {xt} +{off}", flush=True)
+    rng = np.random.default_rng(off)
+    shape = (3, 5, 6, 7)
+    n = int(np.prod(shape))
+    v = rng.standard_normal(n + off).astype(np.float32)
+    codes = v.view(np.uint32) if xt == "f32" else O.cast(v, O.F32, CODE[xt])
+    buf = to_dev(codes, CODE[xt])
+    view = buf[off:off + n]
+    y = torch.empty(shape[:2], device="cuda")
+    rc = _lib.load().novaq_global_avg_pool2d(view.data_ptr(), CODE[xt], None, *shape,
+                                             y.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    assert rc == _lib.EALIGN
+    scale = torch.ones(1, device="cuda")
+    arg = quant.Quantized(view, shape, xt, scale) if xt == "e4m3" else view.view(shape)
+    got = F.avg_pool2d(arg).cpu().numpy()
+    dec = O.cast(codes[off:], CODE[xt], O.F32, n=n).reshape(shape)
+    assert np.array_equal(got.view(np.uint32), R.avg_pool2d(dec).view(np.uint32))
+
+
 def test_layers_like_reference():
     """test_maxpooling2d.py:10-27 and test_gap2d.py:10-17 on the layers."""
     rng = np.random.RandomState(8)
