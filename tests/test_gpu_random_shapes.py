@@ -182,3 +182,56 @@ def test_fused_epilogues_random_geometries(seed):
         wd, ws, _ = TE.quantized_codes(w, wdt, rng)
         run = lambda ep: TE.linear_ex(x, wd, wdt, ws, D_out, ep, bias)  # noqa: E731
         TE.check_all_outputs(run, run(None), D_out, rng)
+
+
+def extras_case(rng):
+    while True:
+        N = int(rng.integers(1, 4))
+        C = int(rng.integers(1, 9))
+        H, W = int(rng.integers(1, 33)), int(rng.integers(1, 33))
+        KH, KW = int(rng.integers(1, 6)), int(rng.integers(1, 6))
+        sh, sw = int(rng.integers(1, 4)), int(rng.integers(1, 4))
+        ph, pw = int(rng.integers(0, 6)), int(rng.integers(0, 6))
+        mode = str(rng.choice(MODES))
+        if H + 2 * ph < KH or W + 2 * pw < KW:
+            continue
+        xt = str(rng.choice(["f32", "f32", "bf16", "e4m3"]))
+        return N, C, H, W, KH, KW, sh, sw, ph, pw, mode, xt
+
+
+@pytest.mark.parametrize("seed", SEEDS)
+def test_extras_random_geometries(seed):
+    """The column matrix and the pooling window view (extras=True) over random
+    geometries, padding wider than the image included (numpy.pad's rules),
+    for fp32, bf16 and scaled E4M3 inputs: bit-equal to the oracle's
+    restatement of the reference's as_strided windows on the decoded input."""
+    from novann_amd import quant
+    rng = np.random.default_rng(seed + 100)
+    for i in range(40):
+        case = extras_case(rng)
+        N, C, H, W, KH, KW, sh, sw, ph, pw, mode, xt = case
+        print(f"extras seed {seed} case {i}: {case}", flush=True)
+        x = rng.standard_normal((N, C, H, W)).astype(np.float32)
+        xd = torch.from_numpy(x).cuda()
+        if xt == "bf16":
+            arg = xd.to(torch.bfloat16)
+            dec = arg.float().cpu().numpy()
+        elif xt == "e4m3":
+            arg = quant.quantize(xd, "e4m3")
+            dec = quant.dequantize(arg).cpu().numpy()
+        else:
+            arg, dec = xd, x
+        col = F.im2col(arg, (KH, KW), (sh, sw), (ph, pw), mode)
+        want, OH, OW = R.im2col(dec, KH, KW, (sh, sw), (ph, pw), mode)
+        assert np.array_equal(col.cpu().numpy().view(np.uint32), want.view(np.uint32)), case
+        _, win, OH2, OW2, pshape = F.max_pool2d(arg, (KH, KW), (sh, sw), (ph, pw),
+                                                padding_mode=mode, extras=True)
+        assert (OH2, OW2, tuple(pshape)) == (OH, OW, (N, C, H + 2 * ph, W + 2 * pw)), case
+        wv = win.float() if xt == "bf16" else win
+        if xt == "e4m3":  # the view holds codes: decode them with the scale
+            flat = quant.dequantize(quant.Quantized(win.contiguous().reshape(-1), win.shape, "e4m3",
+                                                    arg.scale))
+            wv = flat.reshape(win.shape)
+        wwant, _, _, _ = R.pool_windows(dec, (KH, KW), (sh, sw), (ph, pw), mode)
+        got = wv.contiguous().cpu().numpy()
+        assert np.array_equal(got.view(np.uint32), np.ascontiguousarray(wwant).view(np.uint32)), case
