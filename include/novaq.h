@@ -217,7 +217,7 @@ int novaq_max_pool2d(const void *x, int x_dtype, int64_t N, int64_t C, int64_t H
                      void *stream);
 
 /* y[n, c] = mean over H, W of x[n, c] (x_dtype as above, times x_scale for
- * FP8 when given), fp32, evaluated as numpy's np.mean does on float32: 0 plus
+ * FP8 when given; a scale with another dtype is NOVAQ_EDTYPE), fp32, evaluated as numpy's np.mean does on float32: 0 plus
  * numpy's pairwise sums of the plane's 8192-element blocks (its ufunc buffer
  * size), divided by H*W, so bit for bit equal.
  * Replaces: novann.functional.avg_pool2d (novann/functional.py:548-559),

@@ -279,6 +279,7 @@ int novaq_max_pool2d(const void* x, int x_dtype, int64_t N, int64_t C, int64_t H
 int novaq_global_avg_pool2d(const void* x, int x_dtype, const float* x_scale, int64_t N,
                             int64_t C, int64_t H, int64_t W, float* y, void* stream) {
   if (!valid_dtype(x_dtype) || x_dtype == E2M1) return NOVAQ_EDTYPE;
+  if (x_scale && !is_quant(x_dtype)) return NOVAQ_EDTYPE;  // a scale belongs to FP8 codes
   if (N < 0 || C <= 0 || H <= 0 || W <= 0) return NOVAQ_EINVAL;
   if (N == 0) return NOVAQ_OK;
   if (!x || !y) return NOVAQ_EINVAL;

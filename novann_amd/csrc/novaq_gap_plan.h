@@ -66,6 +66,14 @@ inline void depth_range(int n, int depth, int& lo, int& hi) {
   depth_range(n2, depth + 1, lo, hi);
   depth_range(n - n2, depth + 1, lo, hi);
 }
+// the length of the longest (longest = true) or shortest leaf
+inline int leaf_len(int n, bool longest) {
+  if (n <= 128) return n;
+  int n2 = n / 2;
+  n2 -= n2 % 8;
+  const int a = leaf_len(n2, longest), b = leaf_len(n - n2, longest);
+  return (a > b) == longest ? a : b;
+}
 }  // namespace gap_detail
 
 // Fills p for a plane of n elements (1 <= n).  Returns false, leaving p

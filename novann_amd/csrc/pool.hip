@@ -29,6 +29,8 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "novaq_convert.h"
 #include "novaq_gap_plan.h"
 #include "novaq_internal.h"
@@ -530,6 +532,139 @@ __global__ __launch_bounds__(256) void global_avg_pool2d_wave_kernel(
   }
 }
 
+// --- global average, every load issued at once (planes of at most 8192) ----
+//
+// The same leaves and the same tree as the wave kernel, with no staging and
+// no plan table.  The tree is made complete: D is its deepest level, each of
+// the 2^D virtual leaves either is a real leaf (a leaf at depth d < D owns the
+// first of the 2^(D-d) virtual leaves below it) or holds -0.0f, the exact
+// additive identity, so adding neighbours level by level (D levels of
+// shuffles) associates exactly as numpy's recursion.  A lane finds its leaf
+// by walking the D levels from the root with the bits of its virtual leaf
+// index.  Each virtual leaf has 8/Q lanes; lane h of a leaf loads elements
+// h*Q .. h*Q+Q-1 of every whole group of 8 with one Q-element vector load
+// (Q chosen by the host so that every such load is aligned) and keeps Q of
+// the 8 interleaved partial sums; the partials are added pairwise in the lane
+// and shuffles finish ((r0+r1)+(r2+r3))+((r4+r5)+(r6+r7)); the leaf's first
+// lane adds the remainder in order.  W = (8/Q) * 2^D <= 64 lanes per plane,
+// 64/W planes per wave.  The loads are buffer loads through a descriptor
+// over the workgroup's planes: every lane issues the same NG loads (NG = 8
+// or 16, at least the longest leaf's group count), with no branch, so all of
+// them are in flight before the first add and each add waits only for its
+// own load.  Load k of a lane whose leaf has ng <= k groups (and every load of
+// a lane that owns no leaf) gets a vector offset past the descriptor's range
+// and returns +0 without a memory access; the lane adds it like the others:
+// adding +0 changes at most the sign of a zero partial sum, and zeros of
+// either sign leave every non-zero sum as it is and give the same final
+// 0 + sum.  This kernel is issue-bound as much as HBM-bound, so each element
+// costs one add (plus its decode, and SCALED's multiply).
+template <int XT, int Q>
+__device__ __forceinline__ xl_u32x4 bload_q(__amdgpu_buffer_rsrc_t rs, uint32_t off,
+                                            uint32_t soff = 0) {
+  constexpr int BYTES = Q * XL<XT>::bits / 8;
+  xl_u32x4 r = {0u, 0u, 0u, 0u};
+  if constexpr (BYTES == 16) {
+    r = __builtin_amdgcn_raw_buffer_load_b128(rs, off, soff, 0);
+  } else if constexpr (BYTES == 8) {
+    const xl_u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rs, off, soff, 0);
+    r[0] = v[0];
+    r[1] = v[1];
+  } else if constexpr (BYTES == 4) {
+    r[0] = __builtin_amdgcn_raw_buffer_load_b32(rs, off, soff, 0);
+  } else if constexpr (BYTES == 2) {
+    r[0] = __builtin_amdgcn_raw_buffer_load_b16(rs, off, soff, 0);
+  } else {
+    r[0] = __builtin_amdgcn_raw_buffer_load_b8(rs, off, soff, 0);
+  }
+  return r;
+}
+
+constexpr uint32_t GAP_OOB = 0x40000000u;  // a vector offset past any descriptor's range (<= 8 MiB)
+
+template <int XT, int Q, bool SCALED, int NG>
+__global__ __launch_bounds__(256) void global_avg_pool2d_tree_kernel(
+    const uint8_t* __restrict__ x, const float* __restrict__ x_scale, float* __restrict__ y,
+    int64_t planes, int hw, int D, int wshift) {
+  constexpr int B = XL<XT>::bits, EB = B / 8;
+  constexpr int LPL = 8 / Q;  // lanes per leaf
+  constexpr int LSH = LPL == 8 ? 3 : LPL == 4 ? 2 : LPL == 2 ? 1 : 0;
+  const int ppb = 256 >> wshift;  // planes per workgroup
+  const int64_t p0 = (int64_t)blockIdx.x * ppb;
+  const int lp = threadIdx.x >> wshift;
+  const int l = threadIdx.x & ((1 << wshift) - 1);
+  const int vi = l >> LSH, h = l & (LPL - 1);
+  const int W = 1 << wshift;
+  const int64_t left = planes - p0;
+  const int nplanes = left < ppb ? (int)left : ppb;
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(x + p0 * hw * EB), (short)0, nplanes * hw * EB, 0x00020000);
+  const float s = SCALED ? *x_scale : 1.0f;
+  // the leaf of virtual leaf vi
+  bool owner = lp < nplanes;
+  int off = 0, len = hw;
+  for (int lvl = D - 1; lvl >= 0; --lvl) {
+    const int bit = (vi >> lvl) & 1;
+    if (len > 128) {
+      const int n2 = (len >> 1) & ~7;
+      off = bit ? off + n2 : off;
+      len = bit ? len - n2 : n2;
+    } else if (bit) {
+      owner = false;
+    }
+  }
+  const int ng = owner ? len >> 3 : 0;
+  const int nr = owner && h == 0 ? len & 7 : 0;
+  const uint32_t lb = (uint32_t)(lp * hw + off) * EB;  // the leaf's first byte
+  const uint32_t lq = lb + (uint32_t)(h * Q * EB);
+  // every address first, then the NG loads back to back: interleaving the
+  // address arithmetic with the loads measured 20% slower
+  uint32_t ad[NG];
+#pragma unroll
+  for (int k = 0; k < NG; ++k) ad[k] = (k < ng ? lq : GAP_OOB) + 8 * k * EB;
+  __builtin_amdgcn_sched_barrier(0);
+  xl_u32x4 v[NG];
+#pragma unroll
+  for (int k = 0; k < NG; ++k) v[k] = bload_q<XT, Q>(rs, ad[k]);
+  __builtin_amdgcn_sched_barrier(0);
+  float tail[7] = {};
+  if (hw & 7) {  // only then has a leaf a remainder
+#pragma unroll
+    for (int q = 0; q < 7; ++q) {
+      const float f =
+          u2f(decode<XT>(bload_q<XT, 1>(rs, q < nr ? lb + (uint32_t)((8 * ng + q) * EB) : GAP_OOB)[0]));
+      tail[q] = SCALED ? f * s : f;
+    }
+  }
+  auto val = [&](const xl_u32x4& r, int q) {
+    const uint32_t c =
+        B == 32 ? r[q] : (r[(q * B) / 32] >> ((q * B) % 32)) & ((1u << (B & 31)) - 1u);
+    const float f = u2f(decode<XT>(c));
+    return SCALED ? f * s : f;
+  };
+  float r[Q];
+#pragma unroll
+  for (int q = 0; q < Q; ++q) r[q] = val(v[0], q);
+#pragma unroll
+  for (int k = 1; k < NG; ++k)
+#pragma unroll
+    for (int q = 0; q < Q; ++q) r[q] += val(v[k], q);
+  // partials h*Q .. h*Q+Q-1 pairwise, neighbours first, then the other lanes'
+#pragma unroll
+  for (int w = 1; w < Q; w <<= 1)
+#pragma unroll
+    for (int q = 0; q < Q; q += 2 * w) r[q] = r[q] + r[q + w];
+  float c = r[0];
+#pragma unroll
+  for (int d = 1; d < LPL; d <<= 1) c = c + __shfl_down(c, d, W);
+  float res = ng > 0 ? c : 0.0f;  // below 8 elements: 0 plus the elements in order
+#pragma unroll
+  for (int q = 0; q < 7; ++q)
+    if (q < nr) res += tail[q];
+  if (!owner) res = -0.0f;
+  for (int lvl = 0; lvl < D; ++lvl) res = res + __shfl_down(res, LPL << lvl, W);
+  if (l == 0 && lp < nplanes) y[p0 + lp] = (0.0f + res) / (float)hw;
+}
+
 template <int XT>
 int launch_max(const void* x, void* y, const PoolGeom& g, hipStream_t stream) {
   const int64_t npix = (int64_t)g.OH * g.OW;
@@ -580,6 +715,44 @@ int launch_max(const void* x, void* y, const PoolGeom& g, hipStream_t stream) {
 template <int XT>
 int launch_gap(const void* x, const float* x_scale, float* y, int64_t planes, int64_t hw,
                hipStream_t stream) {
+  if (hw <= NP_BUFSIZE) {
+    // the widest Q-element vector (Q * bytes <= 16) that every plane's, leaf's
+    // and group's start keeps aligned, then W = (8/Q) * 2^D lanes per plane
+    constexpr int EB = XL<XT>::bits / 8;
+    int lo = 1 << 30, D = -1;
+    gap_detail::depth_range((int)hw, 0, lo, D);
+    int Q = 16 / EB < 8 ? 16 / EB : 8;
+    while (Q > 1 && (hw % Q != 0 || reinterpret_cast<uintptr_t>(x) % ((uintptr_t)Q * EB) != 0))
+      Q >>= 1;
+    int wshift = D;
+    for (int lpl = 8 / Q; lpl > 1; lpl >>= 1) ++wshift;
+    if (wshift <= 6) {
+      const int64_t blocks = ((planes << wshift) + 255) / 256;
+      if (blocks > 0x7FFFFFFF || planes > ((int64_t)1 << 40)) return NOVAQ_EINVAL;
+      const int ngmax = gap_detail::leaf_len((int)hw, true) >> 3;
+      const bool sc = is_quant(XT) && x_scale != nullptr;  // the C ABI refuses other scales
+      using Kern = decltype(&global_avg_pool2d_tree_kernel<XT, 1, false, 16>);
+      Kern kern = nullptr;
+      auto choose = [&](auto qc) {
+        constexpr int QC = decltype(qc)::value;
+        if (Q != QC) return;
+        if (ngmax <= 8)
+          kern = sc ? global_avg_pool2d_tree_kernel<XT, QC, is_quant(XT), 8>
+                    : global_avg_pool2d_tree_kernel<XT, QC, false, 8>;
+        else
+          kern = sc ? global_avg_pool2d_tree_kernel<XT, QC, is_quant(XT), 16>
+                    : global_avg_pool2d_tree_kernel<XT, QC, false, 16>;
+      };
+      choose(std::integral_constant<int, 1>{});
+      choose(std::integral_constant<int, 2>{});
+      choose(std::integral_constant<int, 4>{});
+      if constexpr (EB < 4) choose(std::integral_constant<int, 8>{});
+      if (!kern) return NOVAQ_EINVAL;
+      hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), 0, stream,
+                         static_cast<const uint8_t*>(x), x_scale, y, planes, (int)hw, D, wshift);
+      return check_launch();
+    }
+  }
   GapPlan plan;
   if (hw <= NP_BUFSIZE && gap_plan((int)hw, plan)) {
     const int leaves = plan.L;

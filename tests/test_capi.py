@@ -214,6 +214,9 @@ def test_optimizer_and_pool_validation():
     assert gap(FAKE, _lib.E2M1, None, 2, 3, 4, 4, FAKE, None) == _lib.EDTYPE
     assert gap(FAKE, _lib.F32, None, 2, 0, 4, 4, FAKE, None) == _lib.EINVAL
     assert gap(FAKE, _lib.F32, None, 0, 3, 4, 4, FAKE, None) == _lib.OK
+    # a scale goes with FP8 codes only
+    assert gap(FAKE, _lib.BF16, FAKE, 2, 3, 4, 4, FAKE, None) == _lib.EDTYPE
+    assert gap(FAKE, _lib.F32, FAKE, 2, 3, 4, 4, FAKE, None) == _lib.EDTYPE
     # the plane loads are 4-element vectors: x must be 16-byte aligned
     assert gap(FAKE + 4, _lib.F32, None, 2, 3, 4, 4, FAKE, None) == _lib.EALIGN
     assert gap(FAKE, _lib.F32, None, 2, 3, 4, 4, FAKE + 2, None) == _lib.EALIGN

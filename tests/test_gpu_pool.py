@@ -130,6 +130,41 @@ def test_avg_pool2d_bit_exact(xs):
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
+# plane sizes for every load width the GAP kernels pick (hw odd, 2 mod 4,
+# 4 mod 8, 0 mod 8), trees 0 to 6 levels deep, leaves at unequal depths (250,
+# 1000, 5000), a remainder in the last leaf (196, 52) and planes too deep for
+# one wave (6400, 8192 for 4-byte x; odd sizes above 1000 for all)
+GAP_HW = [1, 2, 3, 4, 6, 8, 12, 16, 49, 50, 52, 64, 100, 129, 196, 250, 256, 392, 784, 1000,
+          1001, 1024, 2048, 3136, 4096, 5000, 6400, 7689, 8192]
+
+
+@pytest.mark.parametrize("xt", ["f32", "bf16", "f16", "e4m3", "e5m2"])
+def test_avg_pool2d_plane_sizes(xt):
+    """np.mean of the decoded (and, E4M3, scaled) planes bit for bit over
+    GAP_HW, 38 planes each (several planes per wave and a partial last wave);
+    plane 0 is all -0.0, whose mean numpy makes +0.0."""
+    rng = np.random.default_rng(len(xt))
+    for hw in GAP_HW:
+        print(f"avg_pool2d {xt} hw={hw}", flush=True)
+        shape = (2, 19, 1, hw)
+        x = (rng.standard_normal(shape) * np.exp2(rng.integers(-6, 6, shape))).astype(np.float32)
+        x[0, 0] = -0.0
+        if xt == "f32":
+            got = F.avg_pool2d(torch.from_numpy(x).cuda()).cpu().numpy()
+            want = R.avg_pool2d(x)
+        else:
+            scale = 0.75 if xt == "e4m3" else None
+            codes = O.cast(x.reshape(-1), O.F32, CODE[xt], scale=scale)
+            dev = to_dev(codes, CODE[xt])
+            arg = (quant.Quantized(dev, shape, xt, torch.tensor([scale], device="cuda"))
+                   if scale else dev.view(shape))
+            got = F.avg_pool2d(arg).cpu().numpy()
+            dec = O.cast(codes, CODE[xt], O.F32, n=x.size, scale=scale).reshape(shape)
+            want = R.avg_pool2d(dec)
+        assert np.array_equal(got.reshape(-1).view(np.uint32), want.reshape(-1).view(np.uint32)), \
+            (xt, hw)
+
+
 def test_avg_pool2d_known_answer_and_narrow_input():
     """test_gap2d.py:20-27's constant input; bf16 and scaled E4M3 inputs equal
     np.mean of the dequantized arrays."""
