@@ -23,8 +23,10 @@
 // order; longer runs split at n/2 rounded down to a multiple of 8 and the two
 // halves added.  The kernel evaluates exactly that, so the result equals the
 // reference's bit for bit; narrow x is decoded and multiplied by its scale
-// first (the dequantized array the reference would average).  One lane per
-// plane.
+// first (the dequantized array the reference would average).  Planes of at
+// most 8192 elements: lanes per leaf, shuffles across leaves (the tree kernel,
+// or the wave kernel for trees too deep for one wave); larger planes: one
+// lane per plane.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
