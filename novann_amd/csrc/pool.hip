@@ -23,14 +23,15 @@
 // order; longer runs split at n/2 rounded down to a multiple of 8 and the two
 // halves added.  The kernel evaluates exactly that, so the result equals the
 // reference's bit for bit; narrow x is decoded and multiplied by its scale
-// first (the dequantized array the reference would average).  Planes of at
-// most 8192 elements: lanes per leaf, shuffles across leaves (the tree kernel,
-// or the wave kernel for trees too deep for one wave); larger planes: one
-// lane per plane.
+// first (the dequantized array the reference would average).  Lanes per leaf
+// of the tree, shuffles across leaves: several planes per wave when a plane's
+// tree fits a wave's lanes (the tree kernel), else one wave per plane walking
+// numpy's blocks (the plane kernel).
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
 
+#include <algorithm>
 #include <type_traits>
 
 #include "novaq_convert.h"
@@ -285,254 +286,7 @@ __global__ __launch_bounds__(256) void max_pool2d_22_kernel(const uint8_t* __res
   }
 }
 
-template <int XT>
-__device__ __forceinline__ float elem(const uint8_t* __restrict__ x, int64_t i, float s,
-                                      bool scaled) {
-  const float v = x_val<XT>(x, i);
-  return scaled ? v * s : v;
-}
-
-// numpy's pairwise_sum of n <= 128 elements starting at element b.
-template <int XT>
-__device__ float pw_leaf(const uint8_t* __restrict__ x, int64_t b, int n, float s, bool scaled) {
-  if (n < 8) {
-    float res = 0.0f;
-    for (int i = 0; i < n; ++i) res += elem<XT>(x, b + i, s, scaled);
-    return res;
-  }
-  float r[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) r[j] = elem<XT>(x, b + j, s, scaled);
-  int i = 8;
-  for (; i < n - (n % 8); i += 8) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) r[j] += elem<XT>(x, b + i + j, s, scaled);
-  }
-  float res = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
-  for (; i < n; ++i) res += elem<XT>(x, b + i, s, scaled);
-  return res;
-}
-
-// numpy's pairwise_sum of n <= 8192 elements starting at element b: the
-// recursion pw(a, n) = pw(a, n2) + pw(a + n2, n - n2), n2 = n/2 - (n/2) % 8,
-// for n > 128, walked with an explicit stack (at most 7 frames: 8192 halves
-// to a leaf of <= 128 in 6 splits).
-template <int XT>
-__device__ float pw_sum(const uint8_t* __restrict__ x, int64_t b, int64_t n, float s,
-                        bool scaled) {
-  if (n <= 128) return pw_leaf<XT>(x, b, (int)n, s, scaled);
-  struct Frame {
-    int64_t off, len, n2;
-    float left;
-    int stage;
-  };
-  Frame st[8];
-  int sp = 0;
-  st[0] = Frame{b, n, 0, 0.0f, 0};
-  float ret = 0.0f;
-  while (sp >= 0) {
-    Frame& f = st[sp];
-    if (f.stage == 0) {
-      if (f.len <= 128) {
-        ret = pw_leaf<XT>(x, f.off, (int)f.len, s, scaled);
-        --sp;
-        continue;
-      }
-      f.n2 = f.len / 2;
-      f.n2 -= f.n2 % 8;
-      f.stage = 1;
-      st[sp + 1] = Frame{f.off, f.n2, 0, 0.0f, 0};
-      ++sp;
-    } else if (f.stage == 1) {
-      f.left = ret;
-      f.stage = 2;
-      st[sp + 1] = Frame{f.off + f.n2, f.len - f.n2, 0, 0.0f, 0};
-      ++sp;
-    } else {
-      ret = f.left + ret;
-      --sp;
-    }
-  }
-  return ret;
-}
-
 constexpr int64_t NP_BUFSIZE = 8192;  // numpy's default ufunc buffer (np.getbufsize())
-
-template <int XT>
-__global__ __launch_bounds__(256) void global_avg_pool2d_kernel(const uint8_t* __restrict__ x,
-                                                               const float* __restrict__ x_scale,
-                                                               float* __restrict__ y,
-                                                               int64_t planes, int64_t hw) {
-  const int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (p >= planes) return;
-  const bool scaled = x_scale != nullptr;
-  const float s = scaled ? *x_scale : 1.0f;
-  // numpy's reduction hands the inner loop blocks of its ufunc buffer size
-  float sum = 0.0f;
-  for (int64_t b = 0; b < hw; b += NP_BUFSIZE)
-    sum = sum + pw_sum<XT>(x, p * hw + b, hw - b < NP_BUFSIZE ? hw - b : NP_BUFSIZE, s, scaled);
-  y[p] = sum / (float)hw;
-}
-
-// --- global average, wave-parallel (planes of at most 8192 elements) -------
-//
-// numpy's pairwise recursion on a plane of n <= 8192 elements (one buffer
-// block) splits it into leaves of <= 128 elements (at most 65) combined by a
-// fixed binary tree; the host works both out once per launch (every plane
-// has the same n) into a GapPlan: the leaves in order and the tree as a
-// postfix program (bit 1: push the next leaf's sum, bit 0: add the two top
-// values).  8 lanes make a leaf's 8 interleaved partial sums (lane j:
-// elements j, j+8, ... of the leaf's whole groups of 8, in order), shuffles
-// combine them as ((r0+r1)+(r2+r3))+((r4+r5)+(r6+r7)), lane 0 of the 8 adds
-// the leaf's remainder in order; the plane's first lane then runs the program
-// over the leaf sums with an 8-deep register stack (the tree is at most 7
-// levels deep).  Same operations in the same association as numpy.  When the
-// tree is complete (L = 2^d <= 8 leaves at one depth: 28 x 28, 14 x 14 and
-// 7 x 7 planes among them) the leaf sums are added by shuffles instead,
-// neighbours first, which is the same association.
-constexpr int GAP_STAGE = 2048;  // at most this many elements of a wave's planes staged in LDS
-
-// STAGED (a wave's planes hold at most GAP_STAGE elements): the wave first
-// copies its planes, which are contiguous in memory, into LDS with coalesced
-// loads (4 elements per load when the planes start on a multiple of 4),
-// decoded and scaled, and the leaf sums read them from there.
-template <int XT, bool STAGED>
-__global__ __launch_bounds__(256) void global_avg_pool2d_wave_kernel(
-    const uint8_t* __restrict__ x, const float* __restrict__ x_scale, float* __restrict__ y,
-    int64_t planes, int hw, GapPlan plan) {
-  __shared__ float sums[4][GAP_MAX_LEAVES];
-  extern __shared__ __attribute__((aligned(16))) float gap_stage[];  // STAGED: 4 waves x ppw * hw elements
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int L = plan.L;
-  const int G = L < 8 ? L : 8;         // leaves per pass
-  const int ppw = 64 / (8 * G);        // planes per wave
-  const int pi = lane / (8 * G), rem = lane - pi * 8 * G;
-  const int li = rem >> 3, j = rem & 7;
-  const int64_t plane0 = ((int64_t)blockIdx.x * 4 + wave) * ppw;
-  const int64_t plane = plane0 + pi;
-  const bool live = pi < ppw && plane < planes;
-  const int64_t base = plane * hw;
-  const bool scaled = x_scale != nullptr;
-  const float s = scaled ? *x_scale : 1.0f;
-  if constexpr (STAGED) {
-    const int64_t left = planes - plane0;
-    const int np = left <= 0 ? 0 : (left < ppw ? (int)left : ppw);
-    const int n = np * hw;
-    const int64_t e0 = plane0 * hw;
-    float* st = gap_stage + wave * ppw * hw;
-    if ((e0 & 3) == 0) {
-      // one 16-byte LDS store per lane where the wave's region is 16-byte
-      // aligned: consecutive lanes then write consecutive banks (four 4-byte
-      // stores 16 bytes apart would fall 4 lanes to a bank)
-      const bool st16 = (reinterpret_cast<uintptr_t>(st) & 15) == 0;
-      for (int g4 = lane; 4 * g4 < n; g4 += 64) {
-        const int64_t e = e0 + 4 * g4;
-        const bool whole = 4 * g4 + 3 < n;
-        const xl_u32x4 r = whole ? x4_raw<XT>(x, e) : x4_raw_guarded<XT>(x, e, e0 + n);
-        constexpr int B = XL<XT>::bits;
-        float f[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const uint32_t c =
-              B == 32 ? r[q] : (r[(q * B) / 32] >> ((q * B) % 32)) & ((1u << (B & 31)) - 1u);
-          const float v = u2f(decode<XT>(c));
-          f[q] = scaled ? v * s : v;
-        }
-        if (st16 && whole) {
-          *reinterpret_cast<float4*>(st + 4 * g4) = make_float4(f[0], f[1], f[2], f[3]);
-        } else {
-#pragma unroll
-          for (int q = 0; q < 4; ++q)
-            if (4 * g4 + q < n) st[4 * g4 + q] = f[q];
-        }
-      }
-    } else {
-      for (int i = lane; i < n; i += 64) st[i] = elem<XT>(x, e0 + i, s, scaled);
-    }
-    // each wave reads back only the region it staged: a wave-level fence
-    // (its LDS writes complete and visible to its own lanes), no workgroup
-    // barrier, so waves do not wait for one another
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  }
-  // element i of leaf lt of this lane's plane
-  auto val = [&](const GapLeaf& lt, int i) {
-    if constexpr (STAGED) return gap_stage[(wave * ppw + pi) * hw + lt.off + i];
-    else return elem<XT>(x, base + lt.off + i, s, scaled);
-  };
-  const bool bal = plan.balanced != 0;  // uniform: one pass (L <= 8), sums in registers
-  float leafsum = 0.0f;
-  for (int p0 = 0; p0 < L; p0 += G) {
-    const int leaf = p0 + li;
-    const bool on = live && leaf < L;
-    const GapLeaf lt = on ? plan.leaf[leaf] : GapLeaf{0, 0};
-    const int main = lt.len - (lt.len & 7);
-    // a leaf holds at most 16 groups of 8: every load of the lane goes out
-    // before the in-order sum
-    float v[16];
-#pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      const int i = j + 8 * k;
-      v[k] = (on && i < main) ? val(lt, i) : 0.0f;
-    }
-    float r = 0.0f;
-    if (on && lt.len >= 8) {
-      r = v[0];
-#pragma unroll
-      for (int k = 1; k < 16; ++k)
-        if (j + 8 * k < main) r += v[k];
-    }
-    // ((r0+r1)+(r2+r3))+((r4+r5)+(r6+r7)) across the 8 lanes of the leaf
-    r = r + __shfl_down(r, 1, 8);
-    r = r + __shfl_down(r, 2, 8);
-    r = r + __shfl_down(r, 4, 8);
-    if (on && j == 0) {
-      // the leaf's remainder (or, below 8 elements, the whole leaf) in order
-      const int e0 = lt.len < 8 ? 0 : main;
-      float t[7];
-#pragma unroll
-      for (int q = 0; q < 7; ++q) t[q] = e0 + q < lt.len ? val(lt, e0 + q) : 0.0f;
-      float res = lt.len < 8 ? 0.0f : r;
-#pragma unroll
-      for (int q = 0; q < 7; ++q)
-        if (e0 + q < lt.len) res += t[q];
-      if (bal) leafsum = res;
-      else sums[wave][pi * L + leaf] = res;
-    }
-  }
-  if (bal) {
-    // a complete tree: leaf sums sit in lanes 8 li of the plane's 8 L lanes;
-    // adding neighbours, then pairs of neighbours, ... associates as the
-    // plan's program does
-    float v = leafsum;
-    for (int d = 8; d < 8 * L; d <<= 1) v = v + __shfl_down(v, d, 8 * L);
-    if (live && rem == 0) y[plane] = (0.0f + v) / (float)hw;
-    return;
-  }
-  // the leaf sums of this wave's planes, written by its own lanes
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  if (live && rem == 0) {
-    const float* ls = &sums[wave][pi * L];
-    float st[GAP_MAX_STACK] = {};  // the plan's tree never needs more
-    int next = 0;
-    for (int k = 0; k < plan.nops; ++k) {
-      if ((plan.prog[k >> 5] >> (k & 31)) & 1u) {
-        const float v = ls[next++];
-#pragma unroll
-        for (int d = GAP_MAX_STACK - 1; d > 0; --d) st[d] = st[d - 1];
-        st[0] = v;
-      } else {
-        st[0] = st[1] + st[0];
-#pragma unroll
-        for (int d = 1; d < GAP_MAX_STACK - 1; ++d) st[d] = st[d + 1];
-      }
-    }
-    y[plane] = (0.0f + st[0]) / (float)hw;
-  }
-}
 
 // --- global average, every load issued at once (planes of at most 8192) ----
 //
@@ -601,19 +355,8 @@ __global__ __launch_bounds__(256) void global_avg_pool2d_tree_kernel(
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint8_t*>(x + p0 * hw * EB), (short)0, nplanes * hw * EB, 0x00020000);
   const float s = SCALED ? *x_scale : 1.0f;
-  // the leaf of virtual leaf vi
-  bool owner = lp < nplanes;
-  int off = 0, len = hw;
-  for (int lvl = D - 1; lvl >= 0; --lvl) {
-    const int bit = (vi >> lvl) & 1;
-    if (len > 128) {
-      const int n2 = (len >> 1) & ~7;
-      off = bit ? off + n2 : off;
-      len = bit ? len - n2 : n2;
-    } else if (bit) {
-      owner = false;
-    }
-  }
+  int off, len;
+  const bool owner = gap_detail::virtual_leaf(hw, D, vi, off, len) && lp < nplanes;
   const int ng = owner ? len >> 3 : 0;
   const int nr = owner && h == 0 ? len & 7 : 0;
   const uint32_t lb = (uint32_t)(lp * hw + off) * EB;  // the leaf's first byte
@@ -667,6 +410,99 @@ __global__ __launch_bounds__(256) void global_avg_pool2d_tree_kernel(
   if (l == 0 && lp < nplanes) y[p0 + lp] = (0.0f + res) / (float)hw;
 }
 
+// --- global average, one wave per plane (any plane size) -------------------
+//
+// Planes whose tree is too deep for one wave's lanes, or over 8192 elements:
+// the wave walks numpy's 8192-element blocks in order (total = 0, then total
+// + each block's pairwise sum), and runs each block's complete tree (depth D)
+// in passes of P = 64/LPL consecutive virtual leaves -- each pass a complete
+// subtree, reduced by the same lanes, loads and shuffles as the tree kernel.
+// Pass k's sum is parked in lane k, and the passes (a power of two) are then
+// added neighbours first by shuffles, the upper levels of the same tree.
+// Each block has its own buffer descriptor (at most 32 KiB), so no offset
+// outgrows 32 bits whatever the plane size.
+template <int XT, int Q, bool SCALED, int NG>
+__global__ __launch_bounds__(256) void global_avg_pool2d_plane_kernel(
+    const uint8_t* __restrict__ x, const float* __restrict__ x_scale, float* __restrict__ y,
+    int64_t planes, int64_t hw, int D_full, int D_last) {
+  constexpr int B = XL<XT>::bits, EB = B / 8;
+  constexpr int LPL = 8 / Q;  // lanes per leaf
+  constexpr int LSH = LPL == 8 ? 3 : LPL == 4 ? 2 : LPL == 2 ? 1 : 0;
+  constexpr int P = 64 / LPL, PSH = 6 - LSH;  // virtual leaves per pass
+  const int lane = threadIdx.x & 63;
+  const int64_t plane = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (plane >= planes) return;  // the whole wave
+  const int h = lane & (LPL - 1);
+  const float s = SCALED ? *x_scale : 1.0f;
+  auto val = [&](const xl_u32x4& r, int q) {
+    const uint32_t c =
+        B == 32 ? r[q] : (r[(q * B) / 32] >> ((q * B) % 32)) & ((1u << (B & 31)) - 1u);
+    const float f = u2f(decode<XT>(c));
+    return SCALED ? f * s : f;
+  };
+  float total = 0.0f;
+  for (int64_t b0 = 0; b0 < hw; b0 += NP_BUFSIZE) {
+    const int nb = (int)(hw - b0 < NP_BUFSIZE ? hw - b0 : NP_BUFSIZE);
+    const int D = b0 + NP_BUFSIZE < hw ? D_full : D_last;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(x + (plane * hw + b0) * EB), (short)0, nb * EB, 0x00020000);
+    const int passes = D > PSH ? 1 << (D - PSH) : 1;
+    float coll = -0.0f;  // lane k: pass k's sum
+    for (int ps = 0; ps < passes; ++ps) {
+      const int vi = (ps << PSH) + (lane >> LSH);
+      int off, len;
+      const bool owner = gap_detail::virtual_leaf(nb, D, vi, off, len);
+      const int ng = owner ? len >> 3 : 0;
+      const int nr = owner && h == 0 ? len & 7 : 0;
+      const uint32_t lb = (uint32_t)off * EB;
+      const uint32_t lq = lb + (uint32_t)(h * Q * EB);
+      uint32_t ad[NG];
+#pragma unroll
+      for (int k = 0; k < NG; ++k) ad[k] = (k < ng ? lq : GAP_OOB) + 8 * k * EB;
+      __builtin_amdgcn_sched_barrier(0);
+      xl_u32x4 v[NG];
+#pragma unroll
+      for (int k = 0; k < NG; ++k) v[k] = bload_q<XT, Q>(rs, ad[k]);
+      __builtin_amdgcn_sched_barrier(0);
+      float tail[7] = {};
+      if (nb & 7) {
+#pragma unroll
+        for (int q = 0; q < 7; ++q) {
+          const float f = u2f(
+              decode<XT>(bload_q<XT, 1>(rs, q < nr ? lb + (uint32_t)((8 * ng + q) * EB) : GAP_OOB)[0]));
+          tail[q] = SCALED ? f * s : f;
+        }
+      }
+      float r[Q];
+#pragma unroll
+      for (int q = 0; q < Q; ++q) r[q] = val(v[0], q);
+#pragma unroll
+      for (int k = 1; k < NG; ++k)
+#pragma unroll
+        for (int q = 0; q < Q; ++q) r[q] += val(v[k], q);
+#pragma unroll
+      for (int w = 1; w < Q; w <<= 1)
+#pragma unroll
+        for (int q = 0; q < Q; q += 2 * w) r[q] = r[q] + r[q + w];
+      float c = r[0];
+#pragma unroll
+      for (int d = 1; d < LPL; d <<= 1) c = c + __shfl_down(c, d, 64);
+      float res = ng > 0 ? c : 0.0f;
+#pragma unroll
+      for (int q = 0; q < 7; ++q)
+        if (q < nr) res += tail[q];
+      if (!owner) res = -0.0f;
+#pragma unroll
+      for (int l = 0; l < PSH; ++l) res = res + __shfl_down(res, LPL << l, 64);
+      const float pass_sum = __shfl(res, 0, 64);
+      if (lane == ps) coll = pass_sum;
+    }
+    for (int w = 1; w < passes; w <<= 1) coll = coll + __shfl_down(coll, w, 64);
+    total = total + __shfl(coll, 0, 64);
+  }
+  if (lane == 0) y[plane] = total / (float)hw;
+}
+
 template <int XT>
 int launch_max(const void* x, void* y, const PoolGeom& g, hipStream_t stream) {
   const int64_t npix = (int64_t)g.OH * g.OW;
@@ -717,64 +553,71 @@ int launch_max(const void* x, void* y, const PoolGeom& g, hipStream_t stream) {
 template <int XT>
 int launch_gap(const void* x, const float* x_scale, float* y, int64_t planes, int64_t hw,
                hipStream_t stream) {
-  if (hw <= NP_BUFSIZE) {
-    // the widest Q-element vector (Q * bytes <= 16) that every plane's, leaf's
-    // and group's start keeps aligned, then W = (8/Q) * 2^D lanes per plane
-    constexpr int EB = XL<XT>::bits / 8;
-    int lo = 1 << 30, D = -1;
-    gap_detail::depth_range((int)hw, 0, lo, D);
-    int Q = 16 / EB < 8 ? 16 / EB : 8;
-    while (Q > 1 && (hw % Q != 0 || reinterpret_cast<uintptr_t>(x) % ((uintptr_t)Q * EB) != 0))
-      Q >>= 1;
-    int wshift = D;
-    for (int lpl = 8 / Q; lpl > 1; lpl >>= 1) ++wshift;
-    if (wshift <= 6) {
-      const int64_t blocks = ((planes << wshift) + 255) / 256;
-      if (blocks > 0x7FFFFFFF || planes > ((int64_t)1 << 40)) return NOVAQ_EINVAL;
-      const int ngmax = gap_detail::leaf_len((int)hw, true) >> 3;
-      const bool sc = is_quant(XT) && x_scale != nullptr;  // the C ABI refuses other scales
-      using Kern = decltype(&global_avg_pool2d_tree_kernel<XT, 1, false, 16>);
-      Kern kern = nullptr;
-      auto choose = [&](auto qc) {
-        constexpr int QC = decltype(qc)::value;
-        if (Q != QC) return;
-        if (ngmax <= 8)
-          kern = sc ? global_avg_pool2d_tree_kernel<XT, QC, is_quant(XT), 8>
-                    : global_avg_pool2d_tree_kernel<XT, QC, false, 8>;
-        else
-          kern = sc ? global_avg_pool2d_tree_kernel<XT, QC, is_quant(XT), 16>
-                    : global_avg_pool2d_tree_kernel<XT, QC, false, 16>;
-      };
-      choose(std::integral_constant<int, 1>{});
-      choose(std::integral_constant<int, 2>{});
-      choose(std::integral_constant<int, 4>{});
-      if constexpr (EB < 4) choose(std::integral_constant<int, 8>{});
-      if (!kern) return NOVAQ_EINVAL;
-      hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), 0, stream,
-                         static_cast<const uint8_t*>(x), x_scale, y, planes, (int)hw, D, wshift);
-      return check_launch();
-    }
-  }
-  GapPlan plan;
-  if (hw <= NP_BUFSIZE && gap_plan((int)hw, plan)) {
-    const int leaves = plan.L;
-    const int G = leaves < 8 ? leaves : 8;
-    const int64_t ppw = 64 / (8 * G);
-    const int64_t waves = (planes + ppw - 1) / ppw;
-    const int64_t blocks = (waves + 3) / 4;
-    if (blocks > 0x7FFFFFFF) return NOVAQ_EINVAL;
-    const bool staged = ppw * hw <= GAP_STAGE;
-    auto kern = staged ? global_avg_pool2d_wave_kernel<XT, true>
-                       : global_avg_pool2d_wave_kernel<XT, false>;
-    const size_t lds = staged ? (size_t)4 * ppw * hw * sizeof(float) : 0;
-    hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), lds, stream,
-                       static_cast<const uint8_t*>(x), x_scale, y, planes, (int)hw, plan);
+  // the widest Q-element vector (Q * bytes <= 16) that every plane's, block's,
+  // leaf's and group's start keeps aligned
+  constexpr int EB = XL<XT>::bits / 8;
+  int Q = 16 / EB < 8 ? 16 / EB : 8;
+  while (Q > 1 && (hw % Q != 0 || reinterpret_cast<uintptr_t>(x) % ((uintptr_t)Q * EB) != 0))
+    Q >>= 1;
+  int lsh = 0;
+  for (int lpl = 8 / Q; lpl > 1; lpl >>= 1) ++lsh;
+  const bool sc = is_quant(XT) && x_scale != nullptr;  // the C ABI refuses other scales
+  // one block whose tree fits a wave's lanes: several planes per wave
+  const int D1 = hw <= NP_BUFSIZE ? gap_detail::tree_depth((int)hw) : 0;
+  const int wshift = D1 + lsh;
+  if (hw <= NP_BUFSIZE && wshift <= 6) {
+    const int64_t blocks = ((planes << wshift) + 255) / 256;
+    if (blocks > 0x7FFFFFFF || planes > ((int64_t)1 << 40)) return NOVAQ_EINVAL;
+    const int ngmax = gap_detail::leaf_len((int)hw, true) >> 3;
+    using Kern = decltype(&global_avg_pool2d_tree_kernel<XT, 1, false, 16>);
+    Kern kern = nullptr;
+    auto choose = [&](auto qc) {
+      constexpr int QC = decltype(qc)::value;
+      if (Q != QC) return;
+      if (ngmax <= 8)
+        kern = sc ? global_avg_pool2d_tree_kernel<XT, QC, is_quant(XT), 8>
+                  : global_avg_pool2d_tree_kernel<XT, QC, false, 8>;
+      else
+        kern = sc ? global_avg_pool2d_tree_kernel<XT, QC, is_quant(XT), 16>
+                  : global_avg_pool2d_tree_kernel<XT, QC, false, 16>;
+    };
+    choose(std::integral_constant<int, 1>{});
+    choose(std::integral_constant<int, 2>{});
+    choose(std::integral_constant<int, 4>{});
+    if constexpr (EB < 4) choose(std::integral_constant<int, 8>{});
+    if (!kern) return NOVAQ_EINVAL;
+    hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), 0, stream,
+                       static_cast<const uint8_t*>(x), x_scale, y, planes, (int)hw, D1, wshift);
     return check_launch();
   }
-  const int64_t blocks = (planes + 255) / 256;
+  // one wave per plane, over numpy's blocks in order
+  const int64_t full = hw / NP_BUFSIZE, rest = hw - full * NP_BUFSIZE;
+  const int nb_last = rest ? (int)rest : (int)NP_BUFSIZE;
+  const int D_full = gap_detail::tree_depth((int)NP_BUFSIZE), D_last = gap_detail::tree_depth(nb_last);
+  int longest = gap_detail::leaf_len(nb_last, true);
+  if (full > (rest ? 0 : 1)) longest = std::max(longest, gap_detail::leaf_len((int)NP_BUFSIZE, true));
+  const int ngmax = longest >> 3;
+  const int64_t blocks = (planes + 3) / 4;
   if (blocks > 0x7FFFFFFF) return NOVAQ_EINVAL;
-  hipLaunchKernelGGL(global_avg_pool2d_kernel<XT>, dim3((unsigned)blocks), dim3(256), 0, stream,
-                     static_cast<const uint8_t*>(x), x_scale, y, planes, hw);
+  using Kern = decltype(&global_avg_pool2d_plane_kernel<XT, 1, false, 16>);
+  Kern kern = nullptr;
+  auto choose = [&](auto qc) {
+    constexpr int QC = decltype(qc)::value;
+    if (Q != QC) return;
+    if (ngmax <= 8)
+      kern = sc ? global_avg_pool2d_plane_kernel<XT, QC, is_quant(XT), 8>
+                : global_avg_pool2d_plane_kernel<XT, QC, false, 8>;
+    else
+      kern = sc ? global_avg_pool2d_plane_kernel<XT, QC, is_quant(XT), 16>
+                : global_avg_pool2d_plane_kernel<XT, QC, false, 16>;
+  };
+  choose(std::integral_constant<int, 1>{});
+  choose(std::integral_constant<int, 2>{});
+  choose(std::integral_constant<int, 4>{});
+  if constexpr (EB < 4) choose(std::integral_constant<int, 8>{});
+  if (!kern) return NOVAQ_EINVAL;
+  hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(256), 0, stream,
+                     static_cast<const uint8_t*>(x), x_scale, y, planes, hw, D_full, D_last);
   return check_launch();
 }
 

@@ -1,22 +1,22 @@
-// Test helper: prints novaq::gap_plan for n = 1 .. argv[1] (the host-side
-// plan of numpy's pairwise summation used by the GlobalAvgPool2d kernel), one
-// line per n: "n ok L nops balanced prog-words... off,len ...".  Built with g++ by
-// tests/test_gap_plan.py.
+// Test helper: prints the complete-tree walk of numpy's pairwise summation
+// that the GlobalAvgPool2d kernels follow (novaq_gap_plan.h), for n = 1 ..
+// argv[1]: one line per n, "n D longest shortest" then "vi,off,len" for every
+// virtual leaf that owns a real leaf.  Built with g++ by tests/test_gap_plan.py.
 #include <cstdio>
 #include <cstdlib>
 
 #include "../../novann_amd/csrc/novaq_gap_plan.h"
 
 int main(int argc, char** argv) {
+  using namespace novaq::gap_detail;
   const int nmax = argc > 1 ? std::atoi(argv[1]) : 8192;
   for (int n = 1; n <= nmax; ++n) {
-    novaq::GapPlan p;
-    const bool ok = novaq::gap_plan(n, p);
-    std::printf("%d %d %d %d %d", n, ok ? 1 : 0, ok ? p.L : 0, ok ? p.nops : 0,
-                ok ? p.balanced : 0);
-    if (ok) {
-      for (int w = 0; w < novaq::GAP_PROG_WORDS; ++w) std::printf(" %u", p.prog[w]);
-      for (int i = 0; i < p.L; ++i) std::printf(" %d,%d", p.leaf[i].off, p.leaf[i].len);
+    const int D = tree_depth(n);
+    std::printf("%d %d %d %d", n, D, leaf_len(n, true), leaf_len(n, false));
+    // one virtual leaf past the tree too: it must own nothing
+    for (int vi = 0; vi <= (1 << D); ++vi) {
+      int off = -1, len = -1;
+      if (virtual_leaf(n, D, vi, off, len)) std::printf(" %d,%d,%d", vi, off, len);
     }
     std::printf("\n");
   }

@@ -131,11 +131,14 @@ def test_avg_pool2d_bit_exact(xs):
 
 
 # plane sizes for every load width the GAP kernels pick (hw odd, 2 mod 4,
-# 4 mod 8, 0 mod 8), trees 0 to 6 levels deep, leaves at unequal depths (250,
-# 1000, 5000), a remainder in the last leaf (196, 52) and planes too deep for
-# one wave (6400, 8192 for 4-byte x; odd sizes above 1000 for all)
+# 4 mod 8, 0 mod 8), trees 0 to 7 levels deep, leaves at unequal depths (250,
+# 1000, 5000), a remainder in the last leaf (196, 52), planes whose tree is too
+# deep for one wave's lanes (6400, 8192 for 4-byte x; odd sizes above 1000
+# for all: the one-wave-per-plane kernel, in 2 to 16 passes) and planes of
+# several numpy blocks (8193 on: whole blocks, then a short one)
 GAP_HW = [1, 2, 3, 4, 6, 8, 12, 16, 49, 50, 52, 64, 100, 129, 196, 250, 256, 392, 784, 1000,
-          1001, 1024, 2048, 3136, 4096, 5000, 6400, 7689, 8192]
+          1001, 1024, 2048, 3136, 4096, 5000, 6400, 7689, 7921, 8192, 8193, 9001, 12544, 16384,
+          24577, 50176]
 
 
 @pytest.mark.parametrize("xt", ["f32", "bf16", "f16", "e4m3", "e5m2"])
