@@ -421,6 +421,10 @@ struct BandGeom {
   int x_off;     // LDS byte offset of the staged input
   int x_bytes;   // bytes of the staged input
   int ostage;    // narrow output stored through LDS (whole store units per channel row)
+  // dividers for the per-item index arithmetic: c8, W / 4, OW, KW and the
+  // element-wise staged columns (a run-time integer division is a long
+  // instruction sequence; these are a multiply-high, an add and a shift)
+  FastDiv fd_c8, fd_w4, fd_ow, fd_kw, fd_nc;
 };
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -466,8 +470,8 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
 
   // 16-byte-load item `it` of band b: (row r, column group cg, channel group q)
   auto vload = [&](int b, int it, BandItem<XT>& v) {
-    const int q = it % g.c8, rest = it / g.c8;
-    const int cg = rest % W4, r = rest / W4;
+    const int rest = (int)fdiv((uint32_t)it, g.fd_c8), q = it - rest * g.c8;
+    const int r = (int)fdiv((uint32_t)rest, g.fd_w4), cg = rest - r * W4;
     const int hi = pad_index(b * g.R * g.sh - g.ph + r, g.H, g.pad_mode);
     const bool used = cg * 4 + g.pw < g.wp;
 #pragma unroll
@@ -537,7 +541,7 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
     constexpr int BITS = dtype_bits(WT);
     constexpr int NW = 72 * BITS / 32;  // words of one (co, q) run
     for (int item = tid; item < g.co_rows * g.c8; item += THREADS) {
-      const int co = item / g.c8, q = item - co * g.c8;
+      const int co = (int)fdiv((uint32_t)item, g.fd_c8), q = item - co * g.c8;
       uint32_t o[9][GB / 4];
       if (co0 + co < g.C_out) {
         const uint32_t* run = reinterpret_cast<const uint32_t*>(
@@ -616,8 +620,8 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
   for (int gi = tid; gi < g.gpr; gi += THREADS) {
     int koff = -1;
     if (gi < g.groups) {
-      const int tap = gi / g.c8, q = gi - tap * g.c8;
-      const int kh = tap / g.KW, kw = tap - kh * g.KW;
+      const int tap = (int)fdiv((uint32_t)gi, g.fd_c8), q = gi - tap * g.c8;
+      const int kh = (int)fdiv((uint32_t)tap, g.fd_kw), kw = tap - kh * g.KW;
       koff = (kh * g.wp + kw) * g.cstride + q * 8;
     }
     ktab[gi] = koff;
@@ -625,8 +629,8 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
   __syncthreads();  // weights regrouped; the raw copy region is free
 
   auto vstore = [&](uint16_t* xl, int it, const BandItem<XT>& v) {
-    const int q = it % g.c8, rest = it / g.c8;
-    const int cg = rest % W4, r = rest / W4;
+    const int rest = (int)fdiv((uint32_t)it, g.fd_c8), q = it - rest * g.c8;
+    const int r = (int)fdiv((uint32_t)rest, g.fd_w4), cg = rest - r * W4;
     const int col0 = cg * 4 + g.pw;  // staged column of input column 4*cg
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -677,8 +681,8 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
     const int items = g.rows_in * ncols * g.c8;
     const int ih0 = b * g.R * g.sh - g.ph;
     for (int it = tid; it < items; it += THREADS) {
-      const int q = it % g.c8, rest = it / g.c8;
-      const int bi = rest % ncols, r = rest / ncols;
+      const int rest = (int)fdiv((uint32_t)it, g.fd_c8), q = it - rest * g.c8;
+      const int r = (int)fdiv((uint32_t)rest, g.fd_nc), bi = rest - r * ncols;
       const int col = !g.vec ? bi : (bi < left ? bi : g.pw + g.W + (bi - left));
       const int hi = pad_index(ih0 + r, g.H, g.pad_mode);
       const int wi = pad_index(col - g.pw, g.W, g.pad_mode);
@@ -721,7 +725,7 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
     for (int m = 0; m < 4; ++m) {
       int p = (wave + 4 * m) * 16 + lr;
       if (p >= P) p = 0;  // a valid address; the product is never stored
-      const int ohr = p / g.OW, ow = p - ohr * g.OW;
+      const int ohr = (int)fdiv((uint32_t)p, g.fd_ow), ow = p - ohr * g.OW;
       pb[m] = ((ohr * g.sh) * g.wp + ow * g.sw) * g.cstride;
     }
     f32x4 acc[4][4];
@@ -954,6 +958,11 @@ bool band_geometry(const ConvGeom& cg, BandGeom& b, size_t& lds, int* ipt, int o
   b.vec = (cg.W % 4) == 0;
   b.nborder = std::min(cg.pw, b.wp) + std::max(0, b.wp - cg.pw - cg.W);
   b.vitems = b.vec ? b.rows_in * (cg.W / 4) * b.c8 : 0;
+  b.fd_c8 = fast_div((uint32_t)b.c8);
+  b.fd_w4 = fast_div((uint32_t)std::max(1, cg.W / 4));
+  b.fd_ow = fast_div((uint32_t)cg.OW);
+  b.fd_kw = fast_div((uint32_t)cg.KW);
+  b.fd_nc = fast_div((uint32_t)std::max(1, b.vec ? b.nborder : b.wp));
   *ipt = (b.vec && b.vitems <= THREADS) ? 1 : 0;
   // weight row: gpr groups of GB bytes, stride padded so the 16 rows a
   // fragment read touches fall in distinct banks

@@ -28,6 +28,28 @@ __device__ __forceinline__ int pad_index(int i, int n, int mode) {
   return r >= n ? p - r : r;
 }
 
+// n / d for n < 2^31 by a multiply and a shift (Granlund and Montgomery,
+// "Division by invariant integers using multiplication", 1994): with
+// l = ceil(log2 d) and m = floor(2^32 (2^l - d) / d) + 1, n / d =
+// (mulhi(n, m) + n) >> l; the sum stays below 2^32 because n < 2^31.  The
+// host works out (m, l) once per launch for a divisor d >= 1.
+struct FastDiv {
+  uint32_t m;
+  int l;
+};
+
+inline FastDiv fast_div(uint32_t d) {
+  FastDiv f;
+  f.l = 0;
+  while (((uint64_t)1 << f.l) < d) ++f.l;
+  f.m = (uint32_t)((((uint64_t)1 << 32) * (((uint64_t)1 << f.l) - d)) / d + 1);
+  return f;
+}
+
+__device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) {
+  return (__umulhi(n, f.m) + n) >> f.l;
+}
+
 // Records a failed HIP call for novaq_last_hip_error() and maps it to a status.
 int hip_fail(hipError_t e);
 

@@ -102,26 +102,6 @@ __device__ __forceinline__ void take_max(uint32_t c, float v, uint32_t& best, fl
   }
 }
 
-// n / d for n < 2^31 by a multiply and a shift (Granlund and Montgomery,
-// "Division by invariant integers using multiplication", 1994): with
-// l = ceil(log2 d) and m = floor(2^32 (2^l - d) / d) + 1, n / d =
-// (mulhi(n, m) + n) >> l; the sum stays below 2^32 because n < 2^31.
-struct FastDiv {
-  uint32_t m;
-  int l;
-};
-
-FastDiv fast_div(uint32_t d) {
-  FastDiv f;
-  f.l = 0;
-  while (((uint64_t)1 << f.l) < d) ++f.l;
-  f.m = (uint32_t)((((uint64_t)1 << 32) * (((uint64_t)1 << f.l) - d)) / d + 1);
-  return f;
-}
-
-__device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) {
-  return (__umulhi(n, f.m) + n) >> f.l;
-}
 
 // 2-wide windows with stride 2 along W and no W padding (MaxPool2d(2, 2) and
 // its (k, 2) / (k, 2) relatives): an item makes the two adjacent outputs
