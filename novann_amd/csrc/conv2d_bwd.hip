@@ -46,6 +46,7 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x2b __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 template <int WT>
@@ -159,6 +160,7 @@ constexpr int DW_M = 64, DW_N = 64, DW_K = 64;  // workgroup tile and K stage
 constexpr int DW_PITCH = DW_K + 8;              // bf16 per LDS row (144 B: conflict-free reads)
 constexpr int DW_PER_CU = 8;        // target workgroups per CU
 constexpr int DW_MAX_CHUNKS = 512;  // a multiple of 8
+constexpr uint32_t DW_OOB = 0x80000000u;  // a buffer offset past any image (reads 0)
 
 __device__ __forceinline__ uint32_t bf16_pair(float a, float b) {
   f32x2 f = {a, b};
@@ -180,7 +182,12 @@ __device__ __forceinline__ uint32_t bf16_pair(float a, float b) {
 // the stage for the tile rows 2w + l/32 + 8i (i < 8): grad rows are read as
 // 8-byte pairs, 256 contiguous bytes per half-wave.  The (c, kh, kw) of the
 // B rows come from a 64-entry table built once per workgroup.
-template <bool ZEROPAD, bool BIAS_ONLY>
+// BUF (P even, an image's grad and x under 1 GiB each): every stage load is a
+// buffer load through per-image descriptors, a masked slot (a channel, tap
+// or pixel past its end, or padding) carrying an offset past the buffer, so
+// it reads 0 and no load sits behind a branch; all offsets are formed before
+// the loads are issued back to back.  Same values staged, same results.
+template <bool ZEROPAD, bool BIAS_ONLY, bool BUF>
 __global__ __launch_bounds__(DW_THREADS, 2) void dweight_kernel(
     const float* __restrict__ grad, const float* __restrict__ x, float* __restrict__ part,
     float* __restrict__ bpart, BwdGeom g, int ckk, int chunks, int co_blocks, int j_blocks) {
@@ -240,6 +247,65 @@ __global__ __launch_bounds__(DW_THREADS, 2) void dweight_kernel(
     const float* xn = x + (int64_t)n * g.C * HW;
     const int p = p0 + k;
     const bool v0 = p < P, v1 = p + 1 < P;
+    if constexpr (BUF) {
+      // P even: a pair is whole or past the end
+      const __amdgpu_buffer_rsrc_t grs = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<float*>(gn), (short)0, g.C_out * P * 4, 0x00020000);
+      uint32_t aoff[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int co = co0 + rbase + 8 * i;
+        aoff[i] = co < g.C_out && v0 ? (uint32_t)(co * P + p) * 4 : DW_OOB;
+      }
+      uint32_t boff[8][2];
+      int hb[2], wb[2];
+      if constexpr (!BIAS_ONLY) {
+        const int oh = p / g.OW, ow = p - oh * g.OW;
+        hb[0] = oh * g.sh;
+        wb[0] = ow * g.sw;
+        const bool wrap = ow + 1 == g.OW;
+        hb[1] = wrap ? hb[0] + g.sh : hb[0];
+        wb[1] = wrap ? 0 : wb[0] + g.sw;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int4 t = jtab[rbase + 8 * i];
+#pragma unroll
+          for (int q = 0; q < 2; ++q) {
+            int hi = hb[q] + t.y, wi = wb[q] + t.z;
+            bool in;
+            int e;
+            if constexpr (ZEROPAD) {
+              in = (unsigned)hi < (unsigned)g.H && (unsigned)wi < (unsigned)g.W;
+              e = t.x + hb[q] * g.W + wb[q];
+            } else {
+              hi = pad_index(hi, g.H, g.pad_mode);
+              wi = pad_index(wi, g.W, g.pad_mode);
+              in = hi >= 0 && wi >= 0;
+              e = t.x - t.y * g.W - t.z + hi * g.W + wi;
+            }
+            boff[i][q] = t.w && (q ? v1 : v0) && in ? (uint32_t)e * 4 : DW_OOB;
+          }
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const u32x2b v = __builtin_amdgcn_raw_buffer_load_b64(grs, aoff[i], 0, 0);
+        a[i][0] = u2f(v[0]);
+        a[i][1] = u2f(v[1]);
+      }
+      if constexpr (!BIAS_ONLY) {
+        const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(xn), (short)0, g.C * HW * 4, 0x00020000);
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+          for (int q = 0; q < 2; ++q)
+            bv[i][q] = u2f(__builtin_amdgcn_raw_buffer_load_b32(xrs, boff[i][q], 0, 0));
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      return;
+    }
     // A: grad rows co0 + rbase + 8i at pixels p, p+1
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -748,8 +814,13 @@ static int dweight_launch(const float* grad, const float* x, const BwdGeom& g, i
   if (blocks > 0x7FFFFFFF) return NOVAQ_EINVAL;
   const dim3 grid((unsigned)blocks);
   const bool zp = g.pad_mode == NOVAQ_PAD_ZEROS;
-  auto kern = grad_weight ? (zp ? dweight_kernel<true, false> : dweight_kernel<false, false>)
-                          : dweight_kernel<true, true>;
+  // buffer loads: pairs whole (P even), per-image offsets within 31 bits
+  const bool buf = (g.OH * g.OW) % 2 == 0 && C_out * g.OH * g.OW * 4 < ((int64_t)1 << 30) &&
+                   C * g.H * g.W * 4 < ((int64_t)1 << 30);
+  auto kern = grad_weight
+                  ? (zp ? (buf ? dweight_kernel<true, false, true> : dweight_kernel<true, false, false>)
+                        : (buf ? dweight_kernel<false, false, true> : dweight_kernel<false, false, false>))
+                  : (buf ? dweight_kernel<true, true, true> : dweight_kernel<true, true, false>);
   hipLaunchKernelGGL(kern, grid, dim3(DW_THREADS), 0, stream, grad, x, part, bpart, g, (int)ckk,
                      (int)chunks, (int)co_blocks, (int)j_blocks);
   // partials added over the chunks in a fixed order by the finishing launch
