@@ -135,6 +135,66 @@ __global__ __launch_bounds__(THREADS) void im2col_kernel(const uint8_t* __restri
   }
 }
 
+// fp32 x, zeros padding, stride 1, W and OW multiples of 4, x 16-byte
+// aligned and under 2 GiB: a lane's 4 columns share (n, oh) with ow a
+// multiple of 4, so for row (c, kh, kw) its taps are the 4 consecutive
+// elements from column wi0 = ow + kw - pw of input row oh + kh - ph.  Rows
+// start on 16-byte boundaries (W % 4 == 0), so the taps lie in the aligned
+// 4-element chunks a = wi0 >> 2 and a + 1, at the shift wi0 & 3 -- the same
+// for every lane of the row.  A chunk is wholly inside the row or wholly
+// padding, so two aligned 16-byte buffer loads per row (a chunk outside the
+// image carries an offset past the buffer and reads +0, the zero pad) and a
+// uniform select give the 4 values: two coalesced loads where the kernel
+// above makes four 4-byte gathers.
+constexpr uint32_t COL_OOB = 0x80000000u;  // past the buffer of an input under 2 GiB
+
+__global__ __launch_bounds__(THREADS) void im2col_rows4_kernel(const float* __restrict__ x,
+                                                              float* __restrict__ col, ColGeom g,
+                                                              int x_bytes) {
+  const int j0 = blockIdx.x * SPAN + threadIdx.x * PER_LANE;
+  if (j0 >= g.L) return;
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(x), (short)0, x_bytes, 0x00020000);
+  const int q = j0 / g.OW;
+  const int ow = j0 - q * g.OW;
+  const int n = q / g.OH;
+  const int oh = q - n * g.OH;
+  const int plane_hw = g.H * g.W;
+  const int w4 = g.W >> 2;
+  const int xn = n * g.C * plane_hw;
+  const int taps = g.KH * g.KW;
+  const int rpw = (g.rows + gridDim.y - 1) / gridDim.y;
+  const int r_end = min(g.rows, (int)(blockIdx.y + 1) * rpw);
+  int r = blockIdx.y * rpw;
+  int c = r / taps;
+  int kh = (r - c * taps) / g.KW;
+  int kw = r - c * taps - kh * g.KW;
+  for (; r < r_end; ++r) {
+    const int hi = oh + kh - g.ph;
+    const int wi0 = ow + kw - g.pw;
+    const int a = wi0 >> 2, sh = wi0 & 3;  // floor division: wi0 may be negative
+    const bool row_in = (unsigned)hi < (unsigned)g.H;
+    const int e0 = xn + c * plane_hw + hi * g.W + 4 * a;
+    const uint32_t oa = row_in && (unsigned)a < (unsigned)w4 ? (uint32_t)e0 * 4 : COL_OOB;
+    const uint32_t ob = row_in && (unsigned)(a + 1) < (unsigned)w4 ? (uint32_t)e0 * 4 + 16 : COL_OOB;
+    const f32x4 A = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, oa, 0, 0));
+    const f32x4 B = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, ob, 0, 0));
+    f32x4 v;
+    if (sh == 0) v = A;
+    else if (sh == 1) v = f32x4{A[1], A[2], A[3], B[0]};
+    else if (sh == 2) v = f32x4{A[2], A[3], B[0], B[1]};
+    else v = f32x4{A[3], B[0], B[1], B[2]};
+    __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(col + (int64_t)r * g.L + j0));
+    if (++kw == g.KW) {
+      kw = 0;
+      if (++kh == g.KH) {
+        kh = 0;
+        ++c;
+      }
+    }
+  }
+}
+
 struct PadGeom {
   int H, W, ph, pw, pad_mode, Hp, Wp;
   int64_t planes;
@@ -216,6 +276,13 @@ int im2col_launch(const void* x, int x_dtype, const float* x_scale, int64_t N, i
   const int64_t ry = std::max<int64_t>(1, (int64_t)device_cu_count() * WG_PER_CU / g.segs);
   const dim3 grid((unsigned)g.segs, (unsigned)std::min<int64_t>(std::min<int64_t>(rows, ry), MAX_GRID_Y));
   const auto* xb = static_cast<const uint8_t*>(x);
+  const int64_t x_bytes = N * C * H * W * (dtype_bits(x_dtype) / 8);
+  if (x_dtype == F32 && pad_mode == NOVAQ_PAD_ZEROS && sh == 1 && sw == 1 && W % 4 == 0 &&
+      OW % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 && x_bytes < (int64_t)COL_OOB) {
+    hipLaunchKernelGGL(im2col_rows4_kernel, grid, dim3(THREADS), 0, stream,
+                       static_cast<const float*>(x), col, g, (int)x_bytes);
+    return check_launch();
+  }
   auto go = [&](auto xt) {
     constexpr int XT = decltype(xt)::value;
     if (pad_mode == NOVAQ_PAD_ZEROS)

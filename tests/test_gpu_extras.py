@@ -48,6 +48,30 @@ def test_im2col_bit_exact(geo, mode):
     assert np.array_equal(bits(col.cpu().numpy()), bits(want))
 
 
+ALIGNED_ROWS = [  # fp32, zeros, stride 1, W and OW multiples of 4: aligned-chunk path
+    (2, 3, 7, 12, 3, 5, 1, 2),   # taps at shifts 2, 3, 0, 1, 2
+    (1, 2, 5, 8, 1, 1, 0, 0),    # 1 x 1
+    (2, 2, 9, 8, 3, 7, 1, 3),    # 7 wide, every shift
+    (1, 3, 6, 8, 5, 5, 2, 4),    # pw = 4: the first chunk wholly left of the image
+    (3, 1, 4, 4, 2, 1, 0, 0),    # rows of a single chunk
+    (2, 4, 28, 28, 3, 3, 1, 1),  # config [5]'s conv2 geometry, small batch
+]
+
+
+@pytest.mark.parametrize("geo", ALIGNED_ROWS)
+def test_im2col_aligned_rows_bit_exact(geo):
+    N, C, H, W, KH, KW, ph, pw = geo
+    print(f"im2col aligned rows {geo}", flush=True)
+    rng = np.random.default_rng(sum(geo) + 100)
+    x = rng.standard_normal((N, C, H, W)).astype(np.float32)
+    x.reshape(-1)[::5] = -0.0
+    col = F.im2col(torch.from_numpy(x).cuda(), (KH, KW), 1, (ph, pw), "zeros")
+    want, OH, OW = R.im2col(x, KH, KW, (1, 1), (ph, pw), "zeros")
+    assert W % 4 == 0 and OW % 4 == 0
+    assert tuple(col.shape) == want.shape
+    assert np.array_equal(bits(col.cpu().numpy()), bits(want))
+
+
 @pytest.mark.parametrize("xt", ["bf16", "f16", "e4m3", "e5m2"])
 def test_im2col_of_narrow_inputs_is_the_decoded_matrix(xt):
     """A bf16 / f16 device tensor or an FP8 Quantized activation: the column
