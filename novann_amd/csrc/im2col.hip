@@ -135,22 +135,32 @@ __global__ __launch_bounds__(THREADS) void im2col_kernel(const uint8_t* __restri
   }
 }
 
-// fp32 x, zeros padding, stride 1, W and OW multiples of 4, x 16-byte
-// aligned and under 2 GiB: a lane's 4 columns share (n, oh) with ow a
+// fp32 x, zeros padding, stride 1, W and OW multiples of 4, KW <= 7, x
+// 16-byte aligned and under 2 GiB: a lane's 4 columns share (n, oh) with ow a
 // multiple of 4, so for row (c, kh, kw) its taps are the 4 consecutive
-// elements from column wi0 = ow + kw - pw of input row oh + kh - ph.  Rows
-// start on 16-byte boundaries (W % 4 == 0), so the taps lie in the aligned
-// 4-element chunks a = wi0 >> 2 and a + 1, at the shift wi0 & 3 -- the same
-// for every lane of the row.  A chunk is wholly inside the row or wholly
-// padding, so two aligned 16-byte buffer loads per row (a chunk outside the
-// image carries an offset past the buffer and reads +0, the zero pad) and a
-// uniform select give the 4 values: two coalesced loads where the kernel
-// above makes four 4-byte gathers.
+// elements from column ow + kw - pw of input row oh + kh - ph.  Rows start on
+// 16-byte boundaries (W % 4 == 0), so the KW rows of one (c, kh) read columns
+// ow - pw .. ow - pw + KW + 2, which lie in at most 4 aligned 4-element
+// chunks from a0 = (ow - pw) >> 2; each row's taps start s0 + kw elements
+// into them, s0 = (ow - pw) & 3 -- the same for every lane.  A chunk is
+// wholly inside the row or wholly padding: the group's chunks are loaded
+// once with aligned 16-byte buffer loads (a chunk outside the image carries
+// an offset past the buffer and reads +0, the zero pad) and each row's 4
+// values are selected from them -- 3 coalesced loads per 3 rows at 3 x 3,
+// where the kernel above makes four 4-byte gathers per row.  A workgroup's
+// block of rows is a whole number of (c, kh) groups (rpw a multiple of KW).
 constexpr uint32_t COL_OOB = 0x80000000u;  // past the buffer of an input under 2 GiB
+
+__device__ __forceinline__ f32x4 taps4(const f32x4& lo, const f32x4& hi, int sh) {
+  if (sh == 0) return lo;
+  if (sh == 1) return f32x4{lo[1], lo[2], lo[3], hi[0]};
+  if (sh == 2) return f32x4{lo[2], lo[3], hi[0], hi[1]};
+  return f32x4{lo[3], hi[0], hi[1], hi[2]};
+}
 
 __global__ __launch_bounds__(THREADS) void im2col_rows4_kernel(const float* __restrict__ x,
                                                               float* __restrict__ col, ColGeom g,
-                                                              int x_bytes) {
+                                                              int x_bytes, int rpw) {
   const int j0 = blockIdx.x * SPAN + threadIdx.x * PER_LANE;
   if (j0 >= g.L) return;
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
@@ -161,36 +171,32 @@ __global__ __launch_bounds__(THREADS) void im2col_rows4_kernel(const float* __re
   const int oh = q - n * g.OH;
   const int plane_hw = g.H * g.W;
   const int w4 = g.W >> 2;
-  const int xn = n * g.C * plane_hw;
-  const int taps = g.KH * g.KW;
-  const int rpw = (g.rows + gridDim.y - 1) / gridDim.y;
+  const int s_lo = ow - g.pw;
+  const int a0 = s_lo >> 2, s0 = s_lo & 3;  // floor division: s_lo may be negative
+  const int nch = (s0 + g.KW + 6) >> 2;     // chunks of columns s0 .. s0 + KW + 2 (<= 4)
   const int r_end = min(g.rows, (int)(blockIdx.y + 1) * rpw);
   int r = blockIdx.y * rpw;
-  int c = r / taps;
-  int kh = (r - c * taps) / g.KW;
-  int kw = r - c * taps - kh * g.KW;
-  for (; r < r_end; ++r) {
+  int ckh = r / g.KW;  // c * KH + kh
+  for (; r < r_end; r += g.KW, ++ckh) {
+    const int c = ckh / g.KH, kh = ckh - c * g.KH;
     const int hi = oh + kh - g.ph;
-    const int wi0 = ow + kw - g.pw;
-    const int a = wi0 >> 2, sh = wi0 & 3;  // floor division: wi0 may be negative
     const bool row_in = (unsigned)hi < (unsigned)g.H;
-    const int e0 = xn + c * plane_hw + hi * g.W + 4 * a;
-    const uint32_t oa = row_in && (unsigned)a < (unsigned)w4 ? (uint32_t)e0 * 4 : COL_OOB;
-    const uint32_t ob = row_in && (unsigned)(a + 1) < (unsigned)w4 ? (uint32_t)e0 * 4 + 16 : COL_OOB;
-    const f32x4 A = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, oa, 0, 0));
-    const f32x4 B = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, ob, 0, 0));
-    f32x4 v;
-    if (sh == 0) v = A;
-    else if (sh == 1) v = f32x4{A[1], A[2], A[3], B[0]};
-    else if (sh == 2) v = f32x4{A[2], A[3], B[0], B[1]};
-    else v = f32x4{A[3], B[0], B[1], B[2]};
-    __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(col + (int64_t)r * g.L + j0));
-    if (++kw == g.KW) {
-      kw = 0;
-      if (++kh == g.KH) {
-        kh = 0;
-        ++c;
-      }
+    const int e0 = n * g.C * plane_hw + c * plane_hw + hi * g.W + 4 * a0;
+    uint32_t off[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      off[k] = row_in && k < nch && (unsigned)(a0 + k) < (unsigned)w4 ? (uint32_t)(e0 + 4 * k) * 4
+                                                                   : COL_OOB;
+    f32x4 ch[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      ch[k] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off[k], 0, 0));
+    for (int kw = 0; kw < g.KW; ++kw) {
+      const int t = s0 + kw, j = t >> 2;
+      const f32x4 lo = j == 0 ? ch[0] : j == 1 ? ch[1] : j == 2 ? ch[2] : ch[3];
+      const f32x4 nx = j == 0 ? ch[1] : j == 1 ? ch[2] : ch[3];
+      __builtin_nontemporal_store(taps4(lo, nx, t & 3),
+                                  reinterpret_cast<f32x4*>(col + (int64_t)(r + kw) * g.L + j0));
     }
   }
 }
@@ -278,9 +284,14 @@ int im2col_launch(const void* x, int x_dtype, const float* x_scale, int64_t N, i
   const auto* xb = static_cast<const uint8_t*>(x);
   const int64_t x_bytes = N * C * H * W * (dtype_bits(x_dtype) / 8);
   if (x_dtype == F32 && pad_mode == NOVAQ_PAD_ZEROS && sh == 1 && sw == 1 && W % 4 == 0 &&
-      OW % 4 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 && x_bytes < (int64_t)COL_OOB) {
-    hipLaunchKernelGGL(im2col_rows4_kernel, grid, dim3(THREADS), 0, stream,
-                       static_cast<const float*>(x), col, g, (int)x_bytes);
+      OW % 4 == 0 && KW <= 7 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
+      x_bytes < (int64_t)COL_OOB) {
+    // row blocks of whole (c, kh) groups
+    const int64_t per = (rows + grid.y - 1) / grid.y;
+    const int64_t rpw = (per + KW - 1) / KW * KW;
+    const dim3 g2(grid.x, (unsigned)((rows + rpw - 1) / rpw));
+    hipLaunchKernelGGL(im2col_rows4_kernel, g2, dim3(THREADS), 0, stream,
+                       static_cast<const float*>(x), col, g, (int)x_bytes, (int)rpw);
     return check_launch();
   }
   auto go = [&](auto xt) {
