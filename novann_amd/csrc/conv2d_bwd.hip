@@ -48,6 +48,7 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x2b __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 template <int WT>
 __device__ __forceinline__ uint32_t code_at(const uint8_t* __restrict__ w, int64_t e) {
@@ -420,51 +421,85 @@ __global__ __launch_bounds__(DW_THREADS, 2) void dweight_kernel(
 // rows) stages.  Per stage it stages in LDS, as bf16:
 //   - Gs[co][k]: grad of the band, k = r * OWP + ow (rows padded to OWP, a
 //     multiple of 16, with zeros; R * OWP = 128 = 8 MFMA k-steps);
-//   - Xs[c][rr][col] = xpad[c][oh0 + rr - ph][col - pw]: the band's R + KH - 1
-//     input rows, XW = OWP + 8 columns each, the padding mode resolved (zero
-//     rows and columns past what the band's outputs read),
+//   - Xs[c][rr][col] = xpad[c][oh0 + rr - ph][col - xo]: the band's R + KH - 1
+//     input rows, XW = OWP + 8 columns each, input column 0 at staged column
+//     xo >= pw, the padding mode resolved (zero rows and columns past what
+//     the band's outputs read),
 // so wave t = (kh, kw) multiplies A = Gs (8 consecutive pixels of one channel,
-// a 16-byte LDS read) by B = Xs[c][r + kh][ow + kw ..] (8 consecutive
-// columns; for odd kw the 16 bytes sit across 5 dwords and v_alignbit
-// realigns them) with v_mfma_f32_32x32x16_bf16 into the (co, c) block of its
-// tap.  The Xs channel pitch is an odd number of dwords, so the 32 channels
-// of a fragment read fall in distinct banks.
+// a 16-byte LDS read) by B = Xs[c][r + kh][ow + kw - pw + xo ..] (8
+// consecutive columns; at an odd start the 16 bytes sit across 5 dwords and
+// v_alignbit realigns them) with v_mfma_f32_32x32x16_bf16 into the (co, c)
+// block of its tap.  The Xs channel pitch is an odd number of dwords, so the
+// 32 channels of a fragment read fall in distinct banks.
 //
-// Staging is one contiguous run per channel: a band's R * OW grad values and
-// a channel's rows_in * XW staged slots are spread over the 64 lanes (GJ = 2
-// and XJ slots per lane), whose byte offsets each lane forms once per stage.
-// The loads are buffer loads: a masked slot (padding, rows past the image,
-// channels past the tensor) carries an offset beyond the buffer's size and
-// reads 0, so no lane branches.  A stage's loads (KH * KW >= 8 makes one step
-// per wave enough) are issued into registers while the previous stage's
-// products run.  Each workgroup writes its chunk's partial as [tap][co][c];
-// the column sum adds the chunks and permutes to [co][c][kh][kw].
+// All DR_WAVES waves stage, so the staging work is the same on every SIMD
+// whatever the tap count; the waves past the taps only stage.  The loads are
+// buffer loads: a masked slot (padding, rows past the image, channels past
+// the tensor) carries an offset beyond the buffer's size and reads 0, so no
+// lane branches.  Per stage a lane forms only its slots' row offsets (the
+// channel offsets are fixed, the image and band are stepped, not divided out
+// of the stage index).  Two register sets: stage t + 2's loads are issued as
+// soon as stage t's registers are in LDS, so they have two stages' products
+// to arrive.  Staging, one of two forms:
+//   - VEC (zero padding, W and OW multiples of 4, 16-byte aligned tensors):
+//     16-byte loads of 4 consecutive grad pixels (one Gs row run, an 8-byte
+//     LDS write) or 4 consecutive input columns (two 4-byte LDS writes; xo is
+//     pw rounded up to even), items spread over all lanes (GU grad and XJ
+//     input items per lane); the padding columns of Xs are zeroed once and
+//     never written;
+//   - otherwise one 4-byte slot at a time: a band's R * OW grad values and a
+//     channel's rows_in * XW staged slots spread over the 64 lanes of a wave
+//     (2 and XJ slots per lane), wave w taking channels w, w + DR_WAVES, ...
+// Each workgroup writes its chunk's partial as [tap][co][c]; the column sum
+// adds the chunks and permutes to [co][c][kh][kw].
 constexpr int DR_K = 128;          // pixels per stage
+constexpr int DR_WAVES = 12;       // waves per workgroup (at most 12 taps)
+constexpr int DR_GC = 6, DR_XC = 3;  // grad / input channels a wave stages (12 x 6 >= 64, 12 x 3 >= 32)
+constexpr int DR_GU = 3;           // VEC: grad quads per lane (64 channels x 32 quads <= 3 x 768)
 constexpr uint32_t DR_OOB = 0x80000000u;  // byte offset past any buffer (reads 0)
 constexpr uint32_t DR_BUF3 = 0x00020000u;  // buffer resource word 3 (raw, 32-bit data)
+constexpr int DR_FAR = 1 << 30;    // a row index no band reaches (masked item)
 
 struct RowsGeom {
   int OWP, R, XW, rows_in, taps, cp, spi;  // padded output row, rows per stage, staged row
                                            // width, staged rows, KH*KW, Xs channel pitch
                                            // (bf16), stages per image
+  int xo;                                  // staged column of input column 0
+};
+
+// One stage's loads in registers.
+template <bool VEC, int XJ>
+struct RowsRegs {
+  float g[2 * DR_GC];
+  float x[DR_XC * XJ];
+};
+template <int XJ>
+struct RowsRegs<true, XJ> {
+  f32x4 g[DR_GU];
+  f32x4 x[XJ];
 };
 
 // MODE 0: grad_weight; 1: grad_weight and grad_bias; 2: grad_bias only (no x,
-// no products).  grad_bias: each lane adds the grad values it loads per
-// channel in stage order, the wave then adds its 64 lanes in a fixed
-// butterfly, and c block 0 writes the chunk's per-channel sum to bpart.
-template <int XJ, int MODE>
-__global__ __launch_bounds__(768) void dweight_rows_kernel(
+// no products).  grad_bias, in a fixed order: VEC: each lane adds each of its
+// grad quads ((v0 + v1) + (v2 + v3)) per stage in stage order, then the
+// quads of a channel are added in band order through LDS; otherwise each
+// lane adds the grad values it loads per channel in stage order and the wave
+// adds its 64 lanes in a fixed butterfly.  c block 0 writes the chunk's
+// per-channel sum to bpart.
+template <int XJ, int MODE, bool VEC>
+__global__ __launch_bounds__(DR_WAVES * 64) void dweight_rows_kernel(
     const float* __restrict__ grad, const float* __restrict__ x, float* __restrict__ part,
     float* __restrict__ bpart, BwdGeom g, RowsGeom rg, int chunks, int co_blocks,
     int c_blocks) {
   constexpr bool WGT = MODE != 2, BIAS = MODE != 0;
+  constexpr int NT = DR_WAVES * 64;
   extern __shared__ __attribute__((aligned(16))) uint8_t dr_lds[];
   constexpr int GP = DR_K + 8;  // Gs row pitch (bf16); slot DR_K takes masked lanes
   __bf16* Gs = reinterpret_cast<__bf16*>(dr_lds);
   __bf16* Xs = Gs + 64 * GP;
   const int tid = threadIdx.x, lane = tid & 63, half = lane >> 5;
-  const int tap = __builtin_amdgcn_readfirstlane(tid >> 6), nthreads = rg.taps * 64;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tap = wave;  // the product of waves below rg.taps
   const int kh = tap / g.KW, kw = tap - kh * g.KW;
   int bid = blockIdx.x;
   const int cb = bid % c_blocks;
@@ -477,6 +512,8 @@ __global__ __launch_bounds__(768) void dweight_rows_kernel(
   const int HW = g.H * g.W;
   const int P = g.OH * g.OW;
   const int xslots = rg.rows_in * rg.XW;
+  const int q4 = rg.R * g.OW / 4;  // VEC: grad quads of a band per channel
+  const int W4 = g.W / 4;
 
   f32x16 acc[2];
 #pragma unroll
@@ -484,111 +521,203 @@ __global__ __launch_bounds__(768) void dweight_rows_kernel(
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[i][r] = 0.0f;
 
-  // Gs padding columns (ow >= OW) are zeroed once and never written again.
+  // Gs padding columns (ow >= OW), and with VEC the Xs slots no stage writes,
+  // are zeroed once.
   if constexpr (WGT) {
     uint32_t* z = reinterpret_cast<uint32_t*>(dr_lds);
-    for (int i = tid; i < 64 * GP / 2; i += nthreads) z[i] = 0u;
+    const int words = VEC ? (64 * GP + 32 * rg.cp) / 2 : 64 * GP / 2;
+    for (int i = tid; i < words; i += NT) z[i] = 0u;
   }
-  float bsum[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-  // Gs slot j of this lane: grad value m = lane + 64 j of the band, its row
-  // and Gs column (DR_K when m is past the band)
-  int gr[2], gk[2];
+  float bsum[VEC ? DR_GU : DR_GC];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int m = lane + 64 * j;
-    gr[j] = m / g.OW;
-    gk[j] = m < rg.R * g.OW ? gr[j] * rg.OWP + (m - gr[j] * g.OW) : DR_K;
-  }
-  // Xs slot j of this lane: staged row xr and input column xw (-1: zero; also
-  // for columns no output of the band reads); slots past the channel's
-  // xslots go to the pitch's spare slot
-  int xr[XJ], xw[XJ], xk[XJ];
-#pragma unroll
-  for (int j = 0; j < XJ; ++j) {
-    const int e = lane + 64 * j;
-    xr[j] = e / rg.XW;
-    const int col = e - xr[j] * rg.XW;
-    xw[j] = (e < xslots && col < g.OW + g.KW - 1) ? pad_index(col - g.pw, g.W, g.pad_mode) : -1;
-    xk[j] = e < xslots ? e : xslots;
-  }
-  const bool odd = kw & 1;
+  for (int i = 0; i < (VEC ? DR_GU : DR_GC); ++i) bsum[i] = 0.0f;
 
-  // Stage t's loads: 8 grad channels (16 slots) and 4 input channels (4 XJ
-  // slots) per wave, which covers the 64 + 32 channels for KH * KW >= 8; all
-  // in flight together, into registers.
-  float gv[16], xv[4 * XJ];
-  auto load_stage = [&](int64_t t) {
-    const int n = (int)(t / rg.spi);
-    const int oh0 = (int)(t - (int64_t)n * rg.spi) * rg.R;
+  // VEC items of this lane: grad quad u = channel co_l = it / q4, pixels
+  // 4 (it % q4) .. + 3 of the band (byte offset gbase before the band's,
+  // band row grow, Gs element gdst; DR_FAR / -1 when masked); input quad u =
+  // channel it / (rows_in W4), staged row xrr, input columns 4q .. 4q + 3
+  // (byte offset xcb before the row's, Xs element xdst)
+  uint32_t gbase[DR_GU], xcb[XJ];
+  int grow[DR_GU], gdst[DR_GU], xrr[XJ], xdst[XJ];
+  // scalar slots of this lane: Gs slot j = grad value m = lane + 64 j of the
+  // band (row gr, Gs column gk: DR_K past the band); Xs slot j = staged row
+  // xr, input column xw (-1: zero, also for columns no output of the band
+  // reads), Xs element xk (the pitch's spare slot past xslots); the byte
+  // offsets of this wave's channels (beyond the buffer past the tile or the
+  // tensor)
+  int gr[2], gk[2], xr[XJ], xw[XJ], xk[XJ];
+  uint32_t gch[DR_GC], xch[DR_XC];
+  if constexpr (VEC) {
+#pragma unroll
+    for (int u = 0; u < DR_GU; ++u) {
+      const int it = tid + NT * u;
+      const int co_l = it / q4, m = 4 * (it - co_l * q4);
+      const int r = m / g.OW, col = m - r * g.OW;
+      const bool live = co_l < 64 && co0 + co_l < g.C_out;
+      gbase[u] = (uint32_t)((co0 + co_l) * P + m) * 4u;
+      grow[u] = live ? r : DR_FAR;
+      gdst[u] = co_l < 64 ? co_l * GP + r * rg.OWP + col : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < XJ; ++u) {
+      const int it = tid + NT * u;
+      const int per = rg.rows_in * W4;
+      const int c_l = it / per, rest = it - c_l * per;
+      const int rr = rest / W4, q = rest - rr * W4;
+      const bool live = c_l < 32 && c0 + c_l < g.C;
+      xcb[u] = (uint32_t)((c0 + c_l) * HW + 4 * q) * 4u;
+      xrr[u] = live ? rr : DR_FAR;
+      xdst[u] = c_l < 32 ? c_l * rg.cp + rr * rg.XW + 4 * q + rg.xo : -1;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int m = lane + 64 * j;
+      gr[j] = m / g.OW;
+      gk[j] = m < rg.R * g.OW ? gr[j] * rg.OWP + (m - gr[j] * g.OW) : DR_K;
+    }
+#pragma unroll
+    for (int j = 0; j < XJ; ++j) {
+      const int e = lane + 64 * j;
+      xr[j] = e / rg.XW;
+      const int col = e - xr[j] * rg.XW;
+      xw[j] = (e < xslots && col < g.OW + g.KW - 1) ? pad_index(col - rg.xo, g.W, g.pad_mode) : -1;
+      xk[j] = e < xslots ? e : xslots;
+    }
+#pragma unroll
+    for (int i = 0; i < DR_GC; ++i) {
+      const int co_l = wave + DR_WAVES * i;
+      gch[i] = (co_l < 64 && co0 + co_l < g.C_out) ? (uint32_t)(co0 + co_l) * (uint32_t)P * 4u
+                                                   : 0x40000000u;
+    }
+#pragma unroll
+    for (int i = 0; i < DR_XC; ++i) {
+      const int c_l = wave + DR_WAVES * i;
+      xch[i] = (c_l < 32 && c0 + c_l < g.C) ? (uint32_t)(c0 + c_l) * (uint32_t)HW * 4u : 0x40000000u;
+    }
+  }
+
+  typedef RowsRegs<VEC, XJ> Regs;
+  // The loads of the stage of band s of image n, all in flight together.
+  auto load_stage = [&](Regs& rv, int n, int s) {
+    const int oh0 = s * rg.R;
     const int rows_left = g.OH - oh0;
     const int rows_read = (rows_left < rg.R ? rows_left : rg.R) + g.KH - 1;
     const __amdgpu_buffer_rsrc_t gbuf = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float*>(grad + (int64_t)n * g.C_out * P), (short)0, g.C_out * P * 4, DR_BUF3);
     const __amdgpu_buffer_rsrc_t xbuf = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float*>(x + (int64_t)n * g.C * HW), (short)0, g.C * HW * 4, DR_BUF3);
-    // byte offsets of this lane's slots within a channel
-    uint32_t goff[2], xoff[XJ];
+    if constexpr (VEC) {
+      const uint32_t band = (uint32_t)(oh0 * g.OW) * 4u;
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
-      goff[j] = (gk[j] < DR_K && gr[j] < rows_left)
-                    ? (uint32_t)(oh0 * g.OW + lane + 64 * j) * 4u : DR_OOB;
-    // input row of staged row rr (lane rr holds it; -1: a zero row)
-    const int hi_l = lane < rows_read ? pad_index(oh0 + lane - g.ph, g.H, g.pad_mode) : -1;
+      for (int u = 0; u < DR_GU; ++u) {
+        const uint32_t off = grow[u] < rows_left ? gbase[u] + band : DR_OOB;
+        rv.g[u] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(gbuf, off, 0, 0));
+      }
+      if constexpr (WGT) {
 #pragma unroll
-    for (int j = 0; j < XJ; ++j) {
-      const int hi = __shfl(hi_l, xr[j] < 63 ? xr[j] : 63);
-      xoff[j] = (hi >= 0 && xw[j] >= 0) ? (uint32_t)(hi * g.W + xw[j]) * 4u : DR_OOB;
+        for (int u = 0; u < XJ; ++u) {
+          const int hi = oh0 - g.ph + xrr[u];
+          const uint32_t off = (xrr[u] < rows_read && hi >= 0 && hi < g.H)
+                                   ? xcb[u] + (uint32_t)(hi * g.W) * 4u : DR_OOB;
+          rv.x[u] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xbuf, off, 0, 0));
+        }
+      }
+    } else {
+      // byte offsets of this lane's slots within a channel
+      uint32_t goff[2], xoff[XJ];
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        goff[j] = (gk[j] < DR_K && gr[j] < rows_left)
+                      ? (uint32_t)(oh0 * g.OW + lane + 64 * j) * 4u : DR_OOB;
+#pragma unroll
+      for (int j = 0; j < XJ; ++j) {
+        const int hi = (xr[j] < rows_read && xw[j] >= 0)
+                           ? pad_index(oh0 - g.ph + xr[j], g.H, g.pad_mode) : -1;
+        xoff[j] = hi >= 0 ? (uint32_t)(hi * g.W + xw[j]) * 4u : DR_OOB;
+      }
+#pragma unroll
+      for (int k = 0; k < 2 * DR_GC; ++k)
+        rv.g[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                gbuf, goff[k & 1] + gch[k >> 1], 0, 0));
+      if constexpr (WGT) {
+#pragma unroll
+        for (int k = 0; k < DR_XC * XJ; ++k)
+          rv.x[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                  xbuf, xoff[k % XJ] + xch[k / XJ], 0, 0));
+      }
     }
+  };
+  // this lane's share of the stage's grad sums
+  auto add_bias = [&](const Regs& rv) {
+    if constexpr (VEC) {
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      const int co_l = tap + (k >> 1) * rg.taps;
-      const uint32_t coff = (co_l < 64 && co0 + co_l < g.C_out)
-                                ? (uint32_t)(co0 + co_l) * (uint32_t)P * 4u : 0x40000000u;
-      gv[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                            gbuf, goff[k & 1] + coff, 0, 0));
+      for (int u = 0; u < DR_GU; ++u) bsum[u] += (rv.g[u][0] + rv.g[u][1]) + (rv.g[u][2] + rv.g[u][3]);
+    } else {
+#pragma unroll
+      for (int k = 0; k < 2 * DR_GC; ++k) bsum[k >> 1] += rv.g[k];
     }
-#pragma unroll
-    for (int k = 0; k < 4 * XJ; ++k) {
-      if constexpr (!WGT) break;
-      const int c_l = tap + (k / XJ) * rg.taps;
-      const uint32_t coff = (c_l < 32 && c0 + c_l < g.C)
-                                ? (uint32_t)(c0 + c_l) * (uint32_t)HW * 4u : 0x40000000u;
-      xv[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                            xbuf, xoff[k % XJ] + coff, 0, 0));
+  };
+  // the next stage to load (image ln, band ls), stepped after each load
+  int ln = (int)(t_begin / rg.spi), ls = (int)(t_begin - (int64_t)ln * rg.spi);
+  auto load_next = [&](Regs& rv) {
+    load_stage(rv, ln, ls);
+    if (++ls == rg.spi) {
+      ls = 0;
+      ++ln;
     }
   };
 
+  Regs rv0, rv1;
   if constexpr (!WGT) {
-    // grad_bias only: the stages' grad values, no LDS and no products
+    // grad_bias only: the stages' grad values, no products
     for (int64_t t = t_begin; t < t_end; ++t) {
-      load_stage(t);
-#pragma unroll
-      for (int k = 0; k < 16; ++k) bsum[k >> 1] += gv[k];
+      load_next(rv0);
+      add_bias(rv0);
     }
   }
-  if (WGT && t_begin < t_end) load_stage(t_begin);
-  for (int64_t t = t_begin; WGT && t < t_end; ++t) {
+  // stage t: its registers into LDS, stage t + 2's loads into the same
+  // registers, the products
+  auto run_stage = [&](Regs& rv, int64_t t) {
     __syncthreads();  // the previous stage's fragment reads are done
-    if constexpr (BIAS) {
+    if constexpr (BIAS) add_bias(rv);
+    if constexpr (VEC) {
 #pragma unroll
-      for (int k = 0; k < 16; ++k) bsum[k >> 1] += gv[k];
-    }
+      for (int u = 0; u < DR_GU; ++u) {
+        if (gdst[u] < 0) continue;
+        const f32x2 lo = {rv.g[u][0], rv.g[u][1]}, hi = {rv.g[u][2], rv.g[u][3]};
+        *reinterpret_cast<u32x2b*>(Gs + gdst[u]) =
+            u32x2b{__builtin_bit_cast(uint32_t, __builtin_convertvector(lo, bf16x2)),
+                   __builtin_bit_cast(uint32_t, __builtin_convertvector(hi, bf16x2))};
+      }
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      const int co_l = tap + (k >> 1) * rg.taps;
-      if (co_l < 64) Gs[co_l * GP + gk[k & 1]] = (__bf16)gv[k];
-    }
+      for (int u = 0; u < XJ; ++u) {
+        if (xdst[u] < 0) continue;
+        const f32x2 lo = {rv.x[u][0], rv.x[u][1]}, hi = {rv.x[u][2], rv.x[u][3]};
+        uint32_t* d = reinterpret_cast<uint32_t*>(Xs + xdst[u]);
+        d[0] = __builtin_bit_cast(uint32_t, __builtin_convertvector(lo, bf16x2));
+        d[1] = __builtin_bit_cast(uint32_t, __builtin_convertvector(hi, bf16x2));
+      }
+    } else {
 #pragma unroll
-    for (int k = 0; k < 4 * XJ; ++k) {
-      const int c_l = tap + (k / XJ) * rg.taps;
-      if (c_l < 32) Xs[c_l * rg.cp + xk[k % XJ]] = (__bf16)xv[k];
+      for (int k = 0; k < 2 * DR_GC; ++k) {
+        const int co_l = wave + DR_WAVES * (k >> 1);
+        if (co_l < 64) Gs[co_l * GP + gk[k & 1]] = (__bf16)rv.g[k];
+      }
+#pragma unroll
+      for (int k = 0; k < DR_XC * XJ; ++k) {
+        const int c_l = wave + DR_WAVES * (k / XJ);
+        if (c_l < 32) Xs[c_l * rg.cp + xk[k % XJ]] = (__bf16)rv.x[k];
+      }
     }
-    // the next stage's loads overlap this stage's products
-    if (t + 1 < t_end) load_stage(t + 1);
+    if (t + 2 < t_end) load_next(rv);
     __syncthreads();
-    // wave `tap`: 8 k-steps of 16 pixels, both 32-channel co tiles
+    if (tap >= rg.taps) return;
+    // wave `tap`: 8 k-steps of 16 pixels, both 32-channel co tiles; B starts
+    // at staged column ow + sft
+    const int sft = kw - g.pw + rg.xo;
     const uint32_t* xd = reinterpret_cast<const uint32_t*>(Xs) + (lane & 31) * (rg.cp >> 1) +
-                         (kw >> 1);
+                         (sft >> 1);
 #pragma unroll
     for (int st = 0; st < DR_K / 16; ++st) {
       const int k0 = st * 16 + half * 8;
@@ -599,7 +728,7 @@ __global__ __launch_bounds__(768) void dweight_rows_kernel(
       for (int i = 0; i < 5; ++i) d[i] = p[i];
       uint32_t bw[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) bw[i] = odd ? __builtin_amdgcn_alignbit(d[i + 1], d[i], 16) : d[i];
+      for (int i = 0; i < 4; ++i) bw[i] = (sft & 1) ? __builtin_amdgcn_alignbit(d[i + 1], d[i], 16) : d[i];
       const bf16x8 b = __builtin_bit_cast(bf16x8, bw);
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
@@ -607,20 +736,43 @@ __global__ __launch_bounds__(768) void dweight_rows_kernel(
         acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[i], 0, 0, 0);
       }
     }
+  };
+  if constexpr (WGT) {
+    if (t_begin < t_end) load_next(rv0);
+    if (t_begin + 1 < t_end) load_next(rv1);
+    for (int64_t t = t_begin; t < t_end; t += 2) {
+      run_stage(rv0, t);
+      if (t + 1 < t_end) run_stage(rv1, t + 1);
+    }
   }
-  if constexpr (BIAS) {
-    // channel co_l = tap + c * taps of this wave: the wave's 64 lanes added
+  if constexpr (BIAS && VEC) {
+    // the quads of each channel added in band order
+    float* red = reinterpret_cast<float*>(dr_lds);
+    __syncthreads();  // the last stage's fragment reads are done
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      float v = bsum[c];
+    for (int u = 0; u < DR_GU; ++u) {
+      const int it = tid + NT * u;
+      if (it < 64 * q4) red[it] = bsum[u];
+    }
+    __syncthreads();
+    if (cb == 0 && tid < 64 && co0 + tid < g.C_out) {
+      float v = 0.0f;
+      for (int q = 0; q < q4; ++q) v += red[tid * q4 + q];
+      bpart[(int64_t)chunk * g.C_out + co0 + tid] = v;
+    }
+  } else if constexpr (BIAS) {
+    // channel co_l = wave + i * DR_WAVES: the wave's 64 lanes added
+#pragma unroll
+    for (int i = 0; i < DR_GC; ++i) {
+      float v = bsum[i];
 #pragma unroll
       for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-      const int co_l = tap + c * rg.taps;
+      const int co_l = wave + DR_WAVES * i;
       if (cb == 0 && lane == 0 && co_l < 64 && co0 + co_l < g.C_out)
         bpart[(int64_t)chunk * g.C_out + co0 + co_l] = v;
     }
   }
-  if constexpr (!WGT) return;
+  if (!WGT || tap >= rg.taps) return;
   // lane holds input channel c0 + (lane & 31), output channel rows
   // 8*(r/4) + 4*half + r%4 of tile i; the partial is stored as
   // [chunk][tap][co][c] (a half-wave writes 32 consecutive c), which the
@@ -638,13 +790,15 @@ __global__ __launch_bounds__(768) void dweight_rows_kernel(
 
 constexpr int DR_MAX_XJ = 5;
 
-// The stride-1 rows path applies (its LDS bytes and slots per lane XJ), or 0.
-size_t rows_geometry(const BwdGeom& g, RowsGeom& rg, int& xj) {
+// The stride-1 rows path applies (its LDS bytes, input items or slots per
+// lane XJ, and whether its staging is VEC), or 0.  aligned: grad and x start
+// on 16 bytes (always through the C ABI, which requires it).
+size_t rows_geometry(const BwdGeom& g, bool aligned, RowsGeom& rg, int& xj, bool& vec) {
   const int taps = g.KH * g.KW;
   // (fewer than 16 input channels leave most of the 32-channel tile idle: a
   // 1-channel 28x28 batch of 256 takes ~33 us here against 16.5 on dweight_kernel)
-  // (at most 12 taps: 12 waves keep ~170 VGPRs a wave)
-  if (g.sh != 1 || g.sw != 1 || taps < 8 || taps > 12 || g.KW > 8 || g.OW > 64 || g.C < 16)
+  // (at most DR_WAVES taps, one wave each)
+  if (g.sh != 1 || g.sw != 1 || taps < 8 || taps > DR_WAVES || g.KW > 8 || g.OW > 64 || g.C < 16)
     return 0;
   // 32-bit buffer offsets: an image's grad and input stay below 1 GiB
   if ((int64_t)g.C_out * g.OH * g.OW * 4 >= (1 << 30) || (int64_t)g.C * g.H * g.W * 4 >= (1 << 30))
@@ -653,12 +807,18 @@ size_t rows_geometry(const BwdGeom& g, RowsGeom& rg, int& xj) {
   rg.R = DR_K / rg.OWP;
   rg.XW = rg.OWP + 8;
   rg.rows_in = rg.R + g.KH - 1;
-  if (rg.rows_in > 64) return 0;
   rg.taps = taps;
   const int xslots = rg.rows_in * rg.XW;
   rg.cp = xslots + 2;  // odd dword pitch; slot xslots is the spare
   rg.spi = (g.OH + rg.R - 1) / rg.R;
-  xj = (xslots + 63) / 64;
+  // VEC: input quads per lane; xo even (4-byte LDS writes), so xo + W and
+  // the columns the products read stay within XW (stride 1, KW <= 8)
+  const int vitems = 32 * rg.rows_in * (g.W / 4);
+  const int vj = std::max(2, (vitems + DR_WAVES * 64 - 1) / (DR_WAVES * 64));
+  vec = aligned && g.pad_mode == NOVAQ_PAD_ZEROS && g.W % 4 == 0 && g.OW % 4 == 0 &&
+        vj <= DR_MAX_XJ;
+  rg.xo = vec ? (g.pw + 1) & ~1 : g.pw;
+  xj = vec ? vj : (xslots + 63) / 64;
   if (xj < 2 || xj > DR_MAX_XJ) return 0;  // (more slots per lane spill registers)
   const size_t bytes = (size_t)64 * (DR_K + 8) * 2 + (size_t)32 * rg.cp * 2;
   return bytes <= 150 * 1024 ? bytes : 0;
@@ -754,7 +914,9 @@ static int dweight_launch(const float* grad, const float* x, const BwdGeom& g, i
   // chunks, so its bits match a full call's)
   RowsGeom rg{};
   int xj = 0;
-  const size_t rows_lds = rows_geometry(g, rg, xj);
+  bool vec = false;
+  const bool aligned = ((reinterpret_cast<uintptr_t>(grad) | reinterpret_cast<uintptr_t>(x)) & 15) == 0;
+  const size_t rows_lds = rows_geometry(g, aligned, rg, xj, vec);
   if (rows_lds) {
     float* part = reinterpret_cast<float*>(base + ws.part);
     float* bpart = reinterpret_cast<float*>(base + ws.bpart);
@@ -768,25 +930,38 @@ static int dweight_launch(const float* grad, const float* x, const BwdGeom& g, i
     if (blocks > 0x7FFFFFFF) return NOVAQ_EINVAL;
     using RowsKernel = void (*)(const float*, const float*, float*, float*, BwdGeom, RowsGeom,
                                 int, int, int);
-    static const RowsKernel kerns[2][DR_MAX_XJ + 1] = {
-        {nullptr, nullptr, dweight_rows_kernel<2, 0>, dweight_rows_kernel<3, 0>,
-         dweight_rows_kernel<4, 0>, dweight_rows_kernel<5, 0>},
-        {nullptr, nullptr, dweight_rows_kernel<2, 1>, dweight_rows_kernel<3, 1>,
-         dweight_rows_kernel<4, 1>, dweight_rows_kernel<5, 1>}};
-    static bool lds_raised[2][DR_MAX_XJ + 1] = {};
+    static const RowsKernel kerns[2][2][DR_MAX_XJ + 1] = {
+        {{nullptr, nullptr, dweight_rows_kernel<2, 0, false>, dweight_rows_kernel<3, 0, false>,
+          dweight_rows_kernel<4, 0, false>, dweight_rows_kernel<5, 0, false>},
+         {nullptr, nullptr, dweight_rows_kernel<2, 1, false>, dweight_rows_kernel<3, 1, false>,
+          dweight_rows_kernel<4, 1, false>, dweight_rows_kernel<5, 1, false>}},
+        {{nullptr, nullptr, dweight_rows_kernel<2, 0, true>, dweight_rows_kernel<3, 0, true>,
+          dweight_rows_kernel<4, 0, true>, dweight_rows_kernel<5, 0, true>},
+         {nullptr, nullptr, dweight_rows_kernel<2, 1, true>, dweight_rows_kernel<3, 1, true>,
+          dweight_rows_kernel<4, 1, true>, dweight_rows_kernel<5, 1, true>}}};
+    static bool lds_raised[2][2][DR_MAX_XJ + 1] = {};
     if (mode == 2) {
-      hipLaunchKernelGGL((dweight_rows_kernel<2, 2>), dim3((unsigned)blocks), dim3(rg.taps * 64),
-                         0, stream, grad, x, part, bpart, g, rg, (int)rchunks, (int)co_blocks, 1);
+      // the same grad reads and sums as a full call (VEC: the quads' sums
+      // meet in LDS)
+      const size_t red = vec ? (size_t)64 * (rg.R * g.OW / 4) * 4 : 0;
+      if (vec)
+        hipLaunchKernelGGL((dweight_rows_kernel<2, 2, true>), dim3((unsigned)blocks),
+                           dim3(DR_WAVES * 64), red, stream, grad, x, part, bpart, g, rg,
+                           (int)rchunks, (int)co_blocks, 1);
+      else
+        hipLaunchKernelGGL((dweight_rows_kernel<2, 2, false>), dim3((unsigned)blocks),
+                           dim3(DR_WAVES * 64), 0, stream, grad, x, part, bpart, g, rg,
+                           (int)rchunks, (int)co_blocks, 1);
     } else {
-      const RowsKernel kern = kerns[mode][xj];
-      if (!lds_raised[mode][xj]) {
+      const RowsKernel kern = kerns[vec][mode][xj];
+      if (!lds_raised[vec][mode][xj]) {
         const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize,
                                                  150 * 1024);
         if (e != hipSuccess) return hip_fail(e);
-        lds_raised[mode][xj] = true;
+        lds_raised[vec][mode][xj] = true;
       }
-      hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(rg.taps * 64), rows_lds, stream, grad,
+      hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(DR_WAVES * 64), rows_lds, stream, grad,
                          x, part, bpart, g, rg, (int)rchunks, (int)co_blocks, (int)c_blocks);
     }
     fa.rows = rchunks;

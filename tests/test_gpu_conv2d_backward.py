@@ -92,6 +92,71 @@ def test_conv2d_backward_rows_path(geom, wdt):
     check_case(*geom, wdt)
 
 
+# zero padding, W and OW multiples of 4: the rows kernel stages with 16-byte
+# loads (N, C, H, W, C_out, KH, KW, pad)
+VEC_GEOMETRIES = [
+    (2, 16, 12, 12, 8, 3, 3, (1, 1)),    # input column 0 at staged column 2 (pw 1)
+    (2, 16, 12, 8, 8, 8, 1, (0, 0)),     # 8 x 1 window, pw 0
+    (2, 16, 10, 16, 8, 2, 5, (1, 2)),    # pw 2
+    (2, 16, 9, 20, 8, 3, 3, (1, 3)),     # pw 3: staged column 4
+    (1, 16, 6, 60, 8, 3, 3, (1, 1)),     # 60-pixel rows, 3 input quads per lane
+    (3, 24, 13, 16, 40, 3, 3, (1, 1)),   # 16-pixel rows, last band partial, partial blocks
+    (2, 48, 8, 8, 80, 3, 3, (1, 1)),     # two input and two output channel blocks
+    (2, 64, 6, 60, 128, 4, 3, (2, 1)),   # 12 taps, 4 input quads per lane, two blocks each
+]
+
+
+def backward_bits(g, x, N, C, H, W, w, C_out, KH, KW, pad, outs):
+    """One C ABI call (grad_weight and / or grad_bias per outs) -> host arrays."""
+    lib = _lib.load()
+    st = torch.cuda.current_stream().cuda_stream
+    code = _lib.DTYPES["e2m1"]
+    nbytes = lib.novaq_conv2d_backward_workspace(N, C, C_out, KH, KW, code)
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device="cuda")
+    gw = torch.full((C_out, C, KH, KW), 7.0, device="cuda")
+    gb = torch.full((C_out,), 7.0, device="cuda")
+    _lib.check(lib.novaq_conv2d_backward(
+        g.data_ptr(), x.data_ptr(), N, C, H, W, w.codes.data_ptr(), code, w.scale.data_ptr(),
+        C_out, KH, KW, 1, 1, pad[0], pad[1], _lib.PAD_MODES["zeros"], None,
+        gw.data_ptr() if "w" in outs else None, gb.data_ptr() if "b" in outs else None,
+        ws.data_ptr(), nbytes, st), "conv2d backward")
+    torch.cuda.synchronize()
+    return gw.cpu().numpy().view(np.int32), gb.cpu().numpy()
+
+
+def bf16_round(a):
+    """fp32 -> nearest bf16 (ties to even), as fp32 (finite inputs)."""
+    u = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    u = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    return u.astype(np.uint32).view(np.float32)
+
+
+@pytest.mark.parametrize("geom", VEC_GEOMETRIES, ids=lambda g: "x".join(map(str, g[:7])))
+def test_conv2d_backward_rows_vec_staging(geom):
+    """The 16-byte staging against the oracle, and grad_weight against the
+    fp64 product of the operands the MFMAs multiply (grad and input rounded to
+    bf16) within 1e-5: a staging slip (a pixel, row or channel dropped or
+    shifted) costs more.  A bias-only and a weight-only call give the full
+    call's bits."""
+    N, C, H, W, C_out, KH, KW, pad = geom
+    check_case(N, C, H, W, C_out, KH, KW, (1, 1), pad, "e2m1")
+    rng = np.random.default_rng(sum(geom[:7]))
+    OH, OW = H + 2 * pad[0] - KH + 1, W + 2 * pad[1] - KW + 1
+    assert W % 4 == 0 and OW % 4 == 0
+    xh = rng.standard_normal((N, C, H, W)).astype(np.float32)
+    gh = rng.standard_normal((N, C_out, OH, OW)).astype(np.float32)
+    x, g = torch.from_numpy(xh).cuda(), torch.from_numpy(gh).cuda()
+    w = QuantizedParameters.from_float(
+        (rng.standard_normal((C_out, C, KH, KW)) * 0.2).astype(np.float32), "e2m1")
+    wv, bv = backward_bits(g, x, N, C, H, W, w, C_out, KH, KW, pad, "wb")
+    wdeq = w.dequantize().cpu().numpy().astype(np.float64).reshape(C_out, C, KH, KW)
+    _, rw, _ = R.conv2d_backward(bf16_round(gh).astype(np.float64),
+                                 bf16_round(xh).astype(np.float64), wdeq, (1, 1), pad, "zeros")
+    assert normwise(wv.view(np.float32), rw) <= 1e-5
+    assert np.array_equal(backward_bits(g, x, N, C, H, W, w, C_out, KH, KW, pad, "w")[0], wv)
+    assert np.array_equal(backward_bits(g, x, N, C, H, W, w, C_out, KH, KW, pad, "b")[1], bv)
+
+
 @pytest.mark.parametrize("mode", ["zeros", "reflect", "replicate", "circular"])
 @pytest.mark.parametrize("geom", [(2, 3, 8, 9, 5, 3, 3, (1, 1), (1, 2)),
                                   (2, 4, 11, 10, 6, 3, 3, (2, 1), (2, 1)),
