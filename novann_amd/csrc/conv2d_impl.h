@@ -64,6 +64,8 @@ constexpr int MAX_CB = 64;
 #define CONV_IB 4
 #endif
 constexpr size_t LDS_LIMIT = 160 * 1024;
+// LDS bytes of a band workgroup that still lets four share a CU
+constexpr size_t BAND_LDS_FOUR = 40 * 1024;
 
 struct ConvGeom {
   int N, C, H, W, C_out, KH, KW, sh, sw, ph, pw, pad_mode;
@@ -404,6 +406,8 @@ __global__ __launch_bounds__(THREADS, CONV_OCC) void conv2d_kernel(
 struct BandGeom {
   int N, C, H, W, C_out, KH, KW, sh, sw, ph, pw, pad_mode, OH, OW;
   int c8;        // 8-channel groups (C padded to a multiple of 8)
+  int passes;    // channel passes: the band's input staged pc8 groups at a time
+  int pc8;       // 8-channel groups staged per pass
   int cstride;   // bf16 per staged pixel
   int taps;      // KH * KW
   int groups;    // taps * c8 K groups of 8
@@ -416,15 +420,15 @@ struct BandGeom {
   int wp;        // staged input columns
   int nborder;   // staged columns outside [0, W) (element-wise path)
   int vec;       // interior columns staged with 16-byte loads (W % 4 == 0)
-  int vitems;    // 16-byte-load items per band (rows_in * W/4 * c8)
+  int vitems;    // 16-byte-load items per band and pass (rows_in * W/4 * pc8)
   int raw_ok;    // packed weights copied to LDS before regrouping
   int x_off;     // LDS byte offset of the staged input
-  int x_bytes;   // bytes of the staged input
+  int x_bytes;   // bytes of the staged input (one pass)
   int ostage;    // narrow output stored through LDS (whole store units per channel row)
   // dividers for the per-item index arithmetic: c8, W / 4, OW, KW and the
   // element-wise staged columns (a run-time integer division is a long
   // instruction sequence; these are a multiply-high, an add and a shift)
-  FastDiv fd_c8, fd_w4, fd_ow, fd_kw, fd_nc;
+  FastDiv fd_c8, fd_w4, fd_ow, fd_kw, fd_nc, fd_pc8;
 };
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -468,15 +472,16 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
   const int64_t xn = (int64_t)n * g.C * HW;  // element offset of image n
   const int W4 = g.W >> 2;
 
-  // 16-byte-load item `it` of band b: (row r, column group cg, channel group q)
-  auto vload = [&](int b, int it, BandItem<XT>& v) {
-    const int rest = (int)fdiv((uint32_t)it, g.fd_c8), q = it - rest * g.c8;
+  // 16-byte-load item `it` of band b, pass ps: (row r, column group cg,
+  // channel group q of the pass)
+  auto vload = [&](int b, int ps, int it, BandItem<XT>& v) {
+    const int rest = (int)fdiv((uint32_t)it, g.fd_pc8), q = it - rest * g.pc8;
     const int r = (int)fdiv((uint32_t)rest, g.fd_w4), cg = rest - r * W4;
     const int hi = pad_index(b * g.R * g.sh - g.ph + r, g.H, g.pad_mode);
     const bool used = cg * 4 + g.pw < g.wp;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const int c = q * 8 + j;
+      const int c = (ps * g.pc8 + q) * 8 + j;
       const bool live = used && hi >= 0 && c < g.C;
       const int64_t e = xn + c * HW + (int64_t)hi * g.W + cg * 4;
       if constexpr (XT == BF16) {
@@ -521,7 +526,7 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
   // then the band's 16-byte loads
   BandRegs<IPT, XT> r0;
   if constexpr (IPT > 0) {
-    if (tid < g.vitems) vload(band, tid, r0.v[0]);
+    if (tid < g.vitems) vload(band, 0, tid, r0.v[0]);
   }
   if (g.raw_ok) {
     uint8_t* raw = lds + g.x_off;
@@ -622,14 +627,14 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
     if (gi < g.groups) {
       const int tap = (int)fdiv((uint32_t)gi, g.fd_c8), q = gi - tap * g.c8;
       const int kh = (int)fdiv((uint32_t)tap, g.fd_kw), kw = tap - kh * g.KW;
-      koff = (kh * g.wp + kw) * g.cstride + q * 8;
+      koff = (kh * g.wp + kw) * g.cstride + (q % g.pc8) * 8;  // within its pass's staging
     }
     ktab[gi] = koff;
   }
   __syncthreads();  // weights regrouped; the raw copy region is free
 
   auto vstore = [&](uint16_t* xl, int it, const BandItem<XT>& v) {
-    const int rest = (int)fdiv((uint32_t)it, g.fd_c8), q = it - rest * g.c8;
+    const int rest = (int)fdiv((uint32_t)it, g.fd_pc8), q = it - rest * g.pc8;
     const int r = (int)fdiv((uint32_t)rest, g.fd_w4), cg = rest - r * W4;
     const int col0 = cg * 4 + g.pw;  // staged column of input column 4*cg
 #pragma unroll
@@ -652,36 +657,15 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
           make_uint4(pk[0], pk[1], pk[2], pk[3]);
     }
   };
-  // stage band b into buffer xl (from the registers when IPT > 0)
-  auto stage = [&](const BandRegs<IPT, XT>& rg, int b, uint16_t* xl) {
-    if (g.vec) {
-      if constexpr (IPT > 0) {
-#pragma unroll
-        for (int k = 0; k < IPT; ++k) {
-          const int it = tid + k * THREADS;
-          if (it < g.vitems) vstore(xl, it, rg.v[k]);
-        }
-      } else {
-        // two items a pass, both items' loads issued before either is
-        // stored: one memory latency per pass
-        for (int it = tid; it < g.vitems; it += 2 * THREADS) {
-          BandItem<XT> v[2];
-          const bool two = it + THREADS < g.vitems;
-          vload(b, it, v[0]);
-          if (two) vload(b, it + THREADS, v[1]);
-          vstore(xl, it, v[0]);
-          if (two) vstore(xl, it + THREADS, v[1]);
-        }
-      }
-    }
-    // element-wise columns: the padding columns, or every column when the
-    // rows are not 16-byte aligned
+  // element-wise columns of pass ps of band b: the padding columns, or
+  // every column when the rows are not 16-byte aligned
+  auto stage_border = [&](int b, int ps, uint16_t* xl) {
     const int ncols = g.vec ? g.nborder : g.wp;
     const int left = min(g.pw, g.wp);
-    const int items = g.rows_in * ncols * g.c8;
+    const int items = g.rows_in * ncols * g.pc8;
     const int ih0 = b * g.R * g.sh - g.ph;
     for (int it = tid; it < items; it += THREADS) {
-      const int rest = (int)fdiv((uint32_t)it, g.fd_c8), q = it - rest * g.c8;
+      const int rest = (int)fdiv((uint32_t)it, g.fd_pc8), q = it - rest * g.pc8;
       const int r = (int)fdiv((uint32_t)rest, g.fd_nc), bi = rest - r * ncols;
       const int col = !g.vec ? bi : (bi < left ? bi : g.pw + g.W + (bi - left));
       const int hi = pad_index(ih0 + r, g.H, g.pad_mode);
@@ -689,7 +673,7 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
       float v[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const int c = q * 8 + j;
+        const int c = (ps * g.pc8 + q) * 8 + j;
         v[j] = (hi >= 0 && wi >= 0 && c < g.C) ? x_val<XT>(x, xn + c * HW + (int64_t)hi * g.W + wi)
                                                : 0.0f;
       }
@@ -703,6 +687,63 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
           make_uint4(pk[0], pk[1], pk[2], pk[3]);
     }
   };
+  // The 16-byte-load items of pass ps > 0 of band b, while the products'
+  // accumulators are live: four channels' loads in flight at a time, written
+  // as channel pairs (4-byte LDS stores), so few registers hold staging data.
+  auto stage_quads = [&](int b, int ps, uint16_t* xl) {
+    for (int it = tid; it < g.vitems; it += THREADS) {
+      const int rest = (int)fdiv((uint32_t)it, g.fd_pc8), q = it - rest * g.pc8;
+      const int r = (int)fdiv((uint32_t)rest, g.fd_w4), cg = rest - r * W4;
+      const int hi = pad_index(b * g.R * g.sh - g.ph + r, g.H, g.pad_mode);
+      const int col0 = cg * 4 + g.pw;  // staged column of input column 4*cg
+      const bool used = col0 < g.wp && hi >= 0;
+      uint16_t* d = &xl[(r * g.wp + col0) * g.cstride + q * 8];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        f32x4 v[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int c = (ps * g.pc8 + q) * 8 + 4 * h + j;
+          v[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+          if (used && c < g.C) v[j] = x4_f32<XT>(x, xn + c * HW + (int64_t)hi * g.W + cg * 4);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (col0 + i >= g.wp) break;
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            const f32x2 f = {v[2 * j][i], v[2 * j + 1][i]};
+            *reinterpret_cast<uint32_t*>(d + i * g.cstride + 4 * h + 2 * j) =
+                __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));
+          }
+        }
+      }
+    }
+  };
+  // stage pass ps of band b into buffer xl (from the registers when IPT > 0)
+  auto stage = [&](const BandRegs<IPT, XT>& rg, int b, int ps, uint16_t* xl) {
+    if (g.vec) {
+      if constexpr (IPT > 0) {
+#pragma unroll
+        for (int k = 0; k < IPT; ++k) {
+          const int it = tid + k * THREADS;
+          if (it < g.vitems) vstore(xl, it, rg.v[k]);
+        }
+      } else {
+        // two items a pass, both items' loads issued before either is
+        // stored: one memory latency per pass
+        for (int it = tid; it < g.vitems; it += 2 * THREADS) {
+          BandItem<XT> v[2];
+          const bool two = it + THREADS < g.vitems;
+          vload(b, ps, it, v[0]);
+          if (two) vload(b, ps, it + THREADS, v[1]);
+          vstore(xl, it, v[0]);
+          if (two) vstore(xl, it + THREADS, v[1]);
+        }
+      }
+    }
+    stage_border(b, ps, xl);
+  };
 
   const float s = product_scale(w_scale, x_scale);
   const float inv_o = epi_inv_scale(ep);
@@ -714,8 +755,9 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
   const int steps = g.gpr >> 2;
   const bf16x8 zero8 = __builtin_bit_cast(bf16x8, make_uint4(0u, 0u, 0u, 0u));
 
-  // MFMA and store of band b from buffer xl; wave w takes M tiles w, w+4, ...
-  auto compute = [&](int b, const uint16_t* xl) {
+  // MFMA and store of band b from buffer xl, which holds pass 0's staging;
+  // wave w takes M tiles w, w+4, ...
+  auto compute = [&](int b, uint16_t* xl) {
     const int oh0 = b * g.R;
     const int P = min(g.R, g.OH - oh0) * g.OW;
     const int mtiles = (P + 15) >> 4;
@@ -754,10 +796,23 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
             acc[m][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[m], bf[t], acc[m][t], 0, 0, 0);
       }
     };
-    for (int st = 0; st < steps; ++st) {
-      bf16x8 af[4], bf[4];
-      frags(st, af, bf);
-      mma(af, bf);
+    // pass ps owns the K steps st = ps (mod passes): the weights' (tap, 8
+    // channels) groups run tap-major, so one step is one tap's four channel
+    // groups of one pass (at most two passes)
+    auto mma_pass = [&](int ps) {
+      for (int st = ps; st < steps; st += g.passes) {
+        bf16x8 af[4], bf[4];
+        frags(st, af, bf);
+        mma(af, bf);
+      }
+    };
+    mma_pass(0);
+    if (g.passes > 1) {
+      __syncthreads();  // every wave's fragment reads of pass 0 are done
+      if (g.vec) stage_quads(b, 1, xl);
+      stage_border(b, 1, xl);
+      __syncthreads();
+      mma_pass(1);
     }
     // lane holds pixels 4*lg .. 4*lg+3 of channel lr of each tile; its four
     // channels' epilogue constants are loaded once
@@ -922,7 +977,7 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
   };
 
   uint16_t* xl = reinterpret_cast<uint16_t*>(lds + g.x_off);
-  stage(r0, band, xl);
+  stage(r0, band, 0, xl);
   __syncthreads();
   compute(band, xl);
   epi_amax_commit(ep, am);
@@ -933,19 +988,25 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
 // number of 16-byte-load items per thread held in registers (0: loaded while
 // staging).
 template <int WT>
-bool band_geometry(const ConvGeom& cg, BandGeom& b, size_t& lds, int* ipt, int out_dtype) {
+bool band_geometry_pass(const ConvGeom& cg, int pc8, BandGeom& b, size_t& lds, int* ipt,
+                        int out_dtype) {
   if (cg.C > MAX_CB || cg.OW > 256) return false;
   b = BandGeom{};
   b.N = cg.N; b.C = cg.C; b.H = cg.H; b.W = cg.W; b.C_out = cg.C_out; b.KH = cg.KH;
   b.KW = cg.KW; b.sh = cg.sh; b.sw = cg.sw; b.ph = cg.ph; b.pw = cg.pw; b.pad_mode = cg.pad_mode;
   b.OH = cg.OH; b.OW = cg.OW;
   b.c8 = (cg.C + 7) / 8;
+  b.pc8 = std::min(pc8, b.c8);
+  b.passes = (b.c8 + b.pc8 - 1) / b.pc8;
+  if (b.passes > 1 && b.c8 % b.pc8 != 0) return false;
   // pixel stride in LDS of 8 mod 16 bf16 (4 mod 8 banks): the 16 pixels of a
   // fragment read fall in distinct banks
-  b.cstride = (b.c8 % 2 == 0) ? b.c8 * 8 + 8 : b.c8 * 8;
+  b.cstride = (b.pc8 % 2 == 0) ? b.pc8 * 8 + 8 : b.pc8 * 8;
   b.taps = cg.KH * cg.KW;
   b.groups = b.taps * b.c8;
   b.gpr = (b.groups + 3) / 4 * 4;
+  // each K step (four groups) within one pass: a tap's pc8 groups in whole steps
+  if (b.passes > 1 && b.pc8 % 4 != 0) return false;
   // bands of whole output rows, at most 256 pixels, balanced across the image
   const int64_t npix = (int64_t)cg.OH * cg.OW;
   const int nb = (int)((npix + 255) / 256);
@@ -957,8 +1018,9 @@ bool band_geometry(const ConvGeom& cg, BandGeom& b, size_t& lds, int* ipt, int o
   b.wp = (cg.OW - 1) * cg.sw + cg.KW;
   b.vec = (cg.W % 4) == 0;
   b.nborder = std::min(cg.pw, b.wp) + std::max(0, b.wp - cg.pw - cg.W);
-  b.vitems = b.vec ? b.rows_in * (cg.W / 4) * b.c8 : 0;
+  b.vitems = b.vec ? b.rows_in * (cg.W / 4) * b.pc8 : 0;
   b.fd_c8 = fast_div((uint32_t)b.c8);
+  b.fd_pc8 = fast_div((uint32_t)b.pc8);
   b.fd_w4 = fast_div((uint32_t)std::max(1, cg.W / 4));
   b.fd_ow = fast_div((uint32_t)cg.OW);
   b.fd_kw = fast_div((uint32_t)cg.KW);
@@ -992,6 +1054,25 @@ bool band_geometry(const ConvGeom& cg, BandGeom& b, size_t& lds, int* ipt, int o
   }
   lds = b.x_off + region;
   return lds <= 80 * 1024;
+}
+
+// The band geometry: the whole band's channels staged at once, or, when that
+// leaves room for fewer than four workgroups per CU (64 channels), in two
+// passes of 32 channels over a smaller staging region.
+template <int WT>
+bool band_geometry(const ConvGeom& cg, BandGeom& b, size_t& lds, int* ipt, int out_dtype) {
+  if (!band_geometry_pass<WT>(cg, MAX_CB / 8, b, lds, ipt, out_dtype)) return false;
+  if (b.c8 == 8 && lds > BAND_LDS_FOUR) {
+    BandGeom b2;
+    size_t lds2 = 0;
+    int ipt2 = 0;
+    if (band_geometry_pass<WT>(cg, 4, b2, lds2, &ipt2, out_dtype) && lds2 <= BAND_LDS_FOUR) {
+      b = b2;
+      lds = lds2;
+      *ipt = ipt2;
+    }
+  }
+  return true;
 }
 
 template <int WT, int XT, int IPT, bool K9>
