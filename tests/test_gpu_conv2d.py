@@ -95,6 +95,12 @@ def test_golden_fixture_all_padding_modes(golden):
     # batch x channel groups large enough for two 8-channel groups per
     # workgroup, the last group partial (37 = 4 x 8 + 5)
     (208, 2, 6, 6, 37, 3, 3, 1, 1, 1, 1),
+    # one output channel (an MFMA tile's 16 columns hold 1): 5 x 5 and 3 x 8
+    # windows, C no multiple of 8, W no multiple of 4
+    (2, 32, 12, 16, 1, 3, 3, 1, 1, 1, 1),
+    (2, 5, 9, 8, 1, 5, 5, 1, 1, 2, 2),
+    (1, 70, 10, 12, 1, 3, 8, 1, 1, 1, 3),
+    (2, 16, 7, 7, 1, 3, 3, 1, 1, 1, 1),
 ])
 def test_shapes_and_modes_vs_oracle(wdt, mode, case):
     N, C, H, W, C_out, KH, KW, sh, sw, ph, pw = case
@@ -110,6 +116,29 @@ def test_shapes_and_modes_vs_oracle(wdt, mode, case):
     r2 = R.conv2d(x.astype(np.float64), wdeq.astype(np.float64), (sh, sw), (ph, pw), mode,
                   b.astype(np.float64))
     assert np.allclose(r, r2, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("case", [
+    # (N, C, H, W, KH, KW, ph, pw, mode)
+    (4, 32, 28, 28, 3, 3, 1, 1, "zeros"),     # config [5] conv1's input gradient, 4 images
+    (2, 37, 13, 20, 2, 5, 0, 2, "reflect"),   # C no multiple of 8
+    (3, 8, 30, 8, 7, 7, 3, 3, "circular"),    # 7 x 7, rows wider than the image's 8 columns
+    (1, 6, 70, 4, 3, 1, 1, 0, "replicate"),   # narrow rows: many rows per band
+])
+def test_one_output_channel_exact_operands(case):
+    """C_out = 1 (the input gradient of a one-channel convolution is one)
+    against the fp64 convolution of the operands the kernel multiplies (x
+    rounded to bf16, the dequantized E4M3 weight) within 1e-5: a staging slip
+    (a row, column or channel dropped or shifted) costs far more."""
+    N, C, H, W, KH, KW, ph, pw, mode = case
+    print(f"conv2d C_out=1 {case}", flush=True)
+    rng = np.random.default_rng(sum(case[:8]))
+    x = rng.standard_normal((N, C, H, W)).astype(np.float32)
+    w = (rng.standard_normal((1, C, KH, KW)) * 0.3).astype(np.float32)
+    codes, s, wdeq = quantize_weights(w, "e4m3")
+    y = run_conv(x, codes, "e4m3", w.shape, s, None, (1, 1), (ph, pw), mode)
+    r = R.conv2d(bf16_round(x).astype(np.float64), wdeq.astype(np.float64), (1, 1), (ph, pw), mode)
+    assert normwise(y, r) <= 1e-5
 
 
 def test_config5_mnist_two_layers():

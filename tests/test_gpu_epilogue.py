@@ -197,6 +197,9 @@ CONV_CASES = [
     ("e4m3", (2, 3, 7, 10), 9, (3, 5), (1, 1), (1, 2), "reflect"),    # small-C, OW % 4 != 0
     # small-C with two 8-channel groups per workgroup and a partial last group
     ("e2m1", (208, 2, 6, 6), 37, (3, 3), (1, 1), (1, 1), "zeros"),
+    # one output channel, C no multiple of 8
+    ("e4m3", (2, 32, 12, 16), 1, (3, 3), (1, 1), (1, 1), "reflect"),
+    ("e2m1", (3, 37, 9, 8), 1, (2, 5), (1, 1), (1, 2), "zeros"),
 ]
 
 
