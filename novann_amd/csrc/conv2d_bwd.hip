@@ -790,6 +790,216 @@ __global__ __launch_bounds__(DR_WAVES * 64) void dweight_rows_kernel(
 
 constexpr int DR_MAX_XJ = 5;
 
+// grad_weight and grad_bias of a one-input-channel convolution (config [5]'s
+// first layer), stride 1, at most 16 window taps: as a GEMM, M = the output
+// channels, N = the taps, K = the output pixels, so v_mfma_f32_16x16x32_bf16
+// tiles fill (the general kernel's N = (c, kh, kw) would hold 9 of 64
+// columns).  A unit is a band of RB output rows of one image; a workgroup
+// walks a chunk of units and writes one partial.  Per unit the band's grad
+// (16-byte loads of 4 pixels, bf16 in Gs[co][r * OWP + ow], rows padded to
+// OWP with zeros) and its RB + KH - 1 input rows (4-byte loads, the padding
+// mode resolved, Xs[rr][col], input column 0 at staged column pw) go to LDS
+// from registers loaded during the previous unit's products; wave w
+// multiplies 16-channel tile w: A = Gs (8 pixels of a channel, one 16-byte
+// read), B = Xs[r + kh][ow + kw ..] (8 columns of tap (kh, kw) read as 5
+// dwords, realigned with v_alignbit for odd kw; taps past KH*KW are 0).
+// grad_bias: each lane adds its grad quads ((v0 + v1) + (v2 + v3)) per unit
+// in unit order, then a channel's quads are added in band order through
+// LDS.  Masked loads (rows past the image, padding, channels past C_out)
+// carry an offset past the buffer and read 0.
+constexpr int D1_GQ = 8;   // grad quads per lane and unit, at most
+constexpr int D1_CHUNKS = 1024;  // partials (workgroups), at most
+constexpr int D1_XS = 2;   // staged input slots per lane and unit, at most
+
+struct D1Geom {
+  int RB, bands, OWP, XW, rows_in, taps, co_tiles, gitems, xslots;
+};
+
+template <int MODE>
+__global__ __launch_bounds__(256) void dweight_c1_kernel(
+    const float* __restrict__ grad, const float* __restrict__ x, float* __restrict__ part,
+    float* __restrict__ bpart, BwdGeom g, D1Geom d, int chunks) {
+  constexpr bool WGT = MODE != 2, BIAS = MODE != 0;
+  extern __shared__ __attribute__((aligned(16))) uint8_t d1_lds[];
+  const int GPW = d.RB * d.OWP + 8;  // Gs row pitch (bf16)
+  __bf16* Gs = reinterpret_cast<__bf16*>(d1_lds);
+  __bf16* Xs = Gs + d.co_tiles * 16 * GPW;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int P = g.OH * g.OW, HW = g.H * g.W, OW4 = g.OW / 4;
+  const int per_co = d.RB * OW4;  // grad quads of one channel in a band
+  const int64_t U = (int64_t)g.N * d.bands;
+  const int64_t u_begin = U * blockIdx.x / chunks, u_end = U * (blockIdx.x + 1) / chunks;
+
+  if constexpr (WGT) {  // Gs padding columns and rows past C_out stay 0
+    uint32_t* z = reinterpret_cast<uint32_t*>(d1_lds);
+    for (int i = tid; i < (d.co_tiles * 16 * GPW + d.rows_in * d.XW) / 2; i += 256) z[i] = 0u;
+  }
+  // this lane's grad quads: item it = (channel co, band row r, quad q)
+  uint32_t gb[D1_GQ];
+  int grow[D1_GQ], gdst[D1_GQ];
+#pragma unroll
+  for (int u = 0; u < D1_GQ; ++u) {
+    const int it = tid + 256 * u;
+    const int co = it / per_co, rest = it - co * per_co;
+    const int r = rest / OW4, q = rest - r * OW4;
+    const bool live = it < d.gitems;
+    gb[u] = (uint32_t)(co * P + 4 * q) * 4u;
+    grow[u] = live ? r : (1 << 30);
+    gdst[u] = live ? co * GPW + r * d.OWP + 4 * q : -1;
+  }
+  // this lane's staged input slots: slot e = (staged row rr, column col)
+  int xrr[D1_XS], xwi[D1_XS];
+#pragma unroll
+  for (int j = 0; j < D1_XS; ++j) {
+    const int e = tid + 256 * j;
+    const int rr = e / d.XW, col = e - rr * d.XW;
+    xrr[j] = e < d.xslots ? rr : (1 << 30);
+    xwi[j] = (e < d.xslots && col < g.OW + g.KW - 1) ? pad_index(col - g.pw, g.W, g.pad_mode) : -1;
+  }
+  f32x4 gv[D1_GQ];
+  float xv[D1_XS];
+  auto load = [&](int64_t unit) {
+    const int n = (int)(unit / d.bands), b = (int)(unit - (int64_t)n * d.bands);
+    const int oh0 = b * d.RB, rows_left = g.OH - oh0;
+    const __amdgpu_buffer_rsrc_t gr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(grad + (int64_t)n * g.C_out * P), (short)0, g.C_out * P * 4, DR_BUF3);
+    const uint32_t band = (uint32_t)(oh0 * g.OW) * 4u;
+#pragma unroll
+    for (int u = 0; u < D1_GQ; ++u) {
+      const uint32_t off = grow[u] < rows_left ? gb[u] + band + (uint32_t)(grow[u] * g.OW) * 4u : DR_OOB;
+      gv[u] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(gr, off, 0, 0));
+    }
+    if constexpr (WGT) {
+      const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<float*>(x + (int64_t)n * HW), (short)0, HW * 4, DR_BUF3);
+      const int rows_read = (rows_left < d.RB ? rows_left : d.RB) + g.KH - 1;
+#pragma unroll
+      for (int j = 0; j < D1_XS; ++j) {
+        const int hi = (xrr[j] < rows_read && xwi[j] >= 0)
+                           ? pad_index(oh0 - g.ph + xrr[j], g.H, g.pad_mode) : -1;
+        const uint32_t off = hi >= 0 ? (uint32_t)(hi * g.W + xwi[j]) * 4u : DR_OOB;
+        xv[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xr, off, 0, 0));
+      }
+    }
+  };
+
+  float bq[D1_GQ];
+#pragma unroll
+  for (int u = 0; u < D1_GQ; ++u) bq[u] = 0.0f;
+  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  const int tap = lane & 15, kq = lane >> 4;  // B: tap column, 8-pixel group of the k-step
+  const int kh = tap / g.KW, kw = tap - kh * g.KW;
+  const bool tap_live = tap < d.taps;
+  const bf16x8 zero8 = __builtin_bit_cast(bf16x8, make_uint4(0u, 0u, 0u, 0u));
+  const int ksteps = d.RB * d.OWP / 32;
+  if (u_begin < u_end) load(u_begin);
+  for (int64_t unit = u_begin; unit < u_end; ++unit) {
+    __syncthreads();  // the previous unit's fragment reads are done
+    if constexpr (BIAS) {
+#pragma unroll
+      for (int u = 0; u < D1_GQ; ++u) bq[u] += (gv[u][0] + gv[u][1]) + (gv[u][2] + gv[u][3]);
+    }
+    if constexpr (WGT) {
+#pragma unroll
+      for (int u = 0; u < D1_GQ; ++u) {
+        if (gdst[u] < 0) continue;
+        const f32x2 lo = {gv[u][0], gv[u][1]}, hi = {gv[u][2], gv[u][3]};
+        *reinterpret_cast<u32x2b*>(Gs + gdst[u]) =
+            u32x2b{__builtin_bit_cast(uint32_t, __builtin_convertvector(lo, bf16x2)),
+                   __builtin_bit_cast(uint32_t, __builtin_convertvector(hi, bf16x2))};
+      }
+#pragma unroll
+      for (int j = 0; j < D1_XS; ++j) {
+        const int e = tid + 256 * j;
+        if (e < d.xslots) Xs[e] = (__bf16)xv[j];
+      }
+    }
+    if (unit + 1 < u_end) load(unit + 1);
+    if constexpr (WGT) {
+      __syncthreads();
+      if (wave < d.co_tiles) {
+        const __bf16* ga = Gs + (wave * 16 + (lane & 15)) * GPW + 8 * kq;
+        for (int st = 0; st < ksteps; ++st) {
+          const int k0 = st * 32;
+          const int r = k0 / d.OWP, ow0 = k0 - r * d.OWP + 8 * kq;
+          const bf16x8 a = *reinterpret_cast<const bf16x8*>(ga + k0);
+          bf16x8 bfr = zero8;
+          if (tap_live) {
+            const uint32_t* p = reinterpret_cast<const uint32_t*>(Xs) +
+                                (((r + kh) * d.XW + ow0 + kw) >> 1);
+            uint32_t dd[5];
+#pragma unroll
+            for (int i = 0; i < 5; ++i) dd[i] = p[i];
+            uint32_t bw[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) bw[i] = (kw & 1) ? __builtin_amdgcn_alignbit(dd[i + 1], dd[i], 16) : dd[i];
+            bfr = __builtin_bit_cast(bf16x8, bw);
+          }
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bfr, acc, 0, 0, 0);
+        }
+      }
+    }
+  }
+  if constexpr (BIAS) {
+    // a channel's quads added in band order
+    float* red = reinterpret_cast<float*>(d1_lds);
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < D1_GQ; ++u) {
+      const int it = tid + 256 * u;
+      if (it < d.gitems) red[it] = bq[u];
+    }
+    __syncthreads();
+    if (tid < g.C_out) {
+      float v = 0.0f;
+      for (int i = 0; i < per_co; ++i) v += red[tid * per_co + i];
+      bpart[(int64_t)blockIdx.x * g.C_out + tid] = v;
+    }
+  }
+  if constexpr (WGT) {
+    // lane holds channels 16 w + 4 kq + i (i < 4) of tap `tap`: the partial
+    // is [chunk][co][tap], grad_weight's own layout (one input channel)
+    if (wave < d.co_tiles && tap_live) {
+      float* pc = part + (int64_t)blockIdx.x * g.C_out * d.taps;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int co = wave * 16 + 4 * kq + i;
+        if (co < g.C_out) pc[co * d.taps + tap] = acc[i];
+      }
+    }
+  }
+}
+
+// The one-input-channel path applies (its LDS bytes), or 0.
+size_t c1_geometry(const BwdGeom& g, D1Geom& d) {
+  const int taps = g.KH * g.KW;
+  if (g.C != 1 || g.sh != 1 || g.sw != 1 || taps > 16 || g.KW > 8 || g.OW % 4 != 0 ||
+      g.OW > 64 || g.C_out > 64 || g.OH < 1)
+    return 0;
+  if ((int64_t)g.C_out * g.OH * g.OW * 4 >= ((int64_t)1 << 30)) return 0;
+  d = D1Geom{};
+  d.OWP = g.OW <= 32 ? 32 : 64;
+  d.taps = taps;
+  d.co_tiles = (g.C_out + 15) / 16;
+  // band rows: a multiple of 32 pixels per channel row, the band's grad quads
+  // within D1_GQ per lane and its input slots within D1_XS per lane
+  d.RB = std::min(g.OH, 8);
+  d.XW = d.OWP + 8;
+  for (;; --d.RB) {
+    if (d.RB < 1) return 0;
+    d.rows_in = d.RB + g.KH - 1;
+    d.gitems = g.C_out * d.RB * (g.OW / 4);
+    d.xslots = d.rows_in * d.XW;
+    if (d.gitems <= 256 * D1_GQ && d.xslots <= 256 * D1_XS) break;
+  }
+  d.bands = (g.OH + d.RB - 1) / d.RB;
+  // (+16 bytes: a fragment read of the last staged row's last columns runs
+  // one dword past them)
+  const size_t bytes = ((size_t)d.co_tiles * 16 * (d.RB * d.OWP + 8) + (size_t)d.rows_in * d.XW) * 2 + 16;
+  return std::max(bytes, (size_t)d.gitems * 4);
+}
+
+
 // The stride-1 rows path applies (its LDS bytes, input items or slots per
 // lane XJ, and whether its staging is VEC), or 0.  aligned: grad and x start
 // on 16 bytes (always through the C ABI, which requires it).
@@ -892,6 +1102,9 @@ ConvBwdWs conv2d_bwd_workspace(int64_t N, int64_t C, int64_t C_out, int KH, int 
   want = std::min<int64_t>(want, DW_MAX_CHUNKS);
   if (want >= 8) want = (want + 7) / 8 * 8;
   (void)N;
+  // one input channel: room for up to D1_CHUNKS partials of C_out x taps
+  // (the one-input-channel kernel's units, one per workgroup)
+  if (C == 1) want = std::max<int64_t>(want, D1_CHUNKS);
   ws.chunks = (int)want;
   ws.wf = 0;
   ws.part = a256(((size_t)C_out * ckk * dtype_bits(w_dtype) + 7) / 8);
@@ -909,6 +1122,37 @@ static int dweight_launch(const float* grad, const float* x, const BwdGeom& g, i
   if (!grad_weight && !grad_bias) return NOVAQ_OK;
   const int64_t C = g.C, C_out = g.C_out;
   const int64_t ckk = C * g.KH * g.KW;
+  // one input channel: the taps as the GEMM's N (a bias-only call runs the
+  // bias-only mode over the same chunks, so its bits match a full call's)
+  D1Geom d1{};
+  const size_t c1_lds = c1_geometry(g, d1);
+  if (c1_lds) {
+    float* part = reinterpret_cast<float*>(base + ws.part);
+    float* bpart = reinterpret_cast<float*>(base + ws.bpart);
+    const int64_t units = (int64_t)g.N * d1.bands;
+    const int64_t rchunks = std::max<int64_t>(1, std::min<int64_t>(ws.chunks, units));
+    if (rchunks > 0x7FFFFFFF) return NOVAQ_EINVAL;
+    const int mode = grad_weight ? (grad_bias ? 1 : 0) : 2;
+    const dim3 grid((unsigned)rchunks);
+    if (mode == 0)
+      hipLaunchKernelGGL((dweight_c1_kernel<0>), grid, dim3(256), c1_lds, stream, grad, x, part, bpart, g, d1, (int)rchunks);
+    else if (mode == 1)
+      hipLaunchKernelGGL((dweight_c1_kernel<1>), grid, dim3(256), c1_lds, stream, grad, x, part, bpart, g, d1, (int)rchunks);
+    else
+      hipLaunchKernelGGL((dweight_c1_kernel<2>), grid, dim3(256), c1_lds, stream, grad, x, part, bpart, g, d1, (int)rchunks);
+    fa.rows = rchunks;
+    if (grad_weight) {
+      fa.part = part;
+      fa.gw = grad_weight;
+      fa.wcols = C_out * ckk;
+    }
+    if (grad_bias) {
+      fa.bpart = bpart;
+      fa.gb = grad_bias;
+      fa.bcols = C_out;
+    }
+    return check_launch();
+  }
   // stride-1 convolutions with short rows: grad_weight and grad_bias on the
   // rows kernel (a bias-only call runs its bias-only mode over the same
   // chunks, so its bits match a full call's)
@@ -1028,7 +1272,7 @@ int conv2d_backward_launch(const float* grad, const float* x, int64_t N, int64_t
   // a multiple of 8 when at least 8 (never above ws.chunks, itself such a
   // multiple); chunks past the last stage add zeros
   const int64_t T = N * (((int64_t)g.OH * g.OW + DW_K - 1) / DW_K);
-  int64_t chunks = std::min<int64_t>(ws.chunks, std::max<int64_t>(T, 1));
+  int64_t chunks = std::min<int64_t>(std::min<int64_t>(ws.chunks, DW_MAX_CHUNKS), std::max<int64_t>(T, 1));
   if (chunks >= 8) chunks = (chunks + 7) / 8 * 8;
   switch (w_dtype) {
     case E4M3: case E5M2: case E2M1: case BF16: case F16: case F32: break;

@@ -106,7 +106,7 @@ VEC_GEOMETRIES = [
 ]
 
 
-def backward_bits(g, x, N, C, H, W, w, C_out, KH, KW, pad, outs):
+def backward_bits(g, x, N, C, H, W, w, C_out, KH, KW, pad, outs, mode="zeros"):
     """One C ABI call (grad_weight and / or grad_bias per outs) -> host arrays."""
     lib = _lib.load()
     st = torch.cuda.current_stream().cuda_stream
@@ -117,7 +117,7 @@ def backward_bits(g, x, N, C, H, W, w, C_out, KH, KW, pad, outs):
     gb = torch.full((C_out,), 7.0, device="cuda")
     _lib.check(lib.novaq_conv2d_backward(
         g.data_ptr(), x.data_ptr(), N, C, H, W, w.codes.data_ptr(), code, w.scale.data_ptr(),
-        C_out, KH, KW, 1, 1, pad[0], pad[1], _lib.PAD_MODES["zeros"], None,
+        C_out, KH, KW, 1, 1, pad[0], pad[1], _lib.PAD_MODES[mode], None,
         gw.data_ptr() if "w" in outs else None, gb.data_ptr() if "b" in outs else None,
         ws.data_ptr(), nbytes, st), "conv2d backward")
     torch.cuda.synchronize()
@@ -155,6 +155,42 @@ def test_conv2d_backward_rows_vec_staging(geom):
     assert normwise(wv.view(np.float32), rw) <= 1e-5
     assert np.array_equal(backward_bits(g, x, N, C, H, W, w, C_out, KH, KW, pad, "w")[0], wv)
     assert np.array_equal(backward_bits(g, x, N, C, H, W, w, C_out, KH, KW, pad, "b")[1], bv)
+
+
+# one input channel, stride 1, at most 16 taps, OW a multiple of 4 and at
+# most 64, C_out <= 64: grad_weight with the taps as the GEMM's N
+# (N, H, W, C_out, KH, KW, pad, mode)
+C1_GEOMETRIES = [
+    (2, 12, 16, 8, 3, 3, (1, 1), "zeros"),
+    (3, 9, 20, 40, 3, 5, (1, 2), "reflect"),      # 15 taps, three channel tiles
+    (1, 17, 39, 64, 4, 4, (2, 2), "replicate"),   # 16 taps, 40-pixel rows (two k-steps a row)
+    (2, 7, 8, 33, 2, 3, (0, 1), "circular"),      # a partial last channel tile
+    (5, 30, 28, 32, 3, 3, (1, 1), "zeros"),       # config [5] conv1's shape, 5 images
+]
+
+
+@pytest.mark.parametrize("geom", C1_GEOMETRIES, ids=lambda g: "x".join(map(str, g[:6])))
+def test_conv2d_backward_one_input_channel(geom):
+    """Against the oracle, grad_weight against the fp64 product of the
+    operands the MFMAs multiply (grad and input rounded to bf16) within 1e-5,
+    and a bias-only and a weight-only call give the full call's bits."""
+    N, H, W, C_out, KH, KW, pad, mode = geom
+    check_case(N, 1, H, W, C_out, KH, KW, (1, 1), pad, "e2m1", mode=mode)
+    rng = np.random.default_rng(sum(geom[:6]) + 3)
+    OH, OW = H + 2 * pad[0] - KH + 1, W + 2 * pad[1] - KW + 1
+    assert OW % 4 == 0
+    xh = rng.standard_normal((N, 1, H, W)).astype(np.float32)
+    gh = rng.standard_normal((N, C_out, OH, OW)).astype(np.float32)
+    x, g = torch.from_numpy(xh).cuda(), torch.from_numpy(gh).cuda()
+    w = QuantizedParameters.from_float(
+        (rng.standard_normal((C_out, 1, KH, KW)) * 0.3).astype(np.float32), "e2m1")
+    wv, bv = backward_bits(g, x, N, 1, H, W, w, C_out, KH, KW, pad, "wb", mode)
+    wdeq = w.dequantize().cpu().numpy().astype(np.float64).reshape(C_out, 1, KH, KW)
+    _, rw, _ = R.conv2d_backward(bf16_round(gh).astype(np.float64),
+                                 bf16_round(xh).astype(np.float64), wdeq, (1, 1), pad, mode)
+    assert normwise(wv.view(np.float32), rw) <= 1e-5
+    assert np.array_equal(backward_bits(g, x, N, 1, H, W, w, C_out, KH, KW, pad, "w", mode)[0], wv)
+    assert np.array_equal(backward_bits(g, x, N, 1, H, W, w, C_out, KH, KW, pad, "b", mode)[1], bv)
 
 
 @pytest.mark.parametrize("mode", ["zeros", "reflect", "replicate", "circular"])
