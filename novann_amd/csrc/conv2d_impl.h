@@ -1094,6 +1094,192 @@ int launch_band(const uint8_t* x, const float* x_scale, const void* w, const flo
   return check_launch();
 }
 
+// One output channel (C_out = 1, stride 1, zero padding, at most 16 taps,
+// KW <= 8, C <= 64, W a multiple of 4: the input gradient of a one-channel
+// convolution).  As the band kernel's GEMM its N would hold 1 of an MFMA
+// tile's 16 output channels; instead the taps are N.  A workgroup owns a
+// band of R output rows of one image and stages its R + KH - 1 input rows
+// channel-last in bf16 as the band kernel does (16-byte loads of 4 columns of
+// 8 channel planes, transposed in registers; padding columns and rows 0);
+// then Y[q][t] = sum over c of x[c][q] w[c][t] for every staged pixel q on
+// v_mfma_f32_16x16x32_bf16 (M = staged pixels, K = channels in steps of 32,
+// N = taps; wave w takes pixel tiles w, w + 4, ...), and a lane makes output
+// pixel p as the sum over taps, in tap order, of Y[p + (kh, kw)][t]; the
+// epilogue as the other kernels.  The operands are the MFMA paths' (x and W
+// rounded to bf16: products exact in fp32).
+struct Co1Geom {
+  int N, C, H, W, KH, KW, ph, pw, OH, OW;
+  int R, bands, rows_in, wp, npin;  // band rows, bands per image, staged rows / columns / pixels
+  int c8, ksteps, cstride, taps;    // 8-channel groups, K steps of 32, bf16 per staged pixel
+  int vitems;                       // 16-byte-load items per band
+  FastDiv fd_c8, fd_w4, fd_ow, fd_kw;
+};
+constexpr int CO1_MT = 8;   // pixel tiles per wave, at most (512 staged pixels)
+constexpr int CO1_YP = 17;  // fp32 pitch of a staged pixel's Y row (odd: fewer bank conflicts)
+
+template <int WT, int XT>
+__global__ __launch_bounds__(256) void conv2d_co1_kernel(
+    const uint8_t* __restrict__ x, const float* __restrict__ x_scale, const uint8_t* __restrict__ w,
+    const float* __restrict__ w_scale, Epilogue ep, void* __restrict__ y, Co1Geom g) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int WS = g.ksteps * 32 + 8;                                 // Ws row pitch (bf16)
+  uint16_t* ws = reinterpret_cast<uint16_t*>(lds);                 // [16 taps][WS]
+  uint16_t* xs = ws + 16 * WS;                                     // [npin][cstride]
+  float* ys = reinterpret_cast<float*>(xs);                        // [npin][CO1_YP] (after the products)
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int band = blockIdx.x % g.bands, n = blockIdx.x / g.bands;
+  const int oh0 = band * g.R;
+  const int64_t HW = (int64_t)g.H * g.W;
+  const int64_t xn = (int64_t)n * g.C * HW;
+  const int W4 = g.W >> 2;
+
+  // the band's 16-byte-load items into registers first: it = (staged row r,
+  // column group cg, channel group q)
+  constexpr int MAXI = 2;
+  f32x4 v[MAXI][8];
+#pragma unroll
+  for (int k = 0; k < MAXI; ++k) {
+    const int it = tid + 256 * k;
+    const int rest = (int)fdiv((uint32_t)it, g.fd_c8), q = it - rest * g.c8;
+    const int r = (int)fdiv((uint32_t)rest, g.fd_w4), cg = rest - r * W4;
+    const int hi = oh0 - g.ph + r;
+    const bool live = it < g.vitems && hi >= 0 && hi < g.H;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int c = q * 8 + j;
+      v[k][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      if (live && c < g.C) v[k][j] = x4_f32<XT>(x, xn + c * HW + (int64_t)hi * g.W + cg * 4);
+    }
+  }
+  // the weights (at most 64 x 16: four a lane), decoded while those loads fly
+  uint16_t wv[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int i = tid + 256 * k;
+    wv[k] = i < g.C * g.taps ? weight_bf16<WT>(w, i) : (uint16_t)0;
+  }
+  // zero the staging (padding columns, channels past C), then the weights as
+  // Ws[t][c] (bf16, taps and channels past the window 0)
+  {
+    uint32_t* z = reinterpret_cast<uint32_t*>(lds);
+    const int words = (16 * WS + g.npin * g.cstride) / 2;
+    for (int i = tid; i < words; i += 256) z[i] = 0u;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int i = tid + 256 * k;
+    if (i >= g.C * g.taps) continue;
+    const int c = (int)fdiv((uint32_t)i, g.fd_kw) / g.KH;  // i = c * taps + t
+    const int t = i - c * g.taps;
+    ws[t * WS + c] = wv[k];
+  }
+#pragma unroll
+  for (int k = 0; k < MAXI; ++k) {
+    const int it = tid + 256 * k;
+    if (it >= g.vitems) continue;
+    const int rest = (int)fdiv((uint32_t)it, g.fd_c8), q = it - rest * g.c8;
+    const int r = (int)fdiv((uint32_t)rest, g.fd_w4), cg = rest - r * W4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int col = cg * 4 + g.pw + i;
+      if (col >= g.wp) break;
+      uint32_t pk[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const f32x2 f = {v[k][2 * j][i], v[k][2 * j + 1][i]};
+        pk[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));
+      }
+      *reinterpret_cast<uint4*>(&xs[(r * g.wp + col) * g.cstride + q * 8]) =
+          make_uint4(pk[0], pk[1], pk[2], pk[3]);
+    }
+  }
+  __syncthreads();
+
+  // Y tiles: lane holds Y[16 m + 4 (lane >> 4) + i][lane & 15]
+  const int lr = lane & 15, lg = lane >> 4;
+  const int mtiles = (g.npin + 15) >> 4;
+  f32x4 acc[CO1_MT];
+#pragma unroll
+  for (int mt = 0; mt < CO1_MT; ++mt) {
+    acc[mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    const int m = wave + 4 * mt;
+    if (m >= mtiles) continue;
+    int q = m * 16 + lr;
+    if (q >= g.npin) q = 0;  // a valid address; its Y row is never read
+    for (int ks = 0; ks < g.ksteps; ++ks) {
+      const bf16x8 a = *reinterpret_cast<const bf16x8*>(&xs[q * g.cstride + ks * 32 + lg * 8]);
+      const bf16x8 b = *reinterpret_cast<const bf16x8*>(&ws[lr * WS + ks * 32 + lg * 8]);
+      acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[mt], 0, 0, 0);
+    }
+  }
+  __syncthreads();  // every wave's staging reads are done: Y replaces the staging
+#pragma unroll
+  for (int mt = 0; mt < CO1_MT; ++mt) {
+    const int m = wave + 4 * mt;
+    if (m >= mtiles || lr >= g.taps) continue;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int q = m * 16 + 4 * lg + i;
+      if (q < g.npin) ys[q * CO1_YP + lr] = acc[mt][i];
+    }
+  }
+  __syncthreads();
+
+  const int P = min(g.R, g.OH - oh0) * g.OW;
+  const float s = product_scale(w_scale, x_scale);
+  const float inv_o = epi_inv_scale(ep);
+  uint32_t am = 0;
+  if (tid < P) {
+    const int orow = (int)fdiv((uint32_t)tid, g.fd_ow), ocol = tid - orow * g.OW;
+    float sum = 0.0f;
+    for (int t = 0; t < g.taps; ++t) {
+      const int kh = (int)fdiv((uint32_t)t, g.fd_kw), kw = t - kh * g.KW;
+      sum += ys[((orow + kh) * g.wp + ocol + kw) * CO1_YP + t];
+    }
+    const float val = epi_value(ep, epi_chan(ep, 0), sum, s);
+    am = epi_track(am, val);
+    epi_store(ep.out_dtype, y, (int64_t)n * g.OH * g.OW + (int64_t)oh0 * g.OW + tid, val, inv_o);
+  }
+  epi_amax_commit(ep, am);
+}
+
+// The one-output-channel geometry, or false when it does not apply.
+inline bool co1_geometry(const ConvGeom& cg, Co1Geom& g, size_t& lds) {
+  if (cg.C_out != 1 || cg.sh != 1 || cg.sw != 1 || cg.pad_mode != NOVAQ_PAD_ZEROS ||
+      cg.W % 4 != 0 || cg.KH * cg.KW > 16 || cg.KW > 8 || cg.C > 64 || cg.C < 1 ||
+      cg.OW > 256 || cg.OH < 1 || cg.OW < 1)
+    return false;
+  g = Co1Geom{};
+  g.N = cg.N; g.C = cg.C; g.H = cg.H; g.W = cg.W; g.KH = cg.KH; g.KW = cg.KW; g.ph = cg.ph;
+  g.pw = cg.pw; g.OH = cg.OH; g.OW = cg.OW;
+  g.taps = cg.KH * cg.KW;
+  g.c8 = (cg.C + 7) / 8;
+  g.ksteps = (cg.C + 31) / 32;
+  g.cstride = g.ksteps * 32 + 8;  // 8 mod 16 bf16: a fragment read's 16 pixels in distinct banks
+  g.wp = cg.OW + cg.KW - 1;
+  const int64_t npix = (int64_t)cg.OH * cg.OW;
+  const int nb = (int)((npix + 255) / 256);
+  g.R = (cg.OH + nb - 1) / nb;
+  while ((int64_t)g.R * cg.OW > 256) --g.R;
+  for (;; --g.R) {
+    if (g.R < 1) return false;
+    g.rows_in = g.R + cg.KH - 1;
+    g.npin = g.rows_in * g.wp;
+    g.vitems = g.rows_in * (cg.W / 4) * g.c8;
+    if (g.npin <= 16 * 4 * CO1_MT && g.vitems <= 2 * 256) break;
+  }
+  g.bands = (cg.OH + g.R - 1) / g.R;
+  g.fd_c8 = fast_div((uint32_t)g.c8);
+  g.fd_w4 = fast_div((uint32_t)(cg.W / 4));
+  g.fd_ow = fast_div((uint32_t)cg.OW);
+  g.fd_kw = fast_div((uint32_t)cg.KW);
+  const size_t wsb = (size_t)16 * (g.ksteps * 32 + 8) * 2;
+  const size_t xsb = std::max((size_t)g.npin * g.cstride * 2, (size_t)g.npin * CO1_YP * 4);
+  lds = wsb + xsb;
+  return lds <= 64 * 1024;
+}
+
 // Any geometry whose staged input rows do not fit in LDS (very wide images):
 // one lane per output element (grid-strided over the NCHW output), the window
 // gathered straight from global memory with the padding mode resolved.  The
@@ -1404,6 +1590,16 @@ int launch(const uint8_t* x, const float* x_scale, const void* w, const float* w
   {
     int rc = NOVAQ_OK;
     if (launch_smallc<WT, XT>(x, x_scale, w, w_scale, ep, y, g, stream, &rc)) return rc;
+  }
+  {
+    Co1Geom c1;
+    size_t lds = 0;
+    if (co1_geometry(g, c1, lds)) {
+      if ((int64_t)g.N * c1.bands > 0x7FFFFFFF) return NOVAQ_EINVAL;
+      hipLaunchKernelGGL((conv2d_co1_kernel<WT, XT>), dim3((unsigned)(g.N * c1.bands)), dim3(256),
+                         lds, stream, x, x_scale, static_cast<const uint8_t*>(w), w_scale, ep, y, c1);
+      return check_launch();
+    }
   }
   {
     BandGeom b;

@@ -124,6 +124,10 @@ def test_shapes_and_modes_vs_oracle(wdt, mode, case):
     (2, 37, 13, 20, 2, 5, 0, 2, "reflect"),   # C no multiple of 8
     (3, 8, 30, 8, 7, 7, 3, 3, "circular"),    # 7 x 7, rows wider than the image's 8 columns
     (1, 6, 70, 4, 3, 1, 1, 0, "replicate"),   # narrow rows: many rows per band
+    # zero padding, W a multiple of 4: the taps as the MFMA's N
+    (2, 64, 10, 12, 4, 4, 2, 1, "zeros"),     # 16 taps, two channel steps of 32
+    (3, 37, 13, 8, 1, 8, 0, 4, "zeros"),      # a 1 x 8 window, C no multiple of 8
+    (2, 8, 40, 20, 2, 2, 0, 0, "zeros"),      # 13-row bands
 ])
 def test_one_output_channel_exact_operands(case):
     """C_out = 1 (the input gradient of a one-channel convolution is one)
