@@ -844,6 +844,36 @@ __global__ __launch_bounds__(THREADS, 2) void conv2d_band_kernel(
       }
       return;
     }
+    if (ep.out_dtype == F32 && (npix & 3) == 0 && ((oh0 * g.OW) & 3) == 0 && (P & 3) == 0) {
+      // an fp32 output with the epilogue, the same addressing (the values of
+      // the general loop below: epi_value_nb per element, the amax over the
+      // band's pixels)
+      const float z = epi_relu_factor(ep);
+      const bool track = ep.amax != nullptr;
+      float* ybase = reinterpret_cast<float*>(y) +
+                     (((int64_t)n * g.C_out + co0 + lr) * npix + (int64_t)oh0 * g.OW);
+      const int64_t tstep = 16 * npix;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        if (m >= my_mt) break;
+        const int p = (wave + 4 * m) * 16 + 4 * lg;
+        if (p >= P) continue;
+        float* dm = ybase + p;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          if (t >= nt_live || co0 + t * 16 + lr >= g.C_out) continue;
+          f32x4 v;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) v[i] = epi_value_nb(kc[t], acc[m][t][i], s, z);
+          if (track) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) am = epi_track(am, v[i]);
+          }
+          *reinterpret_cast<f32x4*>(dm + t * tstep) = v;
+        }
+      }
+      return;
+    }
     if (plain) {
 #pragma unroll
       for (int m = 0; m < 4; ++m) {

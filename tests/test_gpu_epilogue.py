@@ -189,6 +189,7 @@ def test_linear_epilogue_bit_exact(wdt, N, D_in, D_out):
 CONV_CASES = [
     # wdt, (N, C, H, W), C_out, (KH, KW), stride, pad, mode
     ("e2m1", (3, 8, 12, 12), 16, (3, 3), (1, 1), (1, 1), "zeros"),     # band, K9
+    ("e2m1", (2, 32, 28, 28), 64, (3, 3), (1, 1), (1, 1), "zeros"),   # band, config [5] conv2's bands
     ("e4m3", (2, 5, 10, 11), 20, (5, 5), (1, 1), (2, 2), "reflect"),   # band, generic regroup
     ("bf16", (2, 4, 9, 9), 70, (3, 3), (2, 2), (1, 1), "replicate"),  # band, 2 co blocks
     ("e5m2", (2, 65, 7, 7), 24, (3, 3), (1, 1), (1, 1), "circular"),  # conv2d_kernel (C > 64)
