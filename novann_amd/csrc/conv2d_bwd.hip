@@ -27,7 +27,8 @@
 //     workgroup writes one partial grad_weight tile to the workspace, and the
 //     first j block also the per-channel grad sums of its chunk (grad_bias);
 //   - finish_kernel: one launch that adds the chunk partials in a fixed order
-//     (novaq_colsum.h's column sum, so results do not depend on scheduling)
+//     (novaq_colsum.h's column sum, so results do not depend on scheduling;
+//     16 columns a workgroup with one input channel, else 64)
 //     for grad_weight and grad_bias, and flips the weights for grad_input;
 //     grad_input's convolution runs after it.
 #include <hip/hip_runtime.h>
@@ -100,17 +101,20 @@ struct FinishArgs {
   unsigned wb, bb;
 };
 
-template <int WT>
-__global__ __launch_bounds__(CS_COLS * CS_SLICES) void finish_kernel(FinishArgs a, int C_out,
-                                                                     int C, int KH, int KW) {
-  __shared__ float part[CS_SLICES][CS_COLS];
+// COLS: the column sums' block width (16 for the one-input-channel kernel's
+// many short partials, else 64).
+template <int WT, int COLS>
+__global__ __launch_bounds__(1024) void finish_kernel(FinishArgs a, int C_out, int C, int KH,
+                                                      int KW) {
+  constexpr int SLICES = 1024 / COLS;
+  __shared__ float part[SLICES][COLS];
   const unsigned b = blockIdx.x;
   if (b < a.wb) {
-    colsum_block(a.part, a.rows, a.wcols, a.gw, a.pt, a.pco, a.pc, b, part);
+    colsum_block<COLS, SLICES>(a.part, a.rows, a.wcols, a.gw, a.pt, a.pco, a.pc, b, part);
   } else if (b < a.wb + a.bb) {
-    colsum_block(a.bpart, a.rows, a.bcols, a.gb, 0, 0, 0, b - a.wb, part);
+    colsum_block<COLS, SLICES>(a.bpart, a.rows, a.bcols, a.gb, 0, 0, 0, b - a.wb, part);
   } else {
-    const int64_t t = (int64_t)(b - a.wb - a.bb) * (CS_COLS * CS_SLICES) + threadIdx.x;
+    const int64_t t = (int64_t)(b - a.wb - a.bb) * 1024 + threadIdx.x;
     if (t < a.flip_items) flip_item<WT>(a.w, a.wf, t, C_out, C, KH, KW);
   }
 }
@@ -1042,25 +1046,33 @@ int64_t flip_items(const BwdGeom& g, int wt) {
   return wt == E2M1 ? (total + 1) / 2 : total;
 }
 
-int launch_finish(FinishArgs a, int wt, const BwdGeom& g, hipStream_t stream) {
-  const int64_t wb = (a.wcols + CS_COLS - 1) / CS_COLS, bb = (a.bcols + CS_COLS - 1) / CS_COLS;
-  const int64_t fb = (a.flip_items + CS_COLS * CS_SLICES - 1) / (CS_COLS * CS_SLICES);
+template <int COLS>
+int launch_finish_cols(FinishArgs a, int wt, const BwdGeom& g, hipStream_t stream) {
+  const int64_t wb = (a.wcols + COLS - 1) / COLS, bb = (a.bcols + COLS - 1) / COLS;
+  const int64_t fb = (a.flip_items + 1023) / 1024;
   const int64_t blocks = wb + bb + fb;
   if (blocks == 0) return NOVAQ_OK;
   if (blocks > 0x7FFFFFFF) return NOVAQ_EINVAL;
   a.wb = (unsigned)wb;
   a.bb = (unsigned)bb;
-  const dim3 grid((unsigned)blocks), block(CS_COLS * CS_SLICES);
+  const dim3 grid((unsigned)blocks), block(1024);
   switch (wt) {
-    case E4M3: hipLaunchKernelGGL(finish_kernel<E4M3>, grid, block, 0, stream, a, g.C_out, g.C, g.KH, g.KW); break;
-    case E5M2: hipLaunchKernelGGL(finish_kernel<E5M2>, grid, block, 0, stream, a, g.C_out, g.C, g.KH, g.KW); break;
-    case E2M1: hipLaunchKernelGGL(finish_kernel<E2M1>, grid, block, 0, stream, a, g.C_out, g.C, g.KH, g.KW); break;
-    case BF16: hipLaunchKernelGGL(finish_kernel<BF16>, grid, block, 0, stream, a, g.C_out, g.C, g.KH, g.KW); break;
-    case F16: hipLaunchKernelGGL(finish_kernel<F16>, grid, block, 0, stream, a, g.C_out, g.C, g.KH, g.KW); break;
-    case F32: hipLaunchKernelGGL(finish_kernel<F32>, grid, block, 0, stream, a, g.C_out, g.C, g.KH, g.KW); break;
+    case E4M3: hipLaunchKernelGGL((finish_kernel<E4M3, COLS>), grid, block, 0, stream, a, g.C_out, g.C, g.KH, g.KW); break;
+    case E5M2: hipLaunchKernelGGL((finish_kernel<E5M2, COLS>), grid, block, 0, stream, a, g.C_out, g.C, g.KH, g.KW); break;
+    case E2M1: hipLaunchKernelGGL((finish_kernel<E2M1, COLS>), grid, block, 0, stream, a, g.C_out, g.C, g.KH, g.KW); break;
+    case BF16: hipLaunchKernelGGL((finish_kernel<BF16, COLS>), grid, block, 0, stream, a, g.C_out, g.C, g.KH, g.KW); break;
+    case F16: hipLaunchKernelGGL((finish_kernel<F16, COLS>), grid, block, 0, stream, a, g.C_out, g.C, g.KH, g.KW); break;
+    case F32: hipLaunchKernelGGL((finish_kernel<F32, COLS>), grid, block, 0, stream, a, g.C_out, g.C, g.KH, g.KW); break;
     default: return NOVAQ_EDTYPE;
   }
   return check_launch();
+}
+
+// With one input channel (C == 1: the one-input-channel kernel's up to
+// D1_CHUNKS partials of C_out x taps columns) the sums take 16 columns a
+// workgroup, otherwise 64.
+int launch_finish(FinishArgs a, int wt, const BwdGeom& g, hipStream_t stream) {
+  return g.C == 1 ? launch_finish_cols<16>(a, wt, g, stream) : launch_finish_cols<64>(a, wt, g, stream);
 }
 
 // wf holds the flipped weights when flip_path(g) (the finishing launch wrote

@@ -1,13 +1,15 @@
 // One workgroup's share of a column sum, shared by the column-sum kernel and
 // the conv backward's finishing kernel.
 //
-// out[c] = sum over r of x[r * cols + c] in fp32 in a fixed order: each of 16
-// row slices is summed in four chains (row r of a slice goes to chain r % 4,
-// in row order), the chains are added (0 + 1) + (2 + 3), then the slices in
-// slice order, so repeated calls agree bit for bit.  A workgroup of 1024
-// lanes owns 64 columns (a wave's load reads 256 contiguous bytes of one
-// row); with pt > 0 the columns form a (pt, pco, pc) array and column
-// (t, co, c) is stored at out[(co * pc + c) * pt + t].
+// out[c] = sum over r of x[r * cols + c] in fp32 in a fixed order: each of
+// SLICES row slices is summed in four chains (row r of a slice goes to chain
+// r % 4, in row order), the chains are added (0 + 1) + (2 + 3), then the
+// slices in slice order, so repeated calls with the same shape agree bit for
+// bit.  A workgroup of COLS x SLICES = 1024 lanes owns COLS columns: 64 by
+// default (a wave's load reads 256 contiguous bytes of one row); 16 with 64
+// slices for few columns over many rows (a quarter of the rows per lane).
+// With pt > 0 the columns form a (pt, pco, pc) array and column (t, co, c)
+// is stored at out[(co * pc + c) * pt + t].
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -18,14 +20,16 @@ namespace novaq {
 constexpr int CS_COLS = 64;    // columns per workgroup
 constexpr int CS_SLICES = 16;  // row slices per workgroup (one wave each)
 
-// blk: the workgroup's column block; part: CS_SLICES x CS_COLS floats of LDS.
+// blk: the workgroup's column block; part: SLICES x COLS floats of LDS.
 // Every lane of the workgroup calls it (it has a barrier).
+template <int COLS = CS_COLS, int SLICES = CS_SLICES>
 __device__ inline void colsum_block(const float* __restrict__ x, int64_t rows, int64_t cols,
                                     float* __restrict__ out, int pt, int pco, int pc,
-                                    int64_t blk, float (*part)[CS_COLS]) {
-  const int tx = threadIdx.x % CS_COLS, ty = threadIdx.x / CS_COLS;
-  const int64_t c = blk * CS_COLS + tx;
-  const int64_t per = (rows + CS_SLICES - 1) / CS_SLICES;
+                                    int64_t blk, float (*part)[COLS]) {
+  static_assert(COLS * SLICES == 1024, "a workgroup of 1024 lanes");
+  const int tx = threadIdx.x % COLS, ty = threadIdx.x / COLS;
+  const int64_t c = blk * COLS + tx;
+  const int64_t per = (rows + SLICES - 1) / SLICES;
   const int64_t rb = ty * per, re = min(rows, rb + per);
   float s = 0.0f;
   if (c < cols) {
@@ -47,7 +51,7 @@ __device__ inline void colsum_block(const float* __restrict__ x, int64_t rows, i
   if (ty == 0 && c < cols) {
     float t = part[0][tx];
 #pragma unroll
-    for (int k = 1; k < CS_SLICES; ++k) t += part[k][tx];
+    for (int k = 1; k < SLICES; ++k) t += part[k][tx];
     int64_t o = c;
     if (pt > 0) {
       const int64_t per_t = (int64_t)pco * pc;
