@@ -408,7 +408,7 @@ __global__ __launch_bounds__(256) void global_avg_pool2d_plane_kernel(
   constexpr int B = XL<XT>::bits, EB = B / 8;
   constexpr int LPL = 8 / Q;  // lanes per leaf
   constexpr int LSH = LPL == 8 ? 3 : LPL == 4 ? 2 : LPL == 2 ? 1 : 0;
-  constexpr int P = 64 / LPL, PSH = 6 - LSH;  // virtual leaves per pass
+  constexpr int PSH = 6 - LSH;  // log2 of the virtual leaves per pass (64 / LPL)
   const int lane = threadIdx.x & 63;
   const int64_t plane = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (plane >= planes) return;  // the whole wave
