@@ -226,6 +226,30 @@ int novaq_max_pool2d(const void *x, int x_dtype, int64_t N, int64_t C, int64_t H
 int novaq_global_avg_pool2d(const void *x, int x_dtype, const float *x_scale, int64_t N,
                             int64_t C, int64_t H, int64_t W, float *y, void *stream);
 
+/* grad_input (N, C, H, W) fp32 = MaxPool2d's input gradient for grad (N, C,
+ * OH, OW) fp32 and the forward's x (N, C, H, W) in x_dtype (as
+ * novaq_max_pool2d; same kernel, stride, padding and pad_mode): over each
+ * window of x padded in pad_mode, the elements equal to the window's maximum
+ * (none when it holds a NaN) share grad / count (count = how many, 1 when
+ * none), each other element gets 0 * (grad / count) (NaN for a non-finite
+ * grad); an input element sums its windows' shares in (oh, ow) order from +0,
+ * and shares that land on the padding are dropped.  fp32, IEEE divide: bit
+ * for bit the reference's result.  grad and grad_input 4-byte aligned, x
+ * element-aligned (NOVAQ_EALIGN otherwise).
+ * Replaces: MaxPool2d.backward (novann/layers/pooling/maxpool/maxpool2d.py:79-129). */
+int novaq_max_pool2d_backward(const float *grad, const void *x, int x_dtype, int64_t N,
+                              int64_t C, int64_t H, int64_t W, int KH, int KW, int sh, int sw,
+                              int ph, int pw, int pad_mode, float *grad_input, void *stream);
+
+/* grad_input (N, C, H, W) fp32 = grad[n, c] * (float)(1.0 / (H * W)) over
+ * each plane, grad (N, C) fp32 (the reference's (N, C, 1, 1)): its
+ * ones * (grad * factor), the double factor made float32 by the product.
+ * grad and grad_input 4-byte aligned (NOVAQ_EALIGN otherwise).
+ * Replaces: GlobalAvgPool2d.backward
+ * (novann/layers/pooling/gap/global_avg_pool2d.py:35-57). */
+int novaq_global_avg_pool2d_backward(const float *grad, int64_t N, int64_t C, int64_t H,
+                                     int64_t W, float *grad_input, void *stream);
+
 /* col (C*KH*KW, N*OH*OW) fp32, row-major = the column matrix of NovaNN's
  * conv2d: col[(c*KH + kh)*KW + kw][(n*OH + oh)*OW + ow] = x padded (ph, pw) in
  * pad_mode with numpy.pad's rules, at [n][c][oh*sh + kh][ow*sw + kw]; rows

@@ -62,6 +62,9 @@ SIGNATURES = {
     "novaq_max_pool2d": (_i32, [_vp, _i32, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32,
                                 _i32, _i32, _vp, _vp]),
     "novaq_global_avg_pool2d": (_i32, [_vp, _i32, _f32p, _i64, _i64, _i64, _i64, _f32p, _vp]),
+    "novaq_max_pool2d_backward": (_i32, [_f32p, _vp, _i32, _i64, _i64, _i64, _i64, _i32, _i32,
+                                         _i32, _i32, _i32, _i32, _i32, _f32p, _vp]),
+    "novaq_global_avg_pool2d_backward": (_i32, [_f32p, _i64, _i64, _i64, _i64, _f32p, _vp]),
     "novaq_im2col": (_i32, [_vp, _i32, _f32p, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _i32,
                             _i32, _i32, _i32, _f32p, _vp]),
     "novaq_pad2d": (_i32, [_vp, _i32, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _vp, _vp]),

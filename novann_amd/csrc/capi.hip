@@ -291,6 +291,40 @@ int novaq_global_avg_pool2d(const void* x, int x_dtype, const float* x_scale, in
                                   static_cast<hipStream_t>(stream));
 }
 
+int novaq_max_pool2d_backward(const float* grad, const void* x, int x_dtype, int64_t N,
+                              int64_t C, int64_t H, int64_t W, int KH, int KW, int sh, int sw,
+                              int ph, int pw, int pad_mode, float* grad_input, void* stream) {
+  if (!valid_dtype(x_dtype) || x_dtype == E2M1) return NOVAQ_EDTYPE;
+  if (pad_mode < NOVAQ_PAD_ZEROS || pad_mode > NOVAQ_PAD_CIRCULAR) return NOVAQ_EPADMODE;
+  if (N < 0 || C <= 0 || H <= 0 || W <= 0 || KH <= 0 || KW <= 0 || sh <= 0 || sw <= 0 ||
+      ph < 0 || pw < 0)
+    return NOVAQ_EINVAL;
+  if (H + 2 * (int64_t)ph < KH || W + 2 * (int64_t)pw < KW) return NOVAQ_ESHAPE;
+  if (H > 0x7FFFFFFF || W > 0x7FFFFFFF) return NOVAQ_EINVAL;
+  if (N == 0) return NOVAQ_OK;
+  if (!grad || !x || !grad_input) return NOVAQ_EINVAL;
+  const uintptr_t eb = (uintptr_t)dtype_bits(x_dtype) / 8;  // element-aligned views only
+  if (reinterpret_cast<uintptr_t>(x) % eb ||
+      ((reinterpret_cast<uintptr_t>(grad) | reinterpret_cast<uintptr_t>(grad_input)) & 3))
+    return NOVAQ_EALIGN;
+  return max_pool2d_backward_launch(grad, x, x_dtype, N, C, H, W, KH, KW, sh, sw, ph, pw,
+                                    pad_mode, grad_input, static_cast<hipStream_t>(stream));
+}
+
+int novaq_global_avg_pool2d_backward(const float* grad, int64_t N, int64_t C, int64_t H,
+                                     int64_t W, float* grad_input, void* stream) {
+  if (N < 0 || C <= 0 || H <= 0 || W <= 0) return NOVAQ_EINVAL;
+  if (N == 0) return NOVAQ_OK;
+  if (!grad || !grad_input) return NOVAQ_EINVAL;
+  if ((reinterpret_cast<uintptr_t>(grad) | reinterpret_cast<uintptr_t>(grad_input)) & 3)
+    return NOVAQ_EALIGN;
+  // the reference's factor 1.0 / (H * W): a double, made float32 by its
+  // product with the float32 grad
+  const float factor = (float)(1.0 / ((double)H * (double)W));
+  return global_avg_pool2d_backward_launch(grad, N * C, H * W, factor, grad_input,
+                                           static_cast<hipStream_t>(stream));
+}
+
 int novaq_im2col(const void* x, int x_dtype, const float* x_scale, int64_t N, int64_t C,
                  int64_t H, int64_t W, int KH, int KW, int sh, int sw, int ph, int pw,
                  int pad_mode, float* col, void* stream) {

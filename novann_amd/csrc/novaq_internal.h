@@ -118,6 +118,12 @@ int max_pool2d_launch(const void* x, int x_dtype, int64_t N, int64_t C, int64_t 
                       hipStream_t stream);
 int global_avg_pool2d_launch(const void* x, int x_dtype, const float* x_scale, int64_t planes,
                              int64_t hw, float* y, hipStream_t stream);
+int max_pool2d_backward_launch(const float* grad, const void* x, int x_dtype, int64_t N,
+                               int64_t C, int64_t H, int64_t W, int KH, int KW, int sh, int sw,
+                               int ph, int pw, int pad_mode, float* grad_input,
+                               hipStream_t stream);
+int global_avg_pool2d_backward_launch(const float* grad, int64_t planes, int64_t hw,
+                                      float factor, float* grad_input, hipStream_t stream);
 
 // col (C*KH*KW, N*OH*OW) fp32 = the conv2d column matrix of x in x_dtype
 // (FP8 times *x_scale when given); pad modes resolved as pad_index does.

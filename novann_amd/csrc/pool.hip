@@ -27,6 +27,13 @@
 // of the tree, shuffles across leaves: several planes per wave when a plane's
 // tree fits a wave's lanes (the tree kernel), else one wave per plane walking
 // numpy's blocks (the plane kernel).
+//
+// Backward passes (MaxPool2d.backward, layers/pooling/maxpool/maxpool2d.py:
+// 79-129; GlobalAvgPool2d.backward, layers/pooling/gap/global_avg_pool2d.py:
+// 35-57): the max pool's input gradient, each window's grad split over the
+// elements equal to its maximum, the windows' shares added per element in
+// window order; the average pool's, grad times float32(1 / (H*W)) over the
+// plane.  Both write fp32, HBM-bound.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -601,6 +608,182 @@ int launch_gap(const void* x, const float* x_scale, float* y, int64_t planes, in
   return check_launch();
 }
 
+
+// ---------------------------------------------------------------------------
+// Backward passes.
+//
+// MaxPool2d (MaxPool2d.backward, novann/layers/pooling/maxpool/maxpool2d.py:
+// 79-129): over the forward's windows of the padded input, a window's maximum
+// is NaN when it holds one (numpy's max) and its count is the number of its
+// elements equal to that maximum, 1 when none is (a NaN maximum).  An element
+// equal to the maximum receives 1 * (grad / count), any other element of the
+// window 0 * (grad / count) -- a NaN where grad is not finite, as the
+// reference's mask product gives; an input element adds what the windows
+// holding it give, in (oh, ow) order, to +0, and what lands on the padding is
+// dropped (the reference scatters into the padded shape and crops it).  fp32
+// throughout, the divide IEEE-rounded.
+
+// Window (i, j)'s maximum and count over the padded plane at base.
+template <int XT>
+__device__ __forceinline__ void window_max_count(const uint8_t* __restrict__ x, int64_t base,
+                                                 const PoolGeom& g, int i, int j, float& mx,
+                                                 int& cnt) {
+  bool nan = false;
+  mx = -INFINITY;
+  for (int kh = 0; kh < g.KH; ++kh) {
+    const int hi = pad_index(i * g.sh + kh - g.ph, g.H, g.pad_mode);
+    for (int kw = 0; kw < g.KW; ++kw) {
+      const int wi = pad_index(j * g.sw + kw - g.pw, g.W, g.pad_mode);
+      const float v = (hi >= 0 && wi >= 0) ? x_val<XT>(x, base + (int64_t)hi * g.W + wi) : 0.0f;
+      nan |= isnan(v);
+      mx = v > mx ? v : mx;
+    }
+  }
+  if (nan) mx = __builtin_nanf("");
+  cnt = 0;
+  for (int kh = 0; kh < g.KH; ++kh) {
+    const int hi = pad_index(i * g.sh + kh - g.ph, g.H, g.pad_mode);
+    for (int kw = 0; kw < g.KW; ++kw) {
+      const int wi = pad_index(j * g.sw + kw - g.pw, g.W, g.pad_mode);
+      const float v = (hi >= 0 && wi >= 0) ? x_val<XT>(x, base + (int64_t)hi * g.W + wi) : 0.0f;
+      cnt += v == mx;
+    }
+  }
+  if (cnt == 0) cnt = 1;
+}
+
+// Any geometry: lane t makes input element t (planes of H x W back to back)
+// from the windows holding it, each window's maximum and count recomputed.
+template <int XT>
+__global__ __launch_bounds__(256) void max_pool2d_bwd_kernel(const float* __restrict__ grad,
+                                                            const uint8_t* __restrict__ x,
+                                                            float* __restrict__ gi, PoolGeom g) {
+  const int64_t hw = (int64_t)g.H * g.W;
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= g.N * g.C * hw) return;
+  const int64_t plane = t / hw;
+  const int pix = (int)(t - plane * hw);
+  const int h = pix / g.W, w = pix - h * g.W;
+  const float xv = x_val<XT>(x, t);
+  // windows i with i*sh <= h + ph < i*sh + KH (and j likewise)
+  const int hp = h + g.ph, wp = w + g.pw;
+  const int i0 = hp >= g.KH ? (hp - g.KH) / g.sh + 1 : 0, i1 = min(g.OH - 1, hp / g.sh);
+  const int j0 = wp >= g.KW ? (wp - g.KW) / g.sw + 1 : 0, j1 = min(g.OW - 1, wp / g.sw);
+  const float* gp = grad + plane * g.OH * g.OW;
+  float sum = 0.0f;
+  for (int i = i0; i <= i1; ++i)
+    for (int j = j0; j <= j1; ++j) {
+      float mx;
+      int cnt;
+      window_max_count<XT>(x, plane * hw, g, i, j, mx, cnt);
+      const float q = gp[(int64_t)i * g.OW + j] / (float)cnt;
+      sum += (xv == mx ? 1.0f : 0.0f) * q;
+    }
+  gi[t] = sum;
+}
+
+// 2 x 2 windows, stride 2, no padding, H and W even (every input element in
+// exactly one window: config [5]'s MaxPool2d(2, 2)): lane t makes window t's
+// four gradients, its two input rows read as 2-element loads and its two
+// gradient rows written as 8-byte stores (x aligned to 2 elements, gi to 8
+// bytes).  t < 2^31: the divisions by the plane's windows and by OW are
+// multiply-shifts.
+template <int XT>
+__global__ __launch_bounds__(256) void max_pool2d_bwd_22_kernel(
+    const float* __restrict__ grad, const uint8_t* __restrict__ x, float* __restrict__ gi,
+    int W, int OW, FastDiv dnpix, FastDiv dow, uint32_t windows, uint32_t npix) {
+  const uint32_t t = blockIdx.x * 256u + threadIdx.x;
+  if (t >= windows) return;
+  const uint32_t plane = fdiv(t, dnpix), pix = t - plane * npix;
+  const uint32_t i = fdiv(pix, dow), j = pix - i * (uint32_t)OW;
+  const int64_t e0 = (int64_t)plane * (4 * (int64_t)npix) + (int64_t)(2 * i) * W + 2 * j;
+  constexpr int B = XL<XT>::bits;
+  uint32_t c[4];
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int64_t e = e0 + (int64_t)r * W;
+    if constexpr (B == 32) {
+      const uint2 v = *reinterpret_cast<const uint2*>(x + e * 4);
+      c[2 * r] = v.x;
+      c[2 * r + 1] = v.y;
+    } else if constexpr (B == 16) {
+      const uint32_t v = *reinterpret_cast<const uint32_t*>(x + e * 2);
+      c[2 * r] = v & 0xFFFFu;
+      c[2 * r + 1] = v >> 16;
+    } else {
+      const uint32_t v = *reinterpret_cast<const uint16_t*>(x + e);
+      c[2 * r] = v & 0xFFu;
+      c[2 * r + 1] = v >> 8;
+    }
+  }
+  float v[4];
+  bool nan = false;
+  float mx = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    v[k] = u2f(decode<XT>(c[k]));
+    nan |= isnan(v[k]);
+    mx = v[k] > mx ? v[k] : mx;
+  }
+  if (nan) mx = __builtin_nanf("");
+  int cnt = 0;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) cnt += v[k] == mx;
+  if (cnt == 0) cnt = 1;
+  const float q = grad[t] / (float)cnt;
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const float a = 0.0f + (v[2 * r] == mx ? 1.0f : 0.0f) * q;
+    const float b = 0.0f + (v[2 * r + 1] == mx ? 1.0f : 0.0f) * q;
+    *reinterpret_cast<float2*>(gi + e0 + (int64_t)r * W) = make_float2(a, b);
+  }
+}
+
+template <int XT>
+int launch_max_bwd(const float* grad, const void* x, float* gi, const PoolGeom& g,
+                   hipStream_t stream) {
+  const auto* xb = static_cast<const uint8_t*>(x);
+  constexpr uintptr_t EB = XL<XT>::bits / 8;
+  const int64_t npix = (int64_t)g.OH * g.OW;
+  const int64_t windows = g.N * g.C * npix;
+  if (g.KH == 2 && g.KW == 2 && g.sh == 2 && g.sw == 2 && g.ph == 0 && g.pw == 0 &&
+      g.H == 2 * g.OH && g.W == 2 * g.OW && windows < ((int64_t)1 << 31) &&
+      reinterpret_cast<uintptr_t>(x) % (2 * EB) == 0 && reinterpret_cast<uintptr_t>(gi) % 8 == 0) {
+    hipLaunchKernelGGL(max_pool2d_bwd_22_kernel<XT>, dim3((unsigned)((windows + 255) / 256)),
+                       dim3(256), 0, stream, grad, xb, gi, g.W, g.OW,
+                       fast_div((uint32_t)npix), fast_div((uint32_t)g.OW), (uint32_t)windows,
+                       (uint32_t)npix);
+    return check_launch();
+  }
+  const int64_t blocks = (g.N * g.C * g.H * (int64_t)g.W + 255) / 256;
+  if (blocks > 0x7FFFFFFF) return NOVAQ_EINVAL;
+  hipLaunchKernelGGL(max_pool2d_bwd_kernel<XT>, dim3((unsigned)blocks), dim3(256), 0, stream,
+                     grad, xb, gi, g);
+  return check_launch();
+}
+
+// GlobalAvgPool2d (GlobalAvgPool2d.backward, novann/layers/pooling/gap/
+// global_avg_pool2d.py:35-57): every element of plane p is grad[p] * f, f =
+// 1 / (H*W) rounded to fp32 by the host (the reference's Python float factor
+// becomes float32 in its product with the float32 grad; the ones it then
+// multiplies by change nothing).  VEC: 4 elements a lane, one 16-byte store
+// (H*W a multiple of 4, gi 16-byte aligned, fewer than 2^31 lanes).
+template <bool VEC>
+__global__ __launch_bounds__(256) void global_avg_pool2d_bwd_kernel(
+    const float* __restrict__ grad, float* __restrict__ gi, int64_t lanes, int64_t hw, float f,
+    FastDiv dq, uint32_t q) {
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (t >= lanes) return;
+  if constexpr (VEC) {
+    const float v = grad[fdiv((uint32_t)t, dq)] * f;
+    *reinterpret_cast<float4*>(gi + 4 * t) = make_float4(v, v, v, v);
+    (void)hw;
+    (void)q;
+  } else {
+    gi[t] = grad[t / hw] * f;
+  }
+}
+
 }  // namespace
 
 int max_pool2d_launch(const void* x, int x_dtype, int64_t N, int64_t C, int64_t H, int64_t W,
@@ -631,6 +814,44 @@ int global_avg_pool2d_launch(const void* x, int x_dtype, const float* x_scale, i
     case E5M2: return launch_gap<E5M2>(x, x_scale, y, planes, hw, stream);
     default: return NOVAQ_EDTYPE;
   }
+}
+
+int max_pool2d_backward_launch(const float* grad, const void* x, int x_dtype, int64_t N,
+                               int64_t C, int64_t H, int64_t W, int KH, int KW, int sh, int sw,
+                               int ph, int pw, int pad_mode, float* grad_input,
+                               hipStream_t stream) {
+  PoolGeom g{};
+  g.N = N; g.C = C; g.H = (int)H; g.W = (int)W; g.KH = KH; g.KW = KW; g.sh = sh; g.sw = sw;
+  g.ph = ph; g.pw = pw; g.pad_mode = pad_mode;
+  g.OH = (int)((H + 2 * (int64_t)ph - KH) / sh + 1);
+  g.OW = (int)((W + 2 * (int64_t)pw - KW) / sw + 1);
+  if ((int64_t)g.OH * g.OW > 0x7FFFFFFF || H * W > 0x7FFFFFFF) return NOVAQ_EINVAL;
+  switch (x_dtype) {
+    case F32: return launch_max_bwd<F32>(grad, x, grad_input, g, stream);
+    case F16: return launch_max_bwd<F16>(grad, x, grad_input, g, stream);
+    case BF16: return launch_max_bwd<BF16>(grad, x, grad_input, g, stream);
+    case E4M3: return launch_max_bwd<E4M3>(grad, x, grad_input, g, stream);
+    case E5M2: return launch_max_bwd<E5M2>(grad, x, grad_input, g, stream);
+    default: return NOVAQ_EDTYPE;
+  }
+}
+
+int global_avg_pool2d_backward_launch(const float* grad, int64_t planes, int64_t hw,
+                                      float factor, float* grad_input, hipStream_t stream) {
+  const int64_t total = planes * hw;
+  if (hw % 4 == 0 && total / 4 < ((int64_t)1 << 31) &&
+      reinterpret_cast<uintptr_t>(grad_input) % 16 == 0) {
+    const int64_t lanes = total / 4;
+    hipLaunchKernelGGL(global_avg_pool2d_bwd_kernel<true>, dim3((unsigned)((lanes + 255) / 256)),
+                       dim3(256), 0, stream, grad, grad_input, lanes, hw, factor,
+                       fast_div((uint32_t)(hw / 4)), (uint32_t)(hw / 4));
+    return check_launch();
+  }
+  const int64_t blocks = (total + 255) / 256;
+  if (blocks > 0x7FFFFFFF) return NOVAQ_EINVAL;
+  hipLaunchKernelGGL(global_avg_pool2d_bwd_kernel<false>, dim3((unsigned)blocks), dim3(256), 0,
+                     stream, grad, grad_input, total, hw, factor, FastDiv{}, 0u);
+  return check_launch();
 }
 
 }  // namespace novaq

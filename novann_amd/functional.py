@@ -493,6 +493,52 @@ def max_pool2d(input, kernel_size: IntPair, stride: IntPair, padding: IntPair = 
     return out, windows, OH, OW, (N, C, Hp, Wp)
 
 
+def max_pool2d_backward(grad, input, kernel_size: IntPair, stride: IntPair,
+                        padding: IntPair = 0, padding_mode: str = "zeros"):
+    """MaxPool2d's input gradient (novann/layers/pooling/maxpool/maxpool2d.py:
+    79-129) for grad (N, C, OH, OW) and the forward's input (as max_pool2d
+    takes it: fp32, bf16 / f16 or an FP8 Quantized activation, whose windows
+    compare as stored): each window's grad split over the elements equal to
+    its maximum, the windows' shares added per element in window order, the
+    padding's shares dropped.  Returns (N, C, H, W) fp32, an ndarray for a
+    numpy grad; bit for bit the reference's result."""
+    KH, KW = _pair(kernel_size)
+    ph, pw = _pair(padding)
+    sh, sw = _pair(stride)
+    if padding_mode not in PAD_MODES:
+        raise ValueError(f"padding_mode Only accept {tuple(PAD_MODES)} not '{padding_mode}'")
+    x, xdt, _, xshape, _ = _x_arg(input, "input")
+    if len(xshape) != 4:
+        raise ValueError(f"max_pool2d_backward expects an (N, C, H, W) input, got {xshape}")
+    N, C, H, W = xshape
+    OH = (H + 2 * ph - KH) // sh + 1
+    OW = (W + 2 * pw - KW) // sw + 1
+    g, was_numpy = _to_device_f32(grad, "grad")
+    if tuple(g.shape) != (N, C, OH, OW):
+        raise ValueError(f"grad shape {tuple(g.shape)} is not the output's {(N, C, OH, OW)}")
+    gi = torch.empty((N, C, H, W), dtype=torch.float32, device=x.device)
+    check(_lib.load().novaq_max_pool2d_backward(g.data_ptr(), x.data_ptr(), DTYPES[xdt], N, C, H,
+                                                W, KH, KW, sh, sw, ph, pw,
+                                                PAD_MODES[padding_mode], gi.data_ptr(),
+                                                _stream(x.device)), "max_pool2d_backward")
+    return gi.cpu().numpy() if was_numpy else gi
+
+
+def avg_pool2d_backward(grad, input_shape):
+    """GlobalAvgPool2d's input gradient (novann/layers/pooling/gap/
+    global_avg_pool2d.py:35-57): grad (N, C, 1, 1) spread over the (N, C, H, W)
+    input shape as grad * float32(1 / (H*W)).  Returns fp32, an ndarray for a
+    numpy grad."""
+    N, C, H, W = input_shape
+    g, was_numpy = _to_device_f32(grad, "grad")
+    if g.numel() != N * C:
+        raise ValueError(f"grad has {g.numel()} elements, not N*C = {N * C}")
+    gi = torch.empty((N, C, H, W), dtype=torch.float32, device=g.device)
+    check(_lib.load().novaq_global_avg_pool2d_backward(g.data_ptr(), N, C, H, W, gi.data_ptr(),
+                                                       _stream(g.device)), "avg_pool2d_backward")
+    return gi.cpu().numpy() if was_numpy else gi
+
+
 def avg_pool2d(input):
     """Global average over H and W (novann/functional.py:548-559): returns
     (N, C, 1, 1) fp32, equal bit for bit to the reference's np.mean on the

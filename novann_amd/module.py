@@ -415,8 +415,10 @@ def fuse(*layers, out_dtype: str = "f32", out_scale=None) -> Fused:
 
 
 class MaxPool2d(Module):
-    """novann MaxPool2d (layers/pooling/maxpool/maxpool2d.py:8-79): kernel,
-    stride (None = kernel size), padding, padding_mode; forward on the GPU."""
+    """novann MaxPool2d (layers/pooling/maxpool/maxpool2d.py:8-132): kernel,
+    stride (None = kernel size), padding, padding_mode; forward and backward
+    on the GPU.  The forward input is cached for ``backward`` (the reference
+    caches its window view, :63-75) and released by it (:123)."""
 
     def __init__(self, kernel_size, stride=None, padding=0, padding_mode: str = "zeros") -> None:
         super().__init__()
@@ -424,23 +426,48 @@ class MaxPool2d(Module):
         self.sh, self.sw = _pair(stride if stride is not None else kernel_size)
         self.ph, self.pw = _pair(padding)
         self.pm = padding_mode
+        self._cache_input = None
 
     def __call__(self, x):
         return self.forward(x)
 
     def forward(self, x):
         from . import functional as F
+        self._cache_input = x
         return F.max_pool2d(x, (self.KH, self.KW), (self.sh, self.sw), (self.ph, self.pw),
                             padding_mode=self.pm)
 
+    def backward(self, grad):
+        """The input gradient (maxpool2d.py:79-129)."""
+        from . import functional as F
+        if self._cache_input is None:
+            raise RuntimeError("MaxPool2d.backward called without a forward")
+        gi = F.max_pool2d_backward(grad, self._cache_input, (self.KH, self.KW),
+                                   (self.sh, self.sw), (self.ph, self.pw), padding_mode=self.pm)
+        self._cache_input = None
+        return gi
+
 
 class GlobalAvgPool2d(Module):
-    """novann GlobalAvgPool2d (layers/pooling/gap/global_avg_pool2d.py:7-32):
-    (N, C, H, W) -> (N, C, 1, 1) means, on the GPU."""
+    """novann GlobalAvgPool2d (layers/pooling/gap/global_avg_pool2d.py:7-57):
+    (N, C, H, W) -> (N, C, 1, 1) means and their input gradient, on the GPU;
+    the forward caches the input shape (:30)."""
+
+    def __init__(self) -> None:
+        super().__init__()
+        self._x_shape = None
 
     def __call__(self, x):
         return self.forward(x)
 
     def forward(self, x):
         from . import functional as F
+        self._x_shape = tuple(x.shape)
         return F.avg_pool2d(x)
+
+    def backward(self, grad):
+        """grad / (H*W) over each plane (global_avg_pool2d.py:35-57)."""
+        from . import functional as F
+        if self._x_shape is None:
+            raise RuntimeError("GlobalAvgPool2d.backward called without a forward")
+        return F.avg_pool2d_backward(grad, self._x_shape)

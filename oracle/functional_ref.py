@@ -16,6 +16,10 @@ Restates, with this build's own code, the arithmetic of
     (N, C, OH, OW, KH, KW) window view (returned with extras=True),
     ``max(axis=(4, 5))``; and
     ``avg_pool2d`` (:548-559): ``np.mean(x, axis=(2, 3), keepdims=True)``;
+  - ``MaxPool2d.backward`` (layers/pooling/maxpool/maxpool2d.py:79-129): the
+    window mask of the max, grad split over ties, shares scattered in window
+    order into the padded shape and cropped; ``GlobalAvgPool2d.backward``
+    (layers/pooling/gap/global_avg_pool2d.py:35-57): grad * (1 / (H*W));
   - eval-mode ``BatchNorm2d`` / ``BatchNorm1d`` (batchnorm2d.py:98-102,
     batchnorm1d.py:138-149): ``gamma * (x - mean) / sqrt(var + eps) + beta``
     per channel, in fp64 as the reference's float64 running statistics make it;
@@ -187,3 +191,39 @@ def max_pool2d(x: np.ndarray, kernel_size, stride, padding=(0, 0),
 def avg_pool2d(x: np.ndarray) -> np.ndarray:
     """functional.py:559."""
     return np.mean(x, axis=(2, 3), keepdims=True)
+
+
+def max_pool2d_backward(grad: np.ndarray, x: np.ndarray, kernel_size, stride,
+                        padding=(0, 0), padding_mode: str = "zeros") -> np.ndarray:
+    """MaxPool2d.backward (layers/pooling/maxpool/maxpool2d.py:79-129): over
+    the forward's window view of the padded input, mask = (window == its max)
+    (all 0 when the max is NaN), count = the mask's sum (1 where 0), each
+    window's share = mask * (grad / count) in float32; the shares are added
+    into a zero buffer of the padded shape in (oh, ow) order (:114-124) and
+    the padding is cropped (:126-129)."""
+    KH, KW = _pair(kernel_size)
+    sh, sw = _pair(stride)
+    ph, pw = _pair(padding)
+    N, C, H, W = x.shape
+    win, OH, OW, pshape = pool_windows(np.asarray(x, np.float32), kernel_size, stride,
+                                       padding, padding_mode)
+    g = np.asarray(grad, np.float32).reshape(N, C, OH, OW)
+    mx = win.max(axis=(4, 5), keepdims=True)
+    mask = (win == mx).astype(np.float32)
+    count = mask.sum(axis=(4, 5), keepdims=True)
+    count[count == 0] = 1.0
+    share = mask * (g[:, :, :, :, np.newaxis, np.newaxis] / count)
+    gp = np.zeros(pshape, np.float32)
+    for i in range(OH):
+        for j in range(OW):
+            gp[:, :, i * sh:i * sh + KH, j * sw:j * sw + KW] += share[:, :, i, j]
+    return gp[:, :, ph:ph + H, pw:pw + W]
+
+
+def global_avg_pool2d_backward(grad: np.ndarray, x_shape) -> np.ndarray:
+    """GlobalAvgPool2d.backward (layers/pooling/gap/global_avg_pool2d.py:35-57):
+    ``ones * (grad * (1.0 / (H * W)))`` in float32 (the Python float factor
+    becomes float32 before the product)."""
+    N, C, H, W = x_shape
+    g = np.asarray(grad, np.float32).reshape(N, C, 1, 1)
+    return np.ones((N, C, H, W), np.float32) * (g * (1.0 / (H * W)))
