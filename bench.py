@@ -646,7 +646,9 @@ def bench_optim(dev, iters: int = 20, warmup: int = 3):
 def bench_pool(dev, iters: int = 20, warmup: int = 3):
     """MaxPool2d(2, 2) and GlobalAvgPool2d on a config [5]-sized activation
     (256, 64, 28, 28) in fp32 and bf16, and GlobalAvgPool2d on main.py's 7x7
-    map at batch 256: algorithmic bytes = read x once + write y once."""
+    map at batch 256: algorithmic bytes = read x once + write y once; their
+    backward passes on the same activation: read x (MaxPool2d) and the output
+    gradient once, write the fp32 input gradient once."""
     import torch
 
     from novann_amd import _lib
@@ -676,7 +678,31 @@ def bench_pool(dev, iters: int = 20, warmup: int = 3):
         out.append({"op": f"global_avg_pool2d {shape} f32", "ms": round(ms, 4),
                     "GB/s": round(nb / (ms * 1e-3) / 1e9, 1),
                     "frac": round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
-    return {"workload": "pools on config [5]-sized and main.py activations", "kernels": out}
+    # backward passes on the same activation: MaxPool2d(2, 2) reads x and the
+    # (256, 64, 14, 14) grad and writes the fp32 input gradient; GlobalAvgPool2d
+    # reads the (256, 64) grad and writes the input gradient
+    gy = torch.randn((256, 64, 14, 14), generator=g, device=dev)
+    for name, x, dt in (("f32", x32, _lib.F32), ("bf16", x32.to(torch.bfloat16), _lib.BF16)):
+        gi = torch.empty((256, 64, 28, 28), device=dev)
+        fn = lambda x=x, gi=gi, dt=dt: _lib.check(lib.novaq_max_pool2d_backward(  # noqa: E731
+            gy.data_ptr(), x.data_ptr(), dt, 256, 64, 28, 28, 2, 2, 2, 2, 0, 0, 0,
+            gi.data_ptr(), stream), "max_pool2d_backward")
+        ms = _timed_flush(dev, fn, iters, warmup)
+        nb = x.numel() * x.element_size() + gy.numel() * 4 + gi.numel() * 4
+        out.append({"op": f"max_pool2d_backward 2x2/2 (256,64,28,28) x {name}",
+                    "ms": round(ms, 4), "GB/s": round(nb / (ms * 1e-3) / 1e9, 1),
+                    "frac": round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
+    gp = torch.randn((256, 64), generator=g, device=dev)
+    gi = torch.empty((256, 64, 28, 28), device=dev)
+    fn = lambda: _lib.check(lib.novaq_global_avg_pool2d_backward(  # noqa: E731
+        gp.data_ptr(), 256, 64, 28, 28, gi.data_ptr(), stream), "avg_pool2d_backward")
+    ms = _timed_flush(dev, fn, iters, warmup)
+    nb = (gp.numel() + gi.numel()) * 4
+    out.append({"op": "global_avg_pool2d_backward (256, 64, 28, 28) f32", "ms": round(ms, 4),
+                "GB/s": round(nb / (ms * 1e-3) / 1e9, 1),
+                "frac": round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
+    return {"workload": "pools on config [5]-sized and main.py activations (forward and backward)",
+            "kernels": out}
 
 
 def bench_extras(dev, iters: int = 20, warmup: int = 3):
