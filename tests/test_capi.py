@@ -79,6 +79,19 @@ def test_other_entry_points_validation():
     assert conv(FAKE, 1, 1, 8, 8, FAKE, 3, None, 2, 3, 3, 0, 1, 1, 1, 0, None, FAKE, None) == _lib.EINVAL
     assert conv(FAKE, 1, 1, 2, 2, FAKE, 3, None, 2, 5, 5, 1, 1, 0, 0, 0, None, FAKE, None) == _lib.ESHAPE
     assert conv(FAKE, 1, 1, 8, 8, FAKE, 9, None, 2, 3, 3, 1, 1, 1, 1, 0, None, FAKE, None) == _lib.EDTYPE
+    # pool backward passes: dtype, pad mode, window larger than the padded
+    # input, alignment, an empty batch
+    mpb = lib.novaq_max_pool2d_backward
+    assert mpb(FAKE, FAKE, 5, 1, 1, 4, 4, 2, 2, 2, 2, 0, 0, 0, FAKE, None) == _lib.EDTYPE
+    assert mpb(FAKE, FAKE, 0, 1, 1, 4, 4, 2, 2, 2, 2, 0, 0, 7, FAKE, None) == _lib.EPADMODE
+    assert mpb(FAKE, FAKE, 0, 1, 1, 1, 1, 2, 2, 2, 2, 0, 0, 0, FAKE, None) == _lib.ESHAPE
+    assert mpb(FAKE + 2, FAKE, 0, 1, 1, 4, 4, 2, 2, 2, 2, 0, 0, 0, FAKE, None) == _lib.EALIGN
+    assert mpb(FAKE, FAKE + 1, 2, 1, 1, 4, 4, 2, 2, 2, 2, 0, 0, 0, FAKE, None) == _lib.EALIGN
+    assert mpb(None, None, 0, 0, 1, 4, 4, 2, 2, 2, 2, 0, 0, 0, None, None) == _lib.OK
+    gpb = lib.novaq_global_avg_pool2d_backward
+    assert gpb(FAKE, 1, 1, 0, 4, FAKE, None) == _lib.EINVAL
+    assert gpb(FAKE, 1, 1, 4, 4, FAKE + 1, None) == _lib.EALIGN
+    assert gpb(None, 0, 1, 4, 4, None, None) == _lib.OK
 
 
 def test_backward_entry_points_validation():
