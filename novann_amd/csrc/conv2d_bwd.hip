@@ -28,7 +28,10 @@
 //     first j block also the per-channel grad sums of its chunk (grad_bias);
 //   - finish_kernel: one launch that adds the chunk partials in a fixed order
 //     (novaq_colsum.h's column sum, so results do not depend on scheduling;
-//     16 columns a workgroup with one input channel, else 64)
+//     16 columns a workgroup with one input channel, else 64); with one input
+//     channel and grad_input on the one-output-channel kernel, c1_tail_kernel
+//     instead: the same sums beside grad_input's bands, the weight read
+//     flipped in place
 //     for grad_weight and grad_bias, and flips the weights for grad_input;
 //     grad_input's convolution runs after it.
 #include <hip/hip_runtime.h>
@@ -37,6 +40,7 @@
 #include <algorithm>
 #include <mutex>
 
+#include "conv2d_impl.h"
 #include "novaq_colsum.h"
 #include "novaq_convert.h"
 #include "novaq_internal.h"
@@ -122,6 +126,33 @@ __global__ __launch_bounds__(1024) void finish_kernel(FinishArgs a, int C_out, i
 struct BwdGeom {
   int N, C, H, W, C_out, KH, KW, sh, sw, ph, pw, pad_mode, OH, OW;
 };
+
+// The last launch of a one-input-channel backward whose grad_input runs on
+// the one-output-channel kernel: blocks [0, a.wb + a.bb) sum the partials
+// (4 columns a 256-lane workgroup over the 64 row slices finish_kernel<WT,
+// 16> uses: the same sums bit for bit), the rest are grad_input's bands --
+// that kernel over grad with the weight read flipped in place, so no flip
+// waits for the sums -- and the latency-bound sums hide under the bands.
+template <int WT>
+__global__ __launch_bounds__(256) void c1_tail_kernel(FinishArgs a, const float* __restrict__ grad,
+                                                      const uint8_t* __restrict__ w,
+                                                      const float* __restrict__ w_scale,
+                                                      float* __restrict__ gi, Co1Geom cg) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t t_lds[];
+  const unsigned b = blockIdx.x;
+  if (b < a.wb + a.bb) {
+    auto part = reinterpret_cast<float(*)[4]>(t_lds);  // 64 x 4 floats
+    if (b < a.wb)
+      colsum_block<4, 64>(a.part, a.rows, a.wcols, a.gw, a.pt, a.pco, a.pc, b, part);
+    else
+      colsum_block<4, 64>(a.bpart, a.rows, a.bcols, a.gb, 0, 0, 0, b - a.wb, part);
+    return;
+  }
+  Epilogue ep{};
+  ep.out_dtype = F32;
+  co1_body<WT, F32, true>(reinterpret_cast<const uint8_t*>(grad), nullptr, w, w_scale, ep, gi,
+                          cg, (int)(b - a.wb - a.bb), t_lds);
+}
 
 // grad_input, one element per thread, fp32 accumulation over (kh, kw, co).
 template <int WT>
@@ -1075,6 +1106,36 @@ int launch_finish(FinishArgs a, int wt, const BwdGeom& g, hipStream_t stream) {
   return g.C == 1 ? launch_finish_cols<16>(a, wt, g, stream) : launch_finish_cols<64>(a, wt, g, stream);
 }
 
+// grad_input of a one-input-channel convolution as the one-output-channel
+// kernel's convolution of grad (N, C_out, OH, OW) -> (N, 1, H, W) with the
+// flipped weight and zero padding (KH-1-ph, KW-1-pw): its band geometry, or
+// false when that convolution would run on another kernel (a few output
+// channels of the layer, C_out <= SC_MAX_C, take the small-channel kernel).
+bool c1_tail_geometry(const BwdGeom& g, Co1Geom& cg, size_t& lds) {
+  if (g.C != 1 || !flip_path(g) || g.C_out <= SC_MAX_C) return false;
+  ConvGeom fg{};
+  fg.N = g.N; fg.C = g.C_out; fg.H = g.OH; fg.W = g.OW; fg.C_out = 1;
+  fg.KH = g.KH; fg.KW = g.KW; fg.sh = 1; fg.sw = 1;
+  fg.ph = g.KH - 1 - g.ph; fg.pw = g.KW - 1 - g.pw; fg.pad_mode = NOVAQ_PAD_ZEROS;
+  fg.OH = g.H; fg.OW = g.W;
+  return co1_geometry(fg, cg, lds);
+}
+
+template <int WT>
+int launch_c1_tail(FinishArgs a, const float* grad, const void* w, const float* w_scale,
+                   float* gi, const BwdGeom& g, const Co1Geom& cg, size_t lds,
+                   hipStream_t stream) {
+  const int64_t wb = (a.wcols + 3) / 4, bb = (a.bcols + 3) / 4;
+  const int64_t blocks = wb + bb + (int64_t)g.N * cg.bands;
+  if (blocks > 0x7FFFFFFF) return NOVAQ_EINVAL;
+  a.wb = (unsigned)wb;
+  a.bb = (unsigned)bb;
+  hipLaunchKernelGGL(c1_tail_kernel<WT>, dim3((unsigned)blocks), dim3(256),
+                     std::max(lds, (size_t)(64 * 4 * sizeof(float))), stream, a, grad,
+                     static_cast<const uint8_t*>(w), w_scale, gi, cg);
+  return check_launch();
+}
+
 // wf holds the flipped weights when flip_path(g) (the finishing launch wrote
 // them); the direct kernel covers the rest.
 template <int WT>
@@ -1298,9 +1359,23 @@ int conv2d_backward_launch(const float* grad, const float* x, int64_t N, int64_t
   FinishArgs fa{};
   fa.w = static_cast<const uint8_t*>(w_q);
   fa.wf = static_cast<uint8_t*>(wf);
-  fa.flip_items = grad_input && N > 0 && flip_path(g) ? flip_items(g, w_dtype) : 0;
+  // one input channel: the sums and grad_input in one last launch (no flip)
+  Co1Geom cg{};
+  size_t co1_lds = 0;
+  const bool tail = grad_input && N > 0 && c1_tail_geometry(g, cg, co1_lds);
+  fa.flip_items = grad_input && N > 0 && flip_path(g) && !tail ? flip_items(g, w_dtype) : 0;
   rc = dweight_launch(grad, x, g, chunks, ws, base, grad_weight, grad_bias, fa, stream);
   if (rc != NOVAQ_OK) return rc;
+  if (tail) {
+    switch (w_dtype) {
+      case E4M3: return launch_c1_tail<E4M3>(fa, grad, w_q, w_scale, grad_input, g, cg, co1_lds, stream);
+      case E5M2: return launch_c1_tail<E5M2>(fa, grad, w_q, w_scale, grad_input, g, cg, co1_lds, stream);
+      case E2M1: return launch_c1_tail<E2M1>(fa, grad, w_q, w_scale, grad_input, g, cg, co1_lds, stream);
+      case BF16: return launch_c1_tail<BF16>(fa, grad, w_q, w_scale, grad_input, g, cg, co1_lds, stream);
+      case F16: return launch_c1_tail<F16>(fa, grad, w_q, w_scale, grad_input, g, cg, co1_lds, stream);
+      default: return launch_c1_tail<F32>(fa, grad, w_q, w_scale, grad_input, g, cg, co1_lds, stream);
+    }
+  }
   rc = launch_finish(fa, w_dtype, g, stream);
   if (rc != NOVAQ_OK || !grad_input || N == 0) return rc;
   switch (w_dtype) {

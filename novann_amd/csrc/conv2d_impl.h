@@ -1147,17 +1147,25 @@ struct Co1Geom {
 constexpr int CO1_MT = 8;   // pixel tiles per wave, at most (512 staged pixels)
 constexpr int CO1_YP = 17;  // fp32 pitch of a staged pixel's Y row (odd: fewer bank conflicts)
 
-template <int WT, int XT>
-__global__ __launch_bounds__(256) void conv2d_co1_kernel(
-    const uint8_t* __restrict__ x, const float* __restrict__ x_scale, const uint8_t* __restrict__ w,
-    const float* __restrict__ w_scale, Epilogue ep, void* __restrict__ y, Co1Geom g) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+//
+// The body takes its band index (bid) and LDS from the caller, so a launch
+// can run it beside other work.  FLIP1: w holds the weights of the
+// one-input-channel convolution whose input gradient this is, (C, 1, KH, KW),
+// and tap t of channel c is read at c * taps + (taps - 1 - t) -- the flipped
+// weight without a flipped copy.
+template <int WT, int XT, bool FLIP1>
+__device__ __forceinline__ void co1_body(const uint8_t* __restrict__ x,
+                                         const float* __restrict__ x_scale,
+                                         const uint8_t* __restrict__ w,
+                                         const float* __restrict__ w_scale, const Epilogue& ep,
+                                         void* __restrict__ y, const Co1Geom& g, int bid,
+                                         uint8_t* lds) {
   const int WS = g.ksteps * 32 + 8;                                 // Ws row pitch (bf16)
   uint16_t* ws = reinterpret_cast<uint16_t*>(lds);                 // [16 taps][WS]
   uint16_t* xs = ws + 16 * WS;                                     // [npin][cstride]
   float* ys = reinterpret_cast<float*>(xs);                        // [npin][CO1_YP] (after the products)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int band = blockIdx.x % g.bands, n = blockIdx.x / g.bands;
+  const int band = bid % g.bands, n = bid / g.bands;
   const int oh0 = band * g.R;
   const int64_t HW = (int64_t)g.H * g.W;
   const int64_t xn = (int64_t)n * g.C * HW;
@@ -1186,7 +1194,9 @@ __global__ __launch_bounds__(256) void conv2d_co1_kernel(
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const int i = tid + 256 * k;
-    wv[k] = i < g.C * g.taps ? weight_bf16<WT>(w, i) : (uint16_t)0;
+    int src = i;
+    if constexpr (FLIP1) src = i + g.taps - 1 - 2 * (i % g.taps);
+    wv[k] = i < g.C * g.taps ? weight_bf16<WT>(w, src) : (uint16_t)0;
   }
   // zero the staging (padding columns, channels past C), then the weights as
   // Ws[t][c] (bf16, taps and channels past the window 0)
@@ -1272,6 +1282,14 @@ __global__ __launch_bounds__(256) void conv2d_co1_kernel(
     epi_store(ep.out_dtype, y, (int64_t)n * g.OH * g.OW + (int64_t)oh0 * g.OW + tid, val, inv_o);
   }
   epi_amax_commit(ep, am);
+}
+
+template <int WT, int XT>
+__global__ __launch_bounds__(256) void conv2d_co1_kernel(
+    const uint8_t* __restrict__ x, const float* __restrict__ x_scale, const uint8_t* __restrict__ w,
+    const float* __restrict__ w_scale, Epilogue ep, void* __restrict__ y, Co1Geom g) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  co1_body<WT, XT, false>(x, x_scale, w, w_scale, ep, y, g, blockIdx.x, lds);
 }
 
 // The one-output-channel geometry, or false when it does not apply.

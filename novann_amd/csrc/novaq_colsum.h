@@ -5,10 +5,11 @@
 // SLICES row slices is summed in four chains (row r of a slice goes to chain
 // r % 4, in row order), the chains are added (0 + 1) + (2 + 3), then the
 // slices in slice order, so repeated calls with the same shape agree bit for
-// bit.  A workgroup of COLS x SLICES = 1024 lanes owns COLS columns: 64 by
-// default (a wave's load reads 256 contiguous bytes of one row); 16 with 64
-// slices for few columns over many rows (a quarter of the rows per lane).
-// With pt > 0 the columns form a (pt, pco, pc) array and column (t, co, c)
+// bit.  A workgroup of COLS x SLICES lanes (1024, or 256) owns COLS columns:
+// 64 by default (a wave's load reads 256 contiguous bytes of one row); 16
+// with 64 slices for few columns over many rows (a quarter of the rows per
+// lane), or 4 with 64 slices in a 256-lane workgroup -- the same slices, so
+// the same sums bit for bit.  With pt > 0 the columns form a (pt, pco, pc) array and column (t, co, c)
 // is stored at out[(co * pc + c) * pt + t].
 #pragma once
 
@@ -26,7 +27,7 @@ template <int COLS = CS_COLS, int SLICES = CS_SLICES>
 __device__ inline void colsum_block(const float* __restrict__ x, int64_t rows, int64_t cols,
                                     float* __restrict__ out, int pt, int pco, int pc,
                                     int64_t blk, float (*part)[COLS]) {
-  static_assert(COLS * SLICES == 1024, "a workgroup of 1024 lanes");
+  static_assert(COLS * SLICES == 1024 || COLS * SLICES == 256, "a workgroup of 1024 or 256 lanes");
   const int tx = threadIdx.x % COLS, ty = threadIdx.x / COLS;
   const int64_t c = blk * COLS + tx;
   const int64_t per = (rows + SLICES - 1) / SLICES;
