@@ -1,8 +1,9 @@
 """novaq_conv2d_backward_noalloc (the allocation-free Conv2d backward, its
 workspace a static device array) against novaq_conv2d_backward with a
 caller-allocated workspace, through the C ABI: the same kernels, so all three
-gradients are bit-identical, on two calls in a row (the second smaller, so it
-runs over what the first left in the shared scratch), and a request beyond
+gradients are bit-identical, on three calls in a row (the second smaller, so it
+runs over what the first left in the shared scratch; the third with one input
+channel, whose sums and grad_input share one launch), and a request beyond
 the scratch's 32 MiB is refused with NOVAQ_ESCRATCH before any launch."""
 import numpy as np
 import pytest
@@ -53,8 +54,10 @@ def inputs(geo, seed):
 
 
 # config [5]'s conv2 at batch 256 (30.8 MB of the 32 MiB scratch), then a
-# smaller, differently shaped call (stride 2, reflect: the general kernels)
-CALLS = [(256, 32, 28, 28, 64, 3, 1, 1, "zeros"), (3, 5, 11, 9, 7, 3, 2, 1, "reflect")]
+# smaller, differently shaped call (stride 2, reflect: the general kernels),
+# then config [5]'s conv1 (one input channel: the one-input-channel kernels)
+CALLS = [(256, 32, 28, 28, 64, 3, 1, 1, "zeros"), (3, 5, 11, 9, 7, 3, 2, 1, "reflect"),
+         (256, 1, 28, 28, 32, 3, 1, 1, "zeros")]
 
 
 def test_noalloc_matches_workspace_entry_point_twice():
