@@ -235,3 +235,43 @@ def test_extras_random_geometries(seed):
         wwant, _, _, _ = R.pool_windows(dec, (KH, KW), (sh, sw), (ph, pw), mode)
         got = wv.contiguous().cpu().numpy()
         assert np.array_equal(got.view(np.uint32), np.ascontiguousarray(wwant).view(np.uint32)), case
+
+
+@pytest.mark.parametrize("seed", SEEDS)
+def test_pool_backward_random_shapes_bit_exact(seed):
+    """MaxPool2d and GlobalAvgPool2d backward on random maps, windows, strides,
+    paddings and padding modes (every third case on a coarse value grid, so
+    windows hold ties; 2x2 stride-2 cases on even maps take the tile path),
+    bit for bit against the restatements (NaN compared as NaN)."""
+    rng = np.random.default_rng(seed + 700)
+    for i in range(20):
+        N, C = int(rng.integers(1, 4)), int(rng.integers(1, 12))
+        if i % 4 == 0:
+            H, W = 2 * int(rng.integers(1, 20)), 2 * int(rng.integers(1, 20))
+            k, st, pd, mode = (2, 2), (2, 2), (0, 0), "zeros"
+        else:
+            H, W = int(rng.integers(1, 40)), int(rng.integers(1, 40))
+            k = (int(rng.integers(1, min(H, 4) + 1)), int(rng.integers(1, min(W, 4) + 1)))
+            st = (int(rng.integers(1, 4)), int(rng.integers(1, 4)))
+            mode = str(rng.choice(MODES))
+            # reflect pads at most size - 1 (numpy.pad's rule)
+            pd = (int(rng.integers(0, min(k[0] // 2, H - 1) + 1)),
+                  int(rng.integers(0, min(k[1] // 2, W - 1) + 1)))
+        if i % 3 == 0:
+            x = rng.choice(np.array([-0.0, 0.0, 0.5, 1.0, 1.0, -2.0], np.float32), (N, C, H, W))
+        else:
+            x = rng.standard_normal((N, C, H, W)).astype(np.float32)
+        OH = (H + 2 * pd[0] - k[0]) // st[0] + 1
+        OW = (W + 2 * pd[1] - k[1]) // st[1] + 1
+        g = rng.standard_normal((N, C, OH, OW)).astype(np.float32)
+        print(f"pool backward seed {seed} case {i}: {(N, C, H, W)} max {k} {st} {pd} {mode}",
+              flush=True)
+        got = F.max_pool2d_backward(g, x, k, st, pd, mode)
+        want = R.max_pool2d_backward(g, x, k, st, pd, mode)
+        nan = np.isnan(want)
+        assert np.array_equal(np.isnan(got), nan)
+        assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+        gp = rng.standard_normal((N, C, 1, 1)).astype(np.float32)
+        got = F.avg_pool2d_backward(gp, (N, C, H, W))
+        want = R.global_avg_pool2d_backward(gp, (N, C, H, W))
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
