@@ -152,3 +152,31 @@ def test_c_abi_refusals():
                                                 st) == _lib.EINVAL
     torch.cuda.synchronize()
     assert torch.isnan(gi).all()  # nothing launched
+
+
+@pytest.mark.parametrize("xt,off_x,off_g,off_gi", [("f32", 1, 0, 0), ("f32", 0, 1, 2),
+                                                    ("f32", 3, 1, 1), ("bf16", 1, 0, 3),
+                                                    ("e4m3", 3, 1, 0)])
+def test_max_pool2d_backward_element_offset_views(xt, off_x, off_g, off_gi):
+    """x, grad and grad_input as views some elements into larger buffers on a
+    2x2 stride-2 map: buffers the vector path cannot take run the general
+    kernel, with the same bits."""
+    print(f"max_pool2d_backward views {xt} +{off_x} +{off_g} +{off_gi}", flush=True)
+    rng = np.random.default_rng(off_x * 100 + off_g * 10 + off_gi)
+    shape, oshape = (2, 3, 8, 12), (2, 3, 4, 6)
+    n, no = int(np.prod(shape)), int(np.prod(oshape))
+    v = tied(rng, (n + off_x,))
+    v[np.isnan(v)] = 0.5
+    codes = v.view(np.uint32) if xt == "f32" else O.cast(v, O.F32, CODE[xt])
+    dec = (v if xt == "f32" else O.cast(codes, CODE[xt], O.F32))[off_x:].reshape(shape)
+    xbuf = to_dev(codes, CODE[xt])
+    g = grads(rng, (no + off_g,))
+    gbuf = torch.from_numpy(g).cuda()
+    gibuf = torch.full((n + off_gi,), np.nan, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    rc = _lib.load().novaq_max_pool2d_backward(gbuf[off_g:].data_ptr(), xbuf[off_x:].data_ptr(),
+                                               CODE[xt], *shape, 2, 2, 2, 2, 0, 0, 0,
+                                               gibuf[off_gi:].data_ptr(), stream)
+    assert rc == _lib.OK
+    got = gibuf[off_gi:].cpu().numpy().reshape(shape)
+    same_bits_or_nan(got, R.max_pool2d_backward(g[off_g:].reshape(oshape), dec, 2, 2))
